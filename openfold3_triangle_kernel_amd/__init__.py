@@ -1,0 +1,21 @@
+"""TurboPairFormer triangle attention and triangle multiplicative update on MI355X.
+
+From-scratch gfx950 implementation of the two TurboPairFormer operators behind
+OpenFold3's TriangleAttention / TriangleMultiplicativeUpdate modules.  All
+compute runs in hand-written HIP kernels in ``libtpf_amd.so`` (C ABI,
+``include/tpf_amd.h``); there is no CPU or PyTorch fallback.
+"""
+
+from .attention import (
+    invocation_count,
+    is_turbopairformer_supported,
+    turbo_attention,
+    turbopairformer_triangle_attention,
+)
+
+__all__ = [
+    "invocation_count",
+    "is_turbopairformer_supported",
+    "turbo_attention",
+    "turbopairformer_triangle_attention",
+]

@@ -1,0 +1,89 @@
+"""ctypes binding of the gfx950 C-ABI library ``libtpf_amd.so``.
+
+The library is the only compute path: there is no CPU or PyTorch fallback.
+Loading fails with a RuntimeError naming the missing file when the library
+has not been built, and every entry point's status code is turned into a
+RuntimeError carrying the library's own message.
+
+Loading is behind a lock and cached per process, mirroring the fail-closed
+loader of the reference (openfold3/core/kernels/turbopairformer/_aot_runtime.py:752-800),
+without its manifest/hash attestation (the library is built in-tree).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libtpf_amd.so"
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F64 = ctypes.c_double
+
+# name -> (restype, argtypes).  Must match include/tpf_amd.h.
+SIGNATURES: dict[str, tuple] = {
+    "tpf_abi_version": (_I32, []),
+    "tpf_last_error": (ctypes.c_char_p, []),
+    "tpf_attn_forward_bf16": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I64, _F64, _P],
+    ),
+    "tpf_attn_delta_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
+    "tpf_attn_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "tpf_attn_backward_bf16": (
+        _I32,
+        [_P] * 13 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
+}
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return the C-ABI library; raise if it is not built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"TurboPairFormer MI355X library not built: {LIB_PATH} is missing "
+                    "(run `python -m openfold3_triangle_kernel_amd.build`)"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _LIB = lib
+    return _LIB
+
+
+def call(name: str, *args) -> int:
+    """Invoke an entry point and raise RuntimeError on a non-zero status."""
+    lib = library()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.tpf_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+    return rc
+
+
+def query(name: str, *args):
+    """Invoke a value-returning entry point (sizes, versions)."""
+    return getattr(library(), name)(*args)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream

@@ -1,0 +1,99 @@
+// Shared device helpers for the gfx950 (CDNA4) TurboPairFormer kernels.
+//
+// Everything here is written for 64-lane wavefronts and the gfx950 bf16 MFMA
+// instructions (v_mfma_f32_32x32x16_bf16).  Operand layouts of that
+// instruction, as used by every kernel in this library:
+//
+//   A (32 x 16, row-major in k):  lane l holds A[l % 32][8*(l/32) .. +8]
+//   B (16 x 32, col-major in k):  lane l holds B[8*(l/32) .. +8][l % 32]
+//   C (32 x 32):                  lane l, register r holds
+//                                 C[8*(r/4) + 4*(l/32) + (r%4)][l % 32]
+//
+// The k index is a pure summation index, so any permutation applied to both
+// A and B gives the same product; the attention kernels use this to feed a
+// C-layout tile straight back in as a B operand without moving data.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tpf {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ float bf2f(u16 h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ float bf2f(__bf16 h) { return static_cast<float>(h); }
+
+// Round-to-nearest-even f32 -> bf16 (hardware v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ __bf16 f2bf(float f) { return static_cast<__bf16>(f); }
+__device__ __forceinline__ u16 f2bf_bits(float f) {
+  __bf16 h = static_cast<__bf16>(f);
+  return *reinterpret_cast<u16*>(&h);
+}
+
+// Exchange with lane l ^ 32 through v_permlane32_swap; returns the pair
+// (lower-half value, upper-half value) so symmetric reductions combine the
+// two in the same order on both halves (bitwise identical results).
+__device__ __forceinline__ float xor32_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// 16-byte global load/store of 8 bf16 values.
+__device__ __forceinline__ bf16x8 ld8(const __bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+__device__ __forceinline__ void st8(__bf16* p, bf16x8 v) {
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+__device__ __forceinline__ bf16x4 ld4(const __bf16* p) {
+  return *reinterpret_cast<const bf16x4*>(p);
+}
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = static_cast<__bf16>(0.f);
+  return z;
+}
+
+// Pack registers r0..r0+7 of a C-layout tile into a bf16 B operand.
+__device__ __forceinline__ bf16x8 pack8(const f32x16& c, int r0) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f2bf(c[r0 + e]);
+  return o;
+}
+
+}  // namespace tpf
