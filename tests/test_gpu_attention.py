@@ -41,7 +41,7 @@ def _run(case, dev, seq_major=False):
     out = turbopairformer_triangle_attention(tq, tk, tv, mask.to(dev), tb)
     out.backward(dout.to(dev, torch.bfloat16))
     torch.cuda.synchronize()
-    return [t.float().cpu().numpy() for t in (out, tq.grad, tk.grad, tv.grad, tb.grad)]
+    return [t.detach().float().cpu().numpy() for t in (out, tq.grad, tk.grad, tv.grad, tb.grad)]
 
 
 @pytest.mark.gpu
