@@ -19,3 +19,7 @@ __all__ = [
     "turbo_attention",
     "turbopairformer_triangle_attention",
 ]
+
+from .trimul import check_stable_trimul_support, run_stable_trimul, turbo_trimul  # noqa: E402
+
+__all__ += ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]

@@ -1,0 +1,24 @@
+// Internal interface of the batched MFMA GEMM (csrc/gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tpf {
+
+struct GemmArgs {
+  const __bf16* A; int64_t a_bs, a_ld;   // batch stride, leading dimension
+  const __bf16* B; int64_t b_bs, b_ld;
+  void* C; int64_t c_bs, c_ld, c_split;  // c_split: element offset between K splits
+  int M, N, K;
+  int ksplit, k_chunk;                   // K range of split s: [s*k_chunk, (s+1)*k_chunk)
+  float alpha;
+};
+
+// a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).
+int gemm_launch(const GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch,
+                hipStream_t stream, const char* fn);
+int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
+                hipStream_t stream, const char* fn);
+
+}  // namespace tpf
