@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the TurboPairFormer hot path on one MI355X.
+
+Metric: tri-attn fwd+bwd ms & TFLOP/s at N=384, H=4, D=32
+bf16; TriMul fwd+bwd ms.
+
+A step is one pass of the hot path over one batch of synthetic input:
+  * triangle attention fwd+bwd, starting node and ending node (config 3:
+    q, k, v [1,384,4,384,32] ~ N(0,1), pair_bias 2*N(0,1) [1,1,4,384,384],
+    res_mask with a random 0-32 key -inf tail per outer row; the ending node
+    runs the same op on the pair transposed over its two N axes, with the
+    bias as a transposed view);
+  * TriMul outgoing + incoming fwd+bwd (config 4: z [1,384,384,128] ~ N(0,1),
+    LN weights 1/0, projections ~ N(0, 1/sqrt(128)), mask all ones), timed
+    as its own loop and reported under "trimul".
+``value`` is the attention fwd+bwd throughput in algorithmic TFLOP/s
+(14*B*O*H*N^2*D per variant), inputs resident in HBM before timing.
+
+Also reported: the roofline of the dominant kernel (the attention backward
+kernel, timed alone with HIP events on the launching stream) and a CPU
+baseline (the numpy oracle on a bounded sample of the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+HBM_PEAK_GBPS = 8000.0           # MI355X HBM3E
+
+B, O, H, N, D = 1, 384, 4, 384, 32
+TM_N, TM_C = 384, 128
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-trimul", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    return ap.parse_args()
+
+
+def attention_inputs(torch, dev, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q, k, v = (torch.randn(B, O, H, N, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    bias = (torch.randn(1, 1, H, N, N, device=dev, generator=g) * 2).to(torch.bfloat16)
+    tails = torch.randint(0, 33, (B, O), device=dev, generator=g)
+    ar = torch.arange(N, device=dev)
+    mask = torch.where(ar[None, None, :] >= (N - tails)[..., None], float("-inf"), 0.0)
+    mask = mask.reshape(B, O, 1, 1, N).float()
+    dout = torch.randn(B, O, N, H, D, device=dev, generator=g).to(torch.bfloat16)
+    return q, k, v, bias, mask, dout
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported; this build measures one MI355X "
+            "(the hot path has no collectives; see DESIGN.md for how it would shard)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from openfold3_triangle_kernel_amd import _native, turbo_trimul, turbopairformer_triangle_attention
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---------------- attention: starting + ending node -----------------
+    q, k, v, bias, mask, dout = attention_inputs(torch, dev)
+    # Ending node: the same op on the pair transposed over its two N axes.
+    qe, ke, ve = (t.transpose(1, 3).contiguous() for t in (q, k, v))
+    mask_e = mask.clone()
+    bias_e = bias.transpose(-1, -2)  # transposed view (reference transpose_bias path)
+    dout_e = dout.clone()
+    variants = [
+        [t.detach().requires_grad_(True) for t in (q, k, v)] + [bias.detach().requires_grad_(True), mask, dout],
+        [t.detach().requires_grad_(True) for t in (qe, ke, ve)]
+        + [bias_e.detach().requires_grad_(True), mask_e, dout_e],
+    ]
+
+    def attn_step():
+        for vq, vk, vv, vb, vm, vd in variants:
+            out = turbopairformer_triangle_attention(vq, vk, vv, vm, vb)
+            torch.autograd.grad(out, (vq, vk, vv, vb), vd)
+
+    for _ in range(args.warmup):
+        attn_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        attn_step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3 / args.steps
+    ms_step = e0.elapsed_time(e1) / args.steps
+    attn_flops = 2 * 14.0 * B * O * H * N * N * D  # two variants
+    attn_tflops = attn_flops / (ms_step * 1e-3) / 1e12
+
+    # Forward-only timing (starting node) for the breakdown.
+    with torch.no_grad():
+        for _ in range(3):
+            turbopairformer_triangle_attention(q, k, v, mask, bias)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            turbopairformer_triangle_attention(q, k, v, mask, bias)
+        e1.record()
+        torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / args.steps
+
+    # ------------- dominant kernel: attention backward, alone -------------
+    stream = torch.cuda.current_stream().cuda_stream
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty(B, O, N, H, D, device=dev, dtype=torch.bfloat16)
+    lse = torch.empty(B, O, H, N, device=dev, dtype=torch.float32)
+    delta = torch.empty_like(lse)
+    mflat = mask.reshape(B, O, N).contiguous()
+    bflat = bias.reshape(1, H, N, N).contiguous()
+    _native.call("tpf_attn_forward_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), mflat.data_ptr(),
+                 bflat.data_ptr(), out.data_ptr(), lse.data_ptr(), B, O, H, N, D, 0, 1, scale, stream)
+    _native.call("tpf_attn_delta_bf16", dout.data_ptr(), out.data_ptr(), delta.data_ptr(), B, O, H, N, D,
+                 stream)
+    dk, dv = torch.empty_like(q), torch.empty_like(q)
+    ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+
+    def bwd_main():
+        _native.call("tpf_attn_backward_main_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                     dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), mflat.data_ptr(),
+                     bflat.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
+                     B, O, H, N, D, 0, 1, scale, stream)
+
+    for _ in range(3):
+        bwd_main()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.kernel_reps):
+        bwd_main()
+    e1.record()
+    torch.cuda.synchronize()
+    bwd_kernel_ms = e0.elapsed_time(e1) / args.kernel_reps
+    bwd_flops = 10.0 * B * O * H * N * N * D
+    achieved = bwd_flops / (bwd_kernel_ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": "attn_bwd_kernel<32>",
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "avg_launch_us": round(bwd_kernel_ms * 1e3, 2),
+        "flops_per_launch": bwd_flops,
+    }
+
+    # --------------------------- TriMul ----------------------------------
+    trimul = None
+    if not args.no_trimul:
+        g = torch.Generator(device=dev).manual_seed(1)
+        C = TM_C
+        z = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+        sd = 1.0 / math.sqrt(C)
+        wts = dict(
+            norm_in_weight=torch.ones(C, device=dev), norm_in_bias=torch.zeros(C, device=dev),
+            p_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
+            g_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
+            norm_out_weight=torch.ones(C, device=dev), norm_out_bias=torch.zeros(C, device=dev),
+            p_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
+            g_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
+        )
+        wts = {kk: vv.requires_grad_(True) for kk, vv in wts.items()}
+        tm_mask = torch.ones(1, TM_N, TM_N, device=dev)
+        tm_dout = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16)
+        params = [z] + list(wts.values())
+
+        def tm_step():
+            for direction in ("outgoing", "incoming"):
+                o = turbo_trimul(z, direction, tm_mask, **wts)
+                torch.autograd.grad(o, params, tm_dout)
+
+        for _ in range(args.warmup):
+            tm_step()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            tm_step()
+        e1.record()
+        torch.cuda.synchronize()
+        tm_ms = e0.elapsed_time(e1) / args.steps
+        R = TM_N * TM_N
+        tm_fwd_flops = 2.0 * R * C * 5 * C + 2.0 * C * TM_N ** 3 + 2.0 * R * C * C
+        tm_flops = 2 * 3 * tm_fwd_flops
+        trimul = {
+            "ms_fwd_bwd_out_plus_in": round(tm_ms, 4),
+            "tflops": round(tm_flops / (tm_ms * 1e-3) / 1e12, 2),
+            "flops": tm_flops,
+            "config": {"N": TM_N, "C": C, "H": C, "directions": ["outgoing", "incoming"]},
+        }
+
+    # -------------------------- CPU baseline -----------------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+
+    line = {
+        "metric": "tri-attn fwd+bwd ms & TFLOP/s (N=384,H=4,D=32 bf16); TriMul fwd+bwd ms",
+        "value": round(attn_tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs of the config-3/config-4 shapes)",
+        "config": {
+            "workload": "triangle attention fwd+bwd, starting + ending node (config 3)",
+            "B": B, "O": O, "H": H, "N": N, "D": D,
+            "parallelism": "single GPU",
+        },
+        "attention": {
+            "ms_fwd_bwd_start_plus_end": round(ms_step, 4),
+            "ms_fwd_start": round(fwd_ms, 4),
+            "host_wall_ms_per_step": round(wall_ms, 4),
+            "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        },
+        "trimul": trimul,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline():
+    """The numpy oracle (fp32) on a bounded sample of the attention workload:
+    the same N=384, H=4, D=32 planes, fwd+bwd, on a subset of outer rows."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle.attention import attention_backward, attention_forward
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = 1
+    o_sample = 8
+    rng = np.random.default_rng(0)
+    q, k, v = (rng.standard_normal((1, o_sample, H, N, D)).astype(np.float32) for _ in range(3))
+    bias = (2 * rng.standard_normal((1, 1, H, N, N))).astype(np.float32)
+    mask = np.zeros((1, o_sample, 1, 1, N), np.float32)
+    dout = rng.standard_normal((1, o_sample, N, H, D)).astype(np.float32)
+    flops = 14.0 * o_sample * H * N * N * D
+    attention_forward(q, k, v, mask, bias, dtype=np.float32)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        attention_forward(q, k, v, mask, bias, dtype=np.float32)
+        attention_backward(q, k, v, mask, bias, dout, dtype=np.float32)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 50:
+            break
+    sec = el / reps
+    return {
+        "value": round(flops / sec / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"numpy fp32 oracle, attention fwd+bwd, {o_sample} of 384 outer rows at N=384 H=4 D=32, "
+                  f"{reps} reps in {el:.1f} s ({sec * 1e3:.1f} ms/rep)",
+        "ms_full_step_extrapolated": round(sec * (O / o_sample) * 2 * 1e3, 1),
+    }
+
+
+if __name__ == "__main__":
+    main()

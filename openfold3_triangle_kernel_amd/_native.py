@@ -39,6 +39,14 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P] * 13 + [_I64] * 6 + [_I32, _I64, _F64, _P],
     ),
+    "tpf_attn_backward_main_bf16": (
+        _I32,
+        [_P] * 11 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
+    "tpf_attn_backward_finish_bf16": (
+        _I32,
+        [_P, _P, _P] + [_I64] * 5 + [_I32, _I64, _F64, _P],
+    ),
     "tpf_gemm_bf16": (
         _I32,
         [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I64, _I64,

@@ -592,30 +592,49 @@ int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64
   return ((dq + 255) / 256) * 256 + db;
 }
 
-int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
-                           const float* lse, const float* delta, const float* mask,
-                           const void* bias, void* dq, void* dk, void* dv, float* dbias,
-                           void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
-                           int64_t H, int64_t N, int64_t D, int seq_major, int64_t bias_batches,
-                           double scale, void* stream) {
-  AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, "tpf_attn_backward_bf16");
+static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const void* k,
+                            const void* v, const void* dout, const float* lse, const float* delta,
+                            const float* mask, const void* bias, const void* workspace,
+                            int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                            int64_t D, int seq_major, int64_t bias_batches, double scale) {
+  int rc = make_geom(g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
   if (rc) return rc;
-  if (!q || !k || !v || !dout || !lse || !delta || !mask || !bias || !dq || !dk || !dv ||
-      !dbias || !workspace)
-    return set_error(TPF_ERR_ARG, "tpf_attn_backward_bf16: null pointer");
+  if (!q || !k || !v || !dout || !lse || !delta || !mask || !bias || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const int64_t need = tpf_attn_backward_workspace_bytes(B, O, H, N, D);
   if (workspace_bytes < need)
-    return set_error(TPF_ERR_ARG, "tpf_attn_backward_bf16: workspace %lld < required %lld",
+    return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  if (B * groups > 65535)
-    return set_error(TPF_ERR_SHAPE, "tpf_attn_backward_bf16: B*ceil(O/4) exceeds grid-z");
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t dq_bytes = (N / 64) * B * O * H * N * D * 4;
-  float* dq_part = (float*)workspace;
-  float* db_part = (float*)((char*)workspace + ((dq_bytes + 255) / 256) * 256);
+  if (B * groups > 65535) return set_error(TPF_ERR_SHAPE, "%s: B*ceil(O/4) exceeds grid-z", fn);
+  return TPF_OK;
+}
+
+static void attn_bwd_parts(const AttnGeom& g, void* workspace, float** dq_part, float** db_part) {
+  const int64_t dq_bytes = (int64_t)(g.N / 64) * g.B * g.O * g.H * g.N * g.D * 4;
+  *dq_part = (float*)workspace;
+  *db_part = (float*)((char*)workspace + ((dq_bytes + 255) / 256) * 256);
+}
+
+// Stage 1 of the backward: the single-reconstruction kernel writing dK, dV
+// and the dQ / dBias partials into the workspace.
+int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, const void* dout,
+                                const float* lse, const float* delta, const float* mask,
+                                const void* bias, void* dk, void* dv, void* workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
+                                int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                                double scale, void* stream) {
+  const char* fn = "tpf_attn_backward_main_bf16";
+  AttnGeom g;
+  int rc = attn_bwd_prepare(&g, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, seq_major, bias_batches, scale);
+  if (rc) return rc;
+  if (!dk || !dv) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  float *dq_part, *db_part;
+  attn_bwd_parts(g, workspace, &dq_part, &db_part);
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
   dim3 grid((unsigned)(N / 64), (unsigned)H, (unsigned)(B * groups));
+  hipStream_t s = (hipStream_t)stream;
   if (D <= 32)
     hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, lse, delta, mask,
@@ -624,18 +643,46 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
     hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, lse, delta, mask,
                        (const __bf16*)bias, (__bf16*)dk, (__bf16*)dv, dq_part, db_part, g);
-  rc = check_launch("tpf_attn_backward_bf16(main)");
+  return check_launch(fn);
+}
+
+// Stage 2 of the backward: fixed-order folds of the dQ and dBias partials.
+int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
+                                  int64_t O, int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t bias_batches, double scale, void* stream) {
+  const char* fn = "tpf_attn_backward_finish_bf16";
+  AttnGeom g;
+  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
   if (rc) return rc;
+  if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  float *dq_part, *db_part;
+  attn_bwd_parts(g, (void*)workspace, &dq_part, &db_part);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
   const int64_t dq_items = B * O * H * N * (D / 4);
   hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
                      0, s, dq_part, (__bf16*)dq, g, (int)(N / 64));
-  rc = check_launch("tpf_attn_backward_bf16(dq)");
-  if (rc) return rc;
+  if ((rc = check_launch(fn))) return rc;
   const int64_t db_items = bias_batches * H * N * N / 4;
   hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
                      dim3(256), 0, s, db_part, dbias, (int)B, (int)bias_batches, (int)groups,
                      (int)H, (int)N);
-  return check_launch("tpf_attn_backward_bf16(dbias)");
+  return check_launch(fn);
+}
+
+int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
+                           const float* lse, const float* delta, const float* mask,
+                           const void* bias, void* dq, void* dk, void* dv, float* dbias,
+                           void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
+                           int64_t H, int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                           double scale, void* stream) {
+  if (!dq || !dbias) return set_error(TPF_ERR_ARG, "tpf_attn_backward_bf16: null pointer");
+  int rc = tpf_attn_backward_main_bf16(q, k, v, dout, lse, delta, mask, bias, dk, dv, workspace,
+                                       workspace_bytes, B, O, H, N, D, seq_major, bias_batches,
+                                       scale, stream);
+  if (rc) return rc;
+  return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, seq_major,
+                                       bias_batches, scale, stream);
 }
 
 }  // extern "C"
