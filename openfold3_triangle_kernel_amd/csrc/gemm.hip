@@ -121,15 +121,21 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs g) {
     }
 }
 
-// out[i] = sum_{s ascending} part[s * stride + i]   (f32, fixed order)
+// Fixed-order fold of split partials: thread (i, j) sums splits
+// [j*chunk, min((j+1)*chunk, splits)) in ascending order and writes the
+// result to dst + j*dst_stride + i.  Repeated passes (chunk 64) reduce any
+// number of splits; the order depends only on the shapes (deterministic).
 __global__ __launch_bounds__(256) void fold_f32_kernel(const float* __restrict__ part,
-                                                       float* __restrict__ out, int64_t n,
-                                                       int64_t stride, int splits) {
+                                                       float* __restrict__ dst, int64_t n,
+                                                       int64_t stride, int splits, int chunk,
+                                                       int64_t dst_stride) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int j = blockIdx.y;
   if (i >= n) return;
-  float acc = part[i];
-  for (int s = 1; s < splits; ++s) acc += part[(int64_t)s * stride + i];
-  out[i] = acc;
+  const int s0 = j * chunk, s1 = min(splits, s0 + chunk);
+  float acc = part[(int64_t)s0 * stride + i];
+  for (int s = s0 + 1; s < s1; ++s) acc += part[(int64_t)s * stride + i];
+  dst[(int64_t)j * dst_stride + i] = acc;
 }
 
 int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
@@ -168,8 +174,21 @@ int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
 
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
                 hipStream_t stream, const char* fn) {
-  hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     part, out, n, stride, splits);
+  // Passes of 64-way chunks, written in place into each chunk's first slot.
+  constexpr int kChunk = 64;
+  float* buf = const_cast<float*>(part);
+  int64_t st = stride;
+  while (splits > kChunk) {
+    const int groups = (splits + kChunk - 1) / kChunk;
+    hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)groups),
+                       dim3(256), 0, stream, buf, buf, n, st, splits, kChunk, st * kChunk);
+    int rc = check_launch(fn);
+    if (rc) return rc;
+    splits = groups;
+    st *= kChunk;
+  }
+  hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256), 1), dim3(256), 0, stream,
+                     buf, out, n, st, splits, splits, (int64_t)0);
   return check_launch(fn);
 }
 
