@@ -1,0 +1,157 @@
+/*
+ * TurboPairFormer on MI355X (gfx950): C ABI of libtpf_amd.so.
+ *
+ * Plain pointers, 64-bit sizes and a hipStream_t passed as void*.  Every
+ * entry point launches asynchronously on the given stream, never
+ * synchronises, and returns 0 on success or a TPF_ERR_* code; the message
+ * of the last failure on the calling thread is tpf_last_error().  Shapes are
+ * validated before any launch (the reference raises on the same conditions
+ * through TORCH_CHECK, e.g. turbopairformer_triangle_forward.cu:1835-1897).
+ * Callers allocate every output and workspace buffer.
+ *
+ * Dtypes: "bf16" pointers are bfloat16 arrays; "f32" are float arrays.
+ */
+#ifndef TPF_AMD_H
+#define TPF_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TPF_OK = 0,
+  TPF_ERR_ARG = 1,    /* null pointer, workspace too small, bad flag */
+  TPF_ERR_SHAPE = 2,  /* unsupported or inconsistent dimensions */
+  TPF_ERR_LAUNCH = 3, /* the HIP runtime rejected a launch */
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tpf_last_error(void);
+/* ABI revision of this header (1). */
+int tpf_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Triangle attention with pair bias.
+ *
+ * q, k, v: bf16 [B, O, H, N, D] in one shared storage order: head-major
+ *   (contiguous, seq_major = 0) or sequence-major (a contiguous
+ *   [B, O, N, H, D] buffer viewed as [B, O, H, N, D], seq_major = 1).
+ * mask: f32 [B, O, N] additive (0 keeps, -inf drops).
+ * bias: bf16 [bias_batches, H, N, N], bias_batches in {1, B} (1 = shared).
+ * out: bf16 [B, O, N, H, D].  lse, delta: f32 [B, O, H, N].
+ * Requirements: N % 64 == 0 (pad on the host with -inf mask entries),
+ * D % 8 == 0 and 8 <= D <= 64, B*O <= 65535.  scale = 1/sqrt(D_true): when
+ * the host zero-pads D it passes the unpadded D's scale.
+ * ---------------------------------------------------------------------- */
+
+/* Forward: out and the per-row logsumexp (-inf for a fully masked row,
+ * whose output is 0).  Replaces turbopairformer_triangle_forward_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_forward.cu:1960-1990). */
+int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
+                          const void* bias, void* out, float* lse, int64_t B, int64_t O,
+                          int64_t H, int64_t N, int64_t D, int seq_major,
+                          int64_t bias_batches, double scale, void* stream);
+
+/* delta = rowsum(f32(dout) * f32(out)) for dout/out bf16 [B, O, N, H, D].
+ * Replaces turbopairformer_triangle_delta_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_delta.cu:292-342). */
+int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,
+                        int64_t H, int64_t N, int64_t D, void* stream);
+
+/* Bytes of device workspace tpf_attn_backward_bf16 needs (dQ and dBias partials). */
+int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
+                                          int64_t D);
+
+/* Single-reconstruction backward: dq, dk, dv (bf16, same storage order as
+ * q) and dbias (f32 [bias_batches, H, N, N], summed over every (b, o) that
+ * shares the bias), all reduced in fixed orders (bitwise reproducible).
+ * Replaces turbopairformer_triangle_sr_backward_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dq_dbias.cu:2526-2648)
+ * together with its planner (turbopairformer_triangle_dq_dbias.py:466-566)
+ * and the broadcast dBias reduction (:1788-1825, .py:326-376). */
+int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
+                           const float* lse, const float* delta, const float* mask,
+                           const void* bias, void* dq, void* dk, void* dv, float* dbias,
+                           void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
+                           int64_t H, int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                           double scale, void* stream);
+
+/* The two stages of tpf_attn_backward_bf16, for callers that time or
+ * schedule them separately: the reconstruction kernel (dk, dv and the
+ * partials in workspace) and the fixed-order folds of the dQ / dBias
+ * partials.  Same split as the reference's sr_leaf_kernel / finalizer /
+ * dq_reduce launches (turbopairformer_triangle_dq_dbias.cu:2358-2499). */
+int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, const void* dout,
+                                const float* lse, const float* delta, const float* mask,
+                                const void* bias, void* dk, void* dv, void* workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
+                                int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                                double scale, void* stream);
+int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
+                                  int64_t O, int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t bias_batches, double scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Triangle multiplicative update (C == H in {32, 64, 96, 128}).
+ *
+ * z: bf16 [B, N, N, C]; mask: f32 [B, N, N].
+ * Weights (bf16): p_in = cat(W_ap, W_bp) [2H, C], g_in = cat(W_ag, W_bg)
+ * [2H, C], p_out = W_z [C, H], g_out = W_g [C, C]; p_out_t = W_z^T [H, C];
+ * w5_t = cat(p_in, g_in, g_out)^T [C, 5H].  LayerNorm weights f32.
+ * Saved state written by the forward: zln [R, C], a, b [B*H, N*Np] (channel
+ * -major stored matrices, Np = tpf_trimul_plane_pitch(N)), x [B*H, N, Np],
+ * xln [R, H], mean/rstd f32 [R] (R = B*N*N).
+ * ---------------------------------------------------------------------- */
+
+/* Row pitch Np (N rounded up to 8) of the channel-major a / b / x buffers. */
+int64_t tpf_trimul_plane_pitch(int64_t N);
+
+/* Forward: LN_in + projections + gates (trimul_in_fwd), the channel
+ * contraction (the reference's torch.bmm), LN_out + projection + gate
+ * (trimul_out_fwd).  outgoing = 1: x_ij = sum_k a_ik b_jk; 0: sum_k a_ki b_kj.
+ * Replaces trimul_in_fwd / torch.bmm / trimul_out_fwd of
+ * _trimul_forward_impl (openfold3/core/kernels/turbopairformer/turbopairformer_trimul.py:184-292;
+ * kernels turbopairformer_trimul_cuda.cu:615-1166, 1191-1530). */
+int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, const void* g_in,
+                            const void* p_out, const void* g_out, const float* ln_in_w,
+                            const float* ln_in_b, const float* ln_out_w, const float* ln_out_b,
+                            int outgoing, int64_t B, int64_t N, int64_t C, void* out, void* zln,
+                            void* a, void* b, void* x, void* xln, float* mean_in, float* rstd_in,
+                            float* mean_out, float* rstd_out, void* stream);
+
+int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C);
+
+/* Backward: dz (bf16) and every parameter gradient in f32 with fixed-order
+ * reductions.  d_w5 is [5H, C] in the order [p_in; g_in; g_out].
+ * Replaces _trimul_backward_combined_impl
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_trimul.py:295-392) with its
+ * kernels sig_mul_bwd_out, transpose_ln_bwd, trimul_gate_split_bwd,
+ * ln_bwd_dx, ln_bwd_dgb, trimul_wgrad_fixed_fold
+ * (turbopairformer_trimul_cuda.cu:196-560, 1532-2160) and its cuBLAS GEMMs. */
+int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
+                             const void* p_in, const void* g_in, const void* p_out_t,
+                             const void* w5_t, const void* p_out, const void* g_out,
+                             const float* ln_in_w, const float* ln_out_w, const void* zln,
+                             const void* a, const void* b, const void* x, const void* xln,
+                             const float* mean_in, const float* rstd_in, const float* mean_out,
+                             const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
+                             void* dz, float* d_w5, float* d_p_out, float* d_ln_in_w,
+                             float* d_ln_in_b, float* d_ln_out_w, float* d_ln_out_b,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Batched bf16 MFMA GEMM C[z] = alpha * A[z] B[z]^T with each operand
+ * K-contiguous (x_kc = 1: X[r*ld + k]) or MN-contiguous (0: X[k*ld + r]);
+ * C row-major, bf16 (out_f32 = 0) or f32.  The channel contraction of
+ * TriMul, which the reference delegates to cuBLAS through torch.bmm
+ * (turbopairformer_trimul.py:244-249, 355-362). */
+int tpf_gemm_bf16(const void* A, int a_kc, int64_t a_ld, int64_t a_bs, const void* B, int b_kc,
+                  int64_t b_ld, int64_t b_bs, void* C, int out_f32, int64_t c_ld, int64_t c_bs,
+                  int64_t M, int64_t N, int64_t K, int64_t batch, double alpha, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TPF_AMD_H */

@@ -109,4 +109,7 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of the tensor's device (0 = null stream off-GPU)."""
+    if t.device.type != "cuda":
+        return 0
     return torch.cuda.current_stream(t.device).cuda_stream

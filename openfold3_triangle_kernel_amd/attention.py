@@ -20,9 +20,9 @@ without a copy, and their gradients come back in the same storage order.
 
 from __future__ import annotations
 
+import contextlib
 import math
 import os
-from typing import Any
 
 import torch
 
@@ -71,6 +71,19 @@ def _is_gfx950(device: torch.device) -> bool:
     return arch.split(":")[0] == "gfx950"
 
 
+def _device_supported(t: torch.Tensor) -> tuple[bool, str]:
+    """Device gate: a gfx950 GPU tensor."""
+    if t.device.type != "cuda":
+        return False, "q/k/v, res_mask, and pair_bias must be GPU tensors"
+    if not _is_gfx950(t.device):
+        return False, "TurboPairFormer MI355X kernels require a gfx950 device"
+    return True, ""
+
+
+def _device_ctx(device: torch.device):
+    return torch.cuda.device(device) if device.type == "cuda" else contextlib.nullcontext()
+
+
 def is_turbopairformer_supported(q, k, v, res_mask, pair_bias) -> tuple[bool, str]:
     """Cached support verdict from metadata only (reference ``:93-220``)."""
     try:
@@ -94,10 +107,9 @@ def _supported_uncached(q, k, v, res_mask, pair_bias) -> tuple[bool, str]:
     named = {"q": q, "k": k, "v": v, "res_mask": res_mask, "pair_bias": pair_bias}
     if any(not isinstance(t, torch.Tensor) for t in named.values()):
         return False, "all inputs must be torch.Tensor instances"
-    if q.device.type != "cuda":
-        return False, "q/k/v, res_mask, and pair_bias must be GPU tensors"
-    if not _is_gfx950(q.device):
-        return False, "TurboPairFormer MI355X kernels require a gfx950 device"
+    ok, reason = _device_supported(q)
+    if not ok:
+        return False, reason
     if q.ndim < 5:
         return False, "q must have shape [*B,O,H,N,D]"
     prefix = tuple(q.shape[:-4])
@@ -163,7 +175,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
         B, O, H, N, D = (int(x) for x in q.shape)
         out = torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype)
         lse = torch.empty((B, O, H, N), device=q.device, dtype=torch.float32)
-        with torch.cuda.device(q.device):
+        with _device_ctx(q.device):
             _native.call(
                 "tpf_attn_forward_bf16",
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
@@ -185,7 +197,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
         d_out = d_out.contiguous()
         if d_out.dtype != torch.bfloat16:
             d_out = d_out.to(torch.bfloat16)
-        with torch.cuda.device(q.device):
+        with _device_ctx(q.device):
             stream = _native.stream_of(q)
             delta = torch.empty_like(lse)
             _native.call(

@@ -5,12 +5,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-enum {
-  TPF_OK = 0,
-  TPF_ERR_ARG = 1,     // null pointer, bad workspace, bad enum value
-  TPF_ERR_SHAPE = 2,   // unsupported or inconsistent dimensions
-  TPF_ERR_LAUNCH = 3,  // the HIP runtime rejected a launch
-};
+#include "tpf_amd.h"  // status codes and the declarations every entry point must match
 
 namespace tpf {
 

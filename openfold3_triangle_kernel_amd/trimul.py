@@ -22,6 +22,7 @@ output gate, so the ``gate`` slot is empty); the schema is unchanged.
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -29,6 +30,10 @@ import torch
 from . import _native
 
 _SUPPORTED_CHANNELS = (32, 64, 96, 128)
+
+
+def _device_ctx(device: torch.device):
+    return torch.cuda.device(device) if device.type == "cuda" else contextlib.nullcontext()
 
 
 def _bf16(t: torch.Tensor) -> torch.Tensor:
@@ -105,7 +110,7 @@ def _trimul_fwd_v1(
     mean_in, rstd_in = torch.empty(rows, **f32), torch.empty(rows, **f32)
     mean_out, rstd_out = torch.empty(rows, **f32), torch.empty(rows, **f32)
     lnw = [t.detach().to(torch.float32).contiguous() for t in (g_in, b_in, g_out, b_out)]
-    with torch.cuda.device(dev):
+    with _device_ctx(dev):
         _native.call(
             "tpf_trimul_forward_bf16",
             z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(), g_in_w.data_ptr(),
@@ -190,7 +195,7 @@ def _trimul_bwd_v1(
     d_gout, d_bout = torch.empty(H, **f32), torch.empty(H, **f32)
     ws_bytes = int(_native.query("tpf_trimul_backward_workspace_bytes", B, N, C))
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-    with torch.cuda.device(dev):
+    with _device_ctx(dev):
         _native.call(
             "tpf_trimul_backward_bf16",
             grad.data_ptr(), z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(),

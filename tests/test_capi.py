@@ -1,0 +1,77 @@
+"""C-ABI contract without a GPU: the library loads, exports every symbol that
+include/tpf_amd.h declares with the argument counts the ctypes binding uses,
+and rejects bad shapes with a status code and message before any launch."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tpf_amd.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(tpf_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(1)] = len(args)
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from openfold3_triangle_kernel_amd import _native
+
+    return _native.library()
+
+
+def test_header_declares_entry_points():
+    decls = _declared()
+    assert {"tpf_attn_forward_bf16", "tpf_attn_backward_bf16", "tpf_trimul_forward_bf16",
+            "tpf_trimul_backward_bf16", "tpf_last_error"} <= set(decls)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from openfold3_triangle_kernel_amd import _native
+
+    decls = _declared()
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _native.SIGNATURES, f"{name} missing from the ctypes binding"
+        assert len(_native.SIGNATURES[name][1]) == nargs, f"{name}: arg count mismatch"
+    assert lib.tpf_abi_version() == 1
+
+
+def test_shape_errors_are_reported_without_launch(lib):
+    from openfold3_triangle_kernel_amd import _native
+
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 1, 2, 4, 100, 32, 0, 1,
+                     0.1767, None)
+    with pytest.raises(RuntimeError, match="D=20"):
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 1, 2, 4, 128, 20, 0, 1,
+                     0.2, None)
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _native.call("tpf_attn_forward_bf16", None, 16, 16, 16, 16, 16, 16, 1, 2, 4, 128, 32, 0, 1,
+                     0.2, None)
+    with pytest.raises(RuntimeError, match="bias batch"):
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 2, 2, 4, 128, 32, 0, 3,
+                     0.2, None)
+    with pytest.raises(RuntimeError, match="C=48"):
+        _native.call("tpf_trimul_forward_bf16", *([16] * 10), 1, 1, 64, 48, *([16] * 10), None)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _native.call("tpf_attn_backward_bf16", *([16] * 13), 0, 1, 4, 4, 128, 32, 0, 1, 0.2, None)
+
+
+def test_workspace_sizes(lib):
+    from openfold3_triangle_kernel_amd import _native
+
+    ws = _native.query("tpf_attn_backward_workspace_bytes", 1, 384, 4, 384, 32)
+    dq = 6 * 384 * 4 * 384 * 32 * 4
+    assert ws >= dq + 96 * 4 * 384 * 384 * 4
+    assert _native.query("tpf_trimul_plane_pitch", 113) == 120
+    assert _native.query("tpf_trimul_plane_pitch", 384) == 384
+    assert _native.query("tpf_trimul_backward_workspace_bytes", 1, 384, 128) > 0
