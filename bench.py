@@ -130,8 +130,11 @@ def main():
     delta = torch.empty_like(lse)
     mflat = mask.reshape(B, O, N).contiguous()
     bflat = bias.reshape(1, H, N, N).contiguous()
+    fws_bytes = int(_native.query("tpf_attn_forward_workspace_bytes", B, H, N, 1))
+    fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8)
     _native.call("tpf_attn_forward_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), mflat.data_ptr(),
-                 bflat.data_ptr(), out.data_ptr(), lse.data_ptr(), B, O, H, N, D, 0, 1, scale, stream)
+                 bflat.data_ptr(), out.data_ptr(), lse.data_ptr(), fws.data_ptr(), fws_bytes,
+                 B, O, H, N, D, 0, 1, scale, stream)
     _native.call("tpf_attn_delta_bf16", dout.data_ptr(), out.data_ptr(), delta.data_ptr(), B, O, H, N, D,
                  stream)
     dk, dv = torch.empty_like(q), torch.empty_like(q)

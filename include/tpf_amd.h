@@ -46,13 +46,18 @@ int tpf_abi_version(void);
  * the host zero-pads D it passes the unpadded D's scale.
  * ---------------------------------------------------------------------- */
 
+/* Bytes of device workspace tpf_attn_forward_bf16 needs (the bias in f32,
+ * prescaled by 1/scale). */
+int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_t bias_batches);
+
 /* Forward: out and the per-row logsumexp (-inf for a fully masked row,
  * whose output is 0).  Replaces turbopairformer_triangle_forward_out
  * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_forward.cu:1960-1990). */
 int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
-                          const void* bias, void* out, float* lse, int64_t B, int64_t O,
-                          int64_t H, int64_t N, int64_t D, int seq_major,
-                          int64_t bias_batches, double scale, void* stream);
+                          const void* bias, void* out, float* lse, void* workspace,
+                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                          int64_t D, int seq_major, int64_t bias_batches, double scale,
+                          void* stream);
 
 /* delta = rowsum(f32(dout) * f32(out)) for dout/out bf16 [B, O, N, H, D].
  * Replaces turbopairformer_triangle_delta_out

@@ -29,9 +29,10 @@ _F64 = ctypes.c_double
 SIGNATURES: dict[str, tuple] = {
     "tpf_abi_version": (_I32, []),
     "tpf_last_error": (ctypes.c_char_p, []),
+    "tpf_attn_forward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "tpf_attn_forward_bf16": (
         _I32,
-        [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I64, _F64, _P],
+        [_P] * 8 + [_I64] * 6 + [_I32, _I64, _F64, _P],
     ),
     "tpf_attn_delta_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "tpf_attn_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),

@@ -175,12 +175,15 @@ class _TriangleAttentionFn(torch.autograd.Function):
         B, O, H, N, D = (int(x) for x in q.shape)
         out = torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype)
         lse = torch.empty((B, O, H, N), device=q.device, dtype=torch.float32)
+        Bb = int(bias_k.shape[0])
+        ws_bytes = int(_native.query("tpf_attn_forward_workspace_bytes", B, H, N, Bb))
+        workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
         with _device_ctx(q.device):
             _native.call(
                 "tpf_attn_forward_bf16",
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), B, O, H, N, D, int(seq_major),
-                int(bias_k.shape[0]), float(scale), _native.stream_of(q),
+                out.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ws_bytes, B, O, H, N, D,
+                int(seq_major), Bb, float(scale), _native.stream_of(q),
             )
         ctx.save_for_backward(q, k, v, mask, bias_k, out, lse)
         ctx.seq_major = bool(seq_major)

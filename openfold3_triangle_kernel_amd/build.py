@@ -28,6 +28,10 @@ DEVICE_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Keep MFMA accumulators in ordinary VGPRs (no v_accvgpr copies around
+    # the softmax / epilogue code that reads them).
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -34,30 +34,94 @@ struct AttnGeom {
   float scale;             // softmax scale (1/sqrt(D_true))
 };
 
+// XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
+// XCDs (linear id L goes to XCD L % 8), each with its own L2.  Logical tile
+// T = (h * planes + plane) * qtiles + qtile is head-major, and XCD x takes
+// the contiguous range [x * per, (x + 1) * per): every XCD then touches one
+// head's bias (L2-resident) and walks neighbouring query tiles of a plane
+// back to back (K/V reuse).  Returns false for the padding ids past total.
+struct TileId { int qt, h, plane; };
+__device__ __forceinline__ bool xcd_tile(int64_t total, int qtiles, int planes, TileId* t) {
+  const int64_t L = blockIdx.x;
+  const int64_t per = (total + 7) / 8;
+  const int64_t T = (L % 8) * per + L / 8;
+  if (T >= total) return false;
+  t->qt = (int)(T % qtiles);
+  const int64_t r = T / qtiles;
+  t->plane = (int)(r % planes);
+  t->h = (int)(r / planes);
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Bias pre-pass: bias_s = f32(bias) / scale, so that
+//   scale * <Q, K> + bias = scale * (<Q, K> + bias_s)
+// and the bias seeds the S^T accumulator; the softmax then needs one FMA per
+// score.  bias_s is stored fragment-major: for every 32-query x 32-key block
+// (qb, kb) of head h, 1024 floats laid out as [j][lane][i] where lane
+// (ql + 32*hl) register 4*j + i of the S^T = K Q^T accumulator holds
+// (query 32*qb + ql, key 32*kb + 8*j + 4*hl + i).  Each 16-byte load
+// instruction of a wave then reads one contiguous kilobyte.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* __restrict__ bias,
+                                                                 float* __restrict__ out,
+                                                                 int64_t items, int N,
+                                                                 float inv_scale) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
+  if (i >= items) return;
+  const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
+  const int64_t blk = i >> 8;
+  const int nkb = N / 32;
+  const int kb = (int)(blk % nkb);
+  const int64_t hq = blk / nkb;            // (bb * H + h) * (N / 32) + qb
+  const int qb = (int)(hq % (N / 32));
+  const int64_t bh = hq / (N / 32);
+  const int ql = lane & 31, hl = lane >> 5;
+  const __bf16* src = bias + (bh * N + qb * 32 + ql) * (int64_t)N + kb * 32 + 8 * j + 4 * hl;
+  bf16x4 v = ld4(src);
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = bf2f(v[e]) * inv_scale;
+  *reinterpret_cast<f32x4*>(out + i * 4) = o;
+}
+
 // ---------------------------------------------------------------------------
 // Forward.  One workgroup = 4 waves = 128 queries of one plane; each wave owns
-// 32 queries and walks all keys in 64-key tiles staged in LDS.  Scores are
-// produced transposed (S^T = K Q^T) so each lane owns one query column: row
-// max / sum need only the lane^32 exchange, and the C-layout P^T tile is fed
-// directly as the B operand of O^T += V^T P^T.
+// 32 queries and walks all keys in 64-key tiles staged in LDS (double
+// buffered, fetched into registers one tile ahead).  Scores are produced
+// transposed (S^T = K Q^T) so each lane owns one query column: row max / sum
+// need only the lane^32 exchange, and the C-layout P^T block is fed directly
+// as the B operand of O^T += V^T P^T.
+// Softmax works on 32-key blocks.  The S^T accumulator is seeded with the
+// prescaled bias (loaded one block ahead), scores stay in raw units
+// r = <Q,K> + bias_s (+ mask / scale), and p = exp2(r * c2 - m * c2) with
+// c2 = scale * log2(e): one FMA + one exp per score.  Row sums use packed
+// bf16 dot products of the rounded P (the values that also enter P V).  The
+// running max is raised only when a block exceeds it by more than 8 in log2
+// units (p <= 256 otherwise), so the O rescale is rare.
 // ---------------------------------------------------------------------------
 template <int DP>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 4 : 2, 8))) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
-    const __bf16* __restrict__ bias, __bf16* __restrict__ out,
+    const float* __restrict__ bias_s, __bf16* __restrict__ out,
     float* __restrict__ lse, AttnGeom g) {
-  constexpr int KP = DP + 8;     // K tile pitch (bf16)
-  constexpr int VP = 64 + 8;     // V^T tile pitch (bf16)
-  __shared__ __attribute__((aligned(16))) __bf16 Ks[64 * KP];
-  __shared__ __attribute__((aligned(16))) __bf16 Vt[DP * VP];
+  constexpr int KP = DP + 8;     // K tile pitch (bf16): conflict-free 16-byte reads
+  constexpr int VP = 64 + 4;     // V^T tile pitch (bf16): conflict-free 8-byte reads
+  constexpr int KITEMS = 64 * DP / 8;   // 16-byte K chunks per tile (one per thread)
+  constexpr int VITEMS = 16 * DP / 8;   // (4-key group, 8-channel chunk) V items
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[2][64 * KP];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[2][DP * VP];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int ql = lane & 31, hl = lane >> 5;
-  const int h = blockIdx.y, plane = blockIdx.z;
-  const int b = plane / g.O;
   const int N = g.N, D = g.D;
-  const int q0 = blockIdx.x * 128 + w * 32;
+  TileId tile;
+  const int qtiles = (N + 127) / 128;
+  if (!xcd_tile((int64_t)qtiles * g.H * g.B * g.O, qtiles, g.B * g.O, &tile)) return;
+  const int h = tile.h, plane = tile.plane;
+  const int b = plane / g.O;
+  const int q0 = tile.qt * 128 + w * 32;
   const bool active = q0 < N;
   const int qi = q0 + ql;
 
@@ -66,8 +130,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
   const __bf16* kb = k + plane_off;
   const __bf16* vb = v + plane_off;
   const float* mrow = mask + (int64_t)plane * N;
-  const __bf16* brow = bias + (int64_t)b * g.bias_bstride + ((int64_t)h * N + (active ? qi : 0)) * N;
+  // Fragment-major bias blocks of this wave's 32 queries: 1024 floats per
+  // 32-key block, lane-interleaved.
+  const float* brow = bias_s + (int64_t)b * g.bias_bstride +
+                      ((int64_t)h * (N / 32) + (active ? q0 / 32 : 0)) * (int64_t)(N / 32) * 1024 + lane * 4;
   const float c2 = g.scale * kLog2e;
+  const float inv_scale = 1.f / g.scale;
+  const float thr = 8.f / c2;  // lazy-rescale threshold in raw units
 
   bf16x8 qreg[DP / 16];
 #pragma unroll
@@ -76,93 +145,140 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     qreg[s] = (active && d0 < D) ? ld8(qb + (int64_t)qi * g.s_row + d0) : zero8();
   }
 
+  // K: thread -> (key, 8-channel chunk) items; V: thread -> (4-key group,
+  // chunk), transposed into Vt[d][key] with 8-byte stores.
+  constexpr int KPT = (KITEMS + 255) / 256;  // K items per thread
+  const int vgrp = tid % 16, vc = tid / 16;
+  const bool vthread = tid < VITEMS;
+  const bool vload = vthread && vc * 8 < D;
+  bf16x8 kr[KPT], vr[4];
+  auto load_kv = [&](int kt) {
+#pragma unroll
+    for (int it = 0; it < KPT; ++it) {
+      const int idx = it * 256 + tid;
+      const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
+      kr[it] = (idx < KITEMS && kc * 8 < D) ? ld8(kb + (int64_t)(kt + kkey) * g.s_row + kc * 8) : zero8();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      vr[r] = vload ? ld8(vb + (int64_t)(kt + vgrp * 4 + r) * g.s_row + vc * 8) : zero8();
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int it = 0; it < KPT; ++it) {
+      const int idx = it * 256 + tid;
+      const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
+      if (idx < KITEMS) *reinterpret_cast<bf16x8*>(&Ks[buf][kkey * KP + kc * 8]) = kr[it];
+    }
+    if (vthread) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bf16x4 col;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) col[r] = vr[r][e];
+        *reinterpret_cast<bf16x4*>(&Vt[buf][(vc * 8 + e) * VP + vgrp * 4]) = col;
+      }
+    }
+  };
+
+  // Tiles whose 64 mask entries are all zero skip the mask add (the mask
+  // is per plane, so the flag is uniform); computed up front so no wait on
+  // the mask sits inside the pipelined loop.
+  const int ntiles = N / 64;
+  uint64_t mbits = ~0ull;
+  if (ntiles <= 64) {
+    mbits = 0ull;
+    for (int t = 0; t < ntiles; ++t)
+      if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
+  }
+
   f32x16 acc[DP / 32];
 #pragma unroll
   for (int i = 0; i < DP / 32; ++i) acc[i] = zero16();
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f, nm = 0.f;
+  const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 
-  for (int kt = 0; kt < N; kt += 64) {
-    __syncthreads();
-    // Stage K (row-major) and V^T for keys kt..kt+63.
+  // The bias block for the next 32 keys is fetched while the current block
+  // is processed; K/V for the next tile are fetched at the start of a tile
+  // and stored to the other LDS buffer at its end.
+  auto load_bias = [&](int blk) {
+    f32x16 r;
 #pragma unroll
-    for (int it = 0; it < (64 * DP / 8 + 255) / 256; ++it) {
-      const int idx = it * 256 + tid;
-      if (idx < 64 * DP / 8) {
-        const int key = idx / (DP / 8), c = idx % (DP / 8);
-        const int64_t off = (int64_t)(kt + key) * g.s_row + c * 8;
-        bf16x8 kv = zero8(), vv = zero8();
-        if (c * 8 < D) { kv = ld8(kb + off); vv = ld8(vb + off); }
-        *reinterpret_cast<bf16x8*>(&Ks[key * KP + c * 8]) = kv;
+    for (int j = 0; j < 4; ++j) {
+      f32x4 x = *reinterpret_cast<const f32x4*>(brow + (int64_t)blk * 1024 + j * 256);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(c * 8 + e) * VP + key] = vv[e];
-      }
+      for (int i = 0; i < 4; ++i) r[4 * j + i] = x[i];
     }
-    __syncthreads();
-    if (!active) continue;
-
-    f32x16 st[2];
+    return r;
+  };
+  f32x16 bnext = load_bias(0);
+  load_kv(0);
+  store_kv(0);
+  __syncthreads();
+  const int nblk = N / 32;
+  for (int kt = 0, buf = 0; kt < N; kt += 64, buf ^= 1) {
+    const bool more = kt + 64 < N;
+    if (more) load_kv(kt + 64);
+    const bool masked = (mbits >> ((kt >> 6) & 63)) & 1ull;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      f32x16 s = zero16();
+      const int blk = (kt >> 5) + sb;
+      f32x16 s = bnext;
+      if (blk + 1 < nblk) bnext = load_bias(blk + 1);
+      if (!active) continue;
 #pragma unroll
       for (int ks = 0; ks < DP / 16; ++ks) {
-        bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[(sb * 32 + ql) * KP + 16 * ks + 8 * hl]);
+        bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[buf][(sb * 32 + ql) * KP + 16 * ks + 8 * hl]);
         s = mfma32(ka, qreg[ks], s);
       }
+      if (masked) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = kt + sb * 32 + 8 * j + 4 * hl;
-        bf16x4 bv = ld4(brow + key);
-        f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + key);
+        for (int j = 0; j < 4; ++j) {
+          f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + kt + sb * 32 + 8 * j + 4 * hl);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float add = (bf2f(bv[i]) + mv[i]) * kLog2e;
-          s[4 * j + i] = fmaf(s[4 * j + i], c2, add);
+          for (int i = 0; i < 4; ++i) s[4 * j + i] = fmaf(mv[i], inv_scale, s[4 * j + i]);
         }
       }
-      st[sb] = s;
-    }
-    float mx = -INFINITY;
+      float mx = s[0];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+      mx = xor32_max(mx);
+      if (__any(mx > m + thr)) {
+        const float m_new = fmaxf(m, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2((m - m_new) * c2);
+        l *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[sb][r]);
-    mx = xor32_max(mx);
-    const float m_new = fmaxf(m, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
-    float lsum = 0.f;
+        for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(st[sb][r] - m_use);
-        st[sb][r] = p;
-        lsum += p;
+          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        m = m_new;
+        nm = (m == -INFINITY) ? 0.f : -m * c2;
       }
-    l = l * alpha + lsum;
-    m = m_new;
-#pragma unroll
-    for (int db = 0; db < DP / 32; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        bf16x8 pb = pack8(st[sb], 8 * t);
+        bf16x8 pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[e] = f2bf(fast_exp2(fmaf(s[8 * t + e], c2, nm)));
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          bf16x2 pr = {pb[e], pb[e + 1]};
+          l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);
+        }
         const int key0 = sb * 32 + 16 * t + 4 * hl;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db) {
-          const __bf16* vr = &Vt[(db * 32 + ql) * VP + key0];
-          bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-          bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
+          const __bf16* vr2 = &Vt[buf][(db * 32 + ql) * VP + key0];
+          bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr2);
+          bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr2 + 8);
           bf16x8 va;
 #pragma unroll
           for (int e = 0; e < 4; ++e) { va[e] = lo[e]; va[4 + e] = hi[e]; }
           acc[db] = mfma32(va, pb, acc[db]);
         }
       }
+    }
+    if (more) store_kv(buf ^ 1);
+    __syncthreads();
   }
   if (!active) return;
 
@@ -183,7 +299,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     }
   if (hl == 0) {
     lse[((int64_t)plane * g.H + h) * N + qi] =
-        l_tot > 0.f ? (m + log2f(l_tot)) * kLn2 : -INFINITY;
+        l_tot > 0.f ? (m * c2 + log2f(l_tot)) * kLn2 : -INFINITY;
   }
 }
 
@@ -548,28 +664,48 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
 
 extern "C" {
 
+int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                         int64_t bias_batches) {
+  (void)B;
+  return bias_batches * H * N * N * 4;
+}
+
+static int attn_prescale_bias(const AttnGeom& g, const void* bias, float* bias_s,
+                              int64_t bias_batches, hipStream_t s, const char* fn) {
+  const int64_t items = bias_batches * g.H * (int64_t)g.N * g.N / 4;
+  hipLaunchKernelGGL(attn_bias_prescale_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
+                     0, s, (const __bf16*)bias, bias_s, items, g.N, 1.f / g.scale);
+  return check_launch(fn);
+}
+
 int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
-                          const void* bias, void* out, float* lse, int64_t B, int64_t O,
-                          int64_t H, int64_t N, int64_t D, int seq_major,
-                          int64_t bias_batches, double scale, void* stream) {
+                          const void* bias, void* out, float* lse, void* workspace,
+                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                          int64_t D, int seq_major, int64_t bias_batches, double scale,
+                          void* stream) {
+  const char* fn = "tpf_attn_forward_bf16";
   AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, "tpf_attn_forward_bf16");
+  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
   if (rc) return rc;
-  if (!q || !k || !v || !mask || !bias || !out || !lse)
-    return set_error(TPF_ERR_ARG, "tpf_attn_forward_bf16: null pointer");
-  if (B * O > 65535)
-    return set_error(TPF_ERR_SHAPE, "tpf_attn_forward_bf16: B*O=%lld exceeds grid-z", (long long)(B * O));
-  dim3 grid((unsigned)((N + 127) / 128), (unsigned)H, (unsigned)(B * O));
+  if (!q || !k || !v || !mask || !bias || !out || !lse || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  const int64_t total = ((N + 127) / 128) * H * B * O;
+  if ((total + 7) / 8 * 8 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: too many query tiles", fn);
   hipStream_t s = (hipStream_t)stream;
+  float* bias_s = (float*)workspace;
+  if ((rc = attn_prescale_bias(g, bias, bias_s, bias_batches, s, fn))) return rc;
+  g.bias_bstride = (bias_batches == 1) ? 0 : H * N * N;
+  dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
     hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, (const __bf16*)bias,
-                       (__bf16*)out, lse, g);
+                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
   else
     hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, (const __bf16*)bias,
-                       (__bf16*)out, lse, g);
-  return check_launch("tpf_attn_forward_bf16");
+                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
+  return check_launch(fn);
 }
 
 int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,

@@ -49,17 +49,17 @@ def test_shape_errors_are_reported_without_launch(lib):
     from openfold3_triangle_kernel_amd import _native
 
     with pytest.raises(RuntimeError, match="multiple of 64"):
-        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 1, 2, 4, 100, 32, 0, 1,
-                     0.1767, None)
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 16, 1 << 30, 1, 2, 4, 100,
+                     32, 0, 1, 0.1767, None)
     with pytest.raises(RuntimeError, match="D=20"):
-        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 1, 2, 4, 128, 20, 0, 1,
-                     0.2, None)
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 16, 1 << 30, 1, 2, 4, 128,
+                     20, 0, 1, 0.2, None)
     with pytest.raises(RuntimeError, match="null pointer"):
-        _native.call("tpf_attn_forward_bf16", None, 16, 16, 16, 16, 16, 16, 1, 2, 4, 128, 32, 0, 1,
-                     0.2, None)
+        _native.call("tpf_attn_forward_bf16", None, 16, 16, 16, 16, 16, 16, 16, 1 << 30, 1, 2, 4,
+                     128, 32, 0, 1, 0.2, None)
     with pytest.raises(RuntimeError, match="bias batch"):
-        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 2, 2, 4, 128, 32, 0, 3,
-                     0.2, None)
+        _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 16, 1 << 30, 2, 2, 4, 128,
+                     32, 0, 3, 0.2, None)
     with pytest.raises(RuntimeError, match="C=48"):
         _native.call("tpf_trimul_forward_bf16", *([16] * 10), 1, 1, 64, 48, *([16] * 10), None)
     with pytest.raises(RuntimeError, match="workspace"):

@@ -47,7 +47,7 @@ class FakeBackend:
     def __call__(self, name, *a):
         self.calls.append(name)
         if name == "tpf_attn_forward_bf16":
-            q, k, v, mask, bias, out, lse, B, O, H, N, D, sm, Bb, scale, _ = a
+            q, k, v, mask, bias, out, lse, ws, wsb, B, O, H, N, D, sm, Bb, scale, _ = a
             Q, K, V = (self._qkv(p, B, O, H, N, D, sm) for p in (q, k, v))
             M = _arr(mask, (B, O, N), np.float32).reshape(B, O, 1, 1, N)
             Bi = _bf2f(_arr(bias, (Bb, H, N, N), np.uint16))[:, None]
