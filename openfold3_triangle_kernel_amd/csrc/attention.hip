@@ -329,14 +329,60 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Backward preparation.
+//   rowprep: nl2 = -lse * log2(e) (-inf for fully masked rows, whose P is 0)
+//            and nd = -delta, so that in the reconstruction kernel
+//              P = exp2(S_raw * c2 + nl2),  dP - delta = MFMA(dO, V^T; C = nd).
+//   bias_bwd: bias / scale in the fragment-major layout of the S = Q K^T
+//            accumulator: for every 32-key x 32-query block (kb, qb) of head
+//            h, [j][lane][i] holds (query 32*qb + 8*j + 4*hl + i,
+//            key 32*kb + (lane % 32)), hl = lane / 32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_bwd_rowprep_kernel(const float* __restrict__ lse,
+                                                               const float* __restrict__ delta,
+                                                               float* __restrict__ nl2,
+                                                               float* __restrict__ nd, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float l = lse[i];
+  nl2[i] = (l == -INFINITY) ? -INFINITY : -l * kLog2e;
+  nd[i] = -delta[i];
+}
+
+__global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf16* __restrict__ bias,
+                                                                     float* __restrict__ out,
+                                                                     int64_t items, int N,
+                                                                     float inv_scale) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
+  if (i >= items) return;
+  const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
+  const int64_t blk = i >> 8;
+  const int nb = N / 32;
+  const int qb = (int)(blk % nb);
+  const int64_t bk = blk / nb;             // (bh) * nb + kb
+  const int kb = (int)(bk % nb);
+  const int64_t bh = bk / nb;
+  const int kl = lane & 31, hl = lane >> 5;
+  const __bf16* src = bias + (bh * N + qb * 32 + 8 * j + 4 * hl) * (int64_t)N + kb * 32 + kl;
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = bf2f(src[(int64_t)e * N]) * inv_scale;
+  *reinterpret_cast<f32x4*>(out + i * 4) = o;
+}
+
+// ---------------------------------------------------------------------------
 // Backward.  One workgroup = (64-key block, head, group of 4 outer rows); wave
 // w owns outer row o = 4*group + w and keeps its dK / dV accumulators for the
 // 64 keys in registers while streaming all queries in 32-row steps.  Scores are
 // formed as S = Q K^T (lane = key column) so the C-layout P and dS tiles are
-// the B operands of dV^T += dO^T P and dK^T += Q^T dS without data movement.
-// dS goes through LDS once per step for (a) dQ^T = K^T dS^T, written as a
-// per-key-block f32 partial, and (b) the dBias sum over the 4 waves, written
-// as a per-outer-group f32 partial.  Fixed-order reducers finish both.
+// the B operands of dV^T += dO^T P and dK^T += Q^T dS without data movement;
+// the transposed A operands (dO^T, Q^T) and dS^T for dQ^T = K^T dS^T come
+// from row-major LDS tiles through transposing reads.  The S accumulator is
+// seeded with the prescaled bias and the dP accumulator with -delta, so
+//   P = exp2(S * c2 + nl2),  dS = P * dP            (one FMA, one mul).
+// dQ leaves as a bf16 partial per key block; dBias sums the 4 waves in LDS
+// (fixed order) into an f32 partial per outer group.  Fixed-order reducers
+// finish both.  Tiles are ordered XCD-aware by (head, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
 
@@ -344,36 +390,48 @@ template <int DP>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const __bf16* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ delta,
-    const float* __restrict__ mask, const __bf16* __restrict__ bias,
+    const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
+    const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    float* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
-  constexpr int TP = 32 + 8;  // pitch of transposed Q / dO tiles (bf16)
-  constexpr int SP = 64 + 8;  // pitch of the dS tile (bf16)
-  constexpr int BP = 32 + 4;  // pitch of the transposed bias tile (f32)
-  __shared__ __attribute__((aligned(16))) __bf16 Qt[4][DP * TP];
-  __shared__ __attribute__((aligned(16))) __bf16 dOt[4][DP * TP];
-  __shared__ __attribute__((aligned(16))) __bf16 dSs[4][32 * SP];
-  __shared__ __attribute__((aligned(16))) float Bt[64 * BP];
-  __shared__ __attribute__((aligned(16))) float Red[4][32 * 64];
+    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
+  constexpr int TP = DP + 16;  // Q / dO / K tile pitch (bf16): conflict-free transposing reads
+  constexpr int SP = 32 + 16;  // dS^T tile [64 keys][32 queries] pitch (bf16)
+  constexpr int RP = 64 + 4;   // dBias exchange [32 queries][64 keys] pitch (f32)
+  __shared__ __attribute__((aligned(16))) __bf16 QD[4][64 * TP];  // Q rows | dO rows (K at setup)
+  __shared__ __attribute__((aligned(16))) __bf16 dSs[4][64 * SP];
+  __shared__ __attribute__((aligned(16))) float Red[2][4][32 * RP];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kl = lane & 31, hl = lane >> 5;
-  const int kblk = blockIdx.x, h = blockIdx.y;
+  const int N = g.N, D = g.D, H = g.H;
+  const int nkb = N / 64;
   const int groups = (g.O + kBwdGroup - 1) / kBwdGroup;
-  const int b = blockIdx.z / groups, og = blockIdx.z % groups;
+  const int64_t total = (int64_t)H * nkb * g.B * groups;
+  int64_t T;
+  {
+    const int64_t L = blockIdx.x, per = (total + 7) / 8;
+    T = (L % 8) * per + L / 8;
+    if (T >= total) return;
+  }
+  const int bog = (int)(T % ((int64_t)g.B * groups));
+  const int64_t hk = T / ((int64_t)g.B * groups);
+  const int kblk = (int)(hk % nkb), h = (int)(hk / nkb);
+  const int b = bog / groups, og = bog % groups;
   const int o = og * kBwdGroup + w;
   const bool active = o < g.O;
-  const int N = g.N, D = g.D, H = g.H;
   const int plane = b * g.O + (active ? o : 0);
   const int64_t plane_off = (int64_t)plane * H * N * D + (int64_t)h * g.s_head;
   const int key_base = kblk * 64;
   const float c2 = g.scale * kLog2e;
+  const float inv_scale = 1.f / g.scale;
+  __bf16* Qs = QD[w];
+  __bf16* dOs = QD[w] + 32 * TP;
+  __bf16* Ss = dSs[w];
 
   // Per-wave constant operands for this key block.
-  bf16x8 kB[2][DP / 16], vB[2][DP / 16];  // B operands: lane = key column
+  bf16x8 kB[2][DP / 16], vB[2][DP / 16];  // B operands of S and dP (lane = key)
   bf16x8 kA[DP / 32][4];                  // A operand of dQ^T = K^T dS^T
-  float mask2[2];
+  float mk2[2];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
     const int key = key_base + cb * 32 + kl;
@@ -383,21 +441,19 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       const int64_t off = plane_off + (int64_t)key * g.s_row + d0;
       kB[cb][s] = (active && d0 < D) ? ld8(k + off) : zero8();
       vB[cb][s] = (active && d0 < D) ? ld8(v + off) : zero8();
+      *reinterpret_cast<bf16x8*>(&QD[w][(cb * 32 + kl) * TP + d0]) = kB[cb][s];
     }
-    mask2[cb] = active ? mask[(int64_t)plane * N + key] * kLog2e : -INFINITY;
+    mk2[cb] = active ? mask[(int64_t)plane * N + key] * inv_scale : 0.f;
   }
+  const bool wmask = __any(mk2[0] != 0.f || mk2[1] != 0.f);
+  __syncthreads();
 #pragma unroll
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int d = db * 32 + kl;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = key_base + 16 * t + 8 * hl + e;
-        kA[db][t][e] = (active && d < D) ? k[plane_off + (int64_t)key * g.s_row + d]
-                                         : static_cast<__bf16>(0.f);
-      }
-    }
+    for (int t = 0; t < 4; ++t)
+      kA[db][t] = cat8(tr_col4(QD[w], TP, 16 * t, 16 * t + 8, 32 * db),
+                       tr_col4(QD[w], TP, 16 * t + 4, 16 * t + 12, 32 * db));
+  __syncthreads();
 
   f32x16 dKacc[DP / 32][2], dVacc[DP / 32][2];
 #pragma unroll
@@ -405,21 +461,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) { dKacc[db][cb] = zero16(); dVacc[db][cb] = zero16(); }
 
-  const __bf16* bias_h = bias + (int64_t)b * g.bias_bstride + (int64_t)h * N * N;
+  const int64_t bb = (g.bias_bstride == 0) ? 0 : b;
+  const int nb32 = N / 32;
+  // Fragment blocks (kb32, qb) of this head: [(bb*H + h)*nb32 + kb32][qb][1024].
+  const float* bfrag = bias_f + (((bb * H + h) * nb32 + kblk * 2) * nb32) * 1024 + lane * 4;
   const int64_t do_plane = (int64_t)plane * N * H * D + (int64_t)h * D;  // dO is [B,O,N,H,D]
-  const int64_t st_plane = ((int64_t)plane * H + h) * N;                // lse / delta
-  const int nkb = N / 64;
-  float* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
+  const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
+  __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
 
-  for (int q0 = 0; q0 < N; q0 += 32) {
-    // Stage the bias tile (32 queries x 64 keys) transposed, scaled by log2 e.
-    {
-      const int qr = tid >> 3, c = tid & 7;  // 32 rows x 8 chunks of 8 keys
-      bf16x8 bv = ld8(bias_h + (int64_t)(q0 + qr) * N + key_base + c * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Bt[(c * 8 + e) * BP + qr] = bf2f(bv[e]) * kLog2e;
-    }
-    // Q and dO rows (A operands of S and dP), also staged transposed.
+  for (int q0 = 0, it = 0; q0 < N; q0 += 32, ++it) {
+    // Q and dO rows: A operands of S and dP, plus row-major LDS copies.
     bf16x8 qA[DP / 16], doA[DP / 16];
 #pragma unroll
     for (int s = 0; s < DP / 16; ++s) {
@@ -427,70 +478,58 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       const bool ok = active && d0 < D;
       qA[s] = ok ? ld8(q + plane_off + (int64_t)(q0 + kl) * g.s_row + d0) : zero8();
       doA[s] = ok ? ld8(dout + do_plane + (int64_t)(q0 + kl) * H * D + d0) : zero8();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        Qt[w][(d0 + e) * TP + kl] = qA[s][e];
-        dOt[w][(d0 + e) * TP + kl] = doA[s][e];
-      }
+      *reinterpret_cast<bf16x8*>(&Qs[kl * TP + d0]) = qA[s];
+      *reinterpret_cast<bf16x8*>(&dOs[kl * TP + d0]) = doA[s];
     }
-    f32x4 lse4[4], del4[4];
+    f32x16 nl2v, ndv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int qq = q0 + 8 * j + 4 * hl;
-      if (active) {
-        lse4[j] = *reinterpret_cast<const f32x4*>(lse + st_plane + qq);
-        del4[j] = *reinterpret_cast<const f32x4*>(delta + st_plane + qq);
-      } else {
+      f32x4 a4 = *reinterpret_cast<const f32x4*>(nl2_g + st_plane + qq);
+      f32x4 d4 = *reinterpret_cast<const f32x4*>(nd_g + st_plane + qq);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { lse4[j][i] = INFINITY; del4[j][i] = 0.f; }
+      for (int i = 0; i < 4; ++i) {
+        nl2v[4 * j + i] = active ? a4[i] : -INFINITY;
+        ndv[4 * j + i] = d4[i];
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        lse4[j][i] = (lse4[j][i] == -INFINITY) ? INFINITY : lse4[j][i] * kLog2e;
     }
-    __syncthreads();
-
     f32x16 P[2], dS[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int ks = 0; ks < DP / 16; ++ks) {
-        s = mfma32(qA[ks], kB[cb][ks], s);
-        dp = mfma32(doA[ks], vB[cb][ks], dp);
-      }
-      const float* bcol = &Bt[(cb * 32 + kl) * BP];
+      f32x16 sacc;
+      const float* fb = bfrag + ((int64_t)cb * nb32 + (q0 >> 5)) * 1024;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        f32x4 bt = *reinterpret_cast<const f32x4*>(bcol + 8 * j + 4 * hl);
+        f32x4 x = *reinterpret_cast<const f32x4*>(fb + j * 256);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * j + i;
-          const float x = fmaf(s[r], c2, bt[i]) + (mask2[cb] - lse4[j][i]);
-          const float p = fast_exp2(x);
-          P[cb][r] = p;
-          dS[cb][r] = p * (dp[r] - del4[j][i]);
-        }
+        for (int i = 0; i < 4; ++i) sacc[4 * j + i] = x[i];
+      }
+      f32x16 dp = ndv;
+#pragma unroll
+      for (int ks = 0; ks < DP / 16; ++ks) {
+        sacc = mfma32(qA[ks], kB[cb][ks], sacc);
+        dp = mfma32(doA[ks], vB[cb][ks], dp);
+      }
+      if (wmask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] += mk2[cb];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(sacc[r], c2, nl2v[r]));
+        P[cb][r] = p;
+        dS[cb][r] = p * dp[r];
       }
     }
-    // dV^T += dO^T P, dK^T += Q^T dS (16-query k-steps, permuted order).
+    // dV^T += dO^T P, dK^T += Q^T dS (16-query k-steps, C-layout order).
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int db = 0; db < DP / 32; ++db) {
-        const int row = (db * 32 + kl) * TP + 16 * t + 4 * hl;
-        bf16x8 da, qa;
-        {
-          bf16x4 lo = *reinterpret_cast<const bf16x4*>(&dOt[w][row]);
-          bf16x4 hi = *reinterpret_cast<const bf16x4*>(&dOt[w][row + 8]);
-          bf16x4 lo2 = *reinterpret_cast<const bf16x4*>(&Qt[w][row]);
-          bf16x4 hi2 = *reinterpret_cast<const bf16x4*>(&Qt[w][row + 8]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            da[e] = lo[e]; da[4 + e] = hi[e];
-            qa[e] = lo2[e]; qa[4 + e] = hi2[e];
-          }
-        }
+        const bf16x8 da = cat8(tr_col4(dOs, TP, 16 * t, 16 * t + 4, 32 * db),
+                               tr_col4(dOs, TP, 16 * t + 8, 16 * t + 12, 32 * db));
+        const bf16x8 qa = cat8(tr_col4(Qs, TP, 16 * t, 16 * t + 4, 32 * db),
+                               tr_col4(Qs, TP, 16 * t + 8, 16 * t + 12, 32 * db));
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           dVacc[db][cb] = mfma32(da, pack8(P[cb], 8 * t), dVacc[db][cb]);
@@ -498,57 +537,62 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         }
       }
     }
-    // dS -> LDS: bf16 copy for dQ, f32 copy for the dBias wave sum.
+    // dS -> LDS: bf16 [key][query] for dQ, f32 [query][key] for the dBias sum.
+    float* red = Red[it & 1][w];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qq = 8 * (r >> 2) + 4 * hl + (r & 3);
-        const int key = cb * 32 + kl;
-        dSs[w][qq * SP + key] = f2bf(dS[cb][r]);
-        Red[w][qq * 64 + key] = dS[cb][r];
+      for (int j = 0; j < 4; ++j) {
+        bf16x4 s4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s4[i] = f2bf(dS[cb][4 * j + i]);
+          red[(8 * j + 4 * hl + i) * RP + cb * 32 + kl] = dS[cb][4 * j + i];
+        }
+        *reinterpret_cast<bf16x4*>(&Ss[(cb * 32 + kl) * SP + 8 * j + 4 * hl]) = s4;
       }
-    __syncthreads();
-    // dQ^T (d x 32 queries) = K^T dS^T over this block's 64 keys.
+    // dQ^T (d x 32 queries) = K^T dS^T over this block's 64 keys -> bf16 partial.
     if (active) {
 #pragma unroll
       for (int db = 0; db < DP / 32; ++db) {
         f32x16 acc = zero16();
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          bf16x8 sb = *reinterpret_cast<const bf16x8*>(&dSs[w][kl * SP + 16 * t + 8 * hl]);
+          const bf16x8 sb = cat8(tr_col4(Ss, SP, 16 * t, 16 * t + 8, 0),
+                                 tr_col4(Ss, SP, 16 * t + 4, 16 * t + 12, 0));
           acc = mfma32(kA[db][t], sb, acc);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int d0 = db * 32 + 8 * j + 4 * hl;
           if (d0 < D) {
-            f32x4 o4;
+            bf16x4 o4;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o4[i] = acc[4 * j + i];
-            *reinterpret_cast<f32x4*>(dqp + (int64_t)(q0 + kl) * D + d0) = o4;
+            for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[4 * j + i]);
+            *reinterpret_cast<bf16x4*>(dqp + (int64_t)(q0 + kl) * D + d0) = o4;
           }
         }
       }
     }
+    __syncthreads();
     // dBias partial: fixed wave order ((w0 + w1) + w2) + w3.
     {
-      float* dst = dbias_part + (((int64_t)blockIdx.z * H + h) * N + q0) * N + key_base;
+      float* dst = dbias_part + (((int64_t)bog * H + h) * N + q0) * N + key_base;
+      const float* R0 = Red[it & 1][0];
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int idx = it * 256 + tid;          // 32 rows x 16 float4 chunks
+      for (int it2 = 0; it2 < 2; ++it2) {
+        const int idx = it2 * 256 + tid;  // 32 rows x 16 float4 chunks
         const int qr = idx >> 4, c4 = (idx & 15) * 4;
-        f32x4 acc = *reinterpret_cast<const f32x4*>(&Red[0][qr * 64 + c4]);
+        f32x4 acc = *reinterpret_cast<const f32x4*>(&R0[qr * RP + c4]);
 #pragma unroll
         for (int ww = 1; ww < 4; ++ww) {
-          f32x4 x = *reinterpret_cast<const f32x4*>(&Red[ww][qr * 64 + c4]);
+          f32x4 x = *reinterpret_cast<const f32x4*>(&Red[it & 1][ww][qr * RP + c4]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += x[i];
         }
         *reinterpret_cast<f32x4*>(dst + (int64_t)qr * N + c4) = acc;
       }
     }
-    (void)nkb;
   }
   if (!active) return;
   // dK (scaled) and dV, in Q/K/V storage order.
@@ -575,31 +619,36 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     }
 }
 
-// dQ = bf16(scale * sum_kb partial[kb]) in ascending key-block order; written
-// in Q's storage order.  One thread per 4 consecutive d of one row.
+// dQ = bf16(scale * sum_kb partial[kb]) in ascending key-block order; bf16
+// partials [kb][plane][h][q][D], output in Q's storage order.
 __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
-    const float* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
-  const int D4 = g.D / 4;
-  const int64_t total = (int64_t)g.B * g.O * g.H * g.N * D4;
+    const __bf16* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
+  const int D8 = g.D / 8;
+  const int64_t total = (int64_t)g.B * g.O * g.H * g.N * D8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
-  const int d0 = (int)(idx % D4) * 4;
-  int64_t r = idx / D4;                 // [plane][h][q]
+  const int d0 = (int)(idx % D8) * 8;
+  int64_t r = idx / D8;                 // [plane][h][q]
   const int qq = (int)(r % g.N); r /= g.N;
   const int hh = (int)(r % g.H);
   const int64_t plane = r / g.H;
   const int64_t stride = (int64_t)g.B * g.O * g.H * g.N * g.D;
-  const float* src = part + ((plane * g.H + hh) * g.N + qq) * g.D + d0;
-  f32x4 acc = *reinterpret_cast<const f32x4*>(src);
-  for (int kb = 1; kb < nkb; ++kb) {
-    f32x4 x = *reinterpret_cast<const f32x4*>(src + kb * stride);
+  const __bf16* src = part + ((plane * g.H + hh) * g.N + qq) * g.D + d0;
+  float acc[8];
+  {
+    bf16x8 x = ld8(src);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] += x[i];
+    for (int e = 0; e < 8; ++e) acc[e] = bf2f(x[e]);
   }
-  bf16x4 o;
+  for (int kb = 1; kb < nkb; ++kb) {
+    bf16x8 x = ld8(src + kb * stride);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f2bf(acc[i] * g.scale);
-  *reinterpret_cast<bf16x4*>(dq + plane * g.H * g.N * g.D + hh * g.s_head + (int64_t)qq * g.s_row + d0) = o;
+    for (int e = 0; e < 8; ++e) acc[e] += bf2f(x[e]);
+  }
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
+  st8(dq + plane * g.H * g.N * g.D + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
 }
 
 // dBias[bb,h,q,k] (f32) = ascending fold over (b, outer group) partials that
@@ -720,12 +769,40 @@ int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t
   return check_launch("tpf_attn_delta_bf16");
 }
 
+// Backward workspace: bf16 dQ partials [N/64][B,O,H,N,D] | f32 dBias
+// partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
+// f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
+struct BwdParts {
+  __bf16* dq;
+  float* db;
+  float* bias_f;
+  float* nl2;
+  float* nd;
+};
+
+static int64_t a256(int64_t v) { return (v + 255) / 256 * 256; }
+
+static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D, char* base,
+                          BwdParts* parts) {
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  const int64_t rows = B * O * H * N;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
+  char* dq = take((N / 64) * rows * D * 2);
+  char* db = take(B * groups * H * N * N * 4);
+  char* bf = take(B * H * N * N * 4);
+  char* nl = take(rows * 4);
+  char* nd = take(rows * 4);
+  if (parts) {
+    parts->dq = (__bf16*)dq; parts->db = (float*)db; parts->bias_f = (float*)bf;
+    parts->nl2 = (float*)nl; parts->nd = (float*)nd;
+  }
+  return off;
+}
+
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
                                           int64_t D) {
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t dq = (N / 64) * B * O * H * N * D * 4;
-  const int64_t db = B * groups * H * N * N * 4;
-  return ((dq + 255) / 256) * 256 + db;
+  return bwd_layout(B, O, H, N, D, nullptr, nullptr);
 }
 
 static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const void* k,
@@ -742,18 +819,13 @@ static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const vo
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  if (B * groups > 65535) return set_error(TPF_ERR_SHAPE, "%s: B*ceil(O/4) exceeds grid-z", fn);
+  if ((H * (N / 64) * B * groups + 7) / 8 * 8 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
   return TPF_OK;
 }
 
-static void attn_bwd_parts(const AttnGeom& g, void* workspace, float** dq_part, float** db_part) {
-  const int64_t dq_bytes = (int64_t)(g.N / 64) * g.B * g.O * g.H * g.N * g.D * 4;
-  *dq_part = (float*)workspace;
-  *db_part = (float*)((char*)workspace + ((dq_bytes + 255) / 256) * 256);
-}
-
-// Stage 1 of the backward: the single-reconstruction kernel writing dK, dV
-// and the dQ / dBias partials into the workspace.
+// Stage 1 of the backward: row statistics and bias preparation, then the
+// single-reconstruction kernel writing dK, dV and the dQ / dBias partials.
 int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, const void* dout,
                                 const float* lse, const float* delta, const float* mask,
                                 const void* bias, void* dk, void* dv, void* workspace,
@@ -766,19 +838,29 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                             workspace_bytes, B, O, H, N, D, seq_major, bias_batches, scale);
   if (rc) return rc;
   if (!dk || !dv) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  float *dq_part, *db_part;
-  attn_bwd_parts(g, workspace, &dq_part, &db_part);
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  dim3 grid((unsigned)(N / 64), (unsigned)H, (unsigned)(B * groups));
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
   hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = B * O * H * N;
+  hipLaunchKernelGGL(attn_bwd_rowprep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
+                     s, lse, delta, pt.nl2, pt.nd, rows);
+  if ((rc = check_launch(fn))) return rc;
+  const int64_t items = bias_batches * H * N * N / 4;
+  hipLaunchKernelGGL(attn_bias_bwd_prescale_kernel, dim3((unsigned)((items + 255) / 256)),
+                     dim3(256), 0, s, (const __bf16*)bias, pt.bias_f, items, (int)N,
+                     1.f / g.scale);
+  if ((rc = check_launch(fn))) return rc;
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  const int64_t total = H * (N / 64) * B * groups;
+  dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
     hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, lse, delta, mask,
-                       (const __bf16*)bias, (__bf16*)dk, (__bf16*)dv, dq_part, db_part, g);
+                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
   else
     hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, lse, delta, mask,
-                       (const __bf16*)bias, (__bf16*)dk, (__bf16*)dv, dq_part, db_part, g);
+                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
   return check_launch(fn);
 }
 
@@ -791,17 +873,17 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
   int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
   if (rc) return rc;
   if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  float *dq_part, *db_part;
-  attn_bwd_parts(g, (void*)workspace, &dq_part, &db_part);
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
   hipStream_t s = (hipStream_t)stream;
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t dq_items = B * O * H * N * (D / 4);
+  const int64_t dq_items = B * O * H * N * (D / 8);
   hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
-                     0, s, dq_part, (__bf16*)dq, g, (int)(N / 64));
+                     0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
   if ((rc = check_launch(fn))) return rc;
   const int64_t db_items = bias_batches * H * N * N / 4;
   hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
-                     dim3(256), 0, s, db_part, dbias, (int)B, (int)bias_batches, (int)groups,
+                     dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
                      (int)H, (int)N);
   return check_launch(fn);
 }

@@ -88,6 +88,29 @@ __device__ __forceinline__ bf16x8 zero8() {
   return z;
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16).  In each 16-lane group every
+// lane supplies the address of 4 consecutive bf16; lane j of the group
+// receives element j % 4 of the chunks supplied by lanes 4e + j / 4
+// (e = 0..3).  tr_col4 uses it to fetch a column fragment of a row-major LDS
+// matrix M (pitch in elements): lane l receives
+//   { M[r0 + e][c0 + (l % 32)] : e = 0..3 },  r0 = rbase_lo (l < 32) or rbase_hi.
+// Rows are 8-byte aligned when pitch and c0 are multiples of 4.
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+__device__ __forceinline__ bf16x4 tr_col4(const __bf16* M, int pitch, int rbase_lo, int rbase_hi,
+                                          int c0) {
+  const int l = threadIdx.x & 63, g = l >> 4, ip = l & 15;
+  const int r = ((g >> 1) ? rbase_hi : rbase_lo) + (ip >> 2);
+  const __bf16* p = M + r * pitch + c0 + 16 * (g & 1) + 4 * (ip & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
+__device__ __forceinline__ bf16x8 cat8(bf16x4 lo, bf16x4 hi) {
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { o[e] = lo[e]; o[4 + e] = hi[e]; }
+  return o;
+}
+
 // Pack registers r0..r0+7 of a C-layout tile into a bf16 B operand.
 __device__ __forceinline__ bf16x8 pack8(const f32x16& c, int r0) {
   bf16x8 o;
