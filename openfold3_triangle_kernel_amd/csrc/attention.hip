@@ -380,11 +380,57 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // from row-major LDS tiles through transposing reads.  The S accumulator is
 // seeded with the prescaled bias and the dP accumulator with -delta, so
 //   P = exp2(S * c2 + nl2),  dS = P * dP            (one FMA, one mul).
+// Inputs of step i+1 (the bias fragments shared by the 4 waves, each wave's
+// Q / dO rows and row statistics) stream into the other half of a double
+// buffer with direct global->LDS loads while step i computes.
 // dQ leaves as a bf16 partial per key block; dBias sums the 4 waves in LDS
 // (fixed order) into an f32 partial per outer group.  Fixed-order reducers
 // finish both.  Tiles are ordered XCD-aware by (head, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct 16-byte global -> LDS load: lane i writes dst_base + 16*i.
+__device__ __forceinline__ void g2lds16(const void* src, void* dst_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) leaving the other counters untouched (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier that waits only for this wave's LDS operations (the
+// memory clobbers keep the compiler from moving memory accesses across it).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Q / dO tile of 32 rows x DP bf16 stored unpadded, 16-byte chunks permuted
+// per row (phys = c ^ swz(r)) so transposing reads of 4 consecutive rows and
+// row reads of 8 consecutive rows avoid bank conflicts.
+template <int DP>
+__device__ __forceinline__ int qd_swz(int r) {
+  return (DP == 32) ? (((r >> 1) & 1) << 1) : ((r & 3) << 1);
+}
+template <int DP>
+__device__ __forceinline__ int qd_off(int r, int col) {  // element offset of (row, col)
+  return r * DP + (((col >> 3) ^ qd_swz<DP>(r)) << 3) + (col & 7);
+}
+// tr_col4 on a swizzled Q / dO tile (see tr_col4 in common.hpp).
+template <int DP>
+__device__ __forceinline__ bf16x4 qd_tr_col4(const __bf16* M, int rbase_lo, int rbase_hi, int c0) {
+  const int l = threadIdx.x & 63, gq = l >> 4, ip = l & 15;
+  const int r = ((gq >> 1) ? rbase_hi : rbase_lo) + (ip >> 2);
+  const __bf16* p = M + qd_off<DP>(r, c0 + 16 * (gq & 1) + 4 * (ip & 3));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
 
 template <int DP>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
@@ -394,12 +440,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
-  constexpr int TP = DP + 16;  // Q / dO / K tile pitch (bf16): conflict-free transposing reads
+  constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 16;  // dS^T tile [64 keys][32 queries] pitch (bf16)
   constexpr int RP = 64 + 4;   // dBias exchange [32 queries][64 keys] pitch (f32)
-  __shared__ __attribute__((aligned(16))) __bf16 QD[4][64 * TP];  // Q rows | dO rows (K at setup)
-  __shared__ __attribute__((aligned(16))) __bf16 dSs[4][64 * SP];
-  __shared__ __attribute__((aligned(16))) float Red[2][4][32 * RP];
+  constexpr int QDE = 32 * DP;                 // elements of one Q (or dO) tile
+  constexpr int QDI = QDE * 2 / 1024;          // 1 KB async loads per Q (or dO) tile
+  constexpr int NISSUE = 2 + 2 * QDI + 1;      // async loads per wave per step
+  // Double buffers as distinct objects, so the compiler can tell the
+  // in-flight direct-to-LDS loads of one half from reads of the other.
+  __shared__ __attribute__((aligned(16))) float Bf0[2][1024];          // bias fragments [cb]
+  __shared__ __attribute__((aligned(16))) float Bf1[2][1024];
+  __shared__ __attribute__((aligned(16))) __bf16 QD0[4][2 * QDE];      // [wave] Q | dO rows
+  __shared__ __attribute__((aligned(16))) __bf16 QD1[4][2 * QDE];
+  __shared__ __attribute__((aligned(16))) float RS0[4][64];            // [wave] nl2 | nd
+  __shared__ __attribute__((aligned(16))) float RS1[4][64];
+  constexpr int SSE = 64 * (KT > SP ? KT : SP);  // dS^T tile, or the K tile at setup
+  __shared__ __attribute__((aligned(16))) __bf16 dSs[4][SSE];
+  __shared__ __attribute__((aligned(16))) float Red[4][32 * RP];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kl = lane & 31, hl = lane >> 5;
@@ -424,9 +481,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   const int key_base = kblk * 64;
   const float c2 = g.scale * kLog2e;
   const float inv_scale = 1.f / g.scale;
-  __bf16* Qs = QD[w];
-  __bf16* dOs = QD[w] + 32 * TP;
   __bf16* Ss = dSs[w];
+
+  // Zero the Q / dO buffers once: chunks past D are never loaded.
+  for (int i = tid; i < 4 * 2 * QDE / 8; i += 256) {
+    reinterpret_cast<bf16x8*>(&QD0[0][0])[i] = zero8();
+    reinterpret_cast<bf16x8*>(&QD1[0][0])[i] = zero8();
+  }
 
   // Per-wave constant operands for this key block.
   bf16x8 kB[2][DP / 16], vB[2][DP / 16];  // B operands of S and dP (lane = key)
@@ -441,7 +502,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       const int64_t off = plane_off + (int64_t)key * g.s_row + d0;
       kB[cb][s] = (active && d0 < D) ? ld8(k + off) : zero8();
       vB[cb][s] = (active && d0 < D) ? ld8(v + off) : zero8();
-      *reinterpret_cast<bf16x8*>(&QD[w][(cb * 32 + kl) * TP + d0]) = kB[cb][s];
+      *reinterpret_cast<bf16x8*>(&Ss[(cb * 32 + kl) * KT + d0]) = kB[cb][s];
     }
     mk2[cb] = active ? mask[(int64_t)plane * N + key] * inv_scale : 0.f;
   }
@@ -451,9 +512,43 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      kA[db][t] = cat8(tr_col4(QD[w], TP, 16 * t, 16 * t + 8, 32 * db),
-                       tr_col4(QD[w], TP, 16 * t + 4, 16 * t + 12, 32 * db));
-  __syncthreads();
+      kA[db][t] = cat8(tr_col4(Ss, KT, 16 * t, 16 * t + 8, 32 * db),
+                       tr_col4(Ss, KT, 16 * t + 4, 16 * t + 12, 32 * db));
+
+  const int64_t bb = (g.bias_bstride == 0) ? 0 : b;
+  const int nb32 = N / 32;
+  // Fragment blocks (kb32, qb) of this head: [(bb*H + h)*nb32 + kb32][qb][1024].
+  const float* bfrag = bias_f + ((bb * H + h) * nb32 + kblk * 2) * (int64_t)nb32 * 1024;
+  const int64_t do_plane = (int64_t)plane * N * H * D + (int64_t)h * D;  // dO is [B,O,N,H,D]
+  const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
+  __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
+
+  // Issue the direct-to-LDS loads of step q0 into buffer `buf`.
+  typedef float BfT[2][1024];
+  typedef __bf16 QDT[4][2 * QDE];
+  typedef float RST[4][64];
+  auto issue = [&](int q0, BfT& Bf, QDT& QDs, RST& RS) {
+    // Bias fragments: 8 KB per step, wave w loads kilobytes 2w and 2w+1.
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int kbx = 2 * w + x, cb = kbx >> 2, j = kbx & 3;
+      g2lds16(bfrag + ((int64_t)cb * nb32 + (q0 >> 5)) * 1024 + j * 256 + lane * 4,
+              &Bf[cb][j * 256]);
+    }
+    // Q and dO rows, swizzled; lanes past D (or of an idle wave) do not load.
+#pragma unroll
+    for (int n = 0; n < QDI; ++n) {
+      const int gc = n * 64 + lane, r = gc / (DP / 8), c = (gc % (DP / 8)) ^ qd_swz<DP>(r);
+      if (active && c * 8 < D) {
+        g2lds16(q + plane_off + (int64_t)(q0 + r) * g.s_row + c * 8, &QDs[w][n * 512]);
+        g2lds16(dout + do_plane + (int64_t)(q0 + r) * H * D + c * 8, &QDs[w][QDE + n * 512]);
+      }
+    }
+    if (lane < 16) {
+      const float* src = (lane < 8 ? nl2_g : nd_g) + st_plane + q0 + (lane & 7) * 4;
+      g2lds16(src, &RS[w][0]);
+    }
+  };
 
   f32x16 dKacc[DP / 32][2], dVacc[DP / 32][2];
 #pragma unroll
@@ -461,49 +556,51 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) { dKacc[db][cb] = zero16(); dVacc[db][cb] = zero16(); }
 
-  const int64_t bb = (g.bias_bstride == 0) ? 0 : b;
-  const int nb32 = N / 32;
-  // Fragment blocks (kb32, qb) of this head: [(bb*H + h)*nb32 + kb32][qb][1024].
-  const float* bfrag = bias_f + (((bb * H + h) * nb32 + kblk * 2) * nb32) * 1024 + lane * 4;
-  const int64_t do_plane = (int64_t)plane * N * H * D + (int64_t)h * D;  // dO is [B,O,N,H,D]
-  const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
-  __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
-
-  for (int q0 = 0, it = 0; q0 < N; q0 += 32, ++it) {
-    // Q and dO rows: A operands of S and dP, plus row-major LDS copies.
-    bf16x8 qA[DP / 16], doA[DP / 16];
+  __syncthreads();  // zero fill and K-tile reads done before the first loads land
+  // One query step: prefetch step q0+32 into the other buffers, wait for this
+  // step's loads, compute.  Barriers are bare s_barrier with an explicit LDS
+  // counter wait, so the prefetch stays in flight across them.
+  auto step = [&](int q0, BfT& Bc, QDT& QDc, RST& RSc, BfT& Bn, QDT& QDn, RST& RSn) {
+    // This step's loads were issued one step ago; wait for them, read the
+    // shared bias fragments and the row statistics, then start the next
+    // step's loads so they overlap this step's compute.
+    wait_vmcnt<0>();
+    lds_barrier();
+    f32x16 sinit[2];
 #pragma unroll
-    for (int s = 0; s < DP / 16; ++s) {
-      const int d0 = 16 * s + 8 * hl;
-      const bool ok = active && d0 < D;
-      qA[s] = ok ? ld8(q + plane_off + (int64_t)(q0 + kl) * g.s_row + d0) : zero8();
-      doA[s] = ok ? ld8(dout + do_plane + (int64_t)(q0 + kl) * H * D + d0) : zero8();
-      *reinterpret_cast<bf16x8*>(&Qs[kl * TP + d0]) = qA[s];
-      *reinterpret_cast<bf16x8*>(&dOs[kl * TP + d0]) = doA[s];
-    }
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(&Bc[cb][j * 256 + lane * 4]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sinit[cb][4 * j + i] = x[i];
+      }
     f32x16 nl2v, ndv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int qq = q0 + 8 * j + 4 * hl;
-      f32x4 a4 = *reinterpret_cast<const f32x4*>(nl2_g + st_plane + qq);
-      f32x4 d4 = *reinterpret_cast<const f32x4*>(nd_g + st_plane + qq);
+      f32x4 a4 = *reinterpret_cast<const f32x4*>(&RSc[w][8 * j + 4 * hl]);
+      f32x4 d4 = *reinterpret_cast<const f32x4*>(&RSc[w][32 + 8 * j + 4 * hl]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         nl2v[4 * j + i] = active ? a4[i] : -INFINITY;
-        ndv[4 * j + i] = d4[i];
+        ndv[4 * j + i] = active ? d4[i] : 0.f;
       }
     }
+    const __bf16* Qs = QDc[w];
+    const __bf16* dOs = QDc[w] + QDE;
+    bf16x8 qA[DP / 16], doA[DP / 16];
+#pragma unroll
+    for (int s = 0; s < DP / 16; ++s) {
+      const int c = 16 * s + 8 * hl;
+      qA[s] = *reinterpret_cast<const bf16x8*>(&Qs[qd_off<DP>(kl, c)]);
+      doA[s] = *reinterpret_cast<const bf16x8*>(&dOs[qd_off<DP>(kl, c)]);
+    }
+    // The other buffers were last read before the barrier above.
+    if (q0 + 32 < N) issue(q0 + 32, Bn, QDn, RSn);
     f32x16 P[2], dS[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      f32x16 sacc;
-      const float* fb = bfrag + ((int64_t)cb * nb32 + (q0 >> 5)) * 1024;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x4 x = *reinterpret_cast<const f32x4*>(fb + j * 256);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sacc[4 * j + i] = x[i];
-      }
+      f32x16 sacc = sinit[cb];
       f32x16 dp = ndv;
 #pragma unroll
       for (int ks = 0; ks < DP / 16; ++ks) {
@@ -526,10 +623,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
       for (int db = 0; db < DP / 32; ++db) {
-        const bf16x8 da = cat8(tr_col4(dOs, TP, 16 * t, 16 * t + 4, 32 * db),
-                               tr_col4(dOs, TP, 16 * t + 8, 16 * t + 12, 32 * db));
-        const bf16x8 qa = cat8(tr_col4(Qs, TP, 16 * t, 16 * t + 4, 32 * db),
-                               tr_col4(Qs, TP, 16 * t + 8, 16 * t + 12, 32 * db));
+        const bf16x8 da = cat8(qd_tr_col4<DP>(dOs, 16 * t, 16 * t + 4, 32 * db),
+                               qd_tr_col4<DP>(dOs, 16 * t + 8, 16 * t + 12, 32 * db));
+        const bf16x8 qa = cat8(qd_tr_col4<DP>(Qs, 16 * t, 16 * t + 4, 32 * db),
+                               qd_tr_col4<DP>(Qs, 16 * t + 8, 16 * t + 12, 32 * db));
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           dVacc[db][cb] = mfma32(da, pack8(P[cb], 8 * t), dVacc[db][cb]);
@@ -538,7 +635,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       }
     }
     // dS -> LDS: bf16 [key][query] for dQ, f32 [query][key] for the dBias sum.
-    float* red = Red[it & 1][w];
+    float* red = Red[w];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -574,25 +671,29 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     // dBias partial: fixed wave order ((w0 + w1) + w2) + w3.
     {
       float* dst = dbias_part + (((int64_t)bog * H + h) * N + q0) * N + key_base;
-      const float* R0 = Red[it & 1][0];
 #pragma unroll
       for (int it2 = 0; it2 < 2; ++it2) {
         const int idx = it2 * 256 + tid;  // 32 rows x 16 float4 chunks
         const int qr = idx >> 4, c4 = (idx & 15) * 4;
-        f32x4 acc = *reinterpret_cast<const f32x4*>(&R0[qr * RP + c4]);
+        f32x4 acc = *reinterpret_cast<const f32x4*>(&Red[0][qr * RP + c4]);
 #pragma unroll
         for (int ww = 1; ww < 4; ++ww) {
-          f32x4 x = *reinterpret_cast<const f32x4*>(&Red[it & 1][ww][qr * RP + c4]);
+          f32x4 x = *reinterpret_cast<const f32x4*>(&Red[ww][qr * RP + c4]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += x[i];
         }
         *reinterpret_cast<f32x4*>(dst + (int64_t)qr * N + c4) = acc;
       }
     }
+  };
+  issue(0, Bf0, QD0, RS0);
+  for (int q0 = 0; q0 < N; q0 += 64) {
+    step(q0, Bf0, QD0, RS0, Bf1, QD1, RS1);
+    step(q0 + 32, Bf1, QD1, RS1, Bf0, QD0, RS0);
   }
   if (!active) return;
   // dK (scaled) and dV, in Q/K/V storage order.
