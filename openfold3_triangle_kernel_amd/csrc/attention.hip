@@ -391,9 +391,15 @@ constexpr int kBwdGroup = 4;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Direct 16-byte global -> LDS load: lane i writes dst_base + 16*i.
+// Direct 16-byte global -> LDS load (global_load_lds_dwordx4): lane i writes
+// dst_base + 16*i.  Issued through inline assembly so the compiler does not
+// guard every later LDS read with a full vmcnt wait; callers wait explicitly
+// (wait_vmcnt) before reading the destination.  dst_base must be uniform.
 __device__ __forceinline__ void g2lds16(const void* src, void* dst_base) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)dst_base, 16, 0, 0);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
 }
 
 // s_waitcnt vmcnt(n) leaving the other counters untouched (gfx9 encoding).
