@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // buffer with direct global->LDS loads while step i computes.
 // dQ leaves as a bf16 partial per key block; dBias sums the 4 waves in LDS
 // (fixed order) into an f32 partial per outer group.  Fixed-order reducers
-// finish both.  Tiles are ordered XCD-aware by (head, key block).
+// finish both.  Tiles are ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
 
@@ -476,9 +476,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     T = (L % 8) * per + L / 8;
     if (T >= total) return;
   }
-  const int bog = (int)(T % ((int64_t)g.B * groups));
-  const int64_t hk = T / ((int64_t)g.B * groups);
-  const int kblk = (int)(hk % nkb), h = (int)(hk / nkb);
+  // Tile order (head, outer group, key block): the nkb workgroups that share
+  // one group's Q / dO rows run back to back on one XCD (L2 reuse).
+  const int kblk = (int)(T % nkb);
+  const int64_t hb = T / nkb;
+  const int bog = (int)(hb % ((int64_t)g.B * groups));
+  const int h = (int)(hb / ((int64_t)g.B * groups));
   const int b = bog / groups, og = bog % groups;
   const int o = og * kBwdGroup + w;
   const bool active = o < g.O;
