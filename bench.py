@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-trimul", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="launch a 256 MiB calibration copy and one attention backward kernel, "
+                         "then exit (the program profiled by the FETCH_SIZE / WRITE_SIZE passes)")
     return ap.parse_args()
 
 
@@ -58,6 +61,36 @@ def attention_inputs(torch, dev, seed=0):
     mask = mask.reshape(B, O, 1, 1, N).float()
     dout = torch.randn(B, O, N, H, D, device=dev, generator=g).to(torch.bfloat16)
     return q, k, v, bias, mask, dout
+
+
+def dominant_kernel(torch, _native, dev, q, k, v, bias, mask, dout):
+    """Inputs, forward state and workspace of one attention backward launch
+    (starting node); returns a closure that launches the backward kernel."""
+    stream = torch.cuda.current_stream().cuda_stream
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty(B, O, N, H, D, device=dev, dtype=torch.bfloat16)
+    lse = torch.empty(B, O, H, N, device=dev, dtype=torch.float32)
+    delta = torch.empty_like(lse)
+    mflat = mask.reshape(B, O, N).contiguous()
+    bflat = bias.reshape(1, H, N, N).contiguous()
+    fws_bytes = int(_native.query("tpf_attn_forward_workspace_bytes", B, H, N, 1))
+    fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8)
+    _native.call("tpf_attn_forward_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), mflat.data_ptr(),
+                 bflat.data_ptr(), out.data_ptr(), lse.data_ptr(), fws.data_ptr(), fws_bytes,
+                 B, O, H, N, D, 0, 1, scale, stream)
+    _native.call("tpf_attn_delta_bf16", dout.data_ptr(), out.data_ptr(), delta.data_ptr(), B, O, H, N, D,
+                 stream)
+    dk, dv = torch.empty_like(q), torch.empty_like(q)
+    ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+
+    def bwd_main():
+        _native.call("tpf_attn_backward_main_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                     dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), mflat.data_ptr(),
+                     bflat.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
+                     B, O, H, N, D, 0, 1, scale, stream)
+
+    return bwd_main
 
 
 def main():
@@ -79,6 +112,17 @@ def main():
 
     # ---------------- attention: starting + ending node -----------------
     q, k, v, bias, mask, dout = attention_inputs(torch, dev)
+    if args.traffic_probe:
+        bwd_main = dominant_kernel(torch, _native, dev, q, k, v, bias, mask, dout)
+        src = torch.ones(64 * 1024 * 1024, device=dev, dtype=torch.float32)  # 256 MiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        bwd_main()
+        torch.cuda.synchronize()
+        print("traffic probe: copy 268435456 B read + 268435456 B written; one attn_bwd launch", flush=True)
+        return
+
     # Ending node: the same op on the pair transposed over its two N axes.
     qe, ke, ve = (t.transpose(1, 3).contiguous() for t in (q, k, v))
     mask_e = mask.clone()
@@ -123,30 +167,7 @@ def main():
     fwd_ms = e0.elapsed_time(e1) / args.steps
 
     # ------------- dominant kernel: attention backward, alone -------------
-    stream = torch.cuda.current_stream().cuda_stream
-    scale = 1.0 / math.sqrt(D)
-    out = torch.empty(B, O, N, H, D, device=dev, dtype=torch.bfloat16)
-    lse = torch.empty(B, O, H, N, device=dev, dtype=torch.float32)
-    delta = torch.empty_like(lse)
-    mflat = mask.reshape(B, O, N).contiguous()
-    bflat = bias.reshape(1, H, N, N).contiguous()
-    fws_bytes = int(_native.query("tpf_attn_forward_workspace_bytes", B, H, N, 1))
-    fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8)
-    _native.call("tpf_attn_forward_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), mflat.data_ptr(),
-                 bflat.data_ptr(), out.data_ptr(), lse.data_ptr(), fws.data_ptr(), fws_bytes,
-                 B, O, H, N, D, 0, 1, scale, stream)
-    _native.call("tpf_attn_delta_bf16", dout.data_ptr(), out.data_ptr(), delta.data_ptr(), B, O, H, N, D,
-                 stream)
-    dk, dv = torch.empty_like(q), torch.empty_like(q)
-    ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
-    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-
-    def bwd_main():
-        _native.call("tpf_attn_backward_main_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                     dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), mflat.data_ptr(),
-                     bflat.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
-                     B, O, H, N, D, 0, 1, scale, stream)
-
+    bwd_main = dominant_kernel(torch, _native, dev, q, k, v, bias, mask, dout)
     for _ in range(3):
         bwd_main()
     torch.cuda.synchronize()
@@ -165,7 +186,7 @@ def main():
         "peak": MFMA_BF16_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic_bytes(),
         "avg_launch_us": round(bwd_kernel_ms * 1e3, 2),
         "flops_per_launch": bwd_flops,
     }
@@ -250,6 +271,23 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "attn_bwd_N384_H4_D32_traffic.json")
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the attention backward kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes over ``bench.py --traffic-probe``,
+    each scaled by the same counter's reading on a 256 MiB copy (None when the
+    summary is absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(t["fetch_bytes_calibrated"] + t["write_bytes_calibrated"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline():
     """The numpy oracle (fp32) on a bounded sample of the attention workload:
     the same N=384, H=4, D=32 planes, fwd+bwd, on a subset of outer rows."""
@@ -264,7 +302,7 @@ def cpu_baseline():
         threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
     except Exception:  # pragma: no cover
         threads = 1
-    o_sample = 8
+    o_sample = 16
     rng = np.random.default_rng(0)
     q, k, v = (rng.standard_normal((1, o_sample, H, N, D)).astype(np.float32) for _ in range(3))
     bias = (2 * rng.standard_normal((1, 1, H, N, N))).astype(np.float32)
@@ -278,7 +316,7 @@ def cpu_baseline():
         attention_backward(q, k, v, mask, bias, dout, dtype=np.float32)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 50:
+        if el > 12.0:
             break
     sec = el / reps
     return {

@@ -6,7 +6,7 @@ has not been built, and every entry point's status code is turned into a
 RuntimeError carrying the library's own message.
 
 Loading is behind a lock and cached per process, mirroring the fail-closed
-loader of the reference (openfold3/core/kernels/turbopairformer/_aot_runtime.py:752-800),
+loader of the reference (openfold3/core/kernels/turbopairformer/_aot_runtime.py:273-321),
 without its manifest/hash attestation (the library is built in-tree).
 """
 
