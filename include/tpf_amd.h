@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (1). */
+/* ABI revision of this header (2). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -103,15 +103,18 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
  *
  * z: bf16 [B, N, N, C]; mask: f32 [B, N, N].
  * Weights (bf16): p_in = cat(W_ap, W_bp) [2H, C], g_in = cat(W_ag, W_bg)
- * [2H, C], p_out = W_z [C, H], g_out = W_g [C, C]; p_out_t = W_z^T [H, C];
- * w5_t = cat(p_in, g_in, g_out)^T [C, 5H].  LayerNorm weights f32.
- * Saved state written by the forward: zln [R, C], a, b [B*H, N*Np] (channel
- * -major stored matrices, Np = tpf_trimul_plane_pitch(N)), x [B*H, N, Np],
- * xln [R, H], mean/rstd f32 [R] (R = B*N*N).
+ * [2H, C], p_out = W_z [C, H], g_out = W_g [C, C].  LayerNorm weights f32.
+ * Saved state written by the forward (R = B*N*N rows): zln [R, C], gate =
+ * output-gate logits zln W_g^T [R, C], a, b [B*H, N*Np] (channel-major
+ * stored matrices, Np = tpf_trimul_plane_pitch(N)), x [B*H, N, Np], xln
+ * [R, H], mean/rstd f32 [R].
  * ---------------------------------------------------------------------- */
 
 /* Row pitch Np (N rounded up to 8) of the channel-major a / b / x buffers. */
 int64_t tpf_trimul_plane_pitch(int64_t N);
+
+/* Bytes of device workspace tpf_trimul_forward_bf16 needs (packed weights). */
+int64_t tpf_trimul_forward_workspace_bytes(int64_t C);
 
 /* Forward: LN_in + projections + gates (trimul_in_fwd), the channel
  * contraction (the reference's torch.bmm), LN_out + projection + gate
@@ -123,8 +126,9 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, 
                             const void* p_out, const void* g_out, const float* ln_in_w,
                             const float* ln_in_b, const float* ln_out_w, const float* ln_out_b,
                             int outgoing, int64_t B, int64_t N, int64_t C, void* out, void* zln,
-                            void* a, void* b, void* x, void* xln, float* mean_in, float* rstd_in,
-                            float* mean_out, float* rstd_out, void* stream);
+                            void* gate, void* a, void* b, void* x, void* xln, float* mean_in,
+                            float* rstd_in, float* mean_out, float* rstd_out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C);
 
@@ -136,15 +140,15 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C);
  * ln_bwd_dx, ln_bwd_dgb, trimul_wgrad_fixed_fold
  * (turbopairformer_trimul_cuda.cu:196-560, 1532-2160) and its cuBLAS GEMMs. */
 int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
-                             const void* p_in, const void* g_in, const void* p_out_t,
-                             const void* w5_t, const void* p_out, const void* g_out,
-                             const float* ln_in_w, const float* ln_out_w, const void* zln,
-                             const void* a, const void* b, const void* x, const void* xln,
-                             const float* mean_in, const float* rstd_in, const float* mean_out,
-                             const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
-                             void* dz, float* d_w5, float* d_p_out, float* d_ln_in_w,
-                             float* d_ln_in_b, float* d_ln_out_w, float* d_ln_out_b,
-                             void* workspace, int64_t workspace_bytes, void* stream);
+                             const void* p_in, const void* g_in, const void* p_out,
+                             const void* g_out, const float* ln_in_w, const float* ln_out_w,
+                             const void* zln, const void* gate, const void* a, const void* b,
+                             const void* x, const void* xln, const float* mean_in,
+                             const float* rstd_in, const float* mean_out, const float* rstd_out,
+                             int outgoing, int64_t B, int64_t N, int64_t C, void* dz, float* d_w5,
+                             float* d_p_out, float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
+                             float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
+                             void* stream);
 
 /* Batched bf16 MFMA GEMM C[z] = alpha * A[z] B[z]^T with each operand
  * K-contiguous (x_kc = 1: X[r*ld + k]) or MN-contiguous (0: X[k*ld + r]);

@@ -389,35 +389,6 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Direct 16-byte global -> LDS load (global_load_lds_dwordx4): lane i writes
-// dst_base + 16*i.  Issued through inline assembly so the compiler does not
-// guard every later LDS read with a full vmcnt wait; callers wait explicitly
-// (wait_vmcnt) before reading the destination.  dst_base must be uniform.
-__device__ __forceinline__ void g2lds16(const void* src, void* dst_base) {
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(lds_void*)dst_base);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds) : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(n) leaving the other counters untouched (gfx9 encoding).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Workgroup barrier that waits only for this wave's LDS operations (the
-// memory clobbers keep the compiler from moving memory accesses across it).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt untouched
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // Q / dO tile of 32 rows x DP bf16 stored unpadded, 16-byte chunks permuted
 // per row (phys = c ^ swz(r)) so transposing reads of 4 consecutive rows and
 // row reads of 8 consecutive rows avoid bank conflicts.

@@ -119,4 +119,58 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& c, int r0) {
   return o;
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct 16-byte global -> LDS load (global_load_lds_dwordx4): lane i writes
+// dst_base + 16*i.  Issued through inline assembly so the compiler does not
+// guard every later LDS read with a full vmcnt wait; callers wait explicitly
+// (wait_vmcnt) before reading the destination.  dst_base must be uniform.
+__device__ __forceinline__ void g2lds16(const void* src, void* dst_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) leaving the other counters untouched (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier that waits only for this wave's LDS operations (the
+// memory clobbers keep the compiler from moving memory accesses across it).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Buffer resource of a raw (unstructured) buffer starting at base.  The
+// range is 2^31 - 1 bytes, so an offset of kBufOOB (2^31) reads as zeros:
+// loaders use it for elements outside the tensor instead of branching.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kBufOOB = 0x80000000u;
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+  r[2] = 0x7FFFFFFF;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// Direct 16-byte buffer -> LDS load (buffer_load_dwordx4 ... lds): lane i
+// writes dst_base + 16*i with the 16 bytes at byte offset voff of the
+// buffer (zeros when voff is out of range).  Same waiting rules as g2lds16.
+__device__ __forceinline__ void buf2lds16(i32x4 rsrc, uint32_t voff, void* dst_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+
 }  // namespace tpf

@@ -13,6 +13,8 @@ struct GemmArgs {
   int M, N, K;
   int ksplit, k_chunk;                   // K range of split s: [s*k_chunk, (s+1)*k_chunk)
   float alpha;
+  int a_gather_n;                        // KC row gather of A (0 = none), see gemm_core.hpp
+  int batch;                             // set by gemm_launch
 };
 
 // a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).

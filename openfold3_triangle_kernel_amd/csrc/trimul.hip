@@ -1,275 +1,210 @@
-// Triangle multiplicative update (TriMul) on gfx950: fused row-tile kernels
-// around the channel-batched MFMA contraction of csrc/gemm.hip.
+// Triangle multiplicative update (TriMul) on gfx950, built on the MFMA GEMM
+// main loop of gemm_core.hpp with the gating / LayerNorm work fused into
+// GEMM prologues and epilogues.
 //
 // Stock math (openfold3/core/model/layers/triangular_multiplicative_update.py
 // :1263-1284 and :734-760; LayerNorm openfold3/core/model/primitives/
 // normalization.py:54-78, f32 statistics, eps 1e-5):
 //   zln = LN_in(z);  a = mask * sigmoid(zln Wag^T) * (zln Wap^T);  b likewise
 //   outgoing: x[c,i,j] = sum_k a[i,k,c] b[j,k,c];  incoming: sum_k a[k,i,c] b[k,j,c]
-//   out = (LN_out(x) Wz^T) * sigmoid(zln Wg^T)
+//   out = (LN_out(x) Wz^T) * sigmoid(gl),  gl = zln Wg^T
 //
-// Storage (C == H channels, rows rho = (b*N + r)*N + s of z [B,N,N,C]):
-//   z, zln, out, dz: [R][C] bf16 row-major; dgl (output-gate logit grad)
-//   [R][H].  Weight-gradient operands are stored transposed, [channel][Rp]
-//   (Rp = R rounded up to 8, pad zero): dy^T, xln^T, zln^T and dproj5^T
-//   whose channel blocks are [d p_in (2H) | d g_in (2H) | d g_out (H)].
-//   a, b (and da, db) channel-major "stored" matrices A_c[i][k], B_c[j][k]
+// Storage (C == H channels, natural rows rho = (b*N + r)*N + s of z [B,N,N,C]):
+//   z, zln, gl, out, dz, dy: [R][C] bf16 row-major; xln [R][H];
+//   dproj5 [R][5H] with column blocks [d a_p | d b_p | d a_g | d b_g | d gl]
+//   (the row order of W5 = [p_in; g_in; g_out]);
+//   a, b (and da, db): channel-major "stored" matrices A_c[i][k], B_c[j][k]
 //   with plane size N*Np (row pitch Np = N rounded up to 8, pad columns
-//   zero): outgoing A_c[i][k] = a[i,k,c]; incoming A_c[i][k] = a[k,i,c].
-//   Both directions then contract as x_c = A_c B_c^T (an NT GEMM).
+//   zero): outgoing A_c[i][k] = a[i,k,c]; incoming A_c[i][k] = a[k,i,c], so
+//   both directions contract as the NT GEMM x_c = A_c B_c^T;
 //   x, dx: channel-major [B*H][N][Np] in natural (i, j) order.
-// A tile is 64 positions of one batch item; for a/b tiles the position p is
-// i*N + k of the stored matrix, so stores are contiguous in both directions.
+// The projection kernels walk rows in stored-matrix order m (position
+// p = m % NN of batch item m / NN): the natural row is m itself (outgoing) or
+// the transposed position (incoming), read through the GEMM's row gather.
+//
+// Kernels of one direction:
+//   forward:  tm_ln_rows (LN_in) -> tm_in_proj<fwd> (a, b, gl) -> GEMM x ->
+//             tm_ln_planes (LN_out) -> tm_out_proj<fwd> (out)
+//   backward: tm_out_proj<bwd> (dy, d gl) -> tm_ln_bwd<planes> (dx, LN_out
+//             partials) -> GEMMs da, db -> tm_in_proj<bwd> (d a_p .. d b_g)
+//             -> tm_ln_bwd<rows> (dz, LN_in partials) -> split-K weight
+//             GEMMs -> fixed-order folds.
 #include "common.hpp"
+#include "gemm_core.hpp"
 #include "tpf_gemm.hpp"
 #include "tpf_status.hpp"
 
 namespace tpf {
 
 struct TmGeom {
-  int B, N, Np;
-  int64_t NN;     // N*N positions per batch item
-  int64_t PS;     // N*Np elements per channel-major plane
+  int B, N, Np, H;
+  int64_t NN;  // N*N positions per batch item
+  int64_t PS;  // N*Np elements per channel-major plane
+  int64_t R;   // B*N*N rows
   int outgoing;
+  int ntg;     // gated 128-column weight tiles per branch (64 channels each)
 };
 
-// Source row (b, r, s) of stored-matrix position p = i*N + k.
-__device__ __forceinline__ int64_t tm_src_row(const TmGeom& g, int b, int64_t p) {
-  if (g.outgoing) return (int64_t)b * g.NN + p;
-  const int64_t i = p / g.N, k = p % g.N;  // A_c[i][k] = a[k, i, c]
-  return (int64_t)b * g.NN + k * g.N + i;
-}
+constexpr int kSP = 136;  // bf16 pitch of 128-wide LDS staging tiles
+
 // Element offset of position p = i*N + j inside a channel-major plane.
 __device__ __forceinline__ int64_t tm_plane_off(const TmGeom& g, int64_t p) {
   return (g.Np == g.N) ? p : (p / g.N) * g.Np + (p % g.N);
 }
+// Natural row of stored-order row m.
+__device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
+  if (g.outgoing) return m;
+  const int64_t b = m / g.NN, p = m % g.NN;
+  return b * g.NN + (p % g.N) * g.N + p / g.N;
+}
 
-// LayerNorm of 64 rows (4 threads per row) into an LDS bf16 tile.
-// rows[i] < 0 marks a padding row (written as zeros).  Returns nothing;
-// optionally stores mean/rstd and the normalised rows to global memory.
-template <int C>
-__device__ __forceinline__ void tm_layernorm_tile(const __bf16* __restrict__ src,
-                                                  const int64_t* rows, const float* __restrict__ w,
-                                                  const float* __restrict__ bias, __bf16* Ts,
-                                                  int pitch, float* __restrict__ mean_out,
-                                                  float* __restrict__ rstd_out,
-                                                  __bf16* __restrict__ save) {
-  constexpr int CPT = C / 4;  // channels per thread (multiple of 8)
-  const int tid = threadIdx.x, row = tid >> 2, part = tid & 3;
-  const int64_t rho = rows[row];
-  float x[CPT];
-  if (rho >= 0) {
-#pragma unroll
-    for (int c8 = 0; c8 < CPT / 8; ++c8) {
-      bf16x8 v = ld8(src + rho * C + part * CPT + c8 * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[c8 * 8 + e] = bf2f(v[e]);
+// ---------------------------------------------------------------------------
+// Weight packing (per call, tiny): Wp for the projection GEMMs and W5.
+//   Wp tile t < 2*ntg (branch t / ntg, channel block q = t % ntg): rows
+//   [p c0..c0+31 | g c0..c0+31 | p c0+32..c0+63 | g c0+32..c0+63], c0 = 64q,
+//   so the wave holding output columns 64wn.. sees p and g of the same 32
+//   channels in its two accumulator columns; tile 2*ntg holds g_out.
+//   W5 = [p_in; g_in; g_out] [5H][C].  Missing channels are zero rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tm_pack_weights_kernel(
+    const __bf16* __restrict__ p_in, const __bf16* __restrict__ g_in,
+    const __bf16* __restrict__ g_out, __bf16* __restrict__ wp, __bf16* __restrict__ w5, int C,
+    int ntg) {
+  const int cpr = C / 8;
+  const int wp_rows = (2 * ntg + 1) * 128;
+  const int64_t total = (int64_t)(wp_rows + 5 * C) * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * 256) {
+    const int row = (int)(idx / cpr), ch = (int)(idx % cpr);
+    const __bf16* src = nullptr;
+    __bf16* dst;
+    if (row < wp_rows) {
+      dst = wp + (int64_t)row * C + ch * 8;
+      const int t = row / 128, rr = row % 128;
+      if (t < 2 * ntg) {
+        const int br = t / ntg, q = t % ntg;
+        const int c = 64 * q + 32 * (rr / 64) + (rr & 31);
+        const bool isg = (rr >> 5) & 1;
+        if (c < C) src = (isg ? g_in : p_in) + ((int64_t)br * C + c) * C;
+      } else if (rr < C) {
+        src = g_out + (int64_t)rr * C;
+      }
+    } else {
+      const int j = row - wp_rows;
+      dst = w5 + (int64_t)j * C + ch * 8;
+      src = j < 2 * C ? p_in + (int64_t)j * C
+                      : (j < 4 * C ? g_in + (int64_t)(j - 2 * C) * C : g_out + (int64_t)(j - 4 * C) * C);
     }
+    st8(dst, src ? ld8(src + ch * 8) : zero8());
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LN_in over rows of z (16 lanes per row, 8 channels per lane).
+// ---------------------------------------------------------------------------
+template <int C>
+__global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restrict__ z,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ bias,
+                                                         __bf16* __restrict__ out,
+                                                         float* __restrict__ mean_out,
+                                                         float* __restrict__ rstd_out, int64_t R) {
+  const int l16 = threadIdx.x & 15;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool act = (row < R) && (l16 < C / 8);
+  float x[8];
+  if (act) {
+    const bf16x8 v = ld8(z + row * C + l16 * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf2f(v[e]);
   } else {
 #pragma unroll
-    for (int e = 0; e < CPT; ++e) x[e] = 0.f;
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
   }
   float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < CPT; ++e) s += x[e];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
+  for (int e = 0; e < 8; ++e) s += x[e];
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
   const float mean = s * (1.f / C);
   float v2 = 0.f;
 #pragma unroll
-  for (int e = 0; e < CPT; ++e) { const float d = x[e] - mean; v2 = fmaf(d, d, v2); }
-  v2 += __shfl_xor(v2, 1);
-  v2 += __shfl_xor(v2, 2);
-  const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
+  for (int e = 0; e < 8; ++e) {
+    const float d = act ? x[e] - mean : 0.f;
+    v2 = fmaf(d, d, v2);
+  }
 #pragma unroll
-  for (int c8 = 0; c8 < CPT / 8; ++c8) {
+  for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
+  const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
+  if (act) {
     bf16x8 o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = part * CPT + c8 * 8 + e;
-      o[e] = rho >= 0 ? f2bf((x[c8 * 8 + e] - mean) * rstd * w[c] + bias[c]) : f2bf(0.f);
+      const int c = l16 * 8 + e;
+      o[e] = f2bf((x[e] - mean) * rstd * w[c] + bias[c]);
     }
-    *reinterpret_cast<bf16x8*>(&Ts[row * pitch + part * CPT + c8 * 8]) = o;
-    if (save && rho >= 0) st8(save + rho * C + part * CPT + c8 * 8, o);
-  }
-  if (part == 0 && rho >= 0 && mean_out) {
-    mean_out[rho] = mean;
-    rstd_out[rho] = rstd;
+    st8(out + row * C + l16 * 8, o);
+    if (l16 == 0) {
+      mean_out[row] = mean;
+      rstd_out[row] = rstd;
+    }
   }
 }
 
-// acc += A(32 rows of LDS tile, K=KD) * W[n0 + lane col][0..KD)^T
-template <int KD>
-__device__ __forceinline__ f32x16 tile_mm(const __bf16* As, int pitch, int row0,
-                                          const __bf16* __restrict__ W, int ldw, int n, f32x16 acc) {
-  const int lane = threadIdx.x & 63, rl = lane & 31, hl = lane >> 5;
-#pragma unroll
-  for (int s = 0; s < KD / 16; ++s) {
-    bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[(row0 + rl) * pitch + 16 * s + 8 * hl]);
-    bf16x8 b = ld8(W + (int64_t)n * ldw + 16 * s + 8 * hl);
-    acc = mfma32(a, b, acc);
-  }
-  return acc;
-}
-
 // ---------------------------------------------------------------------------
-// Forward stage 1: LN_in, the four branch projections, gating and mask.
-// Wave w: rows 32*(w&1).., branch w>>1 (0 = a, 1 = b).
+// LN_out over the channels of the channel-major product x: 64 positions per
+// workgroup (natural order), written as row-major xln.
 // ---------------------------------------------------------------------------
-template <int C>
-__global__ __launch_bounds__(256) void tm_in_fwd_kernel(
-    const __bf16* __restrict__ z, const float* __restrict__ mask,
-    const __bf16* __restrict__ p_in, const __bf16* __restrict__ g_in,
-    const float* __restrict__ ln_w, const float* __restrict__ ln_b, __bf16* __restrict__ a_out,
-    __bf16* __restrict__ b_out, __bf16* __restrict__ zln, float* __restrict__ mean_in,
-    float* __restrict__ rstd_in, TmGeom g) {
-  constexpr int H = C, P = C + 8;
-  __shared__ __attribute__((aligned(16))) __bf16 Zs[64 * P];
-  __shared__ int64_t rows[64];
+template <int H>
+__global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restrict__ x,
+                                                           const float* __restrict__ w,
+                                                           const float* __restrict__ bias,
+                                                           __bf16* __restrict__ xln,
+                                                           float* __restrict__ mean_out,
+                                                           float* __restrict__ rstd_out,
+                                                           TmGeom g) {
+  constexpr int T = 64, XP = T + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 Xb[H * XP];
   const int tid = threadIdx.x, b = blockIdx.y;
-  const int64_t p0 = (int64_t)blockIdx.x * 64;
-  if (tid < 64) rows[tid] = (p0 + tid < g.NN) ? tm_src_row(g, b, p0 + tid) : -1;
-  __syncthreads();
-  tm_layernorm_tile<C>(z, rows, ln_w, ln_b, Zs, P, mean_in, rstd_in, zln);
-  __syncthreads();
-
-  const int w = tid >> 6, lane = tid & 63, rl = lane & 31, hl = lane >> 5;
-  const int rb = w & 1, br = w >> 1;
-  __bf16* dst = br ? b_out : a_out;
-  float mk[16];
+  const int64_t p0 = (int64_t)blockIdx.x * T;
+  const bool vec = (g.Np == g.N) && (p0 + T <= g.NN);
+  for (int idx = tid; idx < H * (T / 8); idx += 256) {
+    const int c = idx / (T / 8), ch = idx % (T / 8);
+    const __bf16* plane = x + ((int64_t)b * H + c) * g.PS;
+    if (vec) {
+      *reinterpret_cast<bf16x8*>(&Xb[c * XP + ch * 8]) = ld8(plane + p0 + ch * 8);
+    } else {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = rb * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-    mk[r] = rows[row] >= 0 ? mask[rows[row]] : 0.f;
-  }
-  for (int cb = 0; cb < H / 32; ++cb) {
-    const int n = cb * 32 + rl;
-    f32x16 ap = tile_mm<C>(Zs, P, rb * 32, p_in + (int64_t)br * H * C, C, n, zero16());
-    f32x16 ag = tile_mm<C>(Zs, P, rb * 32, g_in + (int64_t)br * H * C, C, n, zero16());
-    __bf16* plane = dst + ((int64_t)b * H + n) * g.PS;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t p = p0 + rb * 32 + 8 * j + 4 * hl;
-      float val[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) val[i] = mk[4 * j + i] * sigmoidf(ag[4 * j + i]) * ap[4 * j + i];
-      if (g.Np == g.N && (g.NN & 3) == 0 && p + 3 < g.NN) {
-        bf16x4 v4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = f2bf(val[i]);
-        *reinterpret_cast<bf16x4*>(plane + p) = v4;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (p + i < g.NN) plane[tm_plane_off(g, p + i)] = f2bf(val[i]);
+      for (int e = 0; e < 8; ++e) {
+        const int64_t p = p0 + ch * 8 + e;
+        Xb[c * XP + ch * 8 + e] = p < g.NN ? plane[tm_plane_off(g, p)] : static_cast<__bf16>(0.f);
       }
     }
   }
-}
-
-// Load a channel-major [H][T positions] tile of x (natural order) as bf16
-// into LDS Xb[c * pitch + pp]; zeros past the end of the plane.
-template <int H, int T>
-__device__ __forceinline__ void tm_load_chmajor(const __bf16* __restrict__ x, const TmGeom& g,
-                                                int b, int64_t p0, __bf16* Xb, int pitch) {
-  const bool vec = (g.Np == g.N) && (g.NN % 8 == 0) && (p0 + T <= g.NN);
-  if (vec) {
-    for (int idx = threadIdx.x; idx < H * (T / 8); idx += 256) {
-      const int c = idx / (T / 8), ch = idx % (T / 8);
-      bf16x8 v = ld8(x + ((int64_t)b * H + c) * g.PS + p0 + ch * 8);
-      *reinterpret_cast<bf16x8*>(&Xb[c * pitch + ch * 8]) = v;
-    }
-  } else {
-    for (int idx = threadIdx.x; idx < H * T; idx += 256) {
-      const int c = idx / T, pp = idx % T;
-      const int64_t p = p0 + pp;
-      Xb[c * pitch + pp] = (p < g.NN) ? x[((int64_t)b * H + c) * g.PS + tm_plane_off(g, p)]
-                                      : static_cast<__bf16>(0.f);
-    }
-  }
-}
-
-// Store 4 values at consecutive row indices tau..tau+3 of a transposed
-// [channel][Rp] buffer row; rows >= lim (end of the batch item) are skipped.
-__device__ __forceinline__ void st4_rows(__bf16* __restrict__ row_base, int64_t tau, int64_t R,
-                                         const float (&v)[4]) {
-  if ((tau & 3) == 0 && tau + 3 < R) {
-    bf16x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = f2bf(v[i]);
-    *reinterpret_cast<bf16x4*>(row_base + tau) = o;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (tau + i < R) row_base[tau + i] = f2bf(v[i]);
-  }
-}
-
-// Write an LDS tile S[row * pitch + c] (T rows x NC channels) transposed to
-// dst[(c0 + c) * Rp + tau0 + row] for rows with tau0 + row < R (R = end of
-// the batch item's rows).
-template <int NC, int T>
-__device__ __forceinline__ void tm_store_transposed(const __bf16* S, int pitch, __bf16* __restrict__ dst,
-                                                    int c0, int64_t Rp, int64_t tau0, int64_t R) {
-  const bool vec = (tau0 % 8 == 0) && (tau0 + T <= R);
-  for (int idx = threadIdx.x; idx < NC * (T / 8); idx += 256) {
-    const int c = idx / (T / 8), ch = idx % (T / 8);
-    __bf16* d = dst + (int64_t)(c0 + c) * Rp + tau0 + ch * 8;
-    if (vec) {
-      bf16x8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = S[(ch * 8 + e) * pitch + c];
-      st8(d, v);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (tau0 + ch * 8 + e < R) d[e] = S[(ch * 8 + e) * pitch + c];
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Forward stage 3: LN_out over the channel-major product, output projection
-// and the sigmoid output gate from zln.  Rows in natural order.
-// ---------------------------------------------------------------------------
-template <int C>
-__global__ __launch_bounds__(256) void tm_out_fwd_kernel(
-    const __bf16* __restrict__ x, const __bf16* __restrict__ zln,
-    const __bf16* __restrict__ p_out, const __bf16* __restrict__ g_out,
-    const float* __restrict__ ln_w, const float* __restrict__ ln_b, __bf16* __restrict__ out,
-    __bf16* __restrict__ xln, float* __restrict__ mean_out, float* __restrict__ rstd_out,
-    TmGeom g) {
-  constexpr int H = C, P = C + 8, XP = 64 + 8;
-  __shared__ __attribute__((aligned(16))) __bf16 Xb[H * XP];
-  __shared__ __attribute__((aligned(16))) __bf16 Xs[64 * P];
-  __shared__ __attribute__((aligned(16))) __bf16 Zs[64 * P];
-  const int tid = threadIdx.x, b = blockIdx.y;
-  const int64_t p0 = (int64_t)blockIdx.x * 64;
-  tm_load_chmajor<H, 64>(x, g, b, p0, Xb, XP);
-  for (int idx = tid; idx < 64 * (C / 8); idx += 256) {
-    const int row = idx / (C / 8), c8 = (idx % (C / 8)) * 8;
-    const int64_t p = p0 + row;
-    bf16x8 v = (p < g.NN) ? ld8(zln + ((int64_t)b * g.NN + p) * C + c8) : zero8();
-    *reinterpret_cast<bf16x8*>(&Zs[row * P + c8]) = v;
-  }
   __syncthreads();
-  {  // LN over channels of each row: 4 threads per row.
-    constexpr int CPT = H / 4;
-    const int row = tid >> 2, part = tid & 3;
-    const int64_t p = p0 + row;
-    float xv[CPT];
-    float s = 0.f;
+  constexpr int CPT = H / 4;
+  const int row = tid >> 2, part = tid & 3;
+  const int64_t p = p0 + row;
+  float xv[CPT];
+  float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < CPT; ++e) { xv[e] = bf2f(Xb[(part * CPT + e) * XP + row]); s += xv[e]; }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    const float mean = s * (1.f / H);
-    float v2 = 0.f;
+  for (int e = 0; e < CPT; ++e) {
+    xv[e] = bf2f(Xb[(part * CPT + e) * XP + row]);
+    s += xv[e];
+  }
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  const float mean = s * (1.f / H);
+  float v2 = 0.f;
 #pragma unroll
-    for (int e = 0; e < CPT; ++e) { const float d = xv[e] - mean; v2 = fmaf(d, d, v2); }
-    v2 += __shfl_xor(v2, 1);
-    v2 += __shfl_xor(v2, 2);
-    const float rstd = rsqrtf(v2 * (1.f / H) + 1e-5f);
+  for (int e = 0; e < CPT; ++e) {
+    const float d = xv[e] - mean;
+    v2 = fmaf(d, d, v2);
+  }
+  v2 += __shfl_xor(v2, 1);
+  v2 += __shfl_xor(v2, 2);
+  const float rstd = rsqrtf(v2 * (1.f / H) + 1e-5f);
+  if (p < g.NN) {
     const int64_t rho = (int64_t)b * g.NN + p;
 #pragma unroll
     for (int c8 = 0; c8 < CPT / 8; ++c8) {
@@ -277,314 +212,393 @@ __global__ __launch_bounds__(256) void tm_out_fwd_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = part * CPT + c8 * 8 + e;
-        o[e] = f2bf((xv[c8 * 8 + e] - mean) * rstd * ln_w[c] + ln_b[c]);
+        o[e] = f2bf((xv[c8 * 8 + e] - mean) * rstd * w[c] + bias[c]);
       }
-      *reinterpret_cast<bf16x8*>(&Xs[row * P + part * CPT + c8 * 8]) = o;
-      if (xln && p < g.NN) st8(xln + rho * H + part * CPT + c8 * 8, o);
+      st8(xln + rho * H + part * CPT + c8 * 8, o);
     }
-    if (part == 0 && p < g.NN && mean_out) { mean_out[rho] = mean; rstd_out[rho] = rstd; }
-  }
-  __syncthreads();
-  const int w = tid >> 6, lane = tid & 63, rl = lane & 31, hl = lane >> 5;
-  const int rb = w & 1;
-  for (int cb = w >> 1; cb < C / 32; cb += 2) {
-    const int n = cb * 32 + rl;
-    f32x16 y = tile_mm<H>(Xs, P, rb * 32, p_out, H, n, zero16());
-    f32x16 gl = tile_mm<C>(Zs, P, rb * 32, g_out, C, n, zero16());
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t p = p0 + rb * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-      if (p < g.NN) out[((int64_t)b * g.NN + p) * C + n] = f2bf(y[r] * sigmoidf(gl[r]));
+    if (part == 0) {
+      mean_out[rho] = mean;
+      rstd_out[rho] = rstd;
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Backward stage 1 (32-row tiles, natural row order): output gate, output
-// projection and LN_out backward.
-//   dy = dout * s(gl); dgl = dout * y * s(gl) (1 - s(gl));  d_xln = dy Wz
-//   dx = rstd * (g - mean(g) - xhat * mean(g * xhat)),  g = d_xln * gamma_out
-// Writes dx channel-major, dgl row-major [R][H], dy^T and xln^T as
-// [channel][Rp] (K-contiguous operands of the weight-gradient GEMM), and
-// per-workgroup partials of d gamma_out / d beta_out.
-// ---------------------------------------------------------------------------
-template <int C>
-__global__ __launch_bounds__(256) void tm_out_bwd_kernel(
-    const __bf16* __restrict__ dout, const __bf16* __restrict__ x,
-    const __bf16* __restrict__ xln, const __bf16* __restrict__ zln,
-    const float* __restrict__ mean_out, const float* __restrict__ rstd_out,
-    const __bf16* __restrict__ p_out, const __bf16* __restrict__ g_out,
-    const __bf16* __restrict__ p_out_t, const float* __restrict__ ln_w,
-    __bf16* __restrict__ dy_t, __bf16* __restrict__ xln_t, __bf16* __restrict__ dgl,
-    __bf16* __restrict__ dx, float* __restrict__ dgamma_part, float* __restrict__ dbeta_part,
-    TmGeom g, int64_t Rp) {
-  constexpr int H = C, T = 32, P = C + 8, XP = T + 8, GP = H + 4;
-  __shared__ __attribute__((aligned(16))) __bf16 Xb[H * XP];     // x tile, channel-major
-  __shared__ __attribute__((aligned(16))) __bf16 XZ[2 * T * P];  // xln | zln, later d_xln f32
-  __shared__ __attribute__((aligned(16))) __bf16 Ds[T * P];      // dy tile
-  __shared__ __attribute__((aligned(16))) __bf16 Dx[H * XP];     // dx tile, channel-major
-  __shared__ float mst[T], rst[T];
-  __bf16* Xs = XZ;
-  __bf16* Zs = XZ + T * P;
-  float* Gf = reinterpret_cast<float*>(XZ);
-  const int tid = threadIdx.x, b = blockIdx.y;
-  const int64_t p0 = (int64_t)blockIdx.x * T;
-  // Transposed stores stop at the end of this batch item's rows.
-  const int64_t lim = (int64_t)b * g.NN + g.NN;
-  const int64_t tau0 = (int64_t)b * g.NN + p0;
-  tm_load_chmajor<H, T>(x, g, b, p0, Xb, XP);
-  for (int idx = tid; idx < T * (C / 8); idx += 256) {
-    const int row = idx / (C / 8), c8 = (idx % (C / 8)) * 8;
-    const bool ok = p0 + row < g.NN;
-    const int64_t rho = tau0 + row;
-    *reinterpret_cast<bf16x8*>(&Zs[row * P + c8]) = ok ? ld8(zln + rho * C + c8) : zero8();
-    *reinterpret_cast<bf16x8*>(&Xs[row * P + c8]) = ok ? ld8(xln + rho * H + c8) : zero8();
+// Accumulator coordinates of this lane inside the 128 x 128 tile.
+struct AccPos {
+  int rl, hl, wm, wn;
+  __device__ __forceinline__ AccPos() {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    rl = lane & 31; hl = lane >> 5; wm = w >> 1; wn = w & 1;
   }
-  if (tid < T) {
-    const bool ok = p0 + tid < g.NN;
-    mst[tid] = ok ? mean_out[tau0 + tid] : 0.f;
-    rst[tid] = ok ? rstd_out[tau0 + tid] : 0.f;
+  __device__ __forceinline__ int row(int i, int r) const {
+    return 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
   }
-  __syncthreads();
-  tm_store_transposed<H, T>(Xs, P, xln_t, 0, Rp, tau0, lim);
-  const int w = tid >> 6, lane = tid & 63, rl = lane & 31, hl = lane >> 5;
-  for (int cb = w; cb < C / 32; cb += 4) {
-    const int n = cb * 32 + rl;
-    f32x16 y = tile_mm<H>(Xs, P, 0, p_out, H, n, zero16());
-    f32x16 gl = tile_mm<C>(Zs, P, 0, g_out, C, n, zero16());
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float dyv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * j + i, row = 8 * j + 4 * hl + i;
-        const bool ok = p0 + row < g.NN;
-        const int64_t rho = tau0 + row;
-        const float go = ok ? bf2f(dout[rho * C + n]) : 0.f;
-        const float sg = sigmoidf(gl[r]);
-        dyv[i] = go * sg;
-        Ds[row * P + n] = f2bf(dyv[i]);
-        if (ok) dgl[rho * H + n] = f2bf(go * y[r] * sg * (1.f - sg));
-      }
-      st4_rows(dy_t + (int64_t)n * Rp, tau0 + 8 * j + 4 * hl, lim, dyv);
-    }
+  __device__ __forceinline__ int col(int j) const { return 64 * wn + 32 * j + rl; }
+};
+
+// Copy a [128 rows][ncols] bf16 LDS tile (pitch kSP) to rows rho_s[row] of a
+// row-major global matrix (pitch ld, column offset c0); rows < 0 skipped.
+__device__ __forceinline__ void tm_store_rows(const __bf16* S, int ncols, const int64_t* rho_s,
+                                              __bf16* __restrict__ dst, int64_t ld, int c0) {
+  const int cpr = ncols / 8;
+  for (int idx = threadIdx.x; idx < 128 * cpr; idx += 256) {
+    const int row = idx / cpr, ch = idx % cpr;
+    const int64_t rho = rho_s[row];
+    if (rho >= 0) st8(dst + rho * ld + c0 + ch * 8, *reinterpret_cast<const bf16x8*>(&S[row * kSP + ch * 8]));
   }
-  __syncthreads();
-  // d_xln (T x H) = dy (T x C) * Wz (C x H); B operand = rows of Wz^T.
-  {
-    f32x16 d = zero16();
-    const bool has = w < H / 32;
-    if (has) d = tile_mm<C>(Ds, P, 0, p_out_t, C, w * 32 + rl, d);
-    if (has) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) Gf[(8 * (r >> 2) + 4 * hl + (r & 3)) * GP + w * 32 + rl] = d[r];
-    }
+}
+__device__ __forceinline__ void tm_load_rows(__bf16* S, int ncols, const int64_t* rho_s,
+                                             const __bf16* __restrict__ src, int64_t ld) {
+  const int cpr = ncols / 8;
+  for (int idx = threadIdx.x; idx < 128 * cpr; idx += 256) {
+    const int row = idx / cpr, ch = idx % cpr;
+    const int64_t rho = rho_s[row];
+    *reinterpret_cast<bf16x8*>(&S[row * kSP + ch * 8]) = rho >= 0 ? ld8(src + rho * ld + ch * 8) : zero8();
   }
-  __syncthreads();
-  {  // LN_out backward: 8 threads per row.
-    constexpr int CPT = H / 8;
-    const int row = tid >> 3, part = tid & 7;
-    const float mean = mst[row], rstd = rst[row];
-    float sg = 0.f, sgx = 0.f;
+}
+
+// Move [nch channels][128 positions] between an LDS tile S[c * kSP + pos]
+// and channel-major planes (plane index b*H + c0 + c, position of tile row
+// pos = m0 + pos within its batch item).  STORE: LDS -> planes.
+template <bool STORE>
+__device__ __forceinline__ void tm_plane_tile(__bf16* S, int nch, __bf16* planes, const TmGeom& g,
+                                              int64_t m0, int c0) {
+  for (int idx = threadIdx.x; idx < nch * 16; idx += 256) {
+    const int cl = idx >> 4, chn = idx & 15;
+    const int c = c0 + cl;
+    if (c >= g.H) continue;
+    const int64_t mb = m0 + 8 * chn;
+    __bf16* s = S + cl * kSP + 8 * chn;
+    if (g.Np == g.N && mb + 7 < g.R) {
+      // NN is a multiple of 64 here, so the 8 positions share a batch item.
+      const int64_t b = mb / g.NN, p = mb % g.NN;
+      __bf16* d = planes + ((int64_t)b * g.H + c) * g.PS + p;
+      if (STORE) st8(d, *reinterpret_cast<const bf16x8*>(s));
+      else *reinterpret_cast<bf16x8*>(s) = ld8(d);
+    } else {
 #pragma unroll
-    for (int e = 0; e < CPT; ++e) {
-      const int c = part * CPT + e;
-      const float xh = (bf2f(Xb[c * XP + row]) - mean) * rstd;
-      const float gv = Gf[row * GP + c] * ln_w[c];
-      sg += gv;
-      sgx = fmaf(gv, xh, sgx);
-    }
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) { sg += __shfl_xor(sg, m); sgx += __shfl_xor(sgx, m); }
-    sg *= 1.f / H;
-    sgx *= 1.f / H;
-#pragma unroll
-    for (int e = 0; e < CPT; ++e) {
-      const int c = part * CPT + e;
-      const float xh = (bf2f(Xb[c * XP + row]) - mean) * rstd;
-      const float gv = Gf[row * GP + c] * ln_w[c];
-      Dx[c * XP + row] = f2bf(rstd * (gv - sg - xh * sgx));
-    }
-  }
-  __syncthreads();
-  {
-    const bool vec = (g.Np == g.N) && (g.NN % 8 == 0) && (p0 + T <= g.NN);
-    for (int idx = tid; idx < H * (T / 8); idx += 256) {
-      const int c = idx / (T / 8), ch = idx % (T / 8);
-      __bf16* plane = dx + ((int64_t)b * H + c) * g.PS;
-      if (vec) {
-        st8(plane + p0 + ch * 8, *reinterpret_cast<const bf16x8*>(&Dx[c * XP + ch * 8]));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int64_t p = p0 + ch * 8 + e;
-          if (p < g.NN) plane[tm_plane_off(g, p)] = Dx[c * XP + ch * 8 + e];
+      for (int e = 0; e < 8; ++e) {
+        const int64_t m = mb + e;
+        if (m < g.R) {
+          const int64_t b = m / g.NN, p = m % g.NN;
+          __bf16* d = planes + ((int64_t)b * g.H + c) * g.PS + tm_plane_off(g, p);
+          if (STORE) *d = s[e];
+          else s[e] = *d;
+        } else if (!STORE) {
+          s[e] = static_cast<__bf16>(0.f);
         }
       }
     }
   }
-  if (tid < H) {
-    float sgm = 0.f, sbt = 0.f;
-    for (int row = 0; row < T; ++row) {
-      const float gr = Gf[row * GP + tid];
-      const float xh = (bf2f(Xb[tid * XP + row]) - mst[row]) * rst[row];
-      sgm = fmaf(gr, xh, sgm);
-      sbt += gr;
+}
+
+// ---------------------------------------------------------------------------
+// Input projections (stored row order).  Forward: tiles nt < 2*ntg produce
+// a / b = mask * sigmoid(g) * p for 64 channels (channel-major stores);
+// tile 2*ntg produces the output-gate logits gl (row-major).  Backward
+// (BWD): recompute p, g and write d p = d * mask * s(g),
+// d g = d * mask * p * s(g) (1 - s(g)) into dproj5, d = da / db.
+// ---------------------------------------------------------------------------
+template <bool BWD>
+__global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
+    const __bf16* __restrict__ zln, const __bf16* __restrict__ wp, const float* __restrict__ mask,
+    __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl,
+    __bf16* __restrict__ dproj5, TmGeom g, int C) {
+  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  __shared__ float mask_s[128];
+  __shared__ int64_t rho_s[128];
+  const int H = g.H;
+  const int tn = 2 * g.ntg + (BWD ? 0 : 1);
+  const int64_t tm = (g.R + 127) / 128;
+  const int64_t T = xcd_order(tm * tn);
+  if (T < 0) return;
+  const int nt = (int)(T % tn);
+  const int64_t m0 = (T / tn) * 128;
+  if (threadIdx.x < 128) {
+    const int64_t m = m0 + threadIdx.x;
+    const int64_t rho = m < g.R ? tm_phys_row(g, m) : -1;
+    rho_s[threadIdx.x] = rho;
+    mask_s[threadIdx.x] = rho >= 0 ? mask[rho] : 0.f;
+  }
+  GemmOperand A{zln, C, (int)g.R, g.outgoing ? 0 : g.N};
+  GemmOperand W{wp, C, (2 * g.ntg + 1) * 128, 0};
+  f32x16 acc[2][2];
+  gemm_tile<true, true>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
+  const AccPos ap;
+  __bf16* S0 = reinterpret_cast<__bf16*>(smem);
+
+  if (!BWD && nt == 2 * g.ntg) {  // output-gate logits, row-major
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S0[ap.row(i, r) * kSP + ap.col(j)] = f2bf(acc[i][j][r]);
+    __syncthreads();
+    tm_store_rows(S0, C, rho_s, gl, C, 0);
+    return;
+  }
+  const int br = nt / g.ntg, q = nt % g.ntg;
+  const int cl = 32 * ap.wn + ap.rl;  // channel 64q + cl
+  if (!BWD) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = ap.row(i, r);
+        S0[cl * kSP + row] = f2bf(mask_s[row] * sigmoidf(acc[i][1][r]) * acc[i][0][r]);
+      }
+    __syncthreads();
+    tm_plane_tile<true>(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
+    return;
+  }
+  // Backward: d tile [64 ch][128 pos] in S0, outputs [128 rows][dp 64 | dg 64] in So.
+  __bf16* So = S0 + 64 * kSP;
+  tm_plane_tile<false>(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = ap.row(i, r);
+      const float d = bf2f(S0[cl * kSP + row]) * mask_s[row];
+      const float p = acc[i][0][r];
+      const float s = sigmoidf(acc[i][1][r]);
+      So[row * kSP + cl] = f2bf(d * s);
+      So[row * kSP + 64 + cl] = f2bf(d * p * s * (1.f - s));
     }
-    const int64_t blk = (int64_t)b * gridDim.x + blockIdx.x;
-    dgamma_part[blk * 4 * H + tid] = sgm;
-    dbeta_part[blk * 4 * H + tid] = sbt;
+  __syncthreads();
+  const int nvalid = min(64, H - 64 * q) / 8;  // 8-channel chunks inside H
+  for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
+    const int row = idx >> 4, k = idx & 15, isg = k >> 3, c8 = k & 7;
+    const int64_t rho = rho_s[row];
+    if (rho < 0 || c8 >= nvalid) continue;
+    const int col = (isg ? 2 * H : 0) + br * H + 64 * q + 8 * c8;
+    st8(dproj5 + rho * 5 * H + col, *reinterpret_cast<const bf16x8*>(&So[row * kSP + isg * 64 + 8 * c8]));
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward stage 3 (32-row tiles in stored-matrix order): gate / mask
-// backward of the four branch projections (recomputed from zln),
-// d_zln = dproj5 * W5, LN_in backward.  Writes dproj5^T and zln^T as
-// [channel][Rp] in tile order (K-contiguous weight-gradient operands).
+// Output projection y = xln Wz^T (natural rows).  Forward: out = y s(gl).
+// Backward (BWD): dy = dout s(gl) (row-major) and
+// d gl = dout y s(gl) (1 - s(gl)) into the last block of dproj5.
 // ---------------------------------------------------------------------------
-template <int C>
-__global__ __launch_bounds__(256) void tm_in_bwd_kernel(
-    const __bf16* __restrict__ z, const __bf16* __restrict__ zln, const float* __restrict__ mask,
-    const __bf16* __restrict__ p_in, const __bf16* __restrict__ g_in,
-    const __bf16* __restrict__ da, const __bf16* __restrict__ db,
-    const __bf16* __restrict__ dgl, const __bf16* __restrict__ w5_t,
-    const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
-    const float* __restrict__ ln_w, __bf16* __restrict__ dproj5_t, __bf16* __restrict__ zln_t,
-    __bf16* __restrict__ dz, float* __restrict__ dgamma_part, float* __restrict__ dbeta_part,
-    TmGeom g, int64_t Rp) {
-  constexpr int H = C, T = 32, P = C + 8, PP = 5 * H + 8, GP = C + 4;
-  __shared__ __attribute__((aligned(16))) __bf16 Zs[T * P];
-  __shared__ __attribute__((aligned(16))) __bf16 Ps[T * PP];  // later: d_zln | xhat (f32)
-  __shared__ int64_t rows[T];
-  __shared__ float mst[T], rst[T];
-  float* Gf = reinterpret_cast<float*>(Ps);
-  float* Xh = Gf + T * GP;
-  const int tid = threadIdx.x, b = blockIdx.y;
-  const int64_t p0 = (int64_t)blockIdx.x * T;
-  // Transposed stores stop at the end of this batch item's rows.
-  const int64_t lim = (int64_t)b * g.NN + g.NN;
-  const int64_t tau0 = (int64_t)b * g.NN + p0;
-  if (tid < T) {
-    const int64_t rho = (p0 + tid < g.NN) ? tm_src_row(g, b, p0 + tid) : -1;
-    rows[tid] = rho;
-    mst[tid] = rho >= 0 ? mean_in[rho] : 0.f;
-    rst[tid] = rho >= 0 ? rstd_in[rho] : 0.f;
-  }
+template <bool BWD>
+__global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
+    const __bf16* __restrict__ xln, const __bf16* __restrict__ p_out,
+    const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, __bf16* __restrict__ out,
+    __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, TmGeom g, int C) {
+  constexpr int kStage = 128 * kSP * 2;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage > kGMainLdsBytes ? 2 * kStage : kGMainLdsBytes];
+  __shared__ int64_t rho_s[128];
+  const int H = g.H;
+  const int64_t T = xcd_order((g.R + 127) / 128);
+  if (T < 0) return;
+  const int64_t m0 = T * 128;
+  if (threadIdx.x < 128) rho_s[threadIdx.x] = m0 + threadIdx.x < g.R ? m0 + threadIdx.x : -1;
+  GemmOperand A{xln, H, (int)g.R, 0};
+  GemmOperand W{p_out, H, C, 0};
+  f32x16 acc[2][2];
+  gemm_tile<true, true>(A, W, (int)m0, 0, 0, H, smem, acc);
+  const AccPos ap;
+  __bf16* Sg = reinterpret_cast<__bf16*>(smem);
+  __bf16* Sd = reinterpret_cast<__bf16*>(smem + kStage);
+  tm_load_rows(Sg, C, rho_s, gl, C);
+  if (BWD) tm_load_rows(Sd, C, rho_s, dout, C);
   __syncthreads();
-  for (int idx = tid; idx < T * (C / 8); idx += 256) {
-    const int row = idx / (C / 8), c8 = (idx % (C / 8)) * 8;
-    const int64_t rho = rows[row];
-    *reinterpret_cast<bf16x8*>(&Zs[row * P + c8]) = rho >= 0 ? ld8(zln + rho * C + c8) : zero8();
-    *reinterpret_cast<bf16x8*>(&Ps[row * PP + 4 * H + c8]) =
-        rho >= 0 ? ld8(dgl + rho * H + c8) : zero8();
-  }
-  __syncthreads();
-  tm_store_transposed<C, T>(Zs, P, zln_t, 0, Rp, tau0, lim);
-  tm_store_transposed<H, T>(Ps + 4 * H, PP, dproj5_t, 4 * H, Rp, tau0, lim);
-  const int w = tid >> 6, lane = tid & 63, rl = lane & 31, hl = lane >> 5;
-  const int br = w >> 1;
-  const __bf16* dsrc = br ? db : da;
-  float mk[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = 8 * (r >> 2) + 4 * hl + (r & 3);
-    mk[r] = rows[row] >= 0 ? mask[rows[row]] : 0.f;
-  }
-  const bool vec = (g.Np == g.N) && (g.NN % 4 == 0);
-  for (int cb = w & 1; cb < H / 32; cb += 2) {
-    const int n = cb * 32 + rl;
-    f32x16 ap = tile_mm<C>(Zs, P, 0, p_in + (int64_t)br * H * C, C, n, zero16());
-    f32x16 ag = tile_mm<C>(Zs, P, 0, g_in + (int64_t)br * H * C, C, n, zero16());
-    const __bf16* plane = dsrc + ((int64_t)b * H + n) * g.PS;
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t pj = p0 + 8 * j + 4 * hl;
-      float dv[4];
-      if (vec && pj + 3 < g.NN) {
-        bf16x4 v4 = ld4(plane + pj);
+    for (int j = 0; j < 2; ++j) {
+      const int col = ap.col(j);
+      if (col >= C) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dv[i] = bf2f(v4[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dv[i] = (pj + i < g.NN) ? bf2f(plane[tm_plane_off(g, pj + i)]) : 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const int o = ap.row(i, r) * kSP + col;
+        const float s = sigmoidf(bf2f(Sg[o]));
+        const float y = acc[i][j][r];
+        if (!BWD) {
+          Sg[o] = f2bf(y * s);
+        } else {
+          const float go = bf2f(Sd[o]);
+          Sd[o] = f2bf(go * s);
+          Sg[o] = f2bf(go * y * s * (1.f - s));
+        }
       }
-      float dpv[4], dgv[4];
+    }
+  __syncthreads();
+  if (!BWD) {
+    tm_store_rows(Sg, C, rho_s, out, C, 0);
+  } else {
+    tm_store_rows(Sd, C, rho_s, dy, C, 0);
+    tm_store_rows(Sg, C, rho_s, dproj5, 5 * H, 4 * H);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm backward fused onto d_xhat-producing GEMMs (natural rows):
+//   PLANES (LN_out):  G = dy Wz  (A = dy [R][C], B = Wz read MN), x from the
+//                     channel-major planes, dx written to planes;
+//   rows   (LN_in):   G = dproj5 W5 (A = dproj5 [R][5H], B = W5 read MN),
+//                     x = z rows, dz written row-major.
+//   g = G * gamma;  dx = rstd (g - mean(g) - xhat mean(g xhat));
+//   per-tile partials d gamma = sum G xhat, d beta = sum G into
+//   lnp[tile][slot0 | slot0 + 1][W] (W channels).
+// The epilogue works on the accumulators in registers: the x tile sits in
+// LDS in a layout whose reads give each lane the 4 consecutive rows of one
+// accumulator column (plain 8-byte reads for [channel][row], transposing
+// reads for [row][channel]); row sums are reduced across the 32 columns of
+// a wave with a transposing butterfly and across the two column waves in
+// LDS, column sums across the two row halves with a lane swap and across
+// the row waves in LDS.  All reductions run in a fixed order.
+// ---------------------------------------------------------------------------
+
+// x values of acc[i][j] rows 4*rq .. 4*rq+3 (of this lane's 16 registers).
+template <bool PLANES>
+__device__ __forceinline__ bf16x4 tm_x4(const __bf16* Xt, const AccPos& ap, int i, int j, int rq) {
+  const int rbase = 64 * ap.wm + 32 * i + 8 * rq;
+  if (PLANES) {
+    const int row = rbase + 4 * ap.hl;
+    return *reinterpret_cast<const bf16x4*>(Xt + ap.col(j) * kSP + row);
+  }
+  return tr_col4(Xt, kSP, rbase, rbase + 4, 64 * ap.wn + 32 * j);
+}
+
+template <bool PLANES>
+__global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
+    const __bf16* __restrict__ a_op, int64_t a_ld, const __bf16* __restrict__ w_op, int K,
+    const __bf16* __restrict__ xsrc, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gamma, __bf16* __restrict__ dst, float* __restrict__ lnp,
+    int slot0, TmGeom g, int W) {
+  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  __shared__ __attribute__((aligned(16))) float mean_s[128], rstd_s[128];
+  __shared__ __attribute__((aligned(16))) float rsum[2][2][128];  // [quantity][wn][row]
+  __shared__ float csum[2][2][128];                               // [quantity][wm][col]
+  __shared__ int64_t rho_s[128];
+  const int tid = threadIdx.x;
+  const int64_t T = xcd_order((g.R + 127) / 128);
+  if (T < 0) return;
+  const int64_t m0 = T * 128;
+  if (tid < 128) {
+    const int64_t m = m0 + tid;
+    const bool ok = m < g.R;
+    rho_s[tid] = ok ? m : -1;
+    mean_s[tid] = ok ? mean[m] : 0.f;
+    rstd_s[tid] = ok ? rstd[m] : 0.f;
+  }
+  GemmOperand A{a_op, a_ld, (int)g.R, 0};
+  GemmOperand B{w_op, W, W, 0};
+  f32x16 acc[2][2];
+  gemm_tile<true, false>(A, B, (int)m0, 0, 0, K, smem, acc);
+  __bf16* Xt = reinterpret_cast<__bf16*>(smem);  // [ch][row] (PLANES) or [row][ch]
+  if (PLANES) tm_plane_tile<false>(Xt, 128, const_cast<__bf16*>(xsrc), g, m0, 0);
+  else tm_load_rows(Xt, W, rho_s, xsrc, W);
+  __syncthreads();
+  const AccPos ap;
+  const int lane = tid & 63;
+  float gam[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * j + i, row = 8 * j + 4 * hl + i;
-        const float sg = sigmoidf(ag[r]);
-        dpv[i] = dv[i] * mk[r] * sg;
-        dgv[i] = dv[i] * mk[r] * ap[r] * sg * (1.f - sg);
-        Ps[row * PP + br * H + n] = f2bf(dpv[i]);
-        Ps[row * PP + 2 * H + br * H + n] = f2bf(dgv[i]);
+  for (int j = 0; j < 2; ++j) gam[j] = ap.col(j) < W ? gamma[ap.col(j)] : 0.f;
+  // Pass 1: per-row partial sums over this lane's two columns, per-column
+  // partial sums over this lane's 32 rows.
+  float rs_g[32], rs_gx[32];
+  float cs_g[2] = {0.f, 0.f}, cs_gx[2] = {0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 32; ++t) { rs_g[t] = 0.f; rs_gx[t] = 0.f; }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int row0 = 64 * ap.wm + 32 * i + 8 * rq + 4 * ap.hl;
+      const f32x4 mu = *reinterpret_cast<const f32x4*>(&mean_s[row0]);
+      const f32x4 rs = *reinterpret_cast<const f32x4*>(&rstd_s[row0]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bf16x4 xv = tm_x4<PLANES>(Xt, ap, i, j, rq);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * rq + e;
+          const float G = acc[i][j][r];
+          const float xh = (bf2f(xv[e]) - mu[e]) * rs[e];
+          const float gv = G * gam[j];
+          rs_g[16 * i + r] += gv;
+          rs_gx[16 * i + r] = fmaf(gv, xh, rs_gx[16 * i + r]);
+          cs_g[j] += G;
+          cs_gx[j] = fmaf(G, xh, cs_gx[j]);
+        }
       }
-      st4_rows(dproj5_t + (int64_t)(br * H + n) * Rp, tau0 + 8 * j + 4 * hl, lim, dpv);
-      st4_rows(dproj5_t + (int64_t)(2 * H + br * H + n) * Rp, tau0 + 8 * j + 4 * hl, lim, dgv);
+    }
+  // Transposing butterfly over the 32 columns of the wave: lane rl ends with
+  // the full sums of value index t = rl.
+#pragma unroll
+  for (int lvl = 0; lvl < 5; ++lvl) {
+    const int m = 16 >> lvl, half = 16 >> lvl;
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int k = 0; k < half; ++k) {
+      const float sg = up ? rs_g[k] : rs_g[k + half];
+      const float sx = up ? rs_gx[k] : rs_gx[k + half];
+      const float rg = __shfl_xor(sg, m);
+      const float rx = __shfl_xor(sx, m);
+      rs_g[k] = (up ? rs_g[k + half] : rs_g[k]) + rg;
+      rs_gx[k] = (up ? rs_gx[k + half] : rs_gx[k]) + rx;
+    }
+  }
+  {
+    const int t = ap.rl, i = t >> 4, r = t & 15;
+    const int row = ap.row(i, r);
+    rsum[0][ap.wn][row] = rs_g[0];
+    rsum[1][ap.wn][row] = rs_gx[0];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float a0 = xor32_sum(cs_g[j]), a1 = xor32_sum(cs_gx[j]);
+    if (ap.hl == 0) {
+      csum[0][ap.wm][ap.col(j)] = a0;
+      csum[1][ap.wm][ap.col(j)] = a1;
     }
   }
   __syncthreads();
-  {  // d_zln (T x C) = dproj5 (T x 5H) * W5 (5H x C); B operand rows of W5^T.
-    f32x16 d = zero16();
-    const bool has = w < C / 32;
-    if (has) d = tile_mm<5 * H>(Ps, PP, 0, w5_t, 5 * H, w * 32 + rl, d);
-    __syncthreads();  // Ps is overwritten by Gf below
-    if (has) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) Gf[(8 * (r >> 2) + 4 * hl + (r & 3)) * GP + w * 32 + rl] = d[r];
-    }
+  if (tid < W) {
+    float* part = lnp + T * 4 * W;
+    part[slot0 * W + tid] = csum[1][0][tid] + csum[1][1][tid];
+    part[(slot0 + 1) * W + tid] = csum[0][0][tid] + csum[0][1][tid];
   }
-  __syncthreads();
-  {  // LN_in backward: 8 threads per row, 4-channel vectors.
-    constexpr int CPT = C / 8;
-    const int row = tid >> 3, part = tid & 7;
-    const int64_t rho = rows[row];
-    const bool ok = rho >= 0;
-    const float mean = mst[row], rstd = rst[row];
-    float xh[CPT];
+  // Pass 2: dx in place of x (each element is read and written by one lane).
+  const float invW = 1.f / W;
 #pragma unroll
-    for (int c4 = 0; c4 < CPT / 4; ++c4) {
-      bf16x4 v = ok ? ld4(z + rho * C + part * CPT + c4 * 4) : bf16x4{};
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) xh[c4 * 4 + e] = ok ? (bf2f(v[e]) - mean) * rstd : 0.f;
-    }
-    float sg = 0.f, sgx = 0.f;
+    for (int rq = 0; rq < 4; ++rq) {
+      const int row0 = 64 * ap.wm + 32 * i + 8 * rq + 4 * ap.hl;
+      const f32x4 mu = *reinterpret_cast<const f32x4*>(&mean_s[row0]);
+      const f32x4 rs = *reinterpret_cast<const f32x4*>(&rstd_s[row0]);
+      const f32x4 sg0 = *reinterpret_cast<const f32x4*>(&rsum[0][0][row0]);
+      const f32x4 sg1 = *reinterpret_cast<const f32x4*>(&rsum[0][1][row0]);
+      const f32x4 sx0 = *reinterpret_cast<const f32x4*>(&rsum[1][0][row0]);
+      const f32x4 sx1 = *reinterpret_cast<const f32x4*>(&rsum[1][1][row0]);
 #pragma unroll
-    for (int e = 0; e < CPT; ++e) {
-      const int c = part * CPT + e;
-      const float gv = Gf[row * GP + c] * ln_w[c];
-      sg += gv;
-      sgx = fmaf(gv, xh[e], sgx);
-      Xh[row * GP + c] = xh[e];
-    }
+      for (int j = 0; j < 2; ++j) {
+        const bf16x4 xv = tm_x4<PLANES>(Xt, ap, i, j, rq);
+        bf16x4 o;
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1) { sg += __shfl_xor(sg, m); sgx += __shfl_xor(sgx, m); }
-    sg *= 1.f / C;
-    sgx *= 1.f / C;
+        for (int e = 0; e < 4; ++e) {
+          const float mg = (sg0[e] + sg1[e]) * invW, mgx = (sx0[e] + sx1[e]) * invW;
+          const float xh = (bf2f(xv[e]) - mu[e]) * rs[e];
+          const float gv = acc[i][j][4 * rq + e] * gam[j];
+          o[e] = f2bf(rs[e] * (gv - mg - xh * mgx));
+        }
+        if (PLANES) {
+          *reinterpret_cast<bf16x4*>(Xt + ap.col(j) * kSP + row0) = o;
+        } else {
 #pragma unroll
-    for (int c4 = 0; c4 < CPT / 4; ++c4) {
-      bf16x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = part * CPT + c4 * 4 + e;
-        const float gv = Gf[row * GP + c] * ln_w[c];
-        o[e] = f2bf(rstd * (gv - sg - xh[c4 * 4 + e] * sgx));
+          for (int e = 0; e < 4; ++e) Xt[(row0 + e) * kSP + ap.col(j)] = o[e];
+        }
       }
-      if (ok) *reinterpret_cast<bf16x4*>(dz + rho * C + part * CPT + c4 * 4) = o;
     }
-  }
   __syncthreads();
-  if (tid < C) {
-    float sgm = 0.f, sbt = 0.f;
-    for (int row = 0; row < T; ++row) {
-      const float gr = Gf[row * GP + tid];
-      sgm = fmaf(gr, Xh[row * GP + tid], sgm);
-      sbt += gr;
-    }
-    const int64_t blk = (int64_t)b * gridDim.x + blockIdx.x;
-    dgamma_part[blk * 4 * C + tid] = sgm;
-    dbeta_part[blk * 4 * C + tid] = sbt;
-  }
+  if (PLANES) tm_plane_tile<true>(Xt, 128, dst, g, m0, 0);
+  else tm_store_rows(Xt, W, rho_s, dst, W, 0);
 }
 
 // Zero-fill (used instead of hipMemsetAsync so callers may capture graphs).
@@ -597,6 +611,7 @@ static int zero_fill(void* p, int64_t bytes, hipStream_t s, const char* fn) {
   const int64_t n = bytes / 4;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) return TPF_OK;
   hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t*)p, n);
   return check_launch(fn);
 }
@@ -612,15 +627,36 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
   if (B < 1 || N < 1) return set_error(TPF_ERR_SHAPE, "%s: B and N must be positive", fn);
   if (C != 32 && C != 64 && C != 96 && C != 128)
     return set_error(TPF_ERR_SHAPE, "%s: C=%lld must be one of 32, 64, 96, 128", fn, (long long)C);
-  if (N > 46340) return set_error(TPF_ERR_SHAPE, "%s: N=%lld too large", fn, (long long)N);
-  g->B = (int)B; g->N = (int)N; g->Np = (int)((N + 7) / 8 * 8);
-  g->NN = N * N; g->PS = N * (int64_t)g->Np; g->outgoing = outgoing ? 1 : 0;
-  if ((g->NN + 63) / 64 > INT32_MAX || B > 65535)
-    return set_error(TPF_ERR_SHAPE, "%s: grid too large", fn);
+  const int64_t Np = (N + 7) / 8 * 8;
+  const int64_t R = B * N * N;
+  // 32-bit row indices in the GEMM and 2 GiB buffer windows per operand.
+  if (R * 5 * C * 2 >= (int64_t)kBufOOB || B * C * N * Np * 2 >= (int64_t)kBufOOB ||
+      R > INT32_MAX / 2)
+    return set_error(TPF_ERR_SHAPE, "%s: B=%lld N=%lld too large", fn, (long long)B, (long long)N);
+  g->B = (int)B; g->N = (int)N; g->Np = (int)Np; g->H = (int)C;
+  g->NN = N * N; g->PS = N * Np; g->R = R; g->outgoing = outgoing ? 1 : 0;
+  g->ntg = (int)((C + 63) / 64);
   return TPF_OK;
 }
 
-#define TM_DISPATCH(C, KERNEL, GRID, ...)                                                     \
+static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+static int64_t tm_wp_rows(int64_t C) { return (2 * ((C + 63) / 64) + 1) * 128; }
+static int64_t tm_weights_bytes(int64_t C) {
+  return align256(tm_wp_rows(C) * C * 2) + align256(5 * C * C * 2);
+}
+
+static int tm_pack(const void* p_in, const void* g_in, const void* g_out, __bf16* wp, __bf16* w5,
+                   int C, int ntg, hipStream_t s, const char* fn) {
+  const int64_t chunks = (tm_wp_rows(C) + 5 * C) * (C / 8);
+  hipLaunchKernelGGL(tm_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     s, (const __bf16*)p_in, (const __bf16*)g_in, (const __bf16*)g_out, wp, w5, C,
+                     ntg);
+  return check_launch(fn);
+}
+
+static unsigned tm_grid(int64_t tiles) { return (unsigned)((tiles + 7) / 8 * 8); }
+
+#define TM_DISPATCH_C(C, KERNEL, GRID, ...)                                                   \
   switch (C) {                                                                               \
     case 32: hipLaunchKernelGGL(KERNEL<32>, GRID, dim3(256), 0, s, __VA_ARGS__); break;     \
     case 64: hipLaunchKernelGGL(KERNEL<64>, GRID, dim3(256), 0, s, __VA_ARGS__); break;     \
@@ -632,30 +668,43 @@ extern "C" {
 
 int64_t tpf_trimul_plane_pitch(int64_t N) { return (N + 7) / 8 * 8; }
 
+int64_t tpf_trimul_forward_workspace_bytes(int64_t C) { return tm_weights_bytes(C); }
+
 int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, const void* g_in,
                             const void* p_out, const void* g_out, const float* ln_in_w,
                             const float* ln_in_b, const float* ln_out_w, const float* ln_out_b,
                             int outgoing, int64_t B, int64_t N, int64_t C, void* out, void* zln,
-                            void* a, void* b, void* x, void* xln, float* mean_in, float* rstd_in,
-                            float* mean_out, float* rstd_out, void* stream) {
+                            void* gate, void* a, void* b, void* x, void* xln, float* mean_in,
+                            float* rstd_in, float* mean_out, float* rstd_out, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
   const char* fn = "tpf_trimul_forward_bf16";
   TmGeom g;
   int rc = tm_geom(&g, B, N, C, outgoing, fn);
   if (rc) return rc;
   if (!z || !mask || !p_in || !g_in || !p_out || !g_out || !ln_in_w || !ln_in_b || !ln_out_w ||
-      !ln_out_b || !out || !zln || !a || !b || !x || !mean_in || !rstd_in)
+      !ln_out_b || !out || !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in ||
+      !mean_out || !rstd_out || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (workspace_bytes < tm_weights_bytes(C))
+    return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
+                     (long long)workspace_bytes, (long long)tm_weights_bytes(C));
   hipStream_t s = (hipStream_t)stream;
+  __bf16* wp = (__bf16*)workspace;
+  __bf16* w5 = (__bf16*)((char*)workspace + align256(tm_wp_rows(C) * C * 2));
+  if ((rc = tm_pack(p_in, g_in, g_out, wp, w5, (int)C, g.ntg, s, fn))) return rc;
   if (g.Np != g.N) {
     // The contraction reads whole rows of Np; pad columns must be zero.
     if ((rc = zero_fill(a, B * C * g.PS * 2, s, fn))) return rc;
     if ((rc = zero_fill(b, B * C * g.PS * 2, s, fn))) return rc;
   }
-  dim3 grid((unsigned)((g.NN + 63) / 64), (unsigned)B);
-  TM_DISPATCH(C, tm_in_fwd_kernel, grid, (const __bf16*)z, mask, (const __bf16*)p_in,
-              (const __bf16*)g_in, ln_in_w, ln_in_b, (__bf16*)a, (__bf16*)b, (__bf16*)zln,
-              mean_in, rstd_in, g);
-  if ((rc = check_launch("tpf_trimul_forward_bf16(in)"))) return rc;
+  TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)((g.R + 15) / 16)), (const __bf16*)z, ln_in_w,
+                ln_in_b, (__bf16*)zln, mean_in, rstd_in, g.R);
+  if ((rc = check_launch("tpf_trimul_forward_bf16(ln_in)"))) return rc;
+  const int64_t tiles = (g.R + 127) / 128;
+  hipLaunchKernelGGL(tm_in_proj_kernel<false>, dim3(tm_grid(tiles * (2 * g.ntg + 1))), dim3(256), 0,
+                     s, (const __bf16*)zln, wp, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate,
+                     (__bf16*)nullptr, g, (int)C);
+  if ((rc = check_launch("tpf_trimul_forward_bf16(in_proj)"))) return rc;
   GemmArgs ga{};
   ga.A = (const __bf16*)a; ga.a_ld = g.Np; ga.a_bs = g.PS;
   ga.B = (const __bf16*)b; ga.b_ld = g.Np; ga.b_bs = g.PS;
@@ -663,100 +712,96 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, 
   ga.M = (int)N; ga.N = (int)N; ga.K = g.Np; ga.ksplit = 1; ga.k_chunk = g.Np; ga.alpha = 1.f;
   if ((rc = gemm_launch(ga, 1, 1, 0, (int)(B * C), s, "tpf_trimul_forward_bf16(contract)")))
     return rc;
-  TM_DISPATCH(C, tm_out_fwd_kernel, grid, (const __bf16*)x, (const __bf16*)zln,
-              (const __bf16*)p_out, (const __bf16*)g_out, ln_out_w, ln_out_b, (__bf16*)out,
-              (__bf16*)xln, mean_out, rstd_out, g);
-  return check_launch("tpf_trimul_forward_bf16(out)");
+  TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
+                (const __bf16*)x, ln_out_w, ln_out_b, (__bf16*)xln, mean_out, rstd_out, g);
+  if ((rc = check_launch("tpf_trimul_forward_bf16(ln_out)"))) return rc;
+  hipLaunchKernelGGL(tm_out_proj_kernel<false>, dim3(tm_grid(tiles)), dim3(256), 0, s,
+                     (const __bf16*)xln, (const __bf16*)p_out, (const __bf16*)gate,
+                     (const __bf16*)nullptr, (__bf16*)out, (__bf16*)nullptr, (__bf16*)nullptr, g,
+                     (int)C);
+  return check_launch("tpf_trimul_forward_bf16(out_proj)");
 }
 
-// Backward workspace (each region 256-byte aligned):
-//   dy^T [C][Rp], xln^T [H][Rp], dproj5^T [5H][Rp], zln^T [C][Rp] (Rp = R
-//   rounded up to 8; K-contiguous weight-gradient operands), dgl [R][H],
-//   dx / da / db channel-major planes, LN parameter partials, split-K
-//   partials of dW5 and dWz.
-static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
-
-static int trimul_wgrad_splits(int64_t R) {
-  int64_t s = R / 2048;
+// Backward workspace (each region 256-byte aligned): packed weights, dy
+// [R][C], dproj5 [R][5H], dx / da / db channel-major planes, LayerNorm
+// parameter partials [tiles][4][C] and their fold, split-K partials of dW5
+// and dWz.
+static int tm_split(int64_t R, int64_t per, int cap) {
+  int64_t s = R / per;
   if (s < 1) s = 1;
-  if (s > 64) s = 64;
+  if (s > cap) s = cap;
   return (int)s;
 }
-
-static int64_t tm_bwd_blocks(int64_t B, int64_t N) { return B * ((N * N + 31) / 32); }
+static int tm_w5_splits(int64_t R) { return tm_split(R, 2304, 64); }
+static int tm_wz_splits(int64_t R) { return tm_split(R, 576, 256); }
 
 int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
-  const int64_t Np = (N + 7) / 8 * 8, R = B * N * N, Rp = (R + 7) / 8 * 8;
-  const int64_t blocks = tm_bwd_blocks(B, N);
-  const int64_t splits = trimul_wgrad_splits(R);
-  int64_t t = 0;
-  t += align256(C * Rp * 2);                      // dy^T
-  t += align256(C * Rp * 2);                      // xln^T
-  t += align256(5 * C * Rp * 2);                  // dproj5^T
-  t += align256(C * Rp * 2);                      // zln^T
-  t += align256(R * C * 2);                       // dgl
-  t += 3 * align256(B * C * N * Np * 2);          // dx, da, db
-  t += align256(blocks * 4 * C * 4);              // LN parameter partials [blocks][4][C]
-  t += align256(4 * C * 4);                       // folded LN parameter grads
-  t += align256(splits * 5 * C * C * 4);          // dW5 partials
-  t += align256(splits * C * C * 4);              // dWz partials
+  const int64_t Np = (N + 7) / 8 * 8, R = B * N * N;
+  const int64_t tiles = (R + 127) / 128;
+  int64_t t = tm_weights_bytes(C);
+  t += align256(R * C * 2);                        // dy
+  t += align256(R * 5 * C * 2);                    // dproj5
+  t += 3 * align256(B * C * N * Np * 2);           // dx, da, db
+  t += align256(tiles * 4 * C * 4);                // LN parameter partials
+  t += align256(4 * C * 4);                        // folded LN parameter grads
+  t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
+  t += align256((int64_t)tm_wz_splits(R) * C * C * 4);
   return t;
 }
 
 int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
-                             const void* p_in, const void* g_in, const void* p_out_t,
-                             const void* w5_t, const void* p_out, const void* g_out,
-                             const float* ln_in_w, const float* ln_out_w, const void* zln,
-                             const void* a, const void* b, const void* x, const void* xln,
-                             const float* mean_in, const float* rstd_in, const float* mean_out,
-                             const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
-                             void* dz, float* d_w5, float* d_p_out, float* d_ln_in_w,
-                             float* d_ln_in_b, float* d_ln_out_w, float* d_ln_out_b,
-                             void* workspace, int64_t workspace_bytes, void* stream) {
+                             const void* p_in, const void* g_in, const void* p_out,
+                             const void* g_out, const float* ln_in_w, const float* ln_out_w,
+                             const void* zln, const void* gate, const void* a, const void* b,
+                             const void* x, const void* xln, const float* mean_in,
+                             const float* rstd_in, const float* mean_out, const float* rstd_out,
+                             int outgoing, int64_t B, int64_t N, int64_t C, void* dz, float* d_w5,
+                             float* d_p_out, float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
+                             float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
   const char* fn = "tpf_trimul_backward_bf16";
   TmGeom g;
   int rc = tm_geom(&g, B, N, C, outgoing, fn);
   if (rc) return rc;
-  if (!grad_out || !z || !mask || !p_in || !g_in || !p_out_t || !w5_t || !p_out || !g_out ||
-      !ln_in_w || !ln_out_w || !zln || !a || !b || !x || !xln || !mean_in || !rstd_in ||
-      !mean_out || !rstd_out || !dz || !d_w5 || !d_p_out || !d_ln_in_w || !d_ln_in_b ||
-      !d_ln_out_w || !d_ln_out_b || !workspace)
+  if (!grad_out || !z || !mask || !p_in || !g_in || !p_out || !g_out || !ln_in_w || !ln_out_w ||
+      !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in || !mean_out || !rstd_out ||
+      !dz || !d_w5 || !d_p_out || !d_ln_in_w || !d_ln_in_b || !d_ln_out_w || !d_ln_out_b ||
+      !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const int64_t need = tpf_trimul_backward_workspace_bytes(B, N, C);
   if (workspace_bytes < need)
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
   hipStream_t s = (hipStream_t)stream;
-  const int64_t R = B * N * N, Rp = (R + 7) / 8 * 8, H = C;
-  const int64_t blocks = tm_bwd_blocks(B, N);
-  const int splits = trimul_wgrad_splits(R);
-  char* wp = (char*)workspace;
-  auto take = [&](int64_t bytes) { char* p = wp; wp += align256(bytes); return p; };
-  __bf16* dy_t = (__bf16*)take(C * Rp * 2);
-  __bf16* xln_t = (__bf16*)take(C * Rp * 2);
-  __bf16* dproj5_t = (__bf16*)take(5 * C * Rp * 2);
-  __bf16* zln_t = (__bf16*)take(C * Rp * 2);
-  __bf16* dgl = (__bf16*)take(R * C * 2);
+  const int64_t R = g.R, H = C;
+  const int64_t tiles = (R + 127) / 128;
+  const int s5 = tm_w5_splits(R), sz = tm_wz_splits(R);
+  char* wp_ = (char*)workspace;
+  auto take = [&](int64_t bytes) { char* p = wp_; wp_ += align256(bytes); return p; };
+  __bf16* wpk = (__bf16*)take(tm_wp_rows(C) * C * 2);
+  __bf16* w5 = (__bf16*)take(5 * C * C * 2);
+  __bf16* dy = (__bf16*)take(R * C * 2);
+  __bf16* dproj5 = (__bf16*)take(R * 5 * H * 2);
   const int64_t plane_bytes = B * C * g.PS * 2;
   __bf16* dx = (__bf16*)take(plane_bytes);
   __bf16* da = (__bf16*)take(plane_bytes);
   __bf16* db = (__bf16*)take(plane_bytes);
-  float* lnp = (float*)take(blocks * 4 * C * 4);
+  float* lnp = (float*)take(tiles * 4 * C * 4);
   float* lnf = (float*)take(4 * C * 4);
-  float *dgo = lnp, *dbo = lnp + C, *dgi = lnp + 2 * C, *dbi = lnp + 3 * C;
-  float* w5p = (float*)take((int64_t)splits * 5 * C * C * 4);
-  float* wzp = (float*)take((int64_t)splits * C * C * 4);
-  // Pad columns of K-contiguous GEMM operands must read as zero.
+  float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
+  float* wzp = (float*)take((int64_t)sz * C * C * 4);
+  if ((rc = tm_pack(p_in, g_in, g_out, wpk, w5, (int)C, g.ntg, s, fn))) return rc;
+  // Pad columns of dx are read by the dA GEMM (K = Np) and must be zero.
   if (g.Np != g.N && (rc = zero_fill(dx, plane_bytes, s, fn))) return rc;
-  if (Rp != R) {
-    if ((rc = zero_fill(dy_t, (int64_t)((char*)dgl - (char*)dy_t), s, fn))) return rc;
-  }
-  dim3 grid((unsigned)((g.NN + 31) / 32), (unsigned)B);
-  TM_DISPATCH(C, tm_out_bwd_kernel, grid, (const __bf16*)grad_out, (const __bf16*)x,
-              (const __bf16*)xln, (const __bf16*)zln, mean_out, rstd_out, (const __bf16*)p_out,
-              (const __bf16*)g_out, (const __bf16*)p_out_t, ln_out_w, dy_t, xln_t, dgl, dx, dgo,
-              dbo, g, Rp);
-  if ((rc = check_launch("tpf_trimul_backward_bf16(out)"))) return rc;
+  const unsigned grid_rows = tm_grid(tiles);
+  hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
+                     (const __bf16*)xln, (const __bf16*)p_out, (const __bf16*)gate,
+                     (const __bf16*)grad_out, (__bf16*)nullptr, dy, dproj5, g, (int)C);
+  if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
+  hipLaunchKernelGGL(tm_ln_bwd_kernel<true>, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
+                     (int64_t)C, (const __bf16*)p_out, (int)C, (const __bf16*)x, mean_out,
+                     rstd_out, ln_out_w, dx, lnp, 0, g, (int)H);
+  if ((rc = check_launch("tpf_trimul_backward_bf16(ln_out_bwd)"))) return rc;
   // Contraction backward: dA_c = dX_c B_c, dB_c = dX_c^T A_c (stored layouts).
   GemmArgs ga{};
   ga.A = dx; ga.a_ld = g.Np; ga.a_bs = g.PS;
@@ -770,28 +815,32 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gb.C = db; gb.c_ld = g.Np; gb.c_bs = g.PS;
   gb.M = (int)N; gb.N = (int)N; gb.K = (int)N; gb.ksplit = 1; gb.k_chunk = (int)N; gb.alpha = 1.f;
   if ((rc = gemm_launch(gb, 0, 0, 0, (int)(B * C), s, "tpf_trimul_backward_bf16(dB)"))) return rc;
-  TM_DISPATCH(C, tm_in_bwd_kernel, grid, (const __bf16*)z, (const __bf16*)zln, mask,
-              (const __bf16*)p_in, (const __bf16*)g_in, da, db, dgl, (const __bf16*)w5_t,
-              mean_in, rstd_in, ln_in_w, dproj5_t, zln_t, (__bf16*)dz, dgi, dbi, g, Rp);
-  if ((rc = check_launch("tpf_trimul_backward_bf16(in)"))) return rc;
-  // Weight gradients over all rows: K-contiguous split-K GEMMs + fixed-order fold.
-  const int k_chunk = (int)((Rp + splits - 1) / splits);
+  hipLaunchKernelGGL(tm_in_proj_kernel<true>, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
+                     (const __bf16*)zln, wpk, mask, da, db, (__bf16*)nullptr, dproj5, g, (int)C);
+  if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
+  hipLaunchKernelGGL(tm_ln_bwd_kernel<false>, dim3(grid_rows), dim3(256), 0, s,
+                     (const __bf16*)dproj5, 5 * H, (const __bf16*)w5, (int)(5 * H),
+                     (const __bf16*)z, mean_in, rstd_in, ln_in_w, (__bf16*)dz, lnp, 2, g, (int)C);
+  if ((rc = check_launch("tpf_trimul_backward_bf16(ln_in_bwd)"))) return rc;
+  // Weight gradients over all rows: MN operands straight from the row-major
+  // tensors, split-K + fixed-order fold.
   GemmArgs gw{};
-  gw.A = dproj5_t; gw.a_ld = Rp; gw.a_bs = 0;
-  gw.B = zln_t; gw.b_ld = Rp; gw.b_bs = 0;
+  gw.A = dproj5; gw.a_ld = 5 * H; gw.a_bs = 0;
+  gw.B = (const __bf16*)zln; gw.b_ld = C; gw.b_bs = 0;
   gw.C = w5p; gw.c_ld = C; gw.c_bs = 0; gw.c_split = 5 * C * C;
-  gw.M = (int)(5 * H); gw.N = (int)C; gw.K = (int)Rp; gw.ksplit = splits; gw.k_chunk = k_chunk;
-  gw.alpha = 1.f;
-  if ((rc = gemm_launch(gw, 1, 1, 1, 1, s, "tpf_trimul_backward_bf16(dW5)"))) return rc;
-  GemmArgs gz = gw;
-  gz.A = dy_t;
-  gz.B = xln_t;
-  gz.C = wzp; gz.c_ld = H; gz.c_split = C * H;
-  gz.M = (int)C; gz.N = (int)H;
-  if ((rc = gemm_launch(gz, 1, 1, 1, 1, s, "tpf_trimul_backward_bf16(dWz)"))) return rc;
-  if ((rc = fold_launch(w5p, d_w5, 5 * C * C, 5 * C * C, splits, s, fn))) return rc;
-  if ((rc = fold_launch(wzp, d_p_out, C * H, C * H, splits, s, fn))) return rc;
-  if ((rc = fold_launch(lnp, lnf, 4 * C, 4 * C, (int)blocks, s, fn))) return rc;
+  gw.M = (int)(5 * H); gw.N = (int)C; gw.K = (int)R; gw.ksplit = s5;
+  gw.k_chunk = (int)((R + s5 - 1) / s5); gw.alpha = 1.f;
+  if ((rc = gemm_launch(gw, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dW5)"))) return rc;
+  GemmArgs gz{};
+  gz.A = dy; gz.a_ld = C; gz.a_bs = 0;
+  gz.B = (const __bf16*)xln; gz.b_ld = H; gz.b_bs = 0;
+  gz.C = wzp; gz.c_ld = H; gz.c_bs = 0; gz.c_split = C * H;
+  gz.M = (int)C; gz.N = (int)H; gz.K = (int)R; gz.ksplit = sz;
+  gz.k_chunk = (int)((R + sz - 1) / sz); gz.alpha = 1.f;
+  if ((rc = gemm_launch(gz, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dWz)"))) return rc;
+  if ((rc = fold_launch(w5p, d_w5, 5 * C * C, 5 * C * C, s5, s, fn))) return rc;
+  if ((rc = fold_launch(wzp, d_p_out, C * H, C * H, sz, s, fn))) return rc;
+  if ((rc = fold_launch(lnp, lnf, 4 * C, 4 * C, (int)tiles, s, fn))) return rc;
   float* outs[4] = {d_ln_out_w, d_ln_out_b, d_ln_in_w, d_ln_in_b};
   for (int i = 0; i < 4; ++i)
     if (hipMemcpyAsync(outs[i], lnf + i * C, C * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)

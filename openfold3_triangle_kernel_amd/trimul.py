@@ -15,9 +15,9 @@ Mirrors the reference TriMul facade
     ``g_out = linear_g``.
 
 All compute runs in ``csrc/trimul.hip`` + ``csrc/gemm.hip`` through the C ABI.
-Backward-state tensors returned by the forward op differ in content from the
-reference's (this implementation saves ``xln`` row-major and recomputes the
-output gate, so the ``gate`` slot is empty); the schema is unchanged.
+Backward-state tensors returned by the forward op follow the reference's
+roles (``gate`` holds the output-gate logits, ``xln`` the normalised product)
+in this implementation's layouts (``xln`` row-major); the schema is unchanged.
 """
 
 from __future__ import annotations
@@ -41,15 +41,10 @@ def _bf16(t: torch.Tensor) -> torch.Tensor:
 
 
 def _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z):
-    """bf16 kernel copies: p_in [2H,C], g_in [2H,C], p_out [C,H], g_out [C,C],
-    p_out^T [H,C] and the d_zln operand (cat(p_in, g_in, g_out))^T [C,5H]."""
+    """bf16 kernel copies: p_in [2H,C], g_in [2H,C], p_out [C,H], g_out [C,C]."""
     p_in = _bf16(torch.cat([w_ap.detach(), w_bp.detach()], 0))
     g_in = _bf16(torch.cat([w_ag.detach(), w_bg.detach()], 0))
-    p_out = _bf16(w_z)
-    g_out = _bf16(w_g)
-    p_out_t = _bf16(w_z.detach().t())
-    w5_t = torch.cat([p_in, g_in, g_out], 0).t().contiguous()
-    return p_in, g_in, p_out, g_out, p_out_t, w5_t
+    return p_in, g_in, _bf16(w_z), _bf16(w_g)
 
 
 def _check_op_inputs(z_bf, w_ap):
@@ -89,7 +84,8 @@ def _trimul_fwd_v1(
     """Forward: (out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out).
 
     ``a``/``b`` are the channel-major stored matrices [B*H, N*Np] and ``x`` the
-    product [B*H, N, Np] (Np = N rounded up to 8); ``gate`` is empty.
+    product [B*H, N, Np] (Np = N rounded up to 8); ``gate`` holds the
+    output-gate logits [B*N*N, C].
     """
     _check_op_inputs(z_bf, w_ap)
     B, N, _, C = (int(s) for s in z_bf.shape)
@@ -99,9 +95,12 @@ def _trimul_fwd_v1(
     mask_f = mask_f.to(torch.float32).contiguous()
     Np = int(_native.query("tpf_trimul_plane_pitch", N))
     rows = B * N * N
-    p_in, g_in_w, p_out, g_out_w, _, _ = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
+    p_in, g_in_w, p_out, g_out_w = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
     out = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
     z_ln = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
+    gate = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
+    ws_bytes = int(_native.query("tpf_trimul_forward_workspace_bytes", C))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     a = torch.empty((B * H, N * Np), device=dev, dtype=torch.bfloat16)
     b = torch.empty((B * H, N * Np), device=dev, dtype=torch.bfloat16)
     x = torch.empty((B * H, N, Np), device=dev, dtype=torch.bfloat16)
@@ -116,11 +115,11 @@ def _trimul_fwd_v1(
             z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(), g_in_w.data_ptr(),
             p_out.data_ptr(), g_out_w.data_ptr(), lnw[0].data_ptr(), lnw[1].data_ptr(),
             lnw[2].data_ptr(), lnw[3].data_ptr(), int(bool(outgoing)), B, N, C,
-            out.data_ptr(), z_ln.data_ptr(), a.data_ptr(), b.data_ptr(), x.data_ptr(),
-            xln.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(), mean_out.data_ptr(),
-            rstd_out.data_ptr(), _native.stream_of(z_bf),
+            out.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(), b.data_ptr(),
+            x.data_ptr(), xln.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(),
+            mean_out.data_ptr(), rstd_out.data_ptr(), ws.data_ptr(), ws_bytes,
+            _native.stream_of(z_bf),
         )
-    gate = z_bf.new_empty((0,))
     return (out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out)
 
 
@@ -134,7 +133,7 @@ def _trimul_fwd_v1_fake(z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_
     return (
         z_bf.new_empty((B, N, N, C)),
         z_bf.new_empty((rows, C)),
-        z_bf.new_empty((0,)),
+        z_bf.new_empty((rows, C)),
         z_bf.new_empty((B * H, N * Np)),
         z_bf.new_empty((B * H, N * Np)),
         z_bf.new_empty((B * H, N, Np)),
@@ -184,7 +183,7 @@ def _trimul_bwd_v1(
     dev = z_bf.device
     grad = grad_out.to(torch.bfloat16).contiguous()
     mask_f = mask_f.to(torch.float32).contiguous()
-    p_in, g_in_w, p_out, g_out_w, p_out_t, w5_t = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
+    p_in, g_in_w, p_out, g_out_w = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
     gin = g_in.detach().to(torch.float32).contiguous()
     gout = g_out.detach().to(torch.float32).contiguous()
     f32 = dict(device=dev, dtype=torch.float32)
@@ -199,8 +198,8 @@ def _trimul_bwd_v1(
         _native.call(
             "tpf_trimul_backward_bf16",
             grad.data_ptr(), z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(),
-            g_in_w.data_ptr(), p_out_t.data_ptr(), w5_t.data_ptr(), p_out.data_ptr(),
-            g_out_w.data_ptr(), gin.data_ptr(), gout.data_ptr(), z_ln.data_ptr(), a.data_ptr(),
+            g_in_w.data_ptr(), p_out.data_ptr(), g_out_w.data_ptr(), gin.data_ptr(),
+            gout.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(),
             b.data_ptr(), x.data_ptr(), xlnT.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(),
             mean_out.data_ptr(), rstd_out.data_ptr(), int(bool(outgoing)), B, N, C,
             d_z.data_ptr(), d_w5_k.data_ptr(), d_wz.data_ptr(), d_gin.data_ptr(),
@@ -239,11 +238,15 @@ def _fwd_setup_context(ctx, inputs, output):
     ctx.save_for_backward(z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
                           rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, out)
     ctx.outgoing = bool(outgoing)
+    # Gradients of the saved-state outputs are never used: skip zero-filling them.
+    ctx.set_materialize_grads(False)
     ctx.weight_dtypes = tuple(t.dtype for t in (w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in,
                                                 g_out, b_out))
 
 
 def _fwd_backward(ctx, grad_out, *unused_grads):
+    if grad_out is None:  # only saved-state outputs were used downstream
+        return (None,) * 14
     (z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out, w_ap, w_ag,
      w_bp, w_bg, w_g, w_z, g_in, g_out, out) = ctx.saved_tensors
     d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout = _trimul_bwd_v1(

@@ -1,0 +1,60 @@
+"""GPU parity of the batched MFMA GEMM (tpf_gemm_bf16) against torch fp32.
+
+C[z] = alpha * A[z] B[z]^T with each operand K-contiguous or MN-contiguous;
+ragged M / N / K (not multiples of the 128 x 128 x 64 tile), batches, and f32
+or bf16 output.  Tolerance: bf16 inputs are exact in fp32, so the only error
+is the f32 accumulation order (and the bf16 rounding of a bf16 output):
+max-rel <= 1e-5 for f32 output, <= 8e-3 for bf16 output.
+"""
+
+import pytest
+import torch
+
+from tests._util import max_rel
+
+
+def _operand(x, kc):
+    """Return (tensor, ld) of the [rows, K] matrix x in the requested layout."""
+    if kc:
+        return x.contiguous(), x.shape[-1]
+    rows = x.shape[-2]
+    ld = (rows + 7) // 8 * 8
+    t = torch.zeros(*x.shape[:-2], x.shape[-1], ld, dtype=x.dtype, device=x.device)
+    t[..., :rows] = x.transpose(-1, -2)
+    return t, ld
+
+
+CASES = [
+    # batch, M, N, K
+    (1, 128, 128, 64),
+    (3, 384, 384, 384),
+    (2, 200, 72, 136),
+    (1, 33, 17, 8),
+    (1, 640, 128, 4096),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("a_kc,b_kc", [(1, 1), (1, 0), (0, 1), (0, 0)], ids=["KK", "KM", "MK", "MM"])
+@pytest.mark.parametrize("out_f32", [1, 0], ids=["f32", "bf16"])
+def test_gemm(gpu, case, a_kc, b_kc, out_f32):
+    from openfold3_triangle_kernel_amd import _native
+
+    bz, M, N, K = case
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N * 3 + K)
+    a = torch.randn(bz, M, K, generator=g).to(torch.bfloat16).to(gpu)
+    b = torch.randn(bz, N, K, generator=g).to(torch.bfloat16).to(gpu)
+    ta, lda = _operand(a, a_kc)
+    tb, ldb = _operand(b, b_kc)
+    c = torch.full((bz, M, N), float("nan"), device=gpu,
+                   dtype=torch.float32 if out_f32 else torch.bfloat16)
+    alpha = 0.5
+    stream = torch.cuda.current_stream().cuda_stream
+    print(f"gemm case={case} a_kc={a_kc} b_kc={b_kc} out_f32={out_f32}", flush=True)
+    _native.call("tpf_gemm_bf16", ta.data_ptr(), a_kc, lda, ta[0].numel(), tb.data_ptr(), b_kc,
+                 ldb, tb[0].numel(), c.data_ptr(), out_f32, N, M * N, M, N, K, bz, alpha, stream)
+    torch.cuda.synchronize()
+    ref = alpha * torch.bmm(a.double().cpu(), b.double().cpu().transpose(1, 2))
+    err = max_rel(c.float().cpu().numpy(), ref.cpu().numpy())
+    assert err <= (1e-5 if out_f32 else 8e-3), err
