@@ -173,4 +173,21 @@ __device__ __forceinline__ void buf2lds16(i32x4 rsrc, uint32_t voff, void* dst_b
                :: "s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
 
+// Division by a run-time invariant d (Granlund-Montgomery): for n < 2^31,
+// n / d = (umulhi(n, m) + n) >> s with s = ceil(log2 d),
+// m = floor(2^32 (2^s - d) / d) + 1.  Replaces 32/64-bit integer division
+// (dozens of instructions each) in index arithmetic.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
 }  // namespace tpf

@@ -31,8 +31,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g) {
   const int m0 = mt * kGM, n0 = nt * kGN;
   const int kbeg = split * g.k_chunk;
   const int kend = min(g.K, kbeg + g.k_chunk);
-  GemmOperand A{g.A + (int64_t)z * g.a_bs, g.a_ld, g.M, g.a_gather_n};
-  GemmOperand B{g.B + (int64_t)z * g.b_bs, g.b_ld, g.N, 0};
+  GemmOperand A{g.A + (int64_t)z * g.a_bs, g.a_ld, g.M, g.a_gather_n, g.a_div_n, g.a_div_nn};
+  GemmOperand B{g.B + (int64_t)z * g.b_bs, g.b_ld, g.N, 0, {}, {}};
   f32x16 acc[2][2];
   gemm_tile<A_KC, B_KC>(A, B, m0, n0, kbeg, kend, smem, acc);
 
@@ -101,6 +101,10 @@ int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
                      fn);
   if (g.a_gather_n > 0 && !a_kc)
     return set_error(TPF_ERR_ARG, "%s: row gather needs a K-contiguous A", fn);
+  if (g.a_gather_n > 0) {
+    g.a_div_n = make_fastdiv((uint32_t)g.a_gather_n);
+    g.a_div_nn = make_fastdiv((uint32_t)g.a_gather_n * (uint32_t)g.a_gather_n);
+  }
   // Buffer offsets of one batch item must stay below 2^31 bytes.
   const int64_t a_span = a_kc ? (int64_t)g.M * g.a_ld : (int64_t)g.K * g.a_ld;
   const int64_t b_span = b_kc ? (int64_t)g.N * g.b_ld : (int64_t)g.K * g.b_ld;

@@ -3,16 +3,16 @@
 //
 //   acc(m, n) = sum_{k in [kbeg, kend)} A(m, k) * B(n, k)
 //
-// Tile 128 (m) x 128 (n) x 64 (k); wave w owns the 64 x 64 sub-tile
+// Tile 128 (m) x 128 (n) x kGK (k); wave w owns the 64 x 64 sub-tile
 // (wm, wn) = (w >> 1, w & 1) as 2 x 2 MFMA 32x32x16 accumulators:
 //   acc[i][j] register r <-> m = 64 wm + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4,
 //                            n = 64 wn + 32 j + lane % 32.
 //
 // Operands are read from HBM straight into LDS (buffer_load ... lds, 16 bytes
-// per lane, zeros outside the tensor), two k-stages in flight.  Either
+// per lane, zeros outside the tensor) through a ring of kGNS stages.  Either
 // operand may be
-//   KC (K-contiguous): X[row * ld + k] -- LDS tile [128 rows][64 k], the 16-
-//      byte chunk c of row r stored at slot c ^ (r & 7); fragments are plain
+//   KC (K-contiguous): X[row * ld + k] -- LDS tile [128 rows][kGK k], the 16-
+//      byte chunk c of row r stored at slot kc_slot(r, c); fragments are plain
 //      16-byte LDS reads;
 //   MN (MN-contiguous): X[k * ld + row] -- LDS tile [64 k][128 rows], chunk c
 //      of k-row r stored at slot c ^ ((r & 3) << 1); fragments come from
@@ -27,26 +27,42 @@
 
 namespace tpf {
 
-constexpr int kGM = 128, kGN = 128, kGK = 64;
-constexpr int kGTileBytes = kGM * kGK * 2;        // one operand tile, 16 KiB
+#ifndef TPF_GEMM_GK
+#define TPF_GEMM_GK 64
+#endif
+#ifndef TPF_GEMM_NS
+#define TPF_GEMM_NS 2
+#endif
+constexpr int kGM = 128, kGN = 128;
+constexpr int kGK = TPF_GEMM_GK;                  // k depth of one stage (32 or 64)
+constexpr int kGNS = TPF_GEMM_NS;                 // stages in the LDS ring
+constexpr int kGTileBytes = kGM * kGK * 2;        // one operand tile
 constexpr int kGStageBytes = 2 * kGTileBytes;     // A + B
-constexpr int kGMainLdsBytes = 2 * kGStageBytes;  // two stages, 64 KiB
+constexpr int kGMainLdsBytes = kGNS * kGStageBytes;
+constexpr int kGInstr = kGTileBytes / 1024 / 4;   // 1 KiB loads per wave per operand tile
+static_assert(kGK == 32 || kGK == 64, "stage depth");
 
 struct GemmOperand {
   const __bf16* p;  // element (0, 0) of this batch item
   int64_t ld;       // leading dimension in elements
   int rows;         // extent of the m (or n) dimension
   int gather_n;     // KC row gather (0 = none); nn = gather_n^2
+  FastDiv div_n, div_nn;  // division by gather_n and gather_n^2 (gather only)
 };
+
+// Slot of 16-byte chunk c in row r of a KC tile (conflict-free row reads).
+__device__ __forceinline__ int kc_slot(int r, int c) {
+  return kGK == 64 ? (c ^ (r & 7)) : (c ^ ((r >> 1) & 3));
+}
 
 // Per-lane loader state of one operand (offsets fixed for the whole k loop).
 template <bool KC>
 struct TileLoader {
   i32x4 rsrc;
-  uint32_t row_off[4];  // KC: byte offset of the row start (kBufOOB if absent)
-  int col_ok;           // MN: column chunk inside the tensor
-  uint32_t col_off;     // MN: byte offset of the column chunk
-  int sub;              // KC: k chunk (elements) of this lane; MN: k-row in instr
+  uint32_t row_off[kGInstr];  // KC: byte offset of the row start (kBufOOB if absent)
+  int col_ok;                 // MN: column chunk inside the tensor
+  uint32_t col_off;           // MN: byte offset of the column chunk
+  int sub;                    // KC: k offset of this lane; MN: k-row in instruction
   int64_t ld;
 
   __device__ __forceinline__ void init(const GemmOperand& op, int r0) {
@@ -54,18 +70,20 @@ struct TileLoader {
     rsrc = buffer_rsrc(op.p);
     ld = op.ld;
     if (KC) {
-      const int rin = lane >> 3;                        // row inside instruction
-      sub = 8 * ((lane & 7) ^ (rin & 7));               // k offset of this lane
+      constexpr int cpr = kGK / 8, rpi = 64 / cpr;  // chunks per row, rows per instruction
+      const int rin = lane / cpr;
+      sub = 8 * kc_slot(rin, lane % cpr);             // rows of one lane differ by rpi (even)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int row = r0 + 8 * (4 * w + t) + rin;
+      for (int t = 0; t < kGInstr; ++t) {
+        const int row = r0 + rpi * (kGInstr * w + t) + rin;
         uint32_t off = kBufOOB;
         if (row < op.rows) {
           int64_t prow = row;
           if (op.gather_n > 0) {
-            const int64_t nn = (int64_t)op.gather_n * op.gather_n;
-            const int64_t b = row / nn, p = row % nn;
-            prow = b * nn + (p % op.gather_n) * op.gather_n + p / op.gather_n;
+            const uint32_t n = op.gather_n, nn = op.div_nn.d;
+            const uint32_t b = fdiv((uint32_t)row, op.div_nn), p = (uint32_t)row - b * nn;
+            const uint32_t i = fdiv(p, op.div_n), k = p - i * n;
+            prow = (int64_t)b * nn + (int64_t)k * n + i;
           }
           off = (uint32_t)(prow * op.ld * 2);
         }
@@ -81,12 +99,12 @@ struct TileLoader {
     }
   }
 
-  // Issue the 4 instructions of this wave for the k-tile at k0 into tile.
+  // Issue this wave's instructions for the k-tile at k0 into tile.
   __device__ __forceinline__ void issue(int k0, int kend, char* tile) const {
     const int w = threadIdx.x >> 6;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int j = 4 * w + t;
+    for (int t = 0; t < kGInstr; ++t) {
+      const int j = kGInstr * w + t;
       uint32_t off;
       if (KC) {
         const int k = k0 + sub;
@@ -106,7 +124,7 @@ __device__ __forceinline__ bf16x8 tile_frag(const __bf16* T, int rbase, int s) {
   const int lane = threadIdx.x & 63;
   if (KC) {
     const int r = rbase + (lane & 31);
-    const int slot = (2 * s + (lane >> 5)) ^ (r & 7);
+    const int slot = kc_slot(r, 2 * s + (lane >> 5));
     return *reinterpret_cast<const bf16x8*>(T + r * kGK + slot * 8);
   } else {
     const int g = lane >> 4, ip = lane & 15;
@@ -125,6 +143,7 @@ __device__ __forceinline__ bf16x8 tile_frag(const __bf16* T, int rbase, int s) {
 
 // Full k loop of one 128 x 128 tile.  smem holds kGMainLdsBytes; on return
 // every wave has finished reading it (callers may reuse it after a barrier).
+// kGNS - 1 stages are in flight while one is multiplied.
 template <bool A_KC, bool B_KC>
 __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperand& B, int m0,
                                           int n0, int kbeg, int kend, char* smem,
@@ -141,16 +160,23 @@ __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperan
   lb.init(B, n0);
   const int nk = (kend - kbeg + kGK - 1) / kGK;
   if (nk <= 0) return;
-  la.issue(kbeg, kend, smem);
-  lb.issue(kbeg, kend, smem + kGTileBytes);
+#pragma unroll
+  for (int st = 0; st < kGNS - 1; ++st) {
+    if (st < nk) {
+      la.issue(kbeg + st * kGK, kend, smem + st * kGStageBytes);
+      lb.issue(kbeg + st * kGK, kend, smem + st * kGStageBytes + kGTileBytes);
+    }
+  }
   for (int kt = 0; kt < nk; ++kt) {
-    char* cur = smem + (kt & 1) * kGStageBytes;
-    wait_vmcnt<0>();
+    char* cur = smem + (kt % kGNS) * kGStageBytes;
+    // Stage kt has landed once at most the later stages' loads are pending.
+    if (kt + kGNS - 2 < nk) wait_vmcnt<(kGNS - 2) * 2 * kGInstr>();
+    else wait_vmcnt<0>();
     lds_barrier();
-    if (kt + 1 < nk) {
-      char* nxt = smem + ((kt + 1) & 1) * kGStageBytes;
-      la.issue(kbeg + (kt + 1) * kGK, kend, nxt);
-      lb.issue(kbeg + (kt + 1) * kGK, kend, nxt + kGTileBytes);
+    if (kt + kGNS - 1 < nk) {
+      char* nxt = smem + ((kt + kGNS - 1) % kGNS) * kGStageBytes;
+      la.issue(kbeg + (kt + kGNS - 1) * kGK, kend, nxt);
+      lb.issue(kbeg + (kt + kGNS - 1) * kGK, kend, nxt + kGTileBytes);
     }
     const __bf16* As = reinterpret_cast<const __bf16*>(cur);
     const __bf16* Bs = reinterpret_cast<const __bf16*>(cur + kGTileBytes);

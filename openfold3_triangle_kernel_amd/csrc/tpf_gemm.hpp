@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.hpp"
+
 namespace tpf {
 
 struct GemmArgs {
@@ -14,6 +16,7 @@ struct GemmArgs {
   int ksplit, k_chunk;                   // K range of split s: [s*k_chunk, (s+1)*k_chunk)
   float alpha;
   int a_gather_n;                        // KC row gather of A (0 = none), see gemm_core.hpp
+  FastDiv a_div_n, a_div_nn;             // set by gemm_launch when a_gather_n > 0
   int batch;                             // set by gemm_launch
 };
 

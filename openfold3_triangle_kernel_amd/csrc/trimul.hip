@@ -40,22 +40,38 @@ struct TmGeom {
   int B, N, Np, H;
   int64_t NN;  // N*N positions per batch item
   int64_t PS;  // N*Np elements per channel-major plane
-  int64_t R;   // B*N*N rows
+  int64_t R;   // B*N*N rows (< 2^30)
   int outgoing;
   int ntg;     // gated 128-column weight tiles per branch (64 channels each)
+  FastDiv div_n, div_nn;
 };
 
 constexpr int kSP = 136;  // bf16 pitch of 128-wide LDS staging tiles
+// LDS of a kernel = max(main loop ring, epilogue staging).
+constexpr int lds_bytes(int epilogue) { return epilogue > kGMainLdsBytes ? epilogue : kGMainLdsBytes; }
+constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2);   // d tile + [dp | dg] tile
+constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2);     // gate + dout tiles
+constexpr int kLnBwdLds = lds_bytes(128 * kSP * 2);           // x tile
 
 // Element offset of position p = i*N + j inside a channel-major plane.
 __device__ __forceinline__ int64_t tm_plane_off(const TmGeom& g, int64_t p) {
-  return (g.Np == g.N) ? p : (p / g.N) * g.Np + (p % g.N);
+  if (g.Np == g.N) return p;
+  const uint32_t i = fdiv((uint32_t)p, g.div_n);
+  return (int64_t)i * g.Np + ((uint32_t)p - i * (uint32_t)g.N);
+}
+// Batch item and position of row m.
+__device__ __forceinline__ void tm_bp(const TmGeom& g, int64_t m, int64_t& b, int64_t& p) {
+  const uint32_t bb = fdiv((uint32_t)m, g.div_nn);
+  b = bb;
+  p = (uint32_t)m - bb * (uint32_t)g.NN;
 }
 // Natural row of stored-order row m.
 __device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
   if (g.outgoing) return m;
-  const int64_t b = m / g.NN, p = m % g.NN;
-  return b * g.NN + (p % g.N) * g.N + p / g.N;
+  int64_t b, p;
+  tm_bp(g, m, b, p);
+  const uint32_t i = fdiv((uint32_t)p, g.div_n), k = (uint32_t)p - i * (uint32_t)g.N;
+  return b * g.NN + (int64_t)k * g.N + i;
 }
 
 // ---------------------------------------------------------------------------
@@ -241,54 +257,106 @@ struct AccPos {
 __device__ __forceinline__ void tm_store_rows(const __bf16* S, int ncols, const int64_t* rho_s,
                                               __bf16* __restrict__ dst, int64_t ld, int c0) {
   const int cpr = ncols / 8;
-  for (int idx = threadIdx.x; idx < 128 * cpr; idx += 256) {
-    const int row = idx / cpr, ch = idx % cpr;
+  for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
+    const int row = idx >> 4, ch = idx & 15;
     const int64_t rho = rho_s[row];
-    if (rho >= 0) st8(dst + rho * ld + c0 + ch * 8, *reinterpret_cast<const bf16x8*>(&S[row * kSP + ch * 8]));
-  }
-}
-__device__ __forceinline__ void tm_load_rows(__bf16* S, int ncols, const int64_t* rho_s,
-                                             const __bf16* __restrict__ src, int64_t ld) {
-  const int cpr = ncols / 8;
-  for (int idx = threadIdx.x; idx < 128 * cpr; idx += 256) {
-    const int row = idx / cpr, ch = idx % cpr;
-    const int64_t rho = rho_s[row];
-    *reinterpret_cast<bf16x8*>(&S[row * kSP + ch * 8]) = rho >= 0 ? ld8(src + rho * ld + ch * 8) : zero8();
+    if (rho >= 0 && ch < cpr)
+      st8(dst + rho * ld + c0 + ch * 8, *reinterpret_cast<const bf16x8*>(&S[row * kSP + ch * 8]));
   }
 }
 
-// Move [nch channels][128 positions] between an LDS tile S[c * kSP + pos]
-// and channel-major planes (plane index b*H + c0 + c, position of tile row
-// pos = m0 + pos within its batch item).  STORE: LDS -> planes.
-template <bool STORE>
-__device__ __forceinline__ void tm_plane_tile(__bf16* S, int nch, __bf16* planes, const TmGeom& g,
-                                              int64_t m0, int c0) {
+// Store an LDS tile S[c * kSP + pos] of [nch channels][128 positions] to
+// channel-major planes (plane b*H + c0 + c, position of tile row m0 + pos
+// within its batch item).
+__device__ __forceinline__ void tm_store_planes(const __bf16* S, int nch, __bf16* planes,
+                                                const TmGeom& g, int64_t m0, int c0) {
   for (int idx = threadIdx.x; idx < nch * 16; idx += 256) {
     const int cl = idx >> 4, chn = idx & 15;
     const int c = c0 + cl;
     if (c >= g.H) continue;
     const int64_t mb = m0 + 8 * chn;
-    __bf16* s = S + cl * kSP + 8 * chn;
+    const __bf16* s = S + cl * kSP + 8 * chn;
     if (g.Np == g.N && mb + 7 < g.R) {
       // NN is a multiple of 64 here, so the 8 positions share a batch item.
-      const int64_t b = mb / g.NN, p = mb % g.NN;
-      __bf16* d = planes + ((int64_t)b * g.H + c) * g.PS + p;
-      if (STORE) st8(d, *reinterpret_cast<const bf16x8*>(s));
-      else *reinterpret_cast<bf16x8*>(s) = ld8(d);
+      int64_t b, p;
+          tm_bp(g, mb, b, p);
+      st8(planes + ((int64_t)b * g.H + c) * g.PS + p, *reinterpret_cast<const bf16x8*>(s));
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int64_t m = mb + e;
         if (m < g.R) {
-          const int64_t b = m / g.NN, p = m % g.NN;
-          __bf16* d = planes + ((int64_t)b * g.H + c) * g.PS + tm_plane_off(g, p);
-          if (STORE) *d = s[e];
-          else s[e] = *d;
-        } else if (!STORE) {
-          s[e] = static_cast<__bf16>(0.f);
+          int64_t b, p;
+          tm_bp(g, m, b, p);
+          planes[((int64_t)b * g.H + c) * g.PS + tm_plane_off(g, p)] = s[e];
         }
       }
     }
+  }
+}
+
+// Register staging of an epilogue operand tile: fetched from HBM before the
+// GEMM main loop (so its latency overlaps the main loop) and written to LDS
+// after it.  Chunk k of thread t is tile chunk idx = t + 256 k.
+struct RegTile {
+  bf16x8 v[8];
+};
+// [128 rows][ncols] of a row-major matrix, natural rows m0 + row.
+__device__ __forceinline__ void fetch_rows(RegTile& t, const __bf16* __restrict__ src, int64_t ld,
+                                           int ncols, int64_t m0, int64_t R) {
+  const int cpr = ncols / 8;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = threadIdx.x + 256 * k;
+    const int row = idx >> 4, ch = idx & 15;
+    const int64_t m = m0 + row;
+    t.v[k] = (ch < cpr && m < R) ? ld8(src + m * ld + ch * 8) : zero8();
+  }
+}
+__device__ __forceinline__ void put_rows(__bf16* S, const RegTile& t) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = threadIdx.x + 256 * k;
+    *reinterpret_cast<bf16x8*>(&S[(idx >> 4) * kSP + (idx & 15) * 8]) = t.v[k];
+  }
+}
+// [nch channels][128 positions] of channel-major planes (channels c0 + c,
+// positions of tile rows m0 ..); nch * 16 <= 2048.
+__device__ __forceinline__ void fetch_planes(RegTile& t, const __bf16* __restrict__ planes,
+                                             const TmGeom& g, int nch, int64_t m0, int c0) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = threadIdx.x + 256 * k;
+    const int cl = idx >> 4, chn = idx & 15;
+    const int c = c0 + cl;
+    const int64_t mb = m0 + 8 * chn;
+    bf16x8 v = zero8();
+    if (cl < nch && c < g.H) {
+      if (g.Np == g.N && mb + 7 < g.R) {
+        int64_t b, p;
+          tm_bp(g, mb, b, p);
+        v = ld8(planes + ((int64_t)b * g.H + c) * g.PS + p);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t m = mb + e;
+          if (m < g.R) {
+            int64_t b, p;
+          tm_bp(g, m, b, p);
+            v[e] = planes[((int64_t)b * g.H + c) * g.PS + tm_plane_off(g, p)];
+          }
+        }
+      }
+    }
+    t.v[k] = v;
+  }
+}
+__device__ __forceinline__ void put_planes(__bf16* S, const RegTile& t, int nch) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int idx = threadIdx.x + 256 * k;
+    const int cl = idx >> 4, chn = idx & 15;
+    if (cl < nch) *reinterpret_cast<bf16x8*>(&S[cl * kSP + 8 * chn]) = t.v[k];
   }
 }
 
@@ -304,7 +372,7 @@ __global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
     const __bf16* __restrict__ zln, const __bf16* __restrict__ wp, const float* __restrict__ mask,
     __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl,
     __bf16* __restrict__ dproj5, TmGeom g, int C) {
-  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kInProjLds];
   __shared__ float mask_s[128];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
@@ -320,8 +388,10 @@ __global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
     rho_s[threadIdx.x] = rho;
     mask_s[threadIdx.x] = rho >= 0 ? mask[rho] : 0.f;
   }
-  GemmOperand A{zln, C, (int)g.R, g.outgoing ? 0 : g.N};
-  GemmOperand W{wp, C, (2 * g.ntg + 1) * 128, 0};
+  GemmOperand A{zln, C, (int)g.R, g.outgoing ? 0 : g.N, g.div_n, g.div_nn};
+  GemmOperand W{wp, C, (2 * g.ntg + 1) * 128, 0, {}, {}};
+  RegTile dreg;
+  if (BWD) fetch_planes(dreg, (nt / g.ntg) ? b_pl : a_pl, g, 64, m0, 64 * (nt % g.ntg));
   f32x16 acc[2][2];
   gemm_tile<true, true>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
   const AccPos ap;
@@ -349,12 +419,12 @@ __global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
         S0[cl * kSP + row] = f2bf(mask_s[row] * sigmoidf(acc[i][1][r]) * acc[i][0][r]);
       }
     __syncthreads();
-    tm_plane_tile<true>(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
+    tm_store_planes(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
     return;
   }
   // Backward: d tile [64 ch][128 pos] in S0, outputs [128 rows][dp 64 | dg 64] in So.
   __bf16* So = S0 + 64 * kSP;
-  tm_plane_tile<false>(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
+  put_planes(S0, dreg, 64);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -389,22 +459,25 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
     const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, __bf16* __restrict__ out,
     __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, TmGeom g, int C) {
   constexpr int kStage = 128 * kSP * 2;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage > kGMainLdsBytes ? 2 * kStage : kGMainLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kOutProjLds];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
   const int64_t T = xcd_order((g.R + 127) / 128);
   if (T < 0) return;
   const int64_t m0 = T * 128;
   if (threadIdx.x < 128) rho_s[threadIdx.x] = m0 + threadIdx.x < g.R ? m0 + threadIdx.x : -1;
-  GemmOperand A{xln, H, (int)g.R, 0};
-  GemmOperand W{p_out, H, C, 0};
+  GemmOperand A{xln, H, (int)g.R, 0, {}, {}};
+  GemmOperand W{p_out, H, C, 0, {}, {}};
+  RegTile greg, dreg;
+  fetch_rows(greg, gl, C, C, m0, g.R);
+  if (BWD) fetch_rows(dreg, dout, C, C, m0, g.R);
   f32x16 acc[2][2];
   gemm_tile<true, true>(A, W, (int)m0, 0, 0, H, smem, acc);
   const AccPos ap;
   __bf16* Sg = reinterpret_cast<__bf16*>(smem);
   __bf16* Sd = reinterpret_cast<__bf16*>(smem + kStage);
-  tm_load_rows(Sg, C, rho_s, gl, C);
-  if (BWD) tm_load_rows(Sd, C, rho_s, dout, C);
+  put_rows(Sg, greg);
+  if (BWD) put_rows(Sd, dreg);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -464,13 +537,30 @@ __device__ __forceinline__ bf16x4 tm_x4(const __bf16* Xt, const AccPos& ap, int 
   return tr_col4(Xt, kSP, rbase, rbase + 4, 64 * ap.wn + 32 * j);
 }
 
+// One level of the transposing butterfly: lanes exchange half of their
+// 2*HALF partial sums with lane ^ HALF and keep the half selected by that
+// lane bit (constant indices only, so the arrays stay in registers).
+template <int HALF>
+__device__ __forceinline__ void tm_butterfly(float* a, float* b, int lane) {
+  const bool up = (lane & HALF) != 0;
+#pragma unroll
+  for (int k = 0; k < HALF; ++k) {
+    const float sa = up ? a[k] : a[k + HALF];
+    const float sb = up ? b[k] : b[k + HALF];
+    const float ra = __shfl_xor(sa, HALF);
+    const float rb = __shfl_xor(sb, HALF);
+    a[k] = (up ? a[k + HALF] : a[k]) + ra;
+    b[k] = (up ? b[k + HALF] : b[k]) + rb;
+  }
+}
+
 template <bool PLANES>
 __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
     const __bf16* __restrict__ a_op, int64_t a_ld, const __bf16* __restrict__ w_op, int K,
     const __bf16* __restrict__ xsrc, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gamma, __bf16* __restrict__ dst, float* __restrict__ lnp,
     int slot0, TmGeom g, int W) {
-  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kLnBwdLds];
   __shared__ __attribute__((aligned(16))) float mean_s[128], rstd_s[128];
   __shared__ __attribute__((aligned(16))) float rsum[2][2][128];  // [quantity][wn][row]
   __shared__ float csum[2][2][128];                               // [quantity][wm][col]
@@ -486,13 +576,16 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
     mean_s[tid] = ok ? mean[m] : 0.f;
     rstd_s[tid] = ok ? rstd[m] : 0.f;
   }
-  GemmOperand A{a_op, a_ld, (int)g.R, 0};
-  GemmOperand B{w_op, W, W, 0};
+  GemmOperand A{a_op, a_ld, (int)g.R, 0, {}, {}};
+  GemmOperand B{w_op, W, W, 0, {}, {}};
+  RegTile xreg;
+  if (PLANES) fetch_planes(xreg, xsrc, g, 128, m0, 0);
+  else fetch_rows(xreg, xsrc, W, W, m0, g.R);
   f32x16 acc[2][2];
   gemm_tile<true, false>(A, B, (int)m0, 0, 0, K, smem, acc);
   __bf16* Xt = reinterpret_cast<__bf16*>(smem);  // [ch][row] (PLANES) or [row][ch]
-  if (PLANES) tm_plane_tile<false>(Xt, 128, const_cast<__bf16*>(xsrc), g, m0, 0);
-  else tm_load_rows(Xt, W, rho_s, xsrc, W);
+  if (PLANES) put_planes(Xt, xreg, 128);
+  else put_rows(Xt, xreg);
   __syncthreads();
   const AccPos ap;
   const int lane = tid & 63;
@@ -530,20 +623,11 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
     }
   // Transposing butterfly over the 32 columns of the wave: lane rl ends with
   // the full sums of value index t = rl.
-#pragma unroll
-  for (int lvl = 0; lvl < 5; ++lvl) {
-    const int m = 16 >> lvl, half = 16 >> lvl;
-    const bool up = (lane & m) != 0;
-#pragma unroll
-    for (int k = 0; k < half; ++k) {
-      const float sg = up ? rs_g[k] : rs_g[k + half];
-      const float sx = up ? rs_gx[k] : rs_gx[k + half];
-      const float rg = __shfl_xor(sg, m);
-      const float rx = __shfl_xor(sx, m);
-      rs_g[k] = (up ? rs_g[k + half] : rs_g[k]) + rg;
-      rs_gx[k] = (up ? rs_gx[k + half] : rs_gx[k]) + rx;
-    }
-  }
+  tm_butterfly<16>(rs_g, rs_gx, lane);
+  tm_butterfly<8>(rs_g, rs_gx, lane);
+  tm_butterfly<4>(rs_g, rs_gx, lane);
+  tm_butterfly<2>(rs_g, rs_gx, lane);
+  tm_butterfly<1>(rs_g, rs_gx, lane);
   {
     const int t = ap.rl, i = t >> 4, r = t & 15;
     const int row = ap.row(i, r);
@@ -597,7 +681,7 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
       }
     }
   __syncthreads();
-  if (PLANES) tm_plane_tile<true>(Xt, 128, dst, g, m0, 0);
+  if (PLANES) tm_store_planes(Xt, 128, dst, g, m0, 0);
   else tm_store_rows(Xt, W, rho_s, dst, W, 0);
 }
 
@@ -636,6 +720,8 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
   g->B = (int)B; g->N = (int)N; g->Np = (int)Np; g->H = (int)C;
   g->NN = N * N; g->PS = N * Np; g->R = R; g->outgoing = outgoing ? 1 : 0;
   g->ntg = (int)((C + 63) / 64);
+  g->div_n = make_fastdiv((uint32_t)N);
+  g->div_nn = make_fastdiv((uint32_t)(N * N));
   return TPF_OK;
 }
 
