@@ -102,8 +102,9 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
  * Triangle multiplicative update (C == H in {32, 64, 96, 128}).
  *
  * z: bf16 [B, N, N, C]; mask: f32 [B, N, N].
- * Weights (bf16): p_in = cat(W_ap, W_bp) [2H, C], g_in = cat(W_ag, W_bg)
- * [2H, C], p_out = W_z [C, H], g_out = W_g [C, C].  LayerNorm weights f32.
+ * Weights (f32, the module's parameters): w_ap, w_ag, w_bp, w_bg [H, C],
+ * w_g [C, C], w_z [C, H]; LayerNorm weights f32 [C].  Both entry points
+ * pack them into bf16 GEMM operands inside the workspace.
  * Saved state written by the forward (R = B*N*N rows): zln [R, C], gate =
  * output-gate logits zln W_g^T [R, C], a, b [B*H, N*Np] (channel-major
  * stored matrices, Np = tpf_trimul_plane_pitch(N)), x [B*H, N, Np], xln
@@ -113,7 +114,7 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
 /* Row pitch Np (N rounded up to 8) of the channel-major a / b / x buffers. */
 int64_t tpf_trimul_plane_pitch(int64_t N);
 
-/* Bytes of device workspace tpf_trimul_forward_bf16 needs (packed weights). */
+/* Bytes of device workspace tpf_trimul_forward_bf16 needs (packed bf16 weights). */
 int64_t tpf_trimul_forward_workspace_bytes(int64_t C);
 
 /* Forward: LN_in + projections + gates (trimul_in_fwd), the channel
@@ -122,31 +123,34 @@ int64_t tpf_trimul_forward_workspace_bytes(int64_t C);
  * Replaces trimul_in_fwd / torch.bmm / trimul_out_fwd of
  * _trimul_forward_impl (openfold3/core/kernels/turbopairformer/turbopairformer_trimul.py:184-292;
  * kernels turbopairformer_trimul_cuda.cu:615-1166, 1191-1530). */
-int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, const void* g_in,
-                            const void* p_out, const void* g_out, const float* ln_in_w,
-                            const float* ln_in_b, const float* ln_out_w, const float* ln_out_b,
-                            int outgoing, int64_t B, int64_t N, int64_t C, void* out, void* zln,
-                            void* gate, void* a, void* b, void* x, void* xln, float* mean_in,
-                            float* rstd_in, float* mean_out, float* rstd_out, void* workspace,
+int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap, const float* w_ag,
+                            const float* w_bp, const float* w_bg, const float* w_g,
+                            const float* w_z, const float* ln_in_w, const float* ln_in_b,
+                            const float* ln_out_w, const float* ln_out_b, int outgoing, int64_t B,
+                            int64_t N, int64_t C, void* out, void* zln, void* gate, void* a,
+                            void* b, void* x, void* xln, float* mean_in, float* rstd_in,
+                            float* mean_out, float* rstd_out, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
 int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C);
 
 /* Backward: dz (bf16) and every parameter gradient in f32 with fixed-order
- * reductions.  d_w5 is [5H, C] in the order [p_in; g_in; g_out].
+ * reductions.  d_w5 is [5H, C] in the order [w_ap; w_ag; w_bp; w_bg; w_g]
+ * (the reference's d_w5), d_w_z [C, H].
  * Replaces _trimul_backward_combined_impl
  * (openfold3/core/kernels/turbopairformer/turbopairformer_trimul.py:295-392) with its
  * kernels sig_mul_bwd_out, transpose_ln_bwd, trimul_gate_split_bwd,
  * ln_bwd_dx, ln_bwd_dgb, trimul_wgrad_fixed_fold
  * (turbopairformer_trimul_cuda.cu:196-560, 1532-2160) and its cuBLAS GEMMs. */
 int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
-                             const void* p_in, const void* g_in, const void* p_out,
-                             const void* g_out, const float* ln_in_w, const float* ln_out_w,
-                             const void* zln, const void* gate, const void* a, const void* b,
-                             const void* x, const void* xln, const float* mean_in,
-                             const float* rstd_in, const float* mean_out, const float* rstd_out,
-                             int outgoing, int64_t B, int64_t N, int64_t C, void* dz, float* d_w5,
-                             float* d_p_out, float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
+                             const float* w_ap, const float* w_ag, const float* w_bp,
+                             const float* w_bg, const float* w_g, const float* w_z,
+                             const float* ln_in_w, const float* ln_out_w, const void* zln,
+                             const void* gate, const void* a, const void* b, const void* x,
+                             const void* xln, const float* mean_in, const float* rstd_in,
+                             const float* mean_out, const float* rstd_out, int outgoing, int64_t B,
+                             int64_t N, int64_t C, void* dz, float* d_w5, float* d_w_z,
+                             float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
                              float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
                              void* stream);
 

@@ -57,12 +57,12 @@ SIGNATURES: dict[str, tuple] = {
     "tpf_trimul_forward_workspace_bytes": (_I64, [_I64]),
     "tpf_trimul_forward_bf16": (
         _I32,
-        [_P] * 10 + [_I32, _I64, _I64, _I64] + [_P] * 12 + [_I64, _P],
+        [_P] * 12 + [_I32, _I64, _I64, _I64] + [_P] * 12 + [_I64, _P],
     ),
     "tpf_trimul_backward_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "tpf_trimul_backward_bf16": (
         _I32,
-        [_P] * 19 + [_I32, _I64, _I64, _I64] + [_P] * 8 + [_I64, _P],
+        [_P] * 21 + [_I32, _I64, _I64, _I64] + [_P] * 8 + [_I64, _P],
     ),
 }
 

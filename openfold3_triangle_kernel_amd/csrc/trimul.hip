@@ -11,8 +11,8 @@
 //
 // Storage (C == H channels, natural rows rho = (b*N + r)*N + s of z [B,N,N,C]):
 //   z, zln, gl, out, dz, dy: [R][C] bf16 row-major; xln [R][H];
-//   dproj5 [R][5H] with column blocks [d a_p | d b_p | d a_g | d b_g | d gl]
-//   (the row order of W5 = [p_in; g_in; g_out]);
+//   dproj5 [R][5H] with column blocks [d a_p | d a_g | d b_p | d b_g | d gl]
+//   (the row order of W5 = [W_ap; W_ag; W_bp; W_bg; W_g]);
 //   a, b (and da, db): channel-major "stored" matrices A_c[i][k], B_c[j][k]
 //   with plane size N*Np (row pitch Np = N rounded up to 8, pad columns
 //   zero): outgoing A_c[i][k] = a[i,k,c]; incoming A_c[i][k] = a[k,i,c], so
@@ -75,24 +75,35 @@ __device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
 }
 
 // ---------------------------------------------------------------------------
-// Weight packing (per call, tiny): Wp for the projection GEMMs and W5.
+// Weight packing (per call, tiny): the f32 module weights to bf16 GEMM
+// operands.
 //   Wp tile t < 2*ntg (branch t / ntg, channel block q = t % ntg): rows
 //   [p c0..c0+31 | g c0..c0+31 | p c0+32..c0+63 | g c0+32..c0+63], c0 = 64q,
 //   so the wave holding output columns 64wn.. sees p and g of the same 32
-//   channels in its two accumulator columns; tile 2*ntg holds g_out.
-//   W5 = [p_in; g_in; g_out] [5H][C].  Missing channels are zero rows.
+//   channels in its two accumulator columns; tile 2*ntg holds W_g.
+//   W5 = [W_ap; W_ag; W_bp; W_bg; W_g] [5H][C] (the reference's d_w5 order);
+//   Wz = W_z [C][H].  Missing channels are zero rows.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void tm_pack_weights_kernel(
-    const __bf16* __restrict__ p_in, const __bf16* __restrict__ g_in,
-    const __bf16* __restrict__ g_out, __bf16* __restrict__ wp, __bf16* __restrict__ w5, int C,
-    int ntg) {
+struct TmWeights {
+  const float* ap;
+  const float* ag;
+  const float* bp;
+  const float* bg;
+  const float* g;
+  const float* z;
+};
+
+__global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf16* __restrict__ wp,
+                                                              __bf16* __restrict__ w5,
+                                                              __bf16* __restrict__ wz, int C,
+                                                              int ntg) {
   const int cpr = C / 8;
   const int wp_rows = (2 * ntg + 1) * 128;
-  const int64_t total = (int64_t)(wp_rows + 5 * C) * cpr;
+  const int64_t total = (int64_t)(wp_rows + 6 * C) * cpr;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * 256) {
     const int row = (int)(idx / cpr), ch = (int)(idx % cpr);
-    const __bf16* src = nullptr;
+    const float* src = nullptr;
     __bf16* dst;
     if (row < wp_rows) {
       dst = wp + (int64_t)row * C + ch * 8;
@@ -101,17 +112,26 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(
         const int br = t / ntg, q = t % ntg;
         const int c = 64 * q + 32 * (rr / 64) + (rr & 31);
         const bool isg = (rr >> 5) & 1;
-        if (c < C) src = (isg ? g_in : p_in) + ((int64_t)br * C + c) * C;
+        if (c < C) src = (br ? (isg ? w.bg : w.bp) : (isg ? w.ag : w.ap)) + (int64_t)c * C;
       } else if (rr < C) {
-        src = g_out + (int64_t)rr * C;
+        src = w.g + (int64_t)rr * C;
       }
-    } else {
-      const int j = row - wp_rows;
+    } else if (row < wp_rows + 5 * C) {
+      const int j = row - wp_rows, blk = j / C, c = j % C;
       dst = w5 + (int64_t)j * C + ch * 8;
-      src = j < 2 * C ? p_in + (int64_t)j * C
-                      : (j < 4 * C ? g_in + (int64_t)(j - 2 * C) * C : g_out + (int64_t)(j - 4 * C) * C);
+      const float* const mats[5] = {w.ap, w.ag, w.bp, w.bg, w.g};
+      src = mats[blk] + (int64_t)c * C;
+    } else {
+      const int c = row - wp_rows - 5 * C;
+      dst = wz + (int64_t)c * C + ch * 8;
+      src = w.z + (int64_t)c * C;
     }
-    st8(dst, src ? ld8(src + ch * 8) : zero8());
+    bf16x8 o = zero8();
+    if (src) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f2bf(src[ch * 8 + e]);
+    }
+    st8(dst, o);
   }
 }
 
@@ -443,7 +463,7 @@ __global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
     const int row = idx >> 4, k = idx & 15, isg = k >> 3, c8 = k & 7;
     const int64_t rho = rho_s[row];
     if (rho < 0 || c8 >= nvalid) continue;
-    const int col = (isg ? 2 * H : 0) + br * H + 64 * q + 8 * c8;
+    const int col = (2 * br + isg) * H + 64 * q + 8 * c8;
     st8(dproj5 + rho * 5 * H + col, *reinterpret_cast<const bf16x8*>(&So[row * kSP + isg * 64 + 8 * c8]));
   }
 }
@@ -728,15 +748,31 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
 static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 static int64_t tm_wp_rows(int64_t C) { return (2 * ((C + 63) / 64) + 1) * 128; }
 static int64_t tm_weights_bytes(int64_t C) {
-  return align256(tm_wp_rows(C) * C * 2) + align256(5 * C * C * 2);
+  return align256(tm_wp_rows(C) * C * 2) + align256(5 * C * C * 2) + align256(C * C * 2);
 }
 
-static int tm_pack(const void* p_in, const void* g_in, const void* g_out, __bf16* wp, __bf16* w5,
-                   int C, int ntg, hipStream_t s, const char* fn) {
-  const int64_t chunks = (tm_wp_rows(C) + 5 * C) * (C / 8);
+// Packed bf16 weights at the start of a workspace.
+struct TmPacked {
+  __bf16* wp;
+  __bf16* w5;
+  __bf16* wz;
+};
+static TmPacked tm_packed(void* ws, int64_t C) {
+  char* p = (char*)ws;
+  TmPacked k;
+  k.wp = (__bf16*)p;
+  p += align256(tm_wp_rows(C) * C * 2);
+  k.w5 = (__bf16*)p;
+  p += align256(5 * C * C * 2);
+  k.wz = (__bf16*)p;
+  return k;
+}
+
+static int tm_pack(const TmWeights& w, const TmPacked& k, int C, int ntg, hipStream_t s,
+                   const char* fn) {
+  const int64_t chunks = (tm_wp_rows(C) + 6 * C) * (C / 8);
   hipLaunchKernelGGL(tm_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
-                     s, (const __bf16*)p_in, (const __bf16*)g_in, (const __bf16*)g_out, wp, w5, C,
-                     ntg);
+                     s, w, k.wp, k.w5, k.wz, C, ntg);
   return check_launch(fn);
 }
 
@@ -756,28 +792,29 @@ int64_t tpf_trimul_plane_pitch(int64_t N) { return (N + 7) / 8 * 8; }
 
 int64_t tpf_trimul_forward_workspace_bytes(int64_t C) { return tm_weights_bytes(C); }
 
-int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, const void* g_in,
-                            const void* p_out, const void* g_out, const float* ln_in_w,
-                            const float* ln_in_b, const float* ln_out_w, const float* ln_out_b,
-                            int outgoing, int64_t B, int64_t N, int64_t C, void* out, void* zln,
-                            void* gate, void* a, void* b, void* x, void* xln, float* mean_in,
-                            float* rstd_in, float* mean_out, float* rstd_out, void* workspace,
+int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap, const float* w_ag,
+                            const float* w_bp, const float* w_bg, const float* w_g,
+                            const float* w_z, const float* ln_in_w, const float* ln_in_b,
+                            const float* ln_out_w, const float* ln_out_b, int outgoing, int64_t B,
+                            int64_t N, int64_t C, void* out, void* zln, void* gate, void* a,
+                            void* b, void* x, void* xln, float* mean_in, float* rstd_in,
+                            float* mean_out, float* rstd_out, void* workspace,
                             int64_t workspace_bytes, void* stream) {
   const char* fn = "tpf_trimul_forward_bf16";
   TmGeom g;
   int rc = tm_geom(&g, B, N, C, outgoing, fn);
   if (rc) return rc;
-  if (!z || !mask || !p_in || !g_in || !p_out || !g_out || !ln_in_w || !ln_in_b || !ln_out_w ||
-      !ln_out_b || !out || !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in ||
-      !mean_out || !rstd_out || !workspace)
+  if (!z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !ln_in_w || !ln_in_b ||
+      !ln_out_w || !ln_out_b || !out || !zln || !gate || !a || !b || !x || !xln || !mean_in ||
+      !rstd_in || !mean_out || !rstd_out || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   if (workspace_bytes < tm_weights_bytes(C))
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)tm_weights_bytes(C));
   hipStream_t s = (hipStream_t)stream;
-  __bf16* wp = (__bf16*)workspace;
-  __bf16* w5 = (__bf16*)((char*)workspace + align256(tm_wp_rows(C) * C * 2));
-  if ((rc = tm_pack(p_in, g_in, g_out, wp, w5, (int)C, g.ntg, s, fn))) return rc;
+  const TmPacked k = tm_packed(workspace, C);
+  const TmWeights w{w_ap, w_ag, w_bp, w_bg, w_g, w_z};
+  if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
   if (g.Np != g.N) {
     // The contraction reads whole rows of Np; pad columns must be zero.
     if ((rc = zero_fill(a, B * C * g.PS * 2, s, fn))) return rc;
@@ -788,7 +825,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, 
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_in)"))) return rc;
   const int64_t tiles = (g.R + 127) / 128;
   hipLaunchKernelGGL(tm_in_proj_kernel<false>, dim3(tm_grid(tiles * (2 * g.ntg + 1))), dim3(256), 0,
-                     s, (const __bf16*)zln, wp, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate,
+                     s, (const __bf16*)zln, k.wp, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate,
                      (__bf16*)nullptr, g, (int)C);
   if ((rc = check_launch("tpf_trimul_forward_bf16(in_proj)"))) return rc;
   GemmArgs ga{};
@@ -802,7 +839,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const void* p_in, 
                 (const __bf16*)x, ln_out_w, ln_out_b, (__bf16*)xln, mean_out, rstd_out, g);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_out)"))) return rc;
   hipLaunchKernelGGL(tm_out_proj_kernel<false>, dim3(tm_grid(tiles)), dim3(256), 0, s,
-                     (const __bf16*)xln, (const __bf16*)p_out, (const __bf16*)gate,
+                     (const __bf16*)xln, k.wz, (const __bf16*)gate,
                      (const __bf16*)nullptr, (__bf16*)out, (__bf16*)nullptr, (__bf16*)nullptr, g,
                      (int)C);
   return check_launch("tpf_trimul_forward_bf16(out_proj)");
@@ -836,23 +873,24 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
 }
 
 int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
-                             const void* p_in, const void* g_in, const void* p_out,
-                             const void* g_out, const float* ln_in_w, const float* ln_out_w,
-                             const void* zln, const void* gate, const void* a, const void* b,
-                             const void* x, const void* xln, const float* mean_in,
-                             const float* rstd_in, const float* mean_out, const float* rstd_out,
-                             int outgoing, int64_t B, int64_t N, int64_t C, void* dz, float* d_w5,
-                             float* d_p_out, float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
+                             const float* w_ap, const float* w_ag, const float* w_bp,
+                             const float* w_bg, const float* w_g, const float* w_z,
+                             const float* ln_in_w, const float* ln_out_w, const void* zln,
+                             const void* gate, const void* a, const void* b, const void* x,
+                             const void* xln, const float* mean_in, const float* rstd_in,
+                             const float* mean_out, const float* rstd_out, int outgoing, int64_t B,
+                             int64_t N, int64_t C, void* dz, float* d_w5, float* d_w_z,
+                             float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
                              float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
                              void* stream) {
   const char* fn = "tpf_trimul_backward_bf16";
   TmGeom g;
   int rc = tm_geom(&g, B, N, C, outgoing, fn);
   if (rc) return rc;
-  if (!grad_out || !z || !mask || !p_in || !g_in || !p_out || !g_out || !ln_in_w || !ln_out_w ||
-      !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in || !mean_out || !rstd_out ||
-      !dz || !d_w5 || !d_p_out || !d_ln_in_w || !d_ln_in_b || !d_ln_out_w || !d_ln_out_b ||
-      !workspace)
+  if (!grad_out || !z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !ln_in_w ||
+      !ln_out_w || !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in || !mean_out ||
+      !rstd_out || !dz || !d_w5 || !d_w_z || !d_ln_in_w || !d_ln_in_b || !d_ln_out_w ||
+      !d_ln_out_b || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const int64_t need = tpf_trimul_backward_workspace_bytes(B, N, C);
   if (workspace_bytes < need)
@@ -862,10 +900,10 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   const int64_t R = g.R, H = C;
   const int64_t tiles = (R + 127) / 128;
   const int s5 = tm_w5_splits(R), sz = tm_wz_splits(R);
-  char* wp_ = (char*)workspace;
+  const TmPacked k = tm_packed(workspace, C);
+  const TmWeights w{w_ap, w_ag, w_bp, w_bg, w_g, w_z};
+  char* wp_ = (char*)workspace + tm_weights_bytes(C);
   auto take = [&](int64_t bytes) { char* p = wp_; wp_ += align256(bytes); return p; };
-  __bf16* wpk = (__bf16*)take(tm_wp_rows(C) * C * 2);
-  __bf16* w5 = (__bf16*)take(5 * C * C * 2);
   __bf16* dy = (__bf16*)take(R * C * 2);
   __bf16* dproj5 = (__bf16*)take(R * 5 * H * 2);
   const int64_t plane_bytes = B * C * g.PS * 2;
@@ -876,16 +914,15 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   float* lnf = (float*)take(4 * C * 4);
   float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
   float* wzp = (float*)take((int64_t)sz * C * C * 4);
-  if ((rc = tm_pack(p_in, g_in, g_out, wpk, w5, (int)C, g.ntg, s, fn))) return rc;
+  if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
   // Pad columns of dx are read by the dA GEMM (K = Np) and must be zero.
   if (g.Np != g.N && (rc = zero_fill(dx, plane_bytes, s, fn))) return rc;
   const unsigned grid_rows = tm_grid(tiles);
   hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
-                     (const __bf16*)xln, (const __bf16*)p_out, (const __bf16*)gate,
-                     (const __bf16*)grad_out, (__bf16*)nullptr, dy, dproj5, g, (int)C);
+                     (const __bf16*)xln, k.wz, (const __bf16*)gate, (const __bf16*)grad_out, (__bf16*)nullptr, dy, dproj5, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
   hipLaunchKernelGGL(tm_ln_bwd_kernel<true>, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
-                     (int64_t)C, (const __bf16*)p_out, (int)C, (const __bf16*)x, mean_out,
+                     (int64_t)C, k.wz, (int)C, (const __bf16*)x, mean_out,
                      rstd_out, ln_out_w, dx, lnp, 0, g, (int)H);
   if ((rc = check_launch("tpf_trimul_backward_bf16(ln_out_bwd)"))) return rc;
   // Contraction backward: dA_c = dX_c B_c, dB_c = dX_c^T A_c (stored layouts).
@@ -902,10 +939,10 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gb.M = (int)N; gb.N = (int)N; gb.K = (int)N; gb.ksplit = 1; gb.k_chunk = (int)N; gb.alpha = 1.f;
   if ((rc = gemm_launch(gb, 0, 0, 0, (int)(B * C), s, "tpf_trimul_backward_bf16(dB)"))) return rc;
   hipLaunchKernelGGL(tm_in_proj_kernel<true>, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
-                     (const __bf16*)zln, wpk, mask, da, db, (__bf16*)nullptr, dproj5, g, (int)C);
+                     (const __bf16*)zln, k.wp, mask, da, db, (__bf16*)nullptr, dproj5, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
   hipLaunchKernelGGL(tm_ln_bwd_kernel<false>, dim3(grid_rows), dim3(256), 0, s,
-                     (const __bf16*)dproj5, 5 * H, (const __bf16*)w5, (int)(5 * H),
+                     (const __bf16*)dproj5, 5 * H, k.w5, (int)(5 * H),
                      (const __bf16*)z, mean_in, rstd_in, ln_in_w, (__bf16*)dz, lnp, 2, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(ln_in_bwd)"))) return rc;
   // Weight gradients over all rows: MN operands straight from the row-major
@@ -925,7 +962,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gz.k_chunk = (int)((R + sz - 1) / sz); gz.alpha = 1.f;
   if ((rc = gemm_launch(gz, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dWz)"))) return rc;
   if ((rc = fold_launch(w5p, d_w5, 5 * C * C, 5 * C * C, s5, s, fn))) return rc;
-  if ((rc = fold_launch(wzp, d_p_out, C * H, C * H, sz, s, fn))) return rc;
+  if ((rc = fold_launch(wzp, d_w_z, C * H, C * H, sz, s, fn))) return rc;
   if ((rc = fold_launch(lnp, lnf, 4 * C, 4 * C, (int)tiles, s, fn))) return rc;
   float* outs[4] = {d_ln_out_w, d_ln_out_b, d_ln_in_w, d_ln_in_b};
   for (int i = 0; i < 4; ++i)

@@ -36,15 +36,9 @@ def _device_ctx(device: torch.device):
     return torch.cuda.device(device) if device.type == "cuda" else contextlib.nullcontext()
 
 
-def _bf16(t: torch.Tensor) -> torch.Tensor:
-    return t.detach().to(torch.bfloat16).contiguous()
-
-
-def _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z):
-    """bf16 kernel copies: p_in [2H,C], g_in [2H,C], p_out [C,H], g_out [C,C]."""
-    p_in = _bf16(torch.cat([w_ap.detach(), w_bp.detach()], 0))
-    g_in = _bf16(torch.cat([w_ag.detach(), w_bg.detach()], 0))
-    return p_in, g_in, _bf16(w_z), _bf16(w_g)
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    """f32 contiguous view of a parameter (no copy for f32 contiguous tensors)."""
+    return t.detach().to(torch.float32).contiguous()
 
 
 def _check_op_inputs(z_bf, w_ap):
@@ -95,7 +89,7 @@ def _trimul_fwd_v1(
     mask_f = mask_f.to(torch.float32).contiguous()
     Np = int(_native.query("tpf_trimul_plane_pitch", N))
     rows = B * N * N
-    p_in, g_in_w, p_out, g_out_w = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
+    wts = [_f32(t) for t in (w_ap, w_ag, w_bp, w_bg, w_g, w_z)]
     out = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
     z_ln = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
     gate = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
@@ -108,13 +102,13 @@ def _trimul_fwd_v1(
     f32 = dict(device=dev, dtype=torch.float32)
     mean_in, rstd_in = torch.empty(rows, **f32), torch.empty(rows, **f32)
     mean_out, rstd_out = torch.empty(rows, **f32), torch.empty(rows, **f32)
-    lnw = [t.detach().to(torch.float32).contiguous() for t in (g_in, b_in, g_out, b_out)]
+    lnw = [_f32(t) for t in (g_in, b_in, g_out, b_out)]
     with _device_ctx(dev):
         _native.call(
             "tpf_trimul_forward_bf16",
-            z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(), g_in_w.data_ptr(),
-            p_out.data_ptr(), g_out_w.data_ptr(), lnw[0].data_ptr(), lnw[1].data_ptr(),
-            lnw[2].data_ptr(), lnw[3].data_ptr(), int(bool(outgoing)), B, N, C,
+            z_bf.data_ptr(), mask_f.data_ptr(), *[t.data_ptr() for t in wts],
+            lnw[0].data_ptr(), lnw[1].data_ptr(), lnw[2].data_ptr(), lnw[3].data_ptr(),
+            int(bool(outgoing)), B, N, C,
             out.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(), b.data_ptr(),
             x.data_ptr(), xln.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(),
             mean_out.data_ptr(), rstd_out.data_ptr(), ws.data_ptr(), ws_bytes,
@@ -183,12 +177,11 @@ def _trimul_bwd_v1(
     dev = z_bf.device
     grad = grad_out.to(torch.bfloat16).contiguous()
     mask_f = mask_f.to(torch.float32).contiguous()
-    p_in, g_in_w, p_out, g_out_w = _kernel_weights(w_ap, w_ag, w_bp, w_bg, w_g, w_z)
-    gin = g_in.detach().to(torch.float32).contiguous()
-    gout = g_out.detach().to(torch.float32).contiguous()
+    wts = [_f32(t) for t in (w_ap, w_ag, w_bp, w_bg, w_g, w_z)]
+    gin, gout = _f32(g_in), _f32(g_out)
     f32 = dict(device=dev, dtype=torch.float32)
     d_z = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
-    d_w5_k = torch.empty((5 * H, C), **f32)  # kernel order [p_in; g_in; g_out]
+    d_w5 = torch.empty((5 * H, C), **f32)  # [ap; ag; bp; bg; g]
     d_wz = torch.empty((C, H), **f32)
     d_gin, d_bin = torch.empty(C, **f32), torch.empty(C, **f32)
     d_gout, d_bout = torch.empty(H, **f32), torch.empty(H, **f32)
@@ -197,19 +190,14 @@ def _trimul_bwd_v1(
     with _device_ctx(dev):
         _native.call(
             "tpf_trimul_backward_bf16",
-            grad.data_ptr(), z_bf.data_ptr(), mask_f.data_ptr(), p_in.data_ptr(),
-            g_in_w.data_ptr(), p_out.data_ptr(), g_out_w.data_ptr(), gin.data_ptr(),
-            gout.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(),
+            grad.data_ptr(), z_bf.data_ptr(), mask_f.data_ptr(), *[t.data_ptr() for t in wts],
+            gin.data_ptr(), gout.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(),
             b.data_ptr(), x.data_ptr(), xlnT.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(),
             mean_out.data_ptr(), rstd_out.data_ptr(), int(bool(outgoing)), B, N, C,
-            d_z.data_ptr(), d_w5_k.data_ptr(), d_wz.data_ptr(), d_gin.data_ptr(),
+            d_z.data_ptr(), d_w5.data_ptr(), d_wz.data_ptr(), d_gin.data_ptr(),
             d_bin.data_ptr(), d_gout.data_ptr(), d_bout.data_ptr(), ws.data_ptr(), ws_bytes,
             _native.stream_of(z_bf),
         )
-    d_ap, d_bp = d_w5_k[0:H], d_w5_k[H:2 * H]
-    d_ag, d_bg = d_w5_k[2 * H:3 * H], d_w5_k[3 * H:4 * H]
-    d_g = d_w5_k[4 * H:5 * H]
-    d_w5 = torch.cat([d_ap, d_ag, d_bp, d_bg, d_g], 0)
     return d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout
 
 

@@ -61,7 +61,7 @@ def test_shape_errors_are_reported_without_launch(lib):
         _native.call("tpf_attn_forward_bf16", 16, 16, 16, 16, 16, 16, 16, 16, 1 << 30, 2, 2, 4, 128,
                      32, 0, 3, 0.2, None)
     with pytest.raises(RuntimeError, match="C=48"):
-        _native.call("tpf_trimul_forward_bf16", *([16] * 10), 1, 1, 64, 48, *([16] * 12), 1 << 20, None)
+        _native.call("tpf_trimul_forward_bf16", *([16] * 12), 1, 1, 64, 48, *([16] * 12), 1 << 20, None)
     with pytest.raises(RuntimeError, match="workspace"):
         _native.call("tpf_attn_backward_bf16", *([16] * 13), 0, 1, 4, 4, 128, 32, 0, 1, 0.2, None)
 
