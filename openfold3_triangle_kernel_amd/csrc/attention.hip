@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // Q / dO rows and row statistics) stream into the other half of a double
 // buffer with direct global->LDS loads while step i computes.
 // dQ leaves as a bf16 partial per key block; dBias sums the 4 waves in LDS
-// (fixed order) into an f32 partial per outer group.  Fixed-order reducers
+// (fixed order) into a bf16 partial per outer group.  Fixed-order reducers
 // finish both.  Tiles are ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
+    __bf16* __restrict__ dq_part, __bf16* __restrict__ dbias_part, AttnGeom g) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 16;  // dS^T tile [64 keys][32 queries] pitch (bf16)
   constexpr int RP = 64 + 4;   // dBias exchange [32 queries][64 keys] pitch (f32)
@@ -654,7 +654,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     lds_barrier();
     // dBias partial: fixed wave order ((w0 + w1) + w2) + w3.
     {
-      float* dst = dbias_part + (((int64_t)bog * H + h) * N + q0) * N + key_base;
+      __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0) * N + key_base;
 #pragma unroll
       for (int it2 = 0; it2 < 2; ++it2) {
         const int idx = it2 * 256 + tid;  // 32 rows x 16 float4 chunks
@@ -666,7 +666,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += x[i];
         }
-        *reinterpret_cast<f32x4*>(dst + (int64_t)qr * N + c4) = acc;
+        bf16x4 o4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[i]);
+        *reinterpret_cast<bf16x4*>(dst + (int64_t)qr * N + c4) = o4;
       }
     }
   };
@@ -732,31 +735,50 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
   st8(dq + plane * g.H * g.N * g.D + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
 }
 
-// dBias[bb,h,q,k] (f32) = ascending fold over (b, outer group) partials that
-// share bias batch bb.  Bb == 1 folds every batch; Bb == B folds per batch.
+// dBias[bb,h,q,k] (f32) = ascending fold over the bf16 (b, outer group)
+// partials that share bias batch bb.  Bb == 1 folds every batch; Bb == B
+// folds per batch.
 __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
-    const float* __restrict__ part, float* __restrict__ dbias, int B, int Bb,
+    const __bf16* __restrict__ part, float* __restrict__ dbias, int B, int Bb,
     int groups, int H, int N) {
-  const int64_t hnn4 = (int64_t)H * N * N / 4;
+  const int64_t hnn8 = (int64_t)H * N * N / 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)Bb * hnn4) return;
-  const int bb = (int)(idx / hnn4);
-  const int64_t e = (idx % hnn4) * 4;
+  if (idx >= (int64_t)Bb * hnn8) return;
+  const int bb = (int)(idx / hnn8);
+  const int64_t e = (idx % hnn8) * 8;
   const int b_lo = (Bb == 1) ? 0 : bb, b_hi = (Bb == 1) ? B : bb + 1;
-  f32x4 acc;
+  // Partials (bi, gi) in ascending order are consecutive slots
+  // b_lo*groups .. b_hi*groups - 1; 8 loads in flight, added in order.
+  const int64_t stride = (int64_t)H * N * N;
+  const __bf16* src = part + (int64_t)b_lo * groups * stride + e;
+  const int n = (b_hi - b_lo) * groups;
+  float acc[8];
+  {
+    const bf16x8 x = ld8(src);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = 0.f;
-  bool first = true;
-  for (int bi = b_lo; bi < b_hi; ++bi)
-    for (int gi = 0; gi < groups; ++gi) {
-      f32x4 x = *reinterpret_cast<const f32x4*>(part + ((int64_t)bi * groups + gi) * H * N * N + e);
-      if (first) { acc = x; first = false; }
-      else {
+    for (int i = 0; i < 8; ++i) acc[i] = bf2f(x[i]);
+  }
+  int s = 1;
+  for (; s + 8 <= n; s += 8) {
+    bf16x8 x[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += x[i];
-      }
-    }
-  *reinterpret_cast<f32x4*>(dbias + (int64_t)bb * H * N * N + e) = acc;
+    for (int u = 0; u < 8; ++u) x[u] = ld8(src + (int64_t)(s + u) * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += bf2f(x[u][i]);
+  }
+  for (; s < n; ++s) {
+    const bf16x8 x = ld8(src + (int64_t)s * stride);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += bf2f(x[i]);
+  }
+  f32x4 lo, hi;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { lo[i] = acc[i]; hi[i] = acc[4 + i]; }
+  float* d = dbias + (int64_t)bb * H * N * N + e;
+  *reinterpret_cast<f32x4*>(d) = lo;
+  *reinterpret_cast<f32x4*>(d + 4) = hi;
 }
 
 }  // namespace tpf
@@ -850,12 +872,12 @@ int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t
   return check_launch("tpf_attn_delta_bf16");
 }
 
-// Backward workspace: bf16 dQ partials [N/64][B,O,H,N,D] | f32 dBias
+// Backward workspace: bf16 dQ partials [N/64][B,O,H,N,D] | bf16 dBias
 // partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
 // f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
 struct BwdParts {
   __bf16* dq;
-  float* db;
+  __bf16* db;
   float* bias_f;
   float* nl2;
   float* nd;
@@ -870,12 +892,12 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   int64_t off = 0;
   auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
   char* dq = take((N / 64) * rows * D * 2);
-  char* db = take(B * groups * H * N * N * 4);
+  char* db = take(B * groups * H * N * N * 2);
   char* bf = take(B * H * N * N * 4);
   char* nl = take(rows * 4);
   char* nd = take(rows * 4);
   if (parts) {
-    parts->dq = (__bf16*)dq; parts->db = (float*)db; parts->bias_f = (float*)bf;
+    parts->dq = (__bf16*)dq; parts->db = (__bf16*)db; parts->bias_f = (float*)bf;
     parts->nl2 = (float*)nl; parts->nd = (float*)nd;
   }
   return off;
@@ -962,7 +984,7 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
   hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
                      0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
   if ((rc = check_launch(fn))) return rc;
-  const int64_t db_items = bias_batches * H * N * N / 4;
+  const int64_t db_items = bias_batches * H * N * N / 8;
   hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
                      dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
                      (int)H, (int)N);
