@@ -98,6 +98,19 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
                                   int64_t O, int64_t H, int64_t N, int64_t D, int seq_major,
                                   int64_t bias_batches, double scale, void* stream);
 
+/* FP32 forward (inference): q, k, v, bias f32 in the layouts above, out f32
+ * [B, O, N, H, D], lse (nullable) f32 [B, O, H, N].  Requirements: N % 64 == 0,
+ * D % 4 == 0 and 4 <= D <= 64.  Products and sums in FP32 MFMA.
+ * Replaces turbopairformer_attention_fp32_forward
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_attention_fp32.py:139-224). */
+int64_t tpf_attn_forward_f32_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                             int64_t bias_batches);
+int tpf_attn_forward_f32(const float* q, const float* k, const float* v, const float* mask,
+                         const float* bias, float* out, float* lse, void* workspace,
+                         int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                         int64_t D, int seq_major, int64_t bias_batches, double scale,
+                         void* stream);
+
 /* ------------------------------------------------------------------------
  * Triangle multiplicative update (C == H in {32, 64, 96, 128}).
  *
@@ -162,6 +175,15 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
 int tpf_gemm_bf16(const void* A, int a_kc, int64_t a_ld, int64_t a_bs, const void* B, int b_kc,
                   int64_t b_ld, int64_t b_bs, void* C, int out_f32, int64_t c_ld, int64_t c_bs,
                   int64_t M, int64_t N, int64_t K, int64_t batch, double alpha, void* stream);
+
+/* Batched FP32 MFMA GEMM C[z] = alpha * A[z] B[z]^T + bias (bias per column,
+ * nullable), operands K- or MN-contiguous as tpf_gemm_bf16, C row-major f32.
+ * The strict-FP32 products of the reference's FP32 TriMul
+ * (turbopairformer_trimul_fp32.py:336-360). */
+int tpf_gemm_f32(const float* A, int a_kc, int64_t a_ld, int64_t a_bs, const float* B, int b_kc,
+                 int64_t b_ld, int64_t b_bs, float* C, int64_t c_ld, int64_t c_bs, int64_t M,
+                 int64_t N, int64_t K, int64_t batch, double alpha, const float* bias,
+                 void* stream);
 
 #ifdef __cplusplus
 }

@@ -23,3 +23,7 @@ __all__ = [
 from .trimul import check_stable_trimul_support, run_stable_trimul, turbo_trimul  # noqa: E402
 
 __all__ += ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]
+
+from .attention_fp32 import is_attention_fp32_supported, turbopairformer_attention_fp32  # noqa: E402
+
+__all__ += ["is_attention_fp32_supported", "turbopairformer_attention_fp32"]

@@ -53,6 +53,16 @@ SIGNATURES: dict[str, tuple] = {
         [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I64, _I64,
          _I64, _F64, _P],
     ),
+    "tpf_attn_forward_f32_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
+    "tpf_attn_forward_f32": (
+        _I32,
+        [_P] * 8 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
+    "tpf_gemm_f32": (
+        _I32,
+        [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+         _F64, _P, _P],
+    ),
     "tpf_trimul_plane_pitch": (_I64, [_I64]),
     "tpf_trimul_forward_workspace_bytes": (_I64, [_I64]),
     "tpf_trimul_forward_bf16": (

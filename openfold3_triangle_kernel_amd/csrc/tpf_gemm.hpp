@@ -20,9 +20,24 @@ struct GemmArgs {
   int batch;                             // set by gemm_launch
 };
 
+// FP32 variant (gemm_core_f32.hpp); bias (nullable) is added per column n.
+struct GemmArgsF32 {
+  const float* A; int64_t a_bs, a_ld;
+  const float* B; int64_t b_bs, b_ld;
+  float* C; int64_t c_bs, c_ld;
+  int M, N, K;
+  float alpha;
+  const float* bias;
+  int a_gather_n;
+  FastDiv a_div_n, a_div_nn;
+  int batch;
+};
+
 // a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).
 int gemm_launch(const GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch,
                 hipStream_t stream, const char* fn);
+int gemm_f32_launch(const GemmArgsF32& g, int a_kc, int b_kc, int batch, hipStream_t stream,
+                    const char* fn);
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
                 hipStream_t stream, const char* fn);
 
