@@ -167,6 +167,23 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
                              float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
                              void* stream);
 
+/* FP32 TriMul forward (inference).  z f32 [B, N, N, C] (rows contiguous),
+ * mask f32 [B, N, N]; weights f32 w_ap, w_ag, w_bp, w_bg [H, C], w_g [C, C],
+ * w_z [C, H]; biases (each nullable) [H] / [C]; LayerNorm affine
+ * parameters nullable, with their eps.  out f32 [B, N, N, C].  C <= 512,
+ * H <= 256.  Replaces run_trimul_fp32
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_trimul_fp32.py:155-400). */
+int64_t tpf_trimul_forward_f32_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t H);
+int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap, const float* w_ag,
+                           const float* w_bp, const float* w_bg, const float* w_g,
+                           const float* w_z, const float* b_ap, const float* b_ag,
+                           const float* b_bp, const float* b_bg, const float* b_g,
+                           const float* b_z, const float* ln_in_w, const float* ln_in_b,
+                           double ln_in_eps, const float* ln_out_w, const float* ln_out_b,
+                           double ln_out_eps, int outgoing, int64_t B, int64_t N, int64_t C,
+                           int64_t H, float* out, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
 /* Batched bf16 MFMA GEMM C[z] = alpha * A[z] B[z]^T with each operand
  * K-contiguous (x_kc = 1: X[r*ld + k]) or MN-contiguous (0: X[k*ld + r]);
  * C row-major, bf16 (out_f32 = 0) or f32.  The channel contraction of

@@ -27,3 +27,7 @@ __all__ += ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]
 from .attention_fp32 import is_attention_fp32_supported, turbopairformer_attention_fp32  # noqa: E402
 
 __all__ += ["is_attention_fp32_supported", "turbopairformer_attention_fp32"]
+
+from .trimul_fp32 import run_trimul_fp32  # noqa: E402
+
+__all__ += ["run_trimul_fp32"]

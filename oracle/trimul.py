@@ -54,26 +54,34 @@ def _contract(a, b, outgoing):
     return np.moveaxis(x, -3, -1)
 
 
-def trimul_forward(z, mask, w, outgoing, dtype=np.float64):
+def trimul_forward(z, mask, w, outgoing, dtype=np.float64, eps_in=EPS, eps_out=EPS):
     """Forward of the stock module.
 
     ``w`` maps names to arrays: w_ap, w_ag, w_bp, w_bg [H, C]; w_g [C, C];
-    w_z [C, H]; g_in, b_in [C]; g_out, b_out [H].  ``mask`` is [..., N, N].
+    w_z [C, H]; g_in, b_in [C]; g_out, b_out [H]; optional linear biases
+    bias_ap, bias_ag, bias_bp, bias_bg [H], bias_g, bias_z [C] (the AF2
+    layouts the reference's FP32 path accepts,
+    ``turbopairformer_trimul_fp32.py:91-152``).  ``mask`` is [..., N, N].
     Returns (out, cache) where cache holds what the backward needs.
     """
     z = np.asarray(z, dtype=dtype)
     W = {k: np.asarray(v, dtype=dtype) for k, v in w.items()}
     m = np.asarray(mask, dtype=dtype)[..., None]
-    zln, xh_in, rstd_in = layer_norm(z, W["g_in"], W["b_in"])
-    ap, ag = zln @ W["w_ap"].T, zln @ W["w_ag"].T
-    bp, bg = zln @ W["w_bp"].T, zln @ W["w_bg"].T
+
+    def lin(x, name):
+        y = x @ W["w_" + name].T
+        return y + W["bias_" + name] if "bias_" + name in W else y
+
+    zln, xh_in, rstd_in = layer_norm(z, W["g_in"], W["b_in"], eps_in)
+    ap, ag = lin(zln, "ap"), lin(zln, "ag")
+    bp, bg = lin(zln, "bp"), lin(zln, "bg")
     sa, sb = sigmoid(ag), sigmoid(bg)
     a = m * sa * ap
     b = m * sb * bp
     x = _contract(a, b, outgoing)
-    xln, xh_out, rstd_out = layer_norm(x, W["g_out"], W["b_out"])
-    y = xln @ W["w_z"].T
-    sg = sigmoid(zln @ W["w_g"].T)
+    xln, xh_out, rstd_out = layer_norm(x, W["g_out"], W["b_out"], eps_out)
+    y = lin(xln, "z")
+    sg = sigmoid(lin(zln, "g"))
     out = y * sg
     cache = dict(W=W, m=m, zln=zln, xh_in=xh_in, rstd_in=rstd_in, ap=ap, bp=bp, sa=sa, sb=sb,
                  a=a, b=b, x=x, xln=xln, xh_out=xh_out, rstd_out=rstd_out, y=y, sg=sg,

@@ -25,3 +25,16 @@ def test_attention_fp32_raises_before_launch():
     q = torch.zeros(1, 2, 4, 8, 16)
     with pytest.raises(ValueError, match="inference-only"):
         turbopairformer_attention_fp32(q, q, q, torch.zeros(1, 2, 1, 1, 8), torch.zeros(1, 1, 4, 8, 8))
+
+
+def test_trimul_fp32_contract():
+    from types import SimpleNamespace
+
+    from openfold3_triangle_kernel_amd.trimul_fp32 import run_trimul_fp32
+
+    m = SimpleNamespace(c_z=8, c_hidden=8, _outgoing=True)
+    z = torch.zeros(1, 4, 4, 8)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        run_trimul_fp32(m, z)
+    with torch.no_grad(), pytest.raises(ValueError, match="CUDA FP32"):
+        run_trimul_fp32(m, z)

@@ -74,3 +74,115 @@ def test_attention_fp32_sequence_major(gpu):
         out = turbopairformer_attention_fp32(qs, ks, vs, mask.to(gpu), bias.to(gpu))
     ref, _, _ = attention_forward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), bias.numpy())
     assert max_rel(out.cpu().numpy(), ref) <= TOL
+
+
+def _trimul_module(C, H, outgoing, *, biases=False, fused=False, affine=True, seed=0):
+    """An object with the official TriMul module's attribute names, FP32 on CPU."""
+    from types import SimpleNamespace
+
+    torch.manual_seed(seed)
+
+    def lin(i, o):
+        layer = torch.nn.Linear(i, o, bias=biases)
+        with torch.no_grad():
+            layer.weight.normal_(0, i ** -0.5)
+            if biases:
+                layer.bias.normal_(0, 0.2)
+        return layer
+
+    m = SimpleNamespace(c_z=C, c_hidden=H, _outgoing=outgoing)
+    if fused:
+        m.linear_ab_p, m.linear_ab_g = lin(C, 2 * H), lin(C, 2 * H)
+    else:
+        m.linear_a_p, m.linear_a_g, m.linear_b_p, m.linear_b_g = (lin(C, H) for _ in range(4))
+    m.linear_g, m.linear_z = lin(C, C), lin(H, C)
+    m.layer_norm_in = torch.nn.LayerNorm(C, eps=1e-5, elementwise_affine=affine)
+    m.layer_norm_out = torch.nn.LayerNorm(H, eps=1e-5, elementwise_affine=affine)
+    if affine:
+        with torch.no_grad():
+            for ln in (m.layer_norm_in, m.layer_norm_out):
+                ln.weight.normal_(1, 0.1)
+                ln.bias.normal_(0, 0.1)
+    return m
+
+
+def _oracle_weights(m, C, H):
+    def wb(layer, lo=None):
+        w = layer.weight.detach().cpu().double().numpy()
+        b = None if layer.bias is None else layer.bias.detach().cpu().double().numpy()
+        if lo is not None:
+            w = w[:H] if lo else w[H:]
+            b = None if b is None else (b[:H] if lo else b[H:])
+        return w, b
+
+    if hasattr(m, "linear_ab_p"):
+        parts = {"ap": wb(m.linear_ab_p, True), "ag": wb(m.linear_ab_g, True),
+                 "bp": wb(m.linear_ab_p, False), "bg": wb(m.linear_ab_g, False)}
+    else:
+        parts = {"ap": wb(m.linear_a_p), "ag": wb(m.linear_a_g), "bp": wb(m.linear_b_p),
+                 "bg": wb(m.linear_b_g)}
+    parts["g"], parts["z"] = wb(m.linear_g), wb(m.linear_z)
+    w = {}
+    for n, (wt, b) in parts.items():
+        w["w_" + n] = wt
+        if b is not None:
+            w["bias_" + n] = b
+
+    def aff(ln, n):
+        if ln.weight is None:
+            return np.ones(n), np.zeros(n)
+        return ln.weight.detach().cpu().double().numpy(), ln.bias.detach().cpu().double().numpy()
+
+    w["g_in"], w["b_in"] = aff(m.layer_norm_in, C)
+    w["g_out"], w["b_out"] = aff(m.layer_norm_out, H)
+    return w
+
+
+def _to(m, dev):
+    from types import SimpleNamespace
+
+    out = SimpleNamespace(**vars(m))
+    for name, v in vars(m).items():
+        if isinstance(v, torch.nn.Module):
+            setattr(out, name, v.to(dev))
+    return out
+
+
+TRIMUL_CASES = [
+    # B, N, C, H, outgoing, biases, fused, affine, mask_kind
+    (1, 64, 128, 128, True, False, False, True, "float"),
+    (1, 64, 128, 128, False, False, False, True, "float"),
+    (1, 33, 64, 64, True, True, False, True, "bool"),
+    (2, 40, 48, 40, False, True, True, True, "float"),
+    (1, 17, 30, 22, True, False, False, False, "none"),
+    (1, 96, 128, 96, False, True, False, True, "bool"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", TRIMUL_CASES,
+                         ids=lambda c: "B{}N{}C{}H{}{}{}{}".format(
+                             c[0], c[1], c[2], c[3], "out" if c[4] else "in",
+                             "_bias" if c[5] else "", "_fused" if c[6] else ""))
+def test_trimul_fp32(gpu, case):
+    from oracle.trimul import trimul_forward
+    from openfold3_triangle_kernel_amd.trimul_fp32 import run_trimul_fp32
+
+    B, N, C, H, outgoing, biases, fused, affine, mk = case
+    m = _trimul_module(C, H, outgoing, biases=biases, fused=fused, affine=affine)
+    g = torch.Generator().manual_seed(1)
+    z = torch.randn(B, N, N, C, generator=g)
+    if mk == "none":
+        mask, mask_np = None, np.ones((B, N, N))
+    else:
+        mb = torch.rand(B, N, N, generator=g) > 0.2
+        mask = mb if mk == "bool" else mb.float()
+        mask_np = mb.double().numpy()
+    print(f"fp32 trimul case={case}", flush=True)
+    with torch.no_grad():
+        out = run_trimul_fp32(_to(m, gpu), z.to(gpu), None if mask is None else mask.to(gpu))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and out.shape == z.shape
+    ref, _ = trimul_forward(z.double().numpy(), mask_np, _oracle_weights(m, C, H), outgoing)
+    err = max_rel(out.cpu().numpy(), ref)
+    assert err <= TOL, err

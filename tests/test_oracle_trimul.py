@@ -73,3 +73,38 @@ def test_masked_rows_do_not_feed_the_product():
     z2[0, 2, :] += 5.0  # masked row: only its own output gate may change
     out2, c2 = trimul_forward(z2, mask, w, True)
     np.testing.assert_allclose(c1["x"], c2["x"], rtol=0, atol=1e-12)
+
+
+def test_forward_with_linear_biases_and_eps_matches_torch_modules():
+    """Pins the optional-bias / eps extension of trimul_forward against an
+    independent torch restatement built from nn.Linear / nn.LayerNorm."""
+    import torch
+
+    from oracle.trimul import trimul_forward
+
+    torch.manual_seed(3)
+    C, H, N = 12, 10, 7
+    lin = {n: torch.nn.Linear(C, H, dtype=torch.float64) for n in ("ap", "ag", "bp", "bg")}
+    lin["g"] = torch.nn.Linear(C, C, dtype=torch.float64)
+    lin["z"] = torch.nn.Linear(H, C, dtype=torch.float64)
+    ln_in = torch.nn.LayerNorm(C, eps=1e-3, dtype=torch.float64)
+    ln_out = torch.nn.LayerNorm(H, eps=1e-4, dtype=torch.float64)
+    with torch.no_grad():
+        for t in (ln_in.weight, ln_in.bias, ln_out.weight, ln_out.bias):
+            t.normal_()
+    z = torch.randn(2, N, N, C, dtype=torch.float64)
+    mask = (torch.rand(2, N, N) > 0.2).double()
+    for outgoing in (True, False):
+        with torch.no_grad():
+            zl = ln_in(z)
+            a = mask[..., None] * torch.sigmoid(lin["ag"](zl)) * lin["ap"](zl)
+            b = mask[..., None] * torch.sigmoid(lin["bg"](zl)) * lin["bp"](zl)
+            eq = "bikc,bjkc->bijc" if outgoing else "bkic,bkjc->bijc"
+            ref = lin["z"](ln_out(torch.einsum(eq, a, b))) * torch.sigmoid(lin["g"](zl))
+        w = {"g_in": ln_in.weight.detach().numpy(), "b_in": ln_in.bias.detach().numpy(),
+             "g_out": ln_out.weight.detach().numpy(), "b_out": ln_out.bias.detach().numpy()}
+        for n, l in lin.items():
+            w["w_" + n] = l.weight.detach().numpy()
+            w["bias_" + n] = l.bias.detach().numpy()
+        got, _ = trimul_forward(z.numpy(), mask.numpy(), w, outgoing, eps_in=1e-3, eps_out=1e-4)
+        np.testing.assert_allclose(got, ref.numpy(), rtol=1e-10, atol=1e-10)
