@@ -44,6 +44,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-trimul", action="store_true")
+    ap.add_argument("--no-fp32", action="store_true", help="skip the FP32 inference-mode timings")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch a 256 MiB calibration copy and one attention backward kernel, "
@@ -235,6 +236,67 @@ def main():
             "config": {"N": TM_N, "C": C, "H": C, "directions": ["outgoing", "incoming"]},
         }
 
+    # ------------------- FP32 inference mode (no autograd) ---------------
+    fp32 = None
+    if not args.no_fp32:
+        from types import SimpleNamespace
+
+        from openfold3_triangle_kernel_amd import run_trimul_fp32, turbopairformer_attention_fp32
+
+        with torch.no_grad():
+            qf, kf, vf, bf = (t.float() for t in (q, k, v, bias))
+            for _ in range(2):
+                turbopairformer_attention_fp32(qf, kf, vf, mask, bf)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                turbopairformer_attention_fp32(qf, kf, vf, mask, bf)
+            e1.record()
+            torch.cuda.synchronize()
+            att32_ms = e0.elapsed_time(e1) / args.steps
+            del qf, kf, vf, bf
+            C = TM_C
+            g32 = torch.Generator(device=dev).manual_seed(2)
+
+            def lin(i, o):
+                layer = torch.nn.Linear(i, o, bias=False, device=dev)
+                with torch.no_grad():
+                    layer.weight.copy_(torch.randn(o, i, device=dev, generator=g32) / math.sqrt(i))
+                return layer
+
+            mod = SimpleNamespace(c_z=C, c_hidden=C, _outgoing=True,
+                                  linear_a_p=lin(C, C), linear_a_g=lin(C, C),
+                                  linear_b_p=lin(C, C), linear_b_g=lin(C, C),
+                                  linear_g=lin(C, C), linear_z=lin(C, C),
+                                  layer_norm_in=torch.nn.LayerNorm(C, device=dev),
+                                  layer_norm_out=torch.nn.LayerNorm(C, device=dev))
+            z32 = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g32)
+            m32 = torch.ones(1, TM_N, TM_N, device=dev)
+
+            def tm32_step():
+                for outgoing in (True, False):
+                    mod._outgoing = outgoing
+                    run_trimul_fp32(mod, z32, m32)
+
+            tm32_step()
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                tm32_step()
+            e1.record()
+            torch.cuda.synchronize()
+            tm32_ms = e0.elapsed_time(e1) / args.steps
+        att32_flops = 4.0 * B * O * H * N * N * D
+        tm32_flops = 2 * (2.0 * TM_N * TM_N * C * 5 * C + 2.0 * C * TM_N ** 3 + 2.0 * TM_N * TM_N * C * C)
+        fp32 = {
+            "attention_fwd_ms": round(att32_ms, 4),
+            "attention_fwd_tflops": round(att32_flops / (att32_ms * 1e-3) / 1e12, 2),
+            "trimul_fwd_out_plus_in_ms": round(tm32_ms, 4),
+            "trimul_fwd_tflops": round(tm32_flops / (tm32_ms * 1e-3) / 1e12, 2),
+            "peak_fp32_mfma_tflops": 157.3,
+            "note": "inference-only FP32 mode (no autograd), config 3 starting node / config 4",
+        }
+
     # -------------------------- CPU baseline -----------------------------
     cpu = None
     if not args.no_cpu_baseline:
@@ -265,6 +327,7 @@ def main():
             "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         },
         "trimul": trimul,
+        "fp32_inference": fp32,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
