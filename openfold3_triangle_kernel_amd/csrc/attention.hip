@@ -223,14 +223,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       const int blk = (kt >> 5) + sb;
-      f32x16 s = bnext;
-      if (blk + 1 < nblk) bnext = load_bias(blk + 1);
       if (!active) continue;
+      // The MFMAs read the prefetched bias as their C operand before the
+      // next block's bias is loaded into the same registers (no copies).
+      f32x16 s = bnext;
 #pragma unroll
       for (int ks = 0; ks < DP / 16; ++ks) {
         bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[buf][(sb * 32 + ql) * KP + 16 * ks + 8 * hl]);
         s = mfma32(ka, qreg[ks], s);
       }
+      if (blk + 1 < nblk) bnext = load_bias(blk + 1);
       if (masked) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -256,14 +258,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        bf16x8 pb;
+        // P in packed bf16 pairs (one v_cvt_pk each), summed by v_dot2 and
+        // reassembled into the B operand without permutes.
+        uint32_t pw[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb[e] = f2bf(fast_exp2(fmaf(s[8 * t + e], c2, nm)));
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          bf16x2 pr = {pb[e], pb[e + 1]};
+        for (int e = 0; e < 4; ++e) {
+          f32x2 f;
+          f[0] = fast_exp2(fmaf(s[8 * t + 2 * e], c2, nm));
+          f[1] = fast_exp2(fmaf(s[8 * t + 2 * e + 1], c2, nm));
+          const bf16x2 pr = __builtin_convertvector(f, bf16x2);
           l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);
+          pw[e] = __builtin_bit_cast(uint32_t, pr);
         }
+        u32x4 pwv = {pw[0], pw[1], pw[2], pw[3]};
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pwv);
         const int key0 = sb * 32 + 16 * t + 4 * hl;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db) {
@@ -418,8 +426,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     __bf16* __restrict__ dq_part, __bf16* __restrict__ dbias_part, AttnGeom g) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
-  constexpr int SP = 32 + 16;  // dS^T tile [64 keys][32 queries] pitch (bf16)
-  constexpr int RP = 64 + 4;   // dBias exchange [32 queries][64 keys] pitch (f32)
+  constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
+                               // 8-byte row writes of 32 lanes cover all banks once
+  constexpr int RP = 64 + 8;   // dBias exchange [32 queries][64 keys] pitch (f32):
+                               // the two lane halves (rows +4) land 32 banks apart
   constexpr int QDE = 32 * DP;                 // elements of one Q (or dO) tile
   constexpr int QDI = QDE * 2 / 1024;          // 1 KB async loads per Q (or dO) tile
   constexpr int NISSUE = 2 + 2 * QDI + 1;      // async loads per wave per step
