@@ -391,8 +391,8 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // Inputs of step i+1 (the bias fragments shared by the 4 waves, each wave's
 // Q / dO rows and row statistics) stream into the other half of a double
 // buffer with direct global->LDS loads while step i computes.
-// dQ leaves as a bf16 partial per key block; dBias sums the 4 waves in LDS
-// (fixed order) into a bf16 partial per outer group.  Fixed-order reducers
+// dQ leaves as a bf16 partial per key block; dBias sums the 4 waves' bf16
+// dS^T tiles in LDS (fixed order) into a bf16 partial per outer group.  Fixed-order reducers
 // finish both.  Tiles are ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
@@ -428,8 +428,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
-  constexpr int RP = 64 + 8;   // dBias exchange [32 queries][64 keys] pitch (f32):
-                               // the two lane halves (rows +4) land 32 banks apart
   constexpr int QDE = 32 * DP;                 // elements of one Q (or dO) tile
   constexpr int QDI = QDE * 2 / 1024;          // 1 KB async loads per Q (or dO) tile
   constexpr int NISSUE = 2 + 2 * QDI + 1;      // async loads per wave per step
@@ -443,7 +441,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   __shared__ __attribute__((aligned(16))) float RS1[4][64];
   constexpr int SSE = 64 * (KT > SP ? KT : SP);  // dS^T tile, or the K tile at setup
   __shared__ __attribute__((aligned(16))) __bf16 dSs[4][SSE];
-  __shared__ __attribute__((aligned(16))) float Red[4][32 * RP];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int kl = lane & 31, hl = lane >> 5;
@@ -477,6 +474,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   for (int i = tid; i < 4 * 2 * QDE / 8; i += 256) {
     reinterpret_cast<bf16x8*>(&QD0[0][0])[i] = zero8();
     reinterpret_cast<bf16x8*>(&QD1[0][0])[i] = zero8();
+  }
+  if (!active) {  // statistics of an idle wave: P = 0 everywhere
+    RS0[w][lane] = lane < 32 ? -INFINITY : 0.f;
+    RS1[w][lane] = lane < 32 ? -INFINITY : 0.f;
   }
 
   // Per-wave constant operands for this key block.
@@ -534,7 +535,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         g2lds16(dout + do_plane + (int64_t)(q0 + r) * H * D + c * 8, &QDs[w][QDE + n * 512]);
       }
     }
-    if (lane < 16) {
+    // An idle wave keeps the -inf / 0 statistics written at setup, so its
+    // P and dS are exactly zero and it adds nothing to the dBias sum.
+    if (active && lane < 16) {
       const float* src = (lane < 8 ? nl2_g : nd_g) + st_plane + q0 + (lane & 7) * 4;
       g2lds16(src, &RS[w][0]);
     }
@@ -572,8 +575,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       f32x4 d4 = *reinterpret_cast<const f32x4*>(&RSc[w][32 + 8 * j + 4 * hl]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        nl2v[4 * j + i] = active ? a4[i] : -INFINITY;
-        ndv[4 * j + i] = active ? d4[i] : 0.f;
+        nl2v[4 * j + i] = a4[i];
+        ndv[4 * j + i] = d4[i];
       }
     }
     const __bf16* Qs = QDc[w];
@@ -608,7 +611,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         dS[cb][r] = p * dp[r];
       }
     }
-    // dV^T += dO^T P, dK^T += Q^T dS (16-query k-steps, C-layout order).
+    // P and dS in bf16, packed once: B operands of dV^T += dO^T P and
+    // dK^T += Q^T dS (16-query k-steps, C-layout order) and the dS^T tile.
+    bf16x8 pP[2][2], pS[2][2];  // [cb][t]
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        pP[cb][t] = pack8(P[cb], 8 * t);
+        pS[cb][t] = pack8(dS[cb], 8 * t);
+      }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -619,23 +631,20 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
                                qd_tr_col4<DP>(Qs, 16 * t + 8, 16 * t + 12, 32 * db));
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-          dVacc[db][cb] = mfma32(da, pack8(P[cb], 8 * t), dVacc[db][cb]);
-          dKacc[db][cb] = mfma32(qa, pack8(dS[cb], 8 * t), dKacc[db][cb]);
+          dVacc[db][cb] = mfma32(da, pP[cb][t], dVacc[db][cb]);
+          dKacc[db][cb] = mfma32(qa, pS[cb][t], dKacc[db][cb]);
         }
       }
     }
-    // dS -> LDS: bf16 [key][query] for dQ, f32 [query][key] for the dBias sum.
-    float* red = Red[w];
+    // dS -> LDS as bf16 [key][query]: the dQ operand and the dBias sum.
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        const bf16x8 h = pS[cb][j >> 1];
         bf16x4 s4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s4[i] = f2bf(dS[cb][4 * j + i]);
-          red[(8 * j + 4 * hl + i) * RP + cb * 32 + kl] = dS[cb][4 * j + i];
-        }
+        for (int i = 0; i < 4; ++i) s4[i] = h[4 * (j & 1) + i];
         *reinterpret_cast<bf16x4*>(&Ss[(cb * 32 + kl) * SP + 8 * j + 4 * hl]) = s4;
       }
     // dQ^T (d x 32 queries) = K^T dS^T over this block's 64 keys -> bf16 partial.
@@ -662,25 +671,27 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       }
     }
     lds_barrier();
-    // dBias partial: fixed wave order ((w0 + w1) + w2) + w3.
+    // dBias partial: the 4 waves' bf16 dS^T tiles summed in the fixed order
+    // ((w0 + w1) + w2) + w3.  Thread = (key, 8-query block): 8-byte reads of
+    // each wave's row, and each store instruction of a wave writes 64
+    // consecutive keys of one query row (128 bytes).
     {
-      __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0) * N + key_base;
+      const int key = tid & 63, qb = tid >> 6;
+      float acc[8];
 #pragma unroll
-      for (int it2 = 0; it2 < 2; ++it2) {
-        const int idx = it2 * 256 + tid;  // 32 rows x 16 float4 chunks
-        const int qr = idx >> 4, c4 = (idx & 15) * 4;
-        f32x4 acc = *reinterpret_cast<const f32x4*>(&Red[0][qr * RP + c4]);
+      for (int ww = 0; ww < 4; ++ww) {
+        const __bf16* src = &dSs[ww][key * SP + 8 * qb];
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(src);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(src + 4);
 #pragma unroll
-        for (int ww = 1; ww < 4; ++ww) {
-          f32x4 x = *reinterpret_cast<const f32x4*>(&Red[ww][qr * RP + c4]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += x[i];
+        for (int e = 0; e < 4; ++e) {
+          acc[e] = ww ? acc[e] + bf2f(lo[e]) : bf2f(lo[e]);
+          acc[4 + e] = ww ? acc[4 + e] + bf2f(hi[e]) : bf2f(hi[e]);
         }
-        bf16x4 o4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[i]);
-        *reinterpret_cast<bf16x4*>(dst + (int64_t)qr * N + c4) = o4;
       }
+      __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0 + 8 * qb) * N + key_base + key;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[(int64_t)e * N] = f2bf(acc[e]);
     }
   };
   issue(0, Bf0, QD0, RS0);
