@@ -31,3 +31,13 @@ __all__ += ["is_attention_fp32_supported", "turbopairformer_attention_fp32"]
 from .trimul_fp32 import run_trimul_fp32  # noqa: E402
 
 __all__ += ["run_trimul_fp32"]
+
+from .modules import (  # noqa: E402
+    TriangleAttention,
+    TriangleMultiplicationIncoming,
+    TriangleMultiplicationOutgoing,
+    TriangleMultiplicativeUpdate,
+)
+
+__all__ += ["TriangleAttention", "TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing",
+            "TriangleMultiplicativeUpdate"]

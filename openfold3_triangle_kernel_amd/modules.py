@@ -1,0 +1,153 @@
+"""Drop-in OpenFold3 pair-stack modules backed by the MI355X kernels.
+
+``TriangleAttention`` and ``TriangleMultiplicativeUpdate`` (with the
+``TriangleMultiplicationOutgoing`` / ``Incoming`` subclasses) register the
+same parameters under the same names as OpenFold3's modules
+(``openfold3/core/model/layers/triangular_attention.py:35-75`` with the
+``Attention`` primitive of ``openfold3/core/model/primitives/attention.py``,
+and ``openfold3/core/model/layers/triangular_multiplicative_update.py:700-830``),
+so a ``state_dict`` of the stock module loads unchanged.  Their forward
+passes follow the stock modules' math and route the hot op the way the
+reference's ``use_stable_*`` path does (``attention.py:640-692``,
+``triangular_multiplicative_update.py:62-120``):
+
+* attention: LayerNorm (statistics in FP32), the additive mask
+  ``inf * (mask - 1)``, the pair bias ``linear_z``, raw (unscaled) q / k / v
+  as the sequence-major view of the projections, the triangle-attention
+  kernel, sigmoid gate and ``linear_o``.  BF16 kernels whenever gradients
+  are recorded or the activations are BF16; FP32 activations under
+  ``torch.no_grad()`` take the FP32 inference kernel.
+* TriMul: ``run_stable_trimul`` (BF16 kernels, autograd) or, for FP32
+  activations under ``torch.no_grad()``, ``run_trimul_fp32``.
+"""
+
+from __future__ import annotations
+
+
+import torch
+from torch import nn
+
+from .attention import turbopairformer_triangle_attention
+from .attention_fp32 import turbopairformer_attention_fp32
+from .trimul import run_stable_trimul
+from .trimul_fp32 import run_trimul_fp32
+
+
+def _layer_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
+    """LayerNorm with FP32 statistics, returned in the input dtype
+    (``openfold3/core/model/primitives/normalization.py:54-78``)."""
+    w = None if ln.weight is None else ln.weight.float()
+    b = None if ln.bias is None else ln.bias.float()
+    return nn.functional.layer_norm(x.float(), ln.normalized_shape, w, b, ln.eps).to(x.dtype)
+
+
+def _fp32_inference(x: torch.Tensor) -> bool:
+    return x.dtype == torch.float32 and not torch.is_grad_enabled()
+
+
+class _MHA(nn.Module):
+    """The parameter container of OpenFold3's ``Attention`` for triangle
+    attention (no biases, gating on): linear_{q,k,v,o,g}."""
+
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int):
+        super().__init__()
+        self.c_hidden = c_hidden
+        self.no_heads = no_heads
+        self.linear_q = nn.Linear(c_in, c_hidden * no_heads, bias=False)
+        self.linear_k = nn.Linear(c_in, c_hidden * no_heads, bias=False)
+        self.linear_v = nn.Linear(c_in, c_hidden * no_heads, bias=False)
+        self.linear_o = nn.Linear(c_hidden * no_heads, c_in, bias=False)
+        self.linear_g = nn.Linear(c_in, c_hidden * no_heads, bias=False)
+
+
+class TriangleAttention(nn.Module):
+    """Triangle attention around the starting (or ending) node."""
+
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int, starting: bool = True,
+                 inf: float = 1e9):
+        super().__init__()
+        self.c_in = c_in
+        self.c_hidden = c_hidden
+        self.no_heads = no_heads
+        self.starting = starting
+        self.inf = inf
+        self.layer_norm = nn.LayerNorm(c_in)
+        self.linear_z = nn.Linear(c_in, no_heads, bias=False)
+        self.mha = _MHA(c_in, c_hidden, no_heads)
+
+    def forward(self, x: torch.Tensor, mask: torch.Tensor | None = None,
+                transpose_bias: bool = False) -> torch.Tensor:
+        """x: [*, I, J, C_in]; mask: [*, I, J] (1 keep, 0 drop)."""
+        if mask is None:
+            mask = x.new_ones(x.shape[:-1])
+        if not self.starting:
+            x = x.transpose(-2, -3)
+            mask = mask.transpose(-1, -2)
+        x = _layer_norm(self.layer_norm, x)
+        mask_bias = (self.inf * (mask.float() - 1))[..., :, None, None, :]
+        zb = self.linear_z(x)
+        perm = (-1, -2, -3) if transpose_bias else (-1, -3, -2)
+        tri_bias = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in perm)).unsqueeze(-4)
+        m = self.mha
+        H, c = m.no_heads, m.c_hidden
+
+        def heads(t):  # [*, I, J, H*c] -> sequence-major view [*, I, H, J, c]
+            return t.view(t.shape[:-1] + (H, c)).transpose(-2, -3)
+
+        q, k, v = heads(m.linear_q(x)), heads(m.linear_k(x)), heads(m.linear_v(x))
+        if _fp32_inference(x):
+            o = turbopairformer_attention_fp32(q, k, v, mask_bias, tri_bias.float())
+        else:
+            o = turbopairformer_triangle_attention(
+                q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
+                tri_bias.to(torch.bfloat16),
+            ).to(x.dtype)
+        g = torch.sigmoid(m.linear_g(x)).view(o.shape)
+        out = m.linear_o((o * g).flatten(-2))
+        if not self.starting:
+            out = out.transpose(-2, -3)
+        return out
+
+
+class TriangleMultiplicativeUpdate(nn.Module):
+    """Triangle multiplicative update (outgoing or incoming edges)."""
+
+    def __init__(self, c_z: int, c_hidden: int, _outgoing: bool = True):
+        super().__init__()
+        self.c_z = c_z
+        self.c_hidden = c_hidden
+        self._outgoing = _outgoing
+        # Registration order of the stock module: linear_g, linear_z, the two
+        # LayerNorms, then the four branch projections.
+        self.linear_g = nn.Linear(c_z, c_z, bias=False)
+        self.linear_z = nn.Linear(c_hidden, c_z, bias=False)
+        self.layer_norm_in = nn.LayerNorm(c_z)
+        self.layer_norm_out = nn.LayerNorm(c_hidden)
+        self.linear_a_p = nn.Linear(c_z, c_hidden, bias=False)
+        self.linear_a_g = nn.Linear(c_z, c_hidden, bias=False)
+        self.linear_b_p = nn.Linear(c_z, c_hidden, bias=False)
+        self.linear_b_g = nn.Linear(c_z, c_hidden, bias=False)
+
+    def forward(self, z: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
+        """z: [*, N, N, C_z]; mask: [*, N, N]."""
+        if _fp32_inference(z):
+            return run_trimul_fp32(self, z, mask)
+        return run_stable_trimul(self, z, mask)
+
+
+class TriangleMultiplicationOutgoing(TriangleMultiplicativeUpdate):
+    def __init__(self, c_z: int, c_hidden: int):
+        super().__init__(c_z, c_hidden, _outgoing=True)
+
+
+class TriangleMultiplicationIncoming(TriangleMultiplicativeUpdate):
+    def __init__(self, c_z: int, c_hidden: int):
+        super().__init__(c_z, c_hidden, _outgoing=False)
+
+
+__all__ = [
+    "TriangleAttention",
+    "TriangleMultiplicationIncoming",
+    "TriangleMultiplicationOutgoing",
+    "TriangleMultiplicativeUpdate",
+]
