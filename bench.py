@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-trimul", action="store_true")
     ap.add_argument("--no-fp32", action="store_true", help="skip the FP32 inference-mode timings")
+    ap.add_argument("--pair-block", action="store_true",
+                    help="also time the config-5 pair-stack block (N=768) through the modules")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch a 256 MiB calibration copy and one attention backward kernel, "
@@ -297,6 +299,52 @@ def main():
             "note": "inference-only FP32 mode (no autograd), config 3 starting node / config 4",
         }
 
+    # ------------- config 5: pair-stack block at N=768 (modules) -----------
+    pair_block = None
+    if args.pair_block:
+        from openfold3_triangle_kernel_amd import (
+            TriangleAttention,
+            TriangleMultiplicationIncoming,
+            TriangleMultiplicationOutgoing,
+        )
+
+        torch.manual_seed(5)
+        Np, Cz = 768, 128
+        mods = [TriangleMultiplicationOutgoing(Cz, Cz), TriangleMultiplicationIncoming(Cz, Cz),
+                TriangleAttention(Cz, 32, 4, starting=True), TriangleAttention(Cz, 32, 4, starting=False)]
+        for mo in mods:
+            for prm in mo.parameters():
+                if prm.dim() == 2:
+                    torch.nn.init.normal_(prm, std=1.0 / math.sqrt(prm.shape[1]))
+        mods = [mo.to(dev, torch.bfloat16) for mo in mods]
+        zp = torch.randn(1, Np, Np, Cz, device=dev).to(torch.bfloat16).requires_grad_(True)
+        mp = torch.ones(1, Np, Np, device=dev, dtype=torch.bfloat16)
+        params = [zp] + [prm for mo in mods for prm in mo.parameters()]
+
+        def block_step():
+            h = zp
+            for mo in mods:
+                h = h + mo(h, mp)
+            torch.autograd.grad(h.float().square().mean(), params)
+
+        for _ in range(2):
+            block_step()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(max(1, args.steps // 4)):
+            block_step()
+        e1.record()
+        torch.cuda.synchronize()
+        blk_ms = e0.elapsed_time(e1) / max(1, args.steps // 4)
+        pair_block = {
+            "ms_fwd_bwd": round(blk_ms, 3),
+            "config": {"N": Np, "C": Cz, "blocks": ["trimul_out", "trimul_in", "tri_att_start",
+                                                      "tri_att_end"], "H": 4, "D": 32},
+            "note": "config 5: residual pair block through the drop-in modules (bf16 params, "
+                    "LayerNorm / projections in torch, hot ops in the HIP kernels)",
+        }
+        del zp, mods, params
+
     # -------------------------- CPU baseline -----------------------------
     cpu = None
     if not args.no_cpu_baseline:
@@ -328,6 +376,7 @@ def main():
         },
         "trimul": trimul,
         "fp32_inference": fp32,
+        "pair_block": pair_block,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
