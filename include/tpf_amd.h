@@ -167,6 +167,16 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
                              float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
                              void* stream);
 
+/* Weight gradient of a linear layer over R rows, dW[m][n] = sum_r dy[r][m] x[r][n]
+ * (dy [R, M], x [R, N] row-major bf16 with leading dimensions ld_dy, ld_x;
+ * dW f32 [M, N]), split over R with a fixed-order fold.  Used for the pair
+ * stack's projection weights (R = B*N^2), the products the reference leaves
+ * to torch / cuBLAS (openfold3/core/model/layers/triangular_attention.py:160-243). */
+int64_t tpf_wgrad_bf16_workspace_bytes(int64_t R, int64_t M, int64_t N);
+int tpf_wgrad_bf16(const void* dy, int64_t ld_dy, const void* x, int64_t ld_x, int64_t R,
+                   int64_t M, int64_t N, float* dw, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 /* FP32 TriMul forward (inference).  z f32 [B, N, N, C] (rows contiguous),
  * mask f32 [B, N, N]; weights f32 w_ap, w_ag, w_bp, w_bg [H, C], w_g [C, C],
  * w_z [C, H]; biases (each nullable) [H] / [C]; LayerNorm affine

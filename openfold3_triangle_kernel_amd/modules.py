@@ -12,9 +12,11 @@ reference's ``use_stable_*`` path does (``attention.py:640-692``,
 ``triangular_multiplicative_update.py:62-120``):
 
 * attention: LayerNorm (statistics in FP32), the additive mask
-  ``inf * (mask - 1)``, the pair bias ``linear_z``, raw (unscaled) q / k / v
-  as the sequence-major view of the projections, the triangle-attention
-  kernel, sigmoid gate and ``linear_o``.  BF16 kernels whenever gradients
+  ``inf * (mask - 1)``, one fused projection GEMM for q / k / v, the gate
+  and the pair bias ``linear_z`` (raw, unscaled q / k / v handed to the
+  kernel as sequence-major views), the triangle-attention kernel, sigmoid
+  gate and ``linear_o``; the projection weight gradients (a contraction
+  over all B*N^2 pair rows) run on the split-K MFMA GEMM.  BF16 kernels whenever gradients
   are recorded or the activations are BF16; FP32 activations under
   ``torch.no_grad()`` take the FP32 inference kernel.
 * TriMul: ``run_stable_trimul`` (BF16 kernels, autograd) or, for FP32
@@ -27,7 +29,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .attention import turbopairformer_triangle_attention
+from . import _native
+from .attention import _device_ctx, turbopairformer_triangle_attention
 from .attention_fp32 import turbopairformer_attention_fp32
 from .trimul import run_stable_trimul
 from .trimul_fp32 import run_trimul_fp32
@@ -43,6 +46,47 @@ def _layer_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
 
 def _fp32_inference(x: torch.Tensor) -> bool:
     return x.dtype == torch.float32 and not torch.is_grad_enabled()
+
+
+class _ProjLinear(torch.autograd.Function):
+    """y = x W^T for BF16 activations over B*N^2 rows, whose weight gradient
+    dW = dy^T x (K = rows) runs on the split-K MFMA GEMM (tpf_wgrad_bf16)."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        wb = w.to(x.dtype)
+        ctx.save_for_backward(x, wb)
+        ctx.w_dtype = w.dtype
+        return x @ wb.t()
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, wb = ctx.saved_tensors
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = dy @ wb
+        if ctx.needs_input_grad[1]:
+            M, K = wb.shape
+            dy2 = dy.reshape(-1, M).to(torch.bfloat16).contiguous()
+            x2 = x.reshape(-1, K).contiguous()
+            R = x2.shape[0]
+            dw32 = torch.empty((M, K), device=x.device, dtype=torch.float32)
+            ws_bytes = int(_native.query("tpf_wgrad_bf16_workspace_bytes", R, M, K))
+            ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+            with _device_ctx(x.device):
+                _native.call("tpf_wgrad_bf16", dy2.data_ptr(), M, x2.data_ptr(), K, R, M, K,
+                             dw32.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(x2))
+            dw = dw32.to(ctx.w_dtype)
+        return dx, dw
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Projection over the pair rows: the split-K weight gradient for BF16
+    activations whose feature sizes are multiples of 8, torch otherwise."""
+    if (x.dtype == torch.bfloat16 and x.is_cuda and w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0
+            and torch.is_grad_enabled()):
+        return _ProjLinear.apply(x, w)
+    return nn.functional.linear(x, w.to(x.dtype))
 
 
 class _MHA(nn.Module):
@@ -85,16 +129,25 @@ class TriangleAttention(nn.Module):
             mask = mask.transpose(-1, -2)
         x = _layer_norm(self.layer_norm, x)
         mask_bias = (self.inf * (mask.float() - 1))[..., :, None, None, :]
-        zb = self.linear_z(x)
-        perm = (-1, -2, -3) if transpose_bias else (-1, -3, -2)
-        tri_bias = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in perm)).unsqueeze(-4)
         m = self.mha
         H, c = m.no_heads, m.c_hidden
+        # One projection GEMM for q, k, v, the gate and the pair bias (rows
+        # padded to a multiple of 8; the pad outputs are unused).
+        hc = H * c
+        pad = (-(4 * hc + H)) % 8
+        w_all = torch.cat([m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
+                           m.linear_g.weight, self.linear_z.weight]
+                          + ([self.linear_z.weight.new_zeros(pad, self.c_in)] if pad else []))
+        proj = _linear(x, w_all)
+        qp, kp, vp, gp = (proj[..., i * hc:(i + 1) * hc] for i in range(4))
+        zb = proj[..., 4 * hc:4 * hc + H]
+        perm = (-1, -2, -3) if transpose_bias else (-1, -3, -2)
+        tri_bias = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in perm)).unsqueeze(-4)
 
-        def heads(t):  # [*, I, J, H*c] -> sequence-major view [*, I, H, J, c]
-            return t.view(t.shape[:-1] + (H, c)).transpose(-2, -3)
+        def heads(t):  # [*, I, J, H*c] -> [*, I, H, J, c]
+            return t.reshape(t.shape[:-1] + (H, c)).transpose(-2, -3)
 
-        q, k, v = heads(m.linear_q(x)), heads(m.linear_k(x)), heads(m.linear_v(x))
+        q, k, v = heads(qp), heads(kp), heads(vp)
         if _fp32_inference(x):
             o = turbopairformer_attention_fp32(q, k, v, mask_bias, tri_bias.float())
         else:
@@ -102,8 +155,8 @@ class TriangleAttention(nn.Module):
                 q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
                 tri_bias.to(torch.bfloat16),
             ).to(x.dtype)
-        g = torch.sigmoid(m.linear_g(x)).view(o.shape)
-        out = m.linear_o((o * g).flatten(-2))
+        g = torch.sigmoid(gp).reshape(o.shape)
+        out = _linear((o * g).flatten(-2), m.linear_o.weight)
         if not self.starting:
             out = out.transpose(-2, -3)
         return out

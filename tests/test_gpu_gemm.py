@@ -58,3 +58,28 @@ def test_gemm(gpu, case, a_kc, b_kc, out_f32):
     ref = alpha * torch.bmm(a.double().cpu(), b.double().cpu().transpose(1, 2))
     err = max_rel(c.float().cpu().numpy(), ref.cpu().numpy())
     assert err <= (1e-5 if out_f32 else 8e-3), err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("R,M,N", [(147456, 520, 128), (4096, 128, 128), (300, 24, 40)])
+def test_wgrad_split_k(gpu, R, M, N):
+    """tpf_wgrad_bf16: dW = dy^T x over R rows (split-K + fixed-order fold)."""
+    from openfold3_triangle_kernel_amd import _native
+
+    g = torch.Generator(device="cpu").manual_seed(R + M)
+    dy = torch.randn(R, M, generator=g).to(torch.bfloat16).to(gpu)
+    x = torch.randn(R, N, generator=g).to(torch.bfloat16).to(gpu)
+    dw = torch.empty(M, N, device=gpu)
+    ws_bytes = int(_native.query("tpf_wgrad_bf16_workspace_bytes", R, M, N))
+    ws = torch.empty(ws_bytes, device=gpu, dtype=torch.uint8)
+    stream = torch.cuda.current_stream().cuda_stream
+    _native.call("tpf_wgrad_bf16", dy.data_ptr(), M, x.data_ptr(), N, R, M, N, dw.data_ptr(),
+                 ws.data_ptr(), ws_bytes, stream)
+    torch.cuda.synchronize()
+    ref = dy.double().t() @ x.double()
+    assert max_rel(dw.cpu().numpy(), ref.cpu().numpy()) <= 1e-5
+    dw2 = torch.empty_like(dw)
+    _native.call("tpf_wgrad_bf16", dy.data_ptr(), M, x.data_ptr(), N, R, M, N, dw2.data_ptr(),
+                 ws.data_ptr(), ws_bytes, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dw, dw2)  # fixed-order fold: bitwise replay

@@ -66,3 +66,62 @@ def test_trimul_module_snapshot_fp32(gpu):
     # The BF16 training kernels need c_hidden == c_z: this module is rejected loudly.
     with pytest.raises(ValueError, match="c_hidden == c_z"):
         m(x.to(gpu).requires_grad_(True), mask.to(gpu).float())
+
+
+def _stock_triangle_attention(m, x, mask, starting):
+    """FP32 torch restatement of OpenFold3's TriangleAttention forward
+    (triangular_attention.py:352-409, attention.py _prep_qkv / _wrap_up)."""
+    import math
+
+    if not starting:
+        x = x.transpose(-2, -3)
+        mask = mask.transpose(-1, -2)
+    x = torch.nn.functional.layer_norm(x, (x.shape[-1],), m.layer_norm.weight, m.layer_norm.bias)
+    mask_bias = (m.inf * (mask - 1))[..., :, None, None, :]
+    tri = (x @ m.linear_z.weight.t()).permute(0, 3, 1, 2).unsqueeze(-4)
+    H, c = m.mha.no_heads, m.mha.c_hidden
+
+    def heads(t):
+        return t.view(t.shape[:-1] + (H, c)).transpose(-2, -3)
+
+    q, k, v = (heads(x @ w.t()) for w in (m.mha.linear_q.weight, m.mha.linear_k.weight,
+                                          m.mha.linear_v.weight))
+    a = torch.softmax(q @ k.transpose(-1, -2) / math.sqrt(c) + mask_bias + tri, -1)
+    o = (a @ v).transpose(-2, -3)
+    g = torch.sigmoid(x @ m.mha.linear_g.weight.t()).view(o.shape)
+    out = ((o * g).flatten(-2)) @ m.mha.linear_o.weight.t()
+    return out.transpose(-2, -3) if not starting else out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("starting", [True, False])
+def test_triangle_attention_module_backward(gpu, starting):
+    """BF16 module forward + every parameter / input gradient vs the FP32
+    stock math on the same (bf16-representable) weights: max-rel <= 2e-2."""
+    from openfold3_triangle_kernel_amd import TriangleAttention
+
+    torch.manual_seed(7)
+    m = TriangleAttention(128, 32, 4, starting=starting)
+    for p in m.parameters():
+        p.data = p.data.normal_(std=0.1 if p.dim() == 2 else 1.0).bfloat16().float()
+    m = m.to(gpu)
+    x = torch.randn(1, 96, 96, 128, device=gpu).bfloat16().float()
+    mask = (torch.rand(1, 96, 96, device=gpu) > 0.1).float()
+    dout = torch.randn(1, 96, 96, 128, device=gpu).bfloat16().float()
+    ref_params = {n: p.detach().clone().requires_grad_(True) for n, p in m.named_parameters()}
+    xr = x.clone().requires_grad_(True)
+    ref_m = TriangleAttention(128, 32, 4, starting=starting).to(gpu)
+    ref_m.load_state_dict({n: p for n, p in ref_params.items()})
+    for n, p in ref_m.named_parameters():
+        p.requires_grad_(True)
+    ref = _stock_triangle_attention(ref_m, xr, mask, starting)
+    ref_grads = torch.autograd.grad(ref, [xr] + list(ref_m.parameters()), dout)
+    mb = m.to(torch.bfloat16)
+    xb = x.bfloat16().requires_grad_(True)
+    out = mb(xb, mask.bfloat16())
+    grads = torch.autograd.grad(out, [xb] + list(mb.parameters()), dout.bfloat16())
+    names = ["out", "x"] + [n for n, _ in mb.named_parameters()]
+    for name, a, b in zip(names, [out] + list(grads), [ref] + list(ref_grads)):
+        err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
+        print(f"module starting={starting} {name} max-rel {err:.3e}", flush=True)
+        assert err <= 2e-2, f"{name}: {err:.3e}"
