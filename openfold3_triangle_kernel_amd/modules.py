@@ -139,8 +139,9 @@ class TriangleAttention(nn.Module):
                            m.linear_g.weight, self.linear_z.weight]
                           + ([self.linear_z.weight.new_zeros(pad, self.c_in)] if pad else []))
         proj = _linear(x, w_all)
-        qp, kp, vp, gp = (proj[..., i * hc:(i + 1) * hc] for i in range(4))
-        zb = proj[..., 4 * hc:4 * hc + H]
+        # split (not slicing): its backward is one concatenation of the part
+        # gradients instead of a zero-filled full-size buffer per part.
+        qp, kp, vp, gp, zb, *_ = torch.split(proj, [hc, hc, hc, hc, H] + ([pad] if pad else []), -1)
         perm = (-1, -2, -3) if transpose_bias else (-1, -3, -2)
         tri_bias = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in perm)).unsqueeze(-4)
 
