@@ -212,6 +212,29 @@ int tpf_gemm_f32(const float* A, int a_kc, int64_t a_ld, int64_t a_bs, const flo
                  int64_t N, int64_t K, int64_t batch, double alpha, const float* bias,
                  void* stream);
 
+/* LayerNorm over the C contiguous bf16 channels of each row of a [B, I, J]
+ * pair grid, FP32 statistics.  x rows are addressed through element strides
+ * (sb, si, sj) (multiples of 8), so a transposed view is read in place; y
+ * [B*I*J, C], mean and rstd [B*I*J] are written in logical row order.  w / b
+ * (f32 [C]) are nullable (no affine).  8 <= C <= 2048, C % 8 == 0.  Replaces
+ * the module's torch LayerNorm with FP32 statistics
+ * (openfold3/core/model/primitives/normalization.py:54-78, applied at
+ * openfold3/core/model/layers/triangular_attention.py:160-170). */
+int tpf_layer_norm_forward_bf16(const void* x, int64_t B, int64_t I, int64_t J, int64_t sb,
+                                int64_t si, int64_t sj, int64_t C, const float* w,
+                                const float* b, double eps, void* y, float* mean, float* rstd,
+                                void* stream);
+
+/* Its backward: dy [B*I*J, C] logical row order, x with strides (sb, si, sj)
+ * and dx written with strides (dsb, dsi, dsj); dw / db f32 [C] (both null to
+ * skip the parameter gradients) from fixed-order partials in the workspace. */
+int64_t tpf_layer_norm_backward_workspace_bytes(int64_t R, int64_t C);
+int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64_t B, int64_t I, int64_t J,
+                                 int64_t sb, int64_t si, int64_t sj, int64_t dsb, int64_t dsi,
+                                 int64_t dsj, int64_t C, const float* mean, const float* rstd,
+                                 const float* w, void* dx, float* dw, float* db, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

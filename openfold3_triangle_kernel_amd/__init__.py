@@ -41,3 +41,7 @@ from .modules import (  # noqa: E402
 
 __all__ += ["TriangleAttention", "TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing",
             "TriangleMultiplicativeUpdate"]
+
+from .layernorm import layer_norm_bf16  # noqa: E402
+
+__all__ += ["layer_norm_bf16"]

@@ -11,7 +11,7 @@ passes follow the stock modules' math and route the hot op the way the
 reference's ``use_stable_*`` path does (``attention.py:640-692``,
 ``triangular_multiplicative_update.py:62-120``):
 
-* attention: LayerNorm (statistics in FP32), the additive mask
+* attention: LayerNorm (statistics in FP32; the BF16 LayerNorm kernel), the additive mask
   ``inf * (mask - 1)``, one fused projection GEMM for q / k / v, the gate
   and the pair bias ``linear_z`` (raw, unscaled q / k / v handed to the
   kernel as sequence-major views), the triangle-attention kernel, sigmoid
@@ -32,13 +32,18 @@ from torch import nn
 from . import _native
 from .attention import _device_ctx, turbopairformer_triangle_attention
 from .attention_fp32 import turbopairformer_attention_fp32
+from .layernorm import layer_norm_bf16
 from .trimul import run_stable_trimul
 from .trimul_fp32 import run_trimul_fp32
 
 
 def _layer_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
     """LayerNorm with FP32 statistics, returned in the input dtype
-    (``openfold3/core/model/primitives/normalization.py:54-78``)."""
+    (``openfold3/core/model/primitives/normalization.py:54-78``); BF16 CUDA
+    activations run on the LayerNorm kernel (strided rows read in place)."""
+    C = x.shape[-1]
+    if x.is_cuda and x.dtype == torch.bfloat16 and C % 8 == 0 and 8 <= C <= 2048:
+        return layer_norm_bf16(x, ln.weight, ln.bias, ln.eps)
     w = None if ln.weight is None else ln.weight.float()
     b = None if ln.bias is None else ln.bias.float()
     return nn.functional.layer_norm(x.float(), ln.normalized_shape, w, b, ln.eps).to(x.dtype)

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), f"{name} not exported"
         assert name in _native.SIGNATURES, f"{name} missing from the ctypes binding"
         assert len(_native.SIGNATURES[name][1]) == nargs, f"{name}: arg count mismatch"
-    assert lib.tpf_abi_version() == 2
+    assert lib.tpf_abi_version() == 3
 
 
 def test_shape_errors_are_reported_without_launch(lib):
@@ -64,6 +64,18 @@ def test_shape_errors_are_reported_without_launch(lib):
         _native.call("tpf_trimul_forward_bf16", *([16] * 12), 1, 1, 64, 48, *([16] * 12), 1 << 20, None)
     with pytest.raises(RuntimeError, match="workspace"):
         _native.call("tpf_attn_backward_bf16", *([16] * 13), 0, 1, 4, 4, 128, 32, 0, 1, 0.2, None)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        _native.call("tpf_layer_norm_forward_bf16", 16, 1, 4, 4, 0, 48, 12, 12, None, None, 1e-5,
+                     16, 16, 16, None)
+    with pytest.raises(RuntimeError, match="strides"):
+        _native.call("tpf_layer_norm_forward_bf16", 16, 1, 4, 4, 0, 20, 5, 16, None, None, 1e-5,
+                     16, 16, 16, None)
+    with pytest.raises(RuntimeError, match="both given or both null"):
+        _native.call("tpf_layer_norm_backward_bf16", 16, 16, 1, 4, 4, 0, 64, 16, 0, 64, 16, 16, 16,
+                     16, None, 16, 16, None, 16, 1 << 20, None)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _native.call("tpf_layer_norm_backward_bf16", 16, 16, 1, 4, 4, 0, 64, 16, 0, 64, 16, 16, 16,
+                     16, None, 16, 16, 16, 16, 8, None)
 
 
 def test_workspace_sizes(lib):
@@ -75,3 +87,7 @@ def test_workspace_sizes(lib):
     assert _native.query("tpf_trimul_plane_pitch", 113) == 120
     assert _native.query("tpf_trimul_plane_pitch", 384) == 384
     assert _native.query("tpf_trimul_backward_workspace_bytes", 1, 384, 128) > 0
+    # LayerNorm parameter partials: at most 2048 workgroups x [dgamma | dbeta]
+    assert _native.query("tpf_layer_norm_backward_workspace_bytes", 384 * 384, 128) == 2048 * 2 * 128 * 4
+    assert _native.query("tpf_layer_norm_backward_workspace_bytes", 16, 128) == 1 * 2 * 128 * 4
+    assert _native.query("tpf_layer_norm_backward_workspace_bytes", 16, 12) == -1
