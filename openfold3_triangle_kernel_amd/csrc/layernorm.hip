@@ -50,6 +50,31 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
   const bool row_ok = row < g.R;
   const int n8 = C / 8;
   const __bf16* xr = x + (row_ok ? ln_row_offset(g, (uint32_t)row) : 0);
+  // The affine parameters are loaded as vectors next to the row, so every
+  // load of the thread is in flight at once.
+  float wv[K][8], bv[K][8];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int ch = k * L + lane;
+    f32x4 w0 = {1.f, 1.f, 1.f, 1.f}, w1 = w0, b0 = {0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (ch < n8) {
+      if (w) {
+        w0 = *(const f32x4*)(w + ch * 8);
+        w1 = *(const f32x4*)(w + ch * 8 + 4);
+      }
+      if (bias) {
+        b0 = *(const f32x4*)(bias + ch * 8);
+        b1 = *(const f32x4*)(bias + ch * 8 + 4);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wv[k][e] = w0[e];
+      wv[k][e + 4] = w1[e];
+      bv[k][e] = b0[e];
+      bv[k][e + 4] = b1[e];
+    }
+  }
   float v[K][8];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -92,13 +117,7 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
     if (ch >= n8) continue;
     bf16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = ch * 8 + e;
-      float t = (v[k][e] - mean) * rstd;
-      if (w) t *= w[c];
-      if (bias) t += bias[c];
-      o[e] = f2bf(t);
-    }
+    for (int e = 0; e < 8; ++e) o[e] = f2bf(fmaf((v[k][e] - mean) * rstd, wv[k][e], bv[k][e]));
     st8(y + row * C + ch * 8, o);
   }
   if (lane == 0) {
@@ -127,59 +146,86 @@ __global__ __launch_bounds__(256) void ln_bwd_bf16_kernel(
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int ch = k * L + lane;
+    f32x4 w0 = {1.f, 1.f, 1.f, 1.f}, w1 = w0;
+    if (w && ch < n8) {
+      w0 = *(const f32x4*)(w + ch * 8);
+      w1 = *(const f32x4*)(w + ch * 8 + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wv[k][e] = w0[e];
+      wv[k][e + 4] = w1[e];
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      wv[k][e] = (w && ch < n8) ? w[ch * 8 + e] : 1.f;
       dgam[k][e] = 0.f;
       dbet[k][e] = 0.f;
     }
   }
-  for (int64_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
-    const int64_t row = grp * RPB + slot;
-    if (row >= gx.R) continue;
-    const __bf16* xr = x + ln_row_offset(gx, (uint32_t)row);
-    const __bf16* dyr = dy + row * C;
-    bf16x8 xt[K], dt[K];
+  // Two row groups per iteration: both rows' loads are issued before either
+  // row's arithmetic.  Rows are still folded into the partials in ascending
+  // group order.
+  for (int64_t grp = blockIdx.x; grp < groups; grp += 2 * (int64_t)gridDim.x) {
+    int64_t rows[2] = {grp * RPB + slot, (grp + gridDim.x) * RPB + slot};
+    bool ok_row[2];
+    bf16x8 xt[2][K], dt[2][K];
+    float mu[2], rs[2];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int ch = k * L + lane;
-      if (ch < n8) {
-        xt[k] = ld8(xr + ch * 8);
-        dt[k] = ld8(dyr + ch * 8);
+    for (int u = 0; u < 2; ++u) {
+      ok_row[u] = (u == 0 || grp + gridDim.x < groups) && rows[u] < gx.R;
+      mu[u] = 0.f;
+      rs[u] = 0.f;
+      if (!ok_row[u]) continue;
+      const __bf16* xr = x + ln_row_offset(gx, (uint32_t)rows[u]);
+      const __bf16* dyr = dy + rows[u] * C;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int ch = k * L + lane;
+        if (ch < n8) {
+          xt[u][k] = ld8(xr + ch * 8);
+          dt[u][k] = ld8(dyr + ch * 8);
+        }
       }
+      mu[u] = mean_in[rows[u]];
+      rs[u] = rstd_in[rows[u]];
     }
-    const float mu = mean_in[row], rs = rstd_in[row];
-    float xh[K][8], gg[K][8];
-    float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const bool ok = k * L + lane < n8;
+    for (int u = 0; u < 2; ++u) {
+      // Lanes of one row share ok_row, so the shuffles below stay within
+      // fully active row groups.
+      if (!ok_row[u]) continue;
+      float xh[K][8], gg[K][8];
+      float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = ok ? bf2f(dt[k][e]) : 0.f;
-        xh[k][e] = ok ? (bf2f(xt[k][e]) - mu) * rs : 0.f;
-        gg[k][e] = d * wv[k][e];
-        s1 += gg[k][e];
-        s2 = fmaf(gg[k][e], xh[k][e], s2);
-        dgam[k][e] = fmaf(d, xh[k][e], dgam[k][e]);
-        dbet[k][e] += d;
+      for (int k = 0; k < K; ++k) {
+        const bool ok = k * L + lane < n8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = ok ? bf2f(dt[u][k][e]) : 0.f;
+          xh[k][e] = ok ? (bf2f(xt[u][k][e]) - mu[u]) * rs[u] : 0.f;
+          gg[k][e] = d * wv[k][e];
+          s1 += gg[k][e];
+          s2 = fmaf(gg[k][e], xh[k][e], s2);
+          dgam[k][e] = fmaf(d, xh[k][e], dgam[k][e]);
+          dbet[k][e] += d;
+        }
       }
-    }
 #pragma unroll
-    for (int m = 1; m < L; m <<= 1) {
-      s1 += __shfl_xor(s1, m);
-      s2 += __shfl_xor(s2, m);
-    }
-    const float m1 = s1 * inv_c, m2 = s2 * inv_c;
-    __bf16* dxr = dx + ln_row_offset(gdx, (uint32_t)row);
+      for (int m = 1; m < L; m <<= 1) {
+        s1 += __shfl_xor(s1, m);
+        s2 += __shfl_xor(s2, m);
+      }
+      const float m1 = s1 * inv_c, m2 = s2 * inv_c;
+      __bf16* dxr = dx + ln_row_offset(gdx, (uint32_t)rows[u]);
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int ch = k * L + lane;
-      if (ch >= n8) continue;
-      bf16x8 o;
+      for (int k = 0; k < K; ++k) {
+        const int ch = k * L + lane;
+        if (ch >= n8) continue;
+        bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = f2bf(rs * (gg[k][e] - m1 - xh[k][e] * m2));
-      st8(dxr + ch * 8, o);
+        for (int e = 0; e < 8; ++e) o[e] = f2bf(rs[u] * (gg[k][e] - m1 - xh[k][e] * m2));
+        st8(dxr + ch * 8, o);
+      }
     }
   }
   if (!want_params) return;
@@ -280,8 +326,8 @@ extern "C" int tpf_layer_norm_forward_bf16(const void* x, int64_t B, int64_t I, 
   LnRows g{};
   if ((rc = ln_rows(B, I, J, sb, si, sj, &g, fn))) return rc;
   if (!(eps > 0.0)) return set_error(TPF_ERR_ARG, "%s: eps must be positive", fn);
-  if (((uintptr_t)x | (uintptr_t)y) % 16 != 0)
-    return set_error(TPF_ERR_ARG, "%s: x and y must be 16-byte aligned", fn);
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) % 16 != 0)
+    return set_error(TPF_ERR_ARG, "%s: x, y, w and b must be 16-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
 #define TPF_LN_FGRID(L) dim3((unsigned)((g.R + 256 / (L) - 1) / (256 / (L))))
 #define TPF_LN_NOSMEM(L) 0
@@ -312,8 +358,8 @@ extern "C" int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64
   LnRows gx{}, gdx{};
   if ((rc = ln_rows(B, I, J, sb, si, sj, &gx, fn))) return rc;
   if ((rc = ln_rows(B, I, J, dsb, dsi, dsj, &gdx, fn))) return rc;
-  if (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) % 16 != 0)
-    return set_error(TPF_ERR_ARG, "%s: x, dy and dx must be 16-byte aligned", fn);
+  if (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx | (uintptr_t)w) % 16 != 0)
+    return set_error(TPF_ERR_ARG, "%s: x, dy, dx and w must be 16-byte aligned", fn);
   const int want = dw != nullptr;
   const int64_t need = tpf_layer_norm_backward_workspace_bytes(gx.R, C);
   if (want && (!workspace || workspace_bytes < need))
