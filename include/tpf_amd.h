@@ -235,6 +235,30 @@ int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64_t B, int64
                                  const float* w, void* dx, float* dw, float* db, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
+/* Attention core of the triangle-attention module over pair rows.  proj
+ * [B, N, N, pitch] bf16 holds, per pair row (i, j), the module's projections
+ * q | k | v | gate (H*D columns each, head-major inside) | pair bias (H) |
+ * pad (pitch a multiple of 8); plane i attends over j.  mask f32 [B, N, N]
+ * additive; transpose_bias selects bias[h, q, k] = proj[b, k, q, 4HD + h]
+ * instead of proj[b, q, k, 4HD + h].  Forward writes o [B, N, N, H*D], lse
+ * [B, N, H, N] f32 and the gated og = o * sigmoid(gate).  Backward takes
+ * d_og and writes the whole projection gradient row into dproj (same
+ * layout as proj, pad columns zeroed).  Replaces the module glue around the
+ * kernel (openfold3/core/model/layers/triangular_attention.py:160-243 with
+ * openfold3/core/model/primitives/attention.py:640-692: q/k/v/gate/bias
+ * projections split into views, gating, and the gradient concatenation). */
+int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H);
+int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
+                               int transpose_bias, void* o, float* lse, void* og, void* workspace,
+                               int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
+                               int64_t D, double scale, void* stream);
+int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D);
+int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
+                                int transpose_bias, const void* o, const float* lse,
+                                const void* d_og, void* dproj, void* workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
+                                int64_t D, double scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,9 @@
 //   Q/K/V  [B, O, H, N, D] with one shared storage order: row stride s_row
 //          between sequence positions and s_head between heads (head-major
 //          s_row = D, s_head = N*D; sequence-major s_row = H*D, s_head = D);
-//          plane stride is always H*N*D.
+//          plane stride s_plane (H*N*D for the standalone op; the pair
+//          projection layout uses N * row pitch, see the tpf_attn_pair_* entry
+//          points).
 //   mask   [B, O, N] f32 additive.    bias [Bb, H, N, N] bf16, Bb in {1, B}.
 //   out    [B, O, N, H, D] bf16.      lse / delta [B, O, H, N] f32.
 // N must be a multiple of 64 (the host pads) and D a multiple of 8, D <= 64.
@@ -30,9 +32,25 @@ namespace tpf {
 struct AttnGeom {
   int B, O, H, N, D;
   int64_t s_row, s_head;   // Q/K/V/dQ/dK/dV element strides
+  int64_t s_plane;         // elements between (b, o) planes of Q/K/V/dQ/dK/dV
   int64_t bias_bstride;    // elements between bias batches (0 = broadcast)
   float scale;             // softmax scale (1/sqrt(D_true))
 };
+
+// Element strides of a pair bias bias[bb, h, q, k]: the standalone op's
+// contiguous [Bb, H, N, N] (s_k = 1), or the pair-bias columns of the
+// projection rows (s_h = 1, s_q / s_k = N * pitch and pitch, swapped for the
+// transposed bias).
+struct BiasView {
+  int64_t s_bb, s_h, s_q, s_k;
+  int H;
+};
+
+__device__ __forceinline__ const __bf16* bias_at(const __bf16* bias, const BiasView& bv,
+                                                 int64_t bh, int64_t q, int64_t k) {
+  const int64_t bb = bh / bv.H, h = bh - bb * bv.H;
+  return bias + bb * bv.s_bb + h * bv.s_h + q * bv.s_q + k * bv.s_k;
+}
 
 // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
 // XCDs (linear id L goes to XCD L % 8), each with its own L2.  Logical tile
@@ -66,7 +84,7 @@ __device__ __forceinline__ bool xcd_tile(int64_t total, int qtiles, int planes, 
 __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* __restrict__ bias,
                                                                  float* __restrict__ out,
                                                                  int64_t items, int N,
-                                                                 float inv_scale) {
+                                                                 float inv_scale, BiasView bv) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
   if (i >= items) return;
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
@@ -77,11 +95,16 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
   const int qb = (int)(hq % (N / 32));
   const int64_t bh = hq / (N / 32);
   const int ql = lane & 31, hl = lane >> 5;
-  const __bf16* src = bias + (bh * N + qb * 32 + ql) * (int64_t)N + kb * 32 + 8 * j + 4 * hl;
-  bf16x4 v = ld4(src);
+  const __bf16* src = bias_at(bias, bv, bh, qb * 32 + ql, kb * 32 + 8 * j + 4 * hl);
   f32x4 o;
+  if (bv.s_k == 1) {
+    const bf16x4 v = ld4(src);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = bf2f(v[e]) * inv_scale;
+    for (int e = 0; e < 4; ++e) o[e] = bf2f(v[e]) * inv_scale;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = bf2f(src[e * bv.s_k]) * inv_scale;
+  }
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
 }
 
@@ -125,7 +148,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
   const bool active = q0 < N;
   const int qi = q0 + ql;
 
-  const int64_t plane_off = (int64_t)plane * g.H * N * D + (int64_t)h * g.s_head;
+  const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
   const __bf16* qb = q + plane_off;
   const __bf16* kb = k + plane_off;
   const __bf16* vb = v + plane_off;
@@ -360,7 +383,7 @@ __global__ __launch_bounds__(256) void attn_bwd_rowprep_kernel(const float* __re
 __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf16* __restrict__ bias,
                                                                      float* __restrict__ out,
                                                                      int64_t items, int N,
-                                                                     float inv_scale) {
+                                                                     float inv_scale, BiasView bv) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
   if (i >= items) return;
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
@@ -371,10 +394,10 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
   const int kb = (int)(bk % nb);
   const int64_t bh = bk / nb;
   const int kl = lane & 31, hl = lane >> 5;
-  const __bf16* src = bias + (bh * N + qb * 32 + 8 * j + 4 * hl) * (int64_t)N + kb * 32 + kl;
+  const __bf16* src = bias_at(bias, bv, bh, qb * 32 + 8 * j + 4 * hl, kb * 32 + kl);
   f32x4 o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = bf2f(src[(int64_t)e * N]) * inv_scale;
+  for (int e = 0; e < 4; ++e) o[e] = bf2f(src[(int64_t)e * bv.s_q]) * inv_scale;
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
 }
 
@@ -464,7 +487,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   const int o = og * kBwdGroup + w;
   const bool active = o < g.O;
   const int plane = b * g.O + (active ? o : 0);
-  const int64_t plane_off = (int64_t)plane * H * N * D + (int64_t)h * g.s_head;
+  const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
   const int key_base = kblk * 64;
   const float c2 = g.scale * kLog2e;
   const float inv_scale = 1.f / g.scale;
@@ -753,7 +776,7 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
   bf16x8 o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
-  st8(dq + plane * g.H * g.N * g.D + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
+  st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
 }
 
 // dBias[bb,h,q,k] (f32) = ascending fold over the bf16 (b, outer group)
@@ -802,6 +825,152 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
   *reinterpret_cast<f32x4*>(d + 4) = hi;
 }
 
+
+// ---------------------------------------------------------------------------
+// Output gate of the pair-row module core.  One thread per (pair row,
+// 8-channel chunk), so consecutive lanes touch consecutive 16 bytes:
+//   forward   og = o * sigmoid(g)
+//   backward  d_o = d_og * sigmoid(g),  dg = d_og * o * s * (1 - s), and
+//             delta[b,i,h,j] = sum_d d_o * o (the softmax backward's row term;
+//             the D/8 chunk partials of a head meet in LDS).
+// o / og / d_og / d_o are [B, N, N, H*D] rows; g and dg sit at the gate
+// columns (offset 3*H*D) of the projection rows (row pitch `pitch`).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gate_sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+
+__global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __restrict__ o,
+                                                            const __bf16* __restrict__ gate,
+                                                            int64_t pitch,
+                                                            __bf16* __restrict__ og,
+                                                            int64_t items, int hc8) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, chunk)
+  if (t >= items) return;
+  const int64_t row = t / hc8;
+  const int c = (int)(t - row * hc8);
+  const bf16x8 ov = ld8(o + t * 8), gv = ld8(gate + row * pitch + c * 8);
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = f2bf(bf2f(ov[e]) * gate_sigmoid(bf2f(gv[e])));
+  st8(og + t * 8, r);
+}
+
+// Workgroup w takes items [w * per, (w + 1) * per) with per a multiple of
+// D/8, so a head's chunks never straddle two workgroups.
+__global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
+    const __bf16* __restrict__ d_og, const __bf16* __restrict__ o,
+    const __bf16* __restrict__ gate, int64_t pitch, __bf16* __restrict__ d_o,
+    float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, int N, int H,
+    int D) {
+  __shared__ float part[256];
+  const int tid = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * per + tid;  // (row, chunk)
+  const int hc8 = H * D / 8, d8 = D / 8;
+  const bool act = tid < per && t < items;
+  float sdot = 0.f;
+  if (act) {
+    const int64_t row = t / hc8;
+    const int c = (int)(t - row * hc8);
+    const bf16x8 dv = ld8(d_og + t * 8), ov = ld8(o + t * 8),
+                 gv = ld8(gate + row * pitch + c * 8);
+    bf16x8 r_do, r_dg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sg = gate_sigmoid(bf2f(gv[e]));
+      const float dd = bf2f(dv[e]), oo = bf2f(ov[e]);
+      r_do[e] = f2bf(dd * sg);
+      r_dg[e] = f2bf(dd * oo * sg * (1.f - sg));
+      // delta pairs the bf16 dO that the backward kernel reads with O.
+      sdot = fmaf(bf2f(r_do[e]), oo, sdot);
+    }
+    st8(d_o + t * 8, r_do);
+    st8(dgate + row * pitch + c * 8, r_dg);
+  }
+  part[tid] = sdot;
+  __syncthreads();
+  if (!act) return;
+  const int64_t row = t / hc8;
+  const int c = (int)(t - row * hc8);
+  if (c % d8 != 0) return;
+  float s = 0.f;
+  for (int u = 0; u < d8; ++u) s += part[tid + u];
+  // row = (b, i, j): plane (b, i), query j; delta is [plane][h][j].
+  const int h = c / d8;
+  const int64_t plane = row / N;
+  const int j = (int)(row - plane * N);
+  delta[(plane * H + h) * N + j] = s;
+}
+
+// Pair-bias gradient into the projection gradient rows: thread = (bias batch
+// bb, query q, 8 consecutive keys); for each head, the bf16 (b, outer group)
+// partials that share bb are folded in ascending order (as in
+// attn_dbias_reduce_kernel), then every key's row receives its H values and
+// zeros over the rest of the row tail [4*H*D, pitch).
+template <int HMAX>
+__global__ __launch_bounds__(256) void attn_dbias_pair_kernel(
+    const __bf16* __restrict__ part, int B, int Bb, int groups, int H, int N,
+    __bf16* __restrict__ dproj, int64_t pitch, int64_t tail_off, int transpose_bias) {
+  const int64_t nn8 = (int64_t)N * N / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)Bb * nn8) return;
+  const int bb = (int)(idx / nn8);
+  const int64_t e = (idx % nn8) * 8;
+  const int q = (int)(e / N), k0 = (int)(e % N);
+  const int b_lo = (Bb == 1) ? 0 : bb, b_hi = (Bb == 1) ? B : bb + 1;
+  const int64_t stride = (int64_t)H * N * N;
+  const int n = (b_hi - b_lo) * groups;
+  float acc[8][HMAX];
+#pragma unroll
+  for (int h = 0; h < HMAX; ++h) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i][h] = 0.f;
+    if (h >= H) continue;
+    const __bf16* src = part + (int64_t)b_lo * groups * stride + (int64_t)h * N * N + e;
+    float a[8];
+    {
+      const bf16x8 x = ld8(src);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = bf2f(x[i]);
+    }
+    int s = 1;
+    for (; s + 4 <= n; s += 4) {
+      bf16x8 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = ld8(src + (int64_t)(s + u) * stride);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] += bf2f(x[u][i]);
+    }
+    for (; s < n; ++s) {
+      const bf16x8 x = ld8(src + (int64_t)s * stride);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += bf2f(x[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i][h] = a[i];
+  }
+  const int tail8 = (int)((pitch - tail_off) / 8);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int k = k0 + i;
+    const int64_t r = (int64_t)bb * N * N + (transpose_bias ? (int64_t)k * N + q : (int64_t)q * N + k);
+    __bf16* dst = dproj + r * pitch + tail_off;
+    for (int c = 0; c < tail8; ++c) {
+      bf16x8 v;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int h = c * 8 + u;
+        float val = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < HMAX; ++hh)
+          if (hh == h) val = acc[i][hh];
+        v[u] = f2bf(val);
+      }
+      st8(dst + c * 8, v);
+    }
+  }
+}
+
 }  // namespace tpf
 
 // ---------------------------------------------------------------------------
@@ -827,6 +996,7 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
   g->B = (int)B; g->O = (int)O; g->H = (int)H; g->N = (int)N; g->D = (int)D;
   g->s_row = seq_major ? H * D : D;
   g->s_head = seq_major ? D : N * D;
+  g->s_plane = H * N * D;
   if (bias_batches != 1 && bias_batches != B)
     return set_error(TPF_ERR_SHAPE, "%s: bias batch count %lld must be 1 or B=%lld", fn,
                      (long long)bias_batches, (long long)B);
@@ -835,62 +1005,45 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
   return check_geom(*g, fn);
 }
 
-extern "C" {
-
-int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N,
-                                         int64_t bias_batches) {
-  (void)B;
-  return bias_batches * H * N * N * 4;
+// Contiguous [Bb, H, N, N] bias.
+static BiasView dense_bias(int64_t H, int64_t N, int64_t bias_batches) {
+  BiasView bv;
+  bv.s_bb = bias_batches == 1 ? 0 : H * N * N;
+  bv.s_h = N * N;
+  bv.s_q = N;
+  bv.s_k = 1;
+  bv.H = (int)H;
+  return bv;
 }
 
-static int attn_prescale_bias(const AttnGeom& g, const void* bias, float* bias_s,
-                              int64_t bias_batches, hipStream_t s, const char* fn) {
+static int attn_prescale_bias(const AttnGeom& g, const void* bias, const BiasView& bv,
+                              float* bias_s, int64_t bias_batches, hipStream_t s,
+                              const char* fn) {
   const int64_t items = bias_batches * g.H * (int64_t)g.N * g.N / 4;
   hipLaunchKernelGGL(attn_bias_prescale_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
-                     0, s, (const __bf16*)bias, bias_s, items, g.N, 1.f / g.scale);
+                     0, s, (const __bf16*)bias, bias_s, items, g.N, 1.f / g.scale, bv);
   return check_launch(fn);
 }
 
-int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
-                          const void* bias, void* out, float* lse, void* workspace,
-                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                          int64_t D, int seq_major, int64_t bias_batches, double scale,
-                          void* stream) {
-  const char* fn = "tpf_attn_forward_bf16";
-  AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
-  if (rc) return rc;
-  if (!q || !k || !v || !mask || !bias || !out || !lse || !workspace)
-    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
-    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
-  const int64_t total = ((N + 127) / 128) * H * B * O;
+static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const void* v,
+                             const float* mask, const void* bias, const BiasView& bv,
+                             int64_t bias_batches, void* out, float* lse, void* workspace,
+                             hipStream_t s, const char* fn) {
+  const int64_t total = ((g.N + 127) / 128) * (int64_t)g.H * g.B * g.O;
   if ((total + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many query tiles", fn);
-  hipStream_t s = (hipStream_t)stream;
   float* bias_s = (float*)workspace;
-  if ((rc = attn_prescale_bias(g, bias, bias_s, bias_batches, s, fn))) return rc;
-  g.bias_bstride = (bias_batches == 1) ? 0 : H * N * N;
+  int rc = attn_prescale_bias(g, bias, bv, bias_s, bias_batches, s, fn);
+  if (rc) return rc;
+  g.bias_bstride = (bias_batches == 1) ? 0 : (int64_t)g.H * g.N * g.N;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
-  if (D <= 32)
+  if (g.D <= 32)
     hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
   else
     hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
   return check_launch(fn);
-}
-
-int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,
-                        int64_t H, int64_t N, int64_t D, void* stream) {
-  if (!dout || !out || !delta) return set_error(TPF_ERR_ARG, "tpf_attn_delta_bf16: null pointer");
-  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 8 || D > 64 || D % 8)
-    return set_error(TPF_ERR_SHAPE, "tpf_attn_delta_bf16: bad shape");
-  const int64_t rows = B * O * N * H;
-  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const __bf16*)dout, (const __bf16*)out, delta, rows,
-                     (int)H, (int)N, (int)D);
-  return check_launch("tpf_attn_delta_bf16");
 }
 
 // Backward workspace: bf16 dQ partials [N/64][B,O,H,N,D] | bf16 dBias
@@ -924,6 +1077,96 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   return off;
 }
 
+static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void* k,
+                                   const void* v, const void* dout, const float* lse,
+                                   const float* delta, const float* mask, const void* bias,
+                                   const BiasView& bv, int64_t bias_batches, void* dk, void* dv,
+                                   void* workspace, hipStream_t s, const char* fn) {
+  const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  if ((H * (N / 64) * B * groups + 7) / 8 * 8 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
+  const int64_t rows = B * O * H * N;
+  hipLaunchKernelGGL(attn_bwd_rowprep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
+                     s, lse, delta, pt.nl2, pt.nd, rows);
+  int rc = check_launch(fn);
+  if (rc) return rc;
+  const int64_t items = bias_batches * H * N * N / 4;
+  hipLaunchKernelGGL(attn_bias_bwd_prescale_kernel, dim3((unsigned)((items + 255) / 256)),
+                     dim3(256), 0, s, (const __bf16*)bias, pt.bias_f, items, (int)N,
+                     1.f / g.scale, bv);
+  if ((rc = check_launch(fn))) return rc;
+  const int64_t total = H * (N / 64) * B * groups;
+  dim3 grid((unsigned)((total + 7) / 8 * 8));
+  if (D <= 32)
+    hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
+  else
+    hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
+                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
+  return check_launch(fn);
+}
+
+static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
+                                     int64_t bias_batches, const void* workspace, hipStream_t s,
+                                     const char* fn) {
+  const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  const int64_t dq_items = B * O * H * N * (D / 8);
+  hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
+                     0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
+  int rc = check_launch(fn);
+  if (rc) return rc;
+  const int64_t db_items = bias_batches * H * N * N / 8;
+  hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
+                     dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
+                     (int)H, (int)N);
+  return check_launch(fn);
+}
+
+extern "C" {
+
+int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N,
+                                         int64_t bias_batches) {
+  (void)B;
+  return bias_batches * H * N * N * 4;
+}
+
+int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
+                          const void* bias, void* out, float* lse, void* workspace,
+                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                          int64_t D, int seq_major, int64_t bias_batches, double scale,
+                          void* stream) {
+  const char* fn = "tpf_attn_forward_bf16";
+  AttnGeom g;
+  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  if (rc) return rc;
+  if (!q || !k || !v || !mask || !bias || !out || !lse || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+                           out, lse, workspace, (hipStream_t)stream, fn);
+}
+
+int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,
+                        int64_t H, int64_t N, int64_t D, void* stream) {
+  if (!dout || !out || !delta) return set_error(TPF_ERR_ARG, "tpf_attn_delta_bf16: null pointer");
+  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 8 || D > 64 || D % 8)
+    return set_error(TPF_ERR_SHAPE, "tpf_attn_delta_bf16: bad shape");
+  const int64_t rows = B * O * N * H;
+  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const __bf16*)dout, (const __bf16*)out, delta, rows,
+                     (int)H, (int)N, (int)D);
+  return check_launch("tpf_attn_delta_bf16");
+}
+
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
                                           int64_t D) {
   return bwd_layout(B, O, H, N, D, nullptr, nullptr);
@@ -942,9 +1185,6 @@ static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const vo
   if (workspace_bytes < need)
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  if ((H * (N / 64) * B * groups + 7) / 8 * 8 > INT32_MAX)
-    return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
   return TPF_OK;
 }
 
@@ -962,30 +1202,9 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                             workspace_bytes, B, O, H, N, D, seq_major, bias_batches, scale);
   if (rc) return rc;
   if (!dk || !dv) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  BwdParts pt;
-  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t rows = B * O * H * N;
-  hipLaunchKernelGGL(attn_bwd_rowprep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
-                     s, lse, delta, pt.nl2, pt.nd, rows);
-  if ((rc = check_launch(fn))) return rc;
-  const int64_t items = bias_batches * H * N * N / 4;
-  hipLaunchKernelGGL(attn_bias_bwd_prescale_kernel, dim3((unsigned)((items + 255) / 256)),
-                     dim3(256), 0, s, (const __bf16*)bias, pt.bias_f, items, (int)N,
-                     1.f / g.scale);
-  if ((rc = check_launch(fn))) return rc;
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t total = H * (N / 64) * B * groups;
-  dim3 grid((unsigned)((total + 7) / 8 * 8));
-  if (D <= 32)
-    hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
-  else
-    hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
-  return check_launch(fn);
+  return attn_backward_main_impl(g, q, k, v, dout, lse, delta, mask, bias,
+                                 dense_bias(H, N, bias_batches), bias_batches, dk, dv, workspace,
+                                 (hipStream_t)stream, fn);
 }
 
 // Stage 2 of the backward: fixed-order folds of the dQ and dBias partials.
@@ -997,19 +1216,8 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
   int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
   if (rc) return rc;
   if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  BwdParts pt;
-  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t dq_items = B * O * H * N * (D / 8);
-  hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
-                     0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
-  if ((rc = check_launch(fn))) return rc;
-  const int64_t db_items = bias_batches * H * N * N / 8;
-  hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
-                     dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
-                     (int)H, (int)N);
-  return check_launch(fn);
+  return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, (hipStream_t)stream,
+                                   fn);
 }
 
 int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
@@ -1025,6 +1233,123 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
   if (rc) return rc;
   return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, seq_major,
                                        bias_batches, scale, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Pair-row entry points: the attention core of the triangle-attention module
+// over one projection buffer proj [B, N, N, pitch] (row = pair (i, j)) whose
+// columns are q | k | v | gate (H*D each) | pair bias (H) | pad.
+// ---------------------------------------------------------------------------
+
+static int pair_geom(AttnGeom* g, BiasView* bv, int64_t pitch, int transpose_bias, int64_t B,
+                     int64_t N, int64_t H, int64_t D, double scale, const char* fn) {
+  int rc = make_geom(g, B, N, H, N, D, 1, B, scale, fn);
+  if (rc) return rc;
+  const int64_t hc = H * D;
+  if (pitch < 4 * hc + H || pitch % 8 != 0)
+    return set_error(TPF_ERR_SHAPE, "%s: pitch %lld must be a multiple of 8 >= 4*H*D + H", fn,
+                     (long long)pitch);
+  if (H > 16) return set_error(TPF_ERR_SHAPE, "%s: H=%lld exceeds 16", fn, (long long)H);
+  g->s_row = pitch;
+  g->s_head = D;
+  g->s_plane = N * pitch;
+  bv->s_bb = N * N * pitch;
+  bv->s_h = 1;
+  bv->s_q = transpose_bias ? pitch : N * pitch;
+  bv->s_k = transpose_bias ? N * pitch : pitch;
+  bv->H = (int)H;
+  return TPF_OK;
+}
+
+int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H) {
+  return B * H * N * N * 4;
+}
+
+int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
+                               int transpose_bias, void* o, float* lse, void* og, void* workspace,
+                               int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
+                               int64_t D, double scale, void* stream) {
+  const char* fn = "tpf_attn_pair_forward_bf16";
+  AttnGeom g;
+  BiasView bv;
+  int rc = pair_geom(&g, &bv, pitch, transpose_bias, B, N, H, D, scale, fn);
+  if (rc) return rc;
+  if (!proj || !mask || !o || !lse || !og || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if ((uintptr_t)proj % 16 || (uintptr_t)o % 16 || (uintptr_t)og % 16)
+    return set_error(TPF_ERR_ARG, "%s: proj, o and og must be 16-byte aligned", fn);
+  if (workspace_bytes < tpf_attn_pair_forward_workspace_bytes(B, N, H))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  const int64_t hc = H * D;
+  const __bf16* p = (const __bf16*)proj;
+  hipStream_t s = (hipStream_t)stream;
+  if ((rc = attn_forward_impl(g, p, p + hc, p + 2 * hc, mask, p + 4 * hc, bv, B, o, lse,
+                              workspace, s, fn)))
+    return rc;
+  const int64_t items = B * N * N * (hc / 8);
+  hipLaunchKernelGGL(attn_gate_fwd_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
+                     (const __bf16*)o, p + 3 * hc, pitch, (__bf16*)og, items, (int)(hc / 8));
+  return check_launch(fn);
+}
+
+// Workspace: the attention backward's, then d_o [B, N, N, H*D] bf16 and
+// delta [B, N, H, N] f32.
+int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D) {
+  return bwd_layout(B, N, H, N, D, nullptr, nullptr) + a256(B * N * N * H * D * 2) +
+         a256(B * N * H * N * 4);
+}
+
+int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
+                                int transpose_bias, const void* o, const float* lse,
+                                const void* d_og, void* dproj, void* workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
+                                int64_t D, double scale, void* stream) {
+  const char* fn = "tpf_attn_pair_backward_bf16";
+  AttnGeom g;
+  BiasView bv;
+  int rc = pair_geom(&g, &bv, pitch, transpose_bias, B, N, H, D, scale, fn);
+  if (rc) return rc;
+  if (!proj || !mask || !o || !lse || !d_og || !dproj || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (((uintptr_t)proj | (uintptr_t)o | (uintptr_t)d_og | (uintptr_t)dproj) % 16)
+    return set_error(TPF_ERR_ARG, "%s: proj, o, d_og and dproj must be 16-byte aligned", fn);
+  if (workspace_bytes < tpf_attn_pair_backward_workspace_bytes(B, N, H, D))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  const int64_t hc = H * D;
+  const int64_t main_bytes = bwd_layout(B, N, H, N, D, nullptr, nullptr);
+  __bf16* d_o = (__bf16*)((char*)workspace + main_bytes);
+  float* delta = (float*)((char*)workspace + main_bytes + a256(B * N * N * hc * 2));
+  const __bf16* p = (const __bf16*)proj;
+  __bf16* dp = (__bf16*)dproj;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t items = B * N * N * (hc / 8);
+  const int per = 256 - 256 % (int)(D / 8);
+  hipLaunchKernelGGL(attn_gate_bwd_kernel, dim3((unsigned)((items + per - 1) / per)), dim3(256), 0,
+                     s, (const __bf16*)d_og, (const __bf16*)o, p + 3 * hc, pitch, d_o, delta,
+                     dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
+  if ((rc = check_launch(fn))) return rc;
+  if ((rc = attn_backward_main_impl(g, p, p + hc, p + 2 * hc, d_o, lse, delta, mask, p + 4 * hc,
+                                    bv, B, dp + hc, dp + 2 * hc, workspace, s, fn)))
+    return rc;
+  BwdParts pt;
+  bwd_layout(B, N, H, N, D, (char*)workspace, &pt);
+  const int64_t dq_items = B * N * H * N * (D / 8);
+  hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
+                     0, s, pt.dq, dp, g, (int)(N / 64));
+  if ((rc = check_launch(fn))) return rc;
+  const int64_t groups = (N + kBwdGroup - 1) / kBwdGroup;
+  const int64_t db_items = B * N * N / 8;
+  const dim3 db_grid((unsigned)((db_items + 255) / 256));
+  if (H <= 4)
+    hipLaunchKernelGGL(attn_dbias_pair_kernel<4>, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
+                       (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
+  else if (H <= 8)
+    hipLaunchKernelGGL(attn_dbias_pair_kernel<8>, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
+                       (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
+  else
+    hipLaunchKernelGGL(attn_dbias_pair_kernel<16>, db_grid, dim3(256), 0, s, pt.db, (int)B,
+                       (int)B, (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
+  return check_launch(fn);
 }
 
 }  // extern "C"

@@ -25,6 +25,7 @@ reference's ``use_stable_*`` path does (``attention.py:640-692``,
 
 from __future__ import annotations
 
+import math
 
 import torch
 from torch import nn
@@ -53,6 +54,83 @@ def _fp32_inference(x: torch.Tensor) -> bool:
     return x.dtype == torch.float32 and not torch.is_grad_enabled()
 
 
+def _wgrad(dy2: torch.Tensor, x2: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """dW = dy2^T x2 over all rows on the split-K MFMA GEMM (f32 accumulate)."""
+    R, M = dy2.shape
+    K = x2.shape[1]
+    dw32 = torch.empty((M, K), device=x2.device, dtype=torch.float32)
+    ws_bytes = int(_native.query("tpf_wgrad_bf16_workspace_bytes", R, M, K))
+    ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8)
+    with _device_ctx(x2.device):
+        _native.call("tpf_wgrad_bf16", dy2.data_ptr(), dy2.stride(0), x2.data_ptr(),
+                     x2.stride(0), R, M, K, dw32.data_ptr(), ws.data_ptr(), ws_bytes,
+                     _native.stream_of(x2))
+    return dw32.to(dtype)
+
+
+class _PairAttentionCore(torch.autograd.Function):
+    """Projection -> triangle attention -> gate -> output projection of the
+    triangle-attention module over BF16 pair rows, with explicit buffers.
+
+    One GEMM forms proj [R, P] = x W_all^T (columns q | k | v | gate | bias |
+    pad); ``tpf_attn_pair_forward_bf16`` reads q / k / v and the pair bias
+    from it in place and writes o and og = o * sigmoid(gate); out = og W_o^T.
+    The backward's ``tpf_attn_pair_backward_bf16`` writes every column of the
+    projection gradient row (gate, q, k, v, bias, zeroed pad) into one
+    buffer, so dx = dproj W_all and dW_all = dproj^T x are single GEMMs.
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_all, w_o, mask_add, H, D, transpose_bias):
+        B, N, _, C = x.shape
+        P = w_all.shape[0]
+        R, hc = B * N * N, H * D
+        dev = x.device
+        x2 = x.reshape(R, C)
+        wa = w_all.to(torch.bfloat16)
+        wo = w_o.to(torch.bfloat16)
+        proj = x2 @ wa.t()
+        o = torch.empty((R, hc), device=dev, dtype=torch.bfloat16)
+        og = torch.empty_like(o)
+        lse = torch.empty((B, N, H, N), device=dev, dtype=torch.float32)
+        ws_bytes = int(_native.query("tpf_attn_pair_forward_workspace_bytes", B, N, H))
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        scale = 1.0 / math.sqrt(D)
+        with _device_ctx(dev):
+            _native.call("tpf_attn_pair_forward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
+                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), og.data_ptr(),
+                         ws.data_ptr(), ws_bytes, B, N, H, D, scale, _native.stream_of(proj))
+        out = og @ wo.t()
+        ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add)
+        ctx.dims = (B, N, H, D, C, P, bool(transpose_bias), scale)
+        ctx.w_dtypes = (w_all.dtype, w_o.dtype)
+        ctx.set_materialize_grads(False)
+        return out.view(B, N, N, C)
+
+    @staticmethod
+    def backward(ctx, dout):
+        if dout is None:
+            return (None,) * 7
+        x2, wa, wo, proj, o, og, lse, mask_add = ctx.saved_tensors
+        B, N, H, D, C, P, transpose_bias, scale = ctx.dims
+        R = B * N * N
+        dev = x2.device
+        dout2 = dout.reshape(R, C).to(torch.bfloat16).contiguous()
+        d_og = dout2 @ wo
+        dw_o = _wgrad(dout2, og, ctx.w_dtypes[1]) if ctx.needs_input_grad[2] else None
+        dproj = torch.empty((R, P), device=dev, dtype=torch.bfloat16)
+        ws_bytes = int(_native.query("tpf_attn_pair_backward_workspace_bytes", B, N, H, D))
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        with _device_ctx(dev):
+            _native.call("tpf_attn_pair_backward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
+                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), d_og.data_ptr(),
+                         dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
+                         _native.stream_of(dproj))
+        dx = (dproj @ wa).view(B, N, N, C) if ctx.needs_input_grad[0] else None
+        dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None
+        return dx, dw_all, dw_o, None, None, None, None
+
+
 class _ProjLinear(torch.autograd.Function):
     """y = x W^T for BF16 activations over B*N^2 rows, whose weight gradient
     dW = dy^T x (K = rows) runs on the split-K MFMA GEMM (tpf_wgrad_bf16)."""
@@ -73,15 +151,7 @@ class _ProjLinear(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             M, K = wb.shape
             dy2 = dy.reshape(-1, M).to(torch.bfloat16).contiguous()
-            x2 = x.reshape(-1, K).contiguous()
-            R = x2.shape[0]
-            dw32 = torch.empty((M, K), device=x.device, dtype=torch.float32)
-            ws_bytes = int(_native.query("tpf_wgrad_bf16_workspace_bytes", R, M, K))
-            ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
-            with _device_ctx(x.device):
-                _native.call("tpf_wgrad_bf16", dy2.data_ptr(), M, x2.data_ptr(), K, R, M, K,
-                             dw32.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(x2))
-            dw = dw32.to(ctx.w_dtype)
+            dw = _wgrad(dy2, x.reshape(-1, K).contiguous(), ctx.w_dtype)
         return dx, dw
 
 
@@ -136,13 +206,30 @@ class TriangleAttention(nn.Module):
         mask_bias = (self.inf * (mask.float() - 1))[..., :, None, None, :]
         m = self.mha
         H, c = m.no_heads, m.c_hidden
-        # One projection GEMM for q, k, v, the gate and the pair bias (rows
-        # padded to a multiple of 8; the pad outputs are unused).
+        # One projection GEMM for q, k, v, the gate and the pair bias.  Rows are
+        # padded to a multiple of 64 outputs (128-byte aligned projection rows
+        # for the pair-row core) or of 8 (per-projection route); the pad
+        # outputs are unused.
         hc = H * c
-        pad = (-(4 * hc + H)) % 8
+        prefix = x.shape[:-3]
+        N = x.shape[-2]
+        pair_core = (x.dtype == torch.bfloat16 and x.is_cuda and x.shape[-3] == N
+                     and N % 64 == 0 and c % 8 == 0 and 8 <= c <= 64 and H <= 16
+                     and self.c_in % 8 == 0 and x.numel() > 0)
+        pad = (-(4 * hc + H)) % (64 if pair_core else 8)
         w_all = torch.cat([m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
                            m.linear_g.weight, self.linear_z.weight]
                           + ([self.linear_z.weight.new_zeros(pad, self.c_in)] if pad else []))
+        if pair_core:
+            B = math.prod(prefix)
+            mask_add = mask_bias.reshape(B, N, N).contiguous()
+            out = _PairAttentionCore.apply(x.reshape(B, N, N, self.c_in), w_all,
+                                           m.linear_o.weight, mask_add, H, c,
+                                           bool(transpose_bias))
+            out = out.reshape(x.shape)
+            if not self.starting:
+                out = out.transpose(-2, -3)
+            return out
         proj = _linear(x, w_all)
         # split (not slicing): its backward is one concatenation of the part
         # gradients instead of a zero-filled full-size buffer per part.
