@@ -34,13 +34,26 @@ __all__ += ["run_trimul_fp32"]
 
 from .modules import (  # noqa: E402
     TriangleAttention,
+    TriangleAttentionEndingNode,
+    TriangleAttentionStartingNode,
     TriangleMultiplicationIncoming,
     TriangleMultiplicationOutgoing,
     TriangleMultiplicativeUpdate,
 )
 
-__all__ += ["TriangleAttention", "TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing",
+__all__ += ["TriangleAttention", "TriangleAttentionEndingNode", "TriangleAttentionStartingNode",
+            "TriangleMultiplicationIncoming", "TriangleMultiplicationOutgoing",
             "TriangleMultiplicativeUpdate"]
+
+from .routing import (  # noqa: E402
+    set_tpf_bf16_cast_for_fp32_training,
+    set_turbopairformer_strict,
+    stock_invocation_count,
+    turbopairformer_strict_enabled,
+)
+
+__all__ += ["set_tpf_bf16_cast_for_fp32_training", "set_turbopairformer_strict",
+            "stock_invocation_count", "turbopairformer_strict_enabled"]
 
 from .layernorm import layer_norm_bf16  # noqa: E402
 

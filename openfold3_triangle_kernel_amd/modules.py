@@ -1,26 +1,37 @@
 """Drop-in OpenFold3 pair-stack modules backed by the MI355X kernels.
 
-``TriangleAttention`` and ``TriangleMultiplicativeUpdate`` (with the
-``TriangleMultiplicationOutgoing`` / ``Incoming`` subclasses) register the
+``TriangleAttention`` (``TriangleAttentionStartingNode`` /
+``TriangleAttentionEndingNode``) and ``TriangleMultiplicativeUpdate`` (with
+the ``TriangleMultiplicationOutgoing`` / ``Incoming`` subclasses) register the
 same parameters under the same names as OpenFold3's modules
 (``openfold3/core/model/layers/triangular_attention.py:35-75`` with the
 ``Attention`` primitive of ``openfold3/core/model/primitives/attention.py``,
 and ``openfold3/core/model/layers/triangular_multiplicative_update.py:700-830``),
-so a ``state_dict`` of the stock module loads unchanged.  Their forward
-passes follow the stock modules' math and route the hot op the way the
-reference's ``use_stable_*`` path does (``attention.py:640-692``,
-``triangular_multiplicative_update.py:62-120``):
+so a ``state_dict`` of the stock module loads unchanged, and take the same
+forward arguments (``triangular_attention.py:245-258``,
+``triangular_multiplicative_update.py:1187-1197``).  Routing follows the
+reference's ``use_stable_*`` policy (``attention.py:520-692``,
+``triangular_multiplicative_update.py:62-120``), with the stable kernels
+selected by default here:
 
-* attention: LayerNorm (statistics in FP32; the BF16 LayerNorm kernel), the additive mask
-  ``inf * (mask - 1)``, one fused projection GEMM for q / k / v, the gate
-  and the pair bias ``linear_z`` (raw, unscaled q / k / v handed to the
-  kernel as sequence-major views), the triangle-attention kernel, sigmoid
-  gate and ``linear_o``; the projection weight gradients (a contraction
-  over all B*N^2 pair rows) run on the split-K MFMA GEMM.  BF16 kernels whenever gradients
-  are recorded or the activations are BF16; FP32 activations under
-  ``torch.no_grad()`` take the FP32 inference kernel.
-* TriMul: ``run_stable_trimul`` (BF16 kernels, autograd) or, for FP32
-  activations under ``torch.no_grad()``, ``run_trimul_fp32``.
+* attention, stable: LayerNorm (FP32 statistics; the BF16 LayerNorm kernel),
+  the additive mask ``inf * (mask - 1)``, one projection GEMM for q / k / v,
+  the gate and the pair bias ``linear_z``; for N a multiple of 64 the
+  pair-row core (``tpf_attn_pair_*``: attention and gate read the projection
+  rows in place, gradients land in one projection-gradient buffer), else the
+  triangle-attention facade on sequence-major views; ``linear_o``.  The
+  projection weight gradients (contractions over all B*N^2 pair rows) run on
+  the split-K MFMA GEMM.  FP32 activations under ``torch.no_grad()`` take
+  the FP32 inference kernel; FP32 training inputs take the stock FP32 math
+  unless ``set_tpf_bf16_cast_for_fp32_training(True)``.
+* TriMul, stable: ``run_trimul_fp32`` for FP32 inference, else
+  ``run_stable_trimul`` (BF16 kernels, autograd) when
+  ``check_stable_trimul_support`` accepts the module.
+* An unsupported stable request raises under strict mode and otherwise logs
+  once and runs the stock PyTorch math (``routing.py``);
+  ``use_stable_*=False`` selects the stock math directly.  The reference's
+  other backends (DeepSpeed, cuEquivariance, Triton, LMA, Protenix) do not
+  exist in this build and raise.
 """
 
 from __future__ import annotations
@@ -30,12 +41,34 @@ import math
 import torch
 from torch import nn
 
-from . import _native
-from .attention import _device_ctx, turbopairformer_triangle_attention
+from . import _native, routing
+from .attention import _device_ctx, is_turbopairformer_supported, turbopairformer_triangle_attention
 from .attention_fp32 import turbopairformer_attention_fp32
 from .layernorm import layer_norm_bf16
-from .trimul import run_stable_trimul
+from .trimul import check_stable_trimul_support, run_stable_trimul
 from .trimul_fp32 import run_trimul_fp32
+
+
+def _reject_backends(**flags) -> None:
+    for name, value in flags.items():
+        if value:
+            raise ValueError(f"{name} is not available in this build (MI355X kernels only)")
+
+
+def _fp32_compute(x: torch.Tensor) -> bool:
+    return x.dtype == torch.float32 and (
+        not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") == torch.float32)
+
+
+def _stock_layer_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
+    w = None if ln.weight is None else ln.weight.float()
+    b = None if ln.bias is None else ln.bias.float()
+    return nn.functional.layer_norm(x.float(), ln.normalized_shape, w, b, ln.eps).to(x.dtype)
+
+
+def _stock_linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    b = None if layer.bias is None else layer.bias.to(x.dtype)
+    return nn.functional.linear(x, layer.weight.to(x.dtype), b)
 
 
 def _layer_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
@@ -195,13 +228,83 @@ class TriangleAttention(nn.Module):
         self.mha = _MHA(c_in, c_hidden, no_heads)
 
     def forward(self, x: torch.Tensor, mask: torch.Tensor | None = None,
-                transpose_bias: bool = False) -> torch.Tensor:
-        """x: [*, I, J, C_in]; mask: [*, I, J] (1 keep, 0 drop)."""
+                transpose_bias: bool = False, chunk_size: int | None = None,
+                use_deepspeed_evo_attention: bool = False,
+                use_cueq_triangle_kernels: bool = False,
+                use_triton_triangle_kernels: bool = False,
+                use_stable_triangle_attention: bool = True, use_lma: bool = False,
+                inplace_safe: bool = False,
+                use_protenix_triangle_attention: bool = False) -> torch.Tensor:
+        """x: [*, I, J, C_in]; mask: [*, I, J] (1 keep, 0 drop).
+
+        ``chunk_size`` and ``inplace_safe`` only bound memory in the reference;
+        one MI355X holds the whole problem, so both are accepted and unused.
+        """
+        _reject_backends(use_deepspeed_evo_attention=use_deepspeed_evo_attention,
+                         use_cueq_triangle_kernels=use_cueq_triangle_kernels,
+                         use_triton_triangle_kernels=use_triton_triangle_kernels,
+                         use_lma=use_lma,
+                         use_protenix_triangle_attention=use_protenix_triangle_attention)
         if mask is None:
             mask = x.new_ones(x.shape[:-1])
         if not self.starting:
             x = x.transpose(-2, -3)
             mask = mask.transpose(-1, -2)
+        if self._stable_route(x, use_stable_triangle_attention):
+            out = self._stable_forward(x, mask, transpose_bias)
+        else:
+            out = self._stock_forward(x, mask, transpose_bias)
+        if not self.starting:
+            out = out.transpose(-2, -3)
+        return out
+
+    def _stable_route(self, x: torch.Tensor, use_stable: bool) -> bool:
+        """The reference's route choice (``attention.py:520-595``)."""
+        if not use_stable:
+            return False
+        native_fp32_inference = _fp32_inference(x)
+        if _fp32_compute(x) and not native_fp32_inference and \
+                not routing.tpf_bf16_cast_for_fp32_training():
+            return False
+        reasons = []
+        if not x.is_cuda:
+            reasons.append("requires GPU inputs")
+        if self.c_hidden > 64:
+            reasons.append("head dimension exceeds 64")
+        if x.shape[-2] < (1 if native_fp32_inference else 2):
+            reasons.append("sequence length is below 2")
+        if reasons:
+            if native_fp32_inference:
+                raise ValueError("unsupported TurboPairFormer FP32 inference attention: "
+                                 + "; ".join(reasons))
+            routing.report_fallback(type(self).__qualname__, tuple(x.shape), "; ".join(reasons))
+            return False
+        return True
+
+    def _stock_forward(self, x, mask, transpose_bias):
+        """The stock module math (``triangular_attention.py:352-409`` with
+        ``Attention._prep_qkv`` / ``_wrap_up``): softmax in FP32."""
+        routing.note_stock_call()
+        m = self.mha
+        H, c = m.no_heads, m.c_hidden
+        x = _stock_layer_norm(self.layer_norm, x)
+        mask_bias = (self.inf * (mask.to(x.dtype) - 1))[..., :, None, None, :]
+        zb = _stock_linear(self.linear_z, x)
+        tri = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in
+                                                  ((-1, -2, -3) if transpose_bias else (-1, -3, -2))))
+        tri = tri.unsqueeze(-4)
+
+        def heads(t):
+            return t.reshape(t.shape[:-1] + (H, c)).transpose(-2, -3)
+
+        q = heads(_stock_linear(m.linear_q, x)) / math.sqrt(c)
+        k, v = heads(_stock_linear(m.linear_k, x)), heads(_stock_linear(m.linear_v, x))
+        s = (q @ k.transpose(-1, -2)).float() + mask_bias.float() + tri.float()
+        o = (torch.softmax(s, -1).to(v.dtype) @ v).transpose(-2, -3)
+        g = torch.sigmoid(_stock_linear(m.linear_g, x)).reshape(o.shape)
+        return _stock_linear(m.linear_o, (o * g).flatten(-2))
+
+    def _stable_forward(self, x, mask, transpose_bias):
         x = _layer_norm(self.layer_norm, x)
         mask_bias = (self.inf * (mask.float() - 1))[..., :, None, None, :]
         m = self.mha
@@ -226,10 +329,7 @@ class TriangleAttention(nn.Module):
             out = _PairAttentionCore.apply(x.reshape(B, N, N, self.c_in), w_all,
                                            m.linear_o.weight, mask_add, H, c,
                                            bool(transpose_bias))
-            out = out.reshape(x.shape)
-            if not self.starting:
-                out = out.transpose(-2, -3)
-            return out
+            return out.reshape(x.shape)
         proj = _linear(x, w_all)
         # split (not slicing): its backward is one concatenation of the part
         # gradients instead of a zero-filled full-size buffer per part.
@@ -244,15 +344,35 @@ class TriangleAttention(nn.Module):
         if _fp32_inference(x):
             o = turbopairformer_attention_fp32(q, k, v, mask_bias, tri_bias.float())
         else:
-            o = turbopairformer_triangle_attention(
-                q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
-                tri_bias.to(torch.bfloat16),
-            ).to(x.dtype)
+            args = (q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
+                    tri_bias.to(torch.bfloat16))
+            ok, reason = is_turbopairformer_supported(*args)
+            if not ok:
+                routing.report_fallback(type(self).__qualname__, tuple(q.shape), reason)
+                return self._stock_forward_from_ln(x, mask_bias, tri_bias, q, k, v, gp)
+            o = turbopairformer_triangle_attention(*args).to(x.dtype)
         g = torch.sigmoid(gp).reshape(o.shape)
-        out = _linear((o * g).flatten(-2), m.linear_o.weight)
-        if not self.starting:
-            out = out.transpose(-2, -3)
-        return out
+        return _linear((o * g).flatten(-2), m.linear_o.weight)
+
+    def _stock_forward_from_ln(self, x, mask_bias, tri_bias, q, k, v, gp):
+        """Stock attention on projections already formed (the reference's
+        fallback after a failed support verdict, ``attention.py:675-692``)."""
+        routing.note_stock_call()
+        c = self.mha.c_hidden
+        s = ((q / math.sqrt(c)) @ k.transpose(-1, -2)).float() + mask_bias.float() + tri_bias.float()
+        o = (torch.softmax(s, -1).to(v.dtype) @ v).transpose(-2, -3)
+        g = torch.sigmoid(gp).reshape(o.shape)
+        return _linear((o * g).flatten(-2), self.mha.linear_o.weight)
+
+
+TriangleAttentionStartingNode = TriangleAttention
+
+
+class TriangleAttentionEndingNode(TriangleAttention):
+    """Triangle attention around the ending node (``triangular_attention.py:413``)."""
+
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int, inf: float = 1e9):
+        super().__init__(c_in, c_hidden, no_heads, starting=False, inf=inf)
 
 
 class TriangleMultiplicativeUpdate(nn.Module):
@@ -274,11 +394,44 @@ class TriangleMultiplicativeUpdate(nn.Module):
         self.linear_b_p = nn.Linear(c_z, c_hidden, bias=False)
         self.linear_b_g = nn.Linear(c_z, c_hidden, bias=False)
 
-    def forward(self, z: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
-        """z: [*, N, N, C_z]; mask: [*, N, N]."""
-        if _fp32_inference(z):
-            return run_trimul_fp32(self, z, mask)
-        return run_stable_trimul(self, z, mask)
+    def forward(self, z: torch.Tensor, mask: torch.Tensor | None = None,
+                inplace_safe: bool = False, use_cueq_triangle_kernels: bool = False,
+                use_triton_triangle_kernels: bool = False,
+                use_stable_triangle_multiplicative: bool = True,
+                _add_with_inplace: bool = False,
+                _inplace_chunk_size: int | None = 256) -> torch.Tensor:
+        """z: [*, N, N, C_z]; mask: [*, N, N].  Returns the update; the stock
+        route with ``inplace_safe`` and ``_add_with_inplace`` returns z + update
+        (the reference overwrites z with it)."""
+        _reject_backends(use_cueq_triangle_kernels=use_cueq_triangle_kernels,
+                         use_triton_triangle_kernels=use_triton_triangle_kernels)
+        if use_stable_triangle_multiplicative:
+            # FP32 inference owns the site (triangular_multiplicative_update.py:64-84):
+            # unsupported metadata raises instead of falling back.
+            if z.is_cuda and _fp32_inference(z) and _fp32_compute(z):
+                return run_trimul_fp32(self, z, mask)
+            ok, reason = check_stable_trimul_support(self, z, mask)
+            if ok:
+                return run_stable_trimul(self, z, mask)
+            routing.report_fallback(type(self).__qualname__, tuple(z.shape), reason)
+        out = self._stock_forward(z, mask)
+        if inplace_safe and _add_with_inplace:
+            out = z + out
+        return out
+
+    def _stock_forward(self, z, mask):
+        """The stock module math (``triangular_multiplicative_update.py:1262-1284``)."""
+        routing.note_stock_call()
+        if mask is None:
+            mask = z.new_ones(z.shape[:-1])
+        mask = mask.to(z.dtype).unsqueeze(-1)
+        zl = _stock_layer_norm(self.layer_norm_in, z)
+        a = mask * torch.sigmoid(_stock_linear(self.linear_a_g, zl)) * _stock_linear(self.linear_a_p, zl)
+        b = mask * torch.sigmoid(_stock_linear(self.linear_b_g, zl)) * _stock_linear(self.linear_b_p, zl)
+        eq = "...ikc,...jkc->...ijc" if self._outgoing else "...kic,...kjc->...ijc"
+        x = torch.einsum(eq, a.float(), b.float()).to(z.dtype)
+        x = _stock_layer_norm(self.layer_norm_out, x)
+        return _stock_linear(self.linear_z, x) * torch.sigmoid(_stock_linear(self.linear_g, zl))
 
 
 class TriangleMultiplicationOutgoing(TriangleMultiplicativeUpdate):
@@ -293,6 +446,8 @@ class TriangleMultiplicationIncoming(TriangleMultiplicativeUpdate):
 
 __all__ = [
     "TriangleAttention",
+    "TriangleAttentionEndingNode",
+    "TriangleAttentionStartingNode",
     "TriangleMultiplicationIncoming",
     "TriangleMultiplicationOutgoing",
     "TriangleMultiplicativeUpdate",

@@ -7,6 +7,7 @@ BF16 route (training kernels): max-rel <= 2e-2; FP32 inference route:
 max-rel <= 1e-4 (the snapshots are FP32 CPU outputs).
 """
 
+import math
 from pathlib import Path
 
 import numpy as np
@@ -63,9 +64,20 @@ def test_trimul_module_snapshot_fp32(gpu):
     with torch.no_grad():
         out = m(x.to(gpu), mask.to(gpu).float())
     assert max_rel(out.cpu().numpy(), ref) <= 1e-4
-    # The BF16 training kernels need c_hidden == c_z: this module is rejected loudly.
-    with pytest.raises(ValueError, match="c_hidden == c_z"):
-        m(x.to(gpu).requires_grad_(True), mask.to(gpu).float())
+    # The BF16 training kernels need c_hidden == c_z: this module falls back to
+    # the stock math (logged), or raises under strict mode.
+    from openfold3_triangle_kernel_amd import set_turbopairformer_strict, stock_invocation_count
+
+    before = stock_invocation_count()
+    out_stock = m(x.to(gpu).requires_grad_(True), mask.to(gpu).float())
+    assert stock_invocation_count() == before + 1
+    assert max_rel(out_stock.detach().cpu().numpy(), ref) <= 1e-4
+    set_turbopairformer_strict(True)
+    try:
+        with pytest.raises(RuntimeError, match="c_hidden == c_z"):
+            m(x.to(gpu).requires_grad_(True), mask.to(gpu).float())
+    finally:
+        set_turbopairformer_strict(False)
 
 
 def _stock_triangle_attention(m, x, mask, starting, transpose_bias=False):
@@ -142,17 +154,68 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
         p.requires_grad_(True)
     ref = _stock_triangle_attention(ref_m, xr, mask, starting, transpose_bias)
     ref_grads = torch.autograd.grad(ref, [xr] + list(ref_m.parameters()), dout)
+    from openfold3_triangle_kernel_amd import stock_invocation_count
+
     mb = m.to(torch.bfloat16)
     xb = x.bfloat16().requires_grad_(True)
+    stock_before = stock_invocation_count()
     out = mb(xb, mask.bfloat16(), transpose_bias=transpose_bias)
     assert _graph_has(out, "_PairAttentionCoreBackward") == (N % 64 == 0)
     grads = torch.autograd.grad(out, [xb] + list(mb.parameters()), dout.bfloat16())
     out2 = mb(xb, mask.bfloat16(), transpose_bias=transpose_bias)
     grads2 = torch.autograd.grad(out2, [xb] + list(mb.parameters()), dout.bfloat16())
     assert torch.equal(out, out2) and all(torch.equal(a, b) for a, b in zip(grads, grads2))
+    assert stock_invocation_count() == stock_before  # the kernels ran, never the stock math
     names = ["out", "x"] + [n for n, _ in mb.named_parameters()]
     for name, a, b in zip(names, [out] + list(grads), [ref] + list(ref_grads)):
         err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
         print(f"module starting={starting} N={N} tb={transpose_bias} {name} max-rel {err:.3e}",
               flush=True)
+        assert err <= (2e-2 if name in ("out", "x") else 3e-2), f"{name}: {err:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N", [64, 50])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_module_backward(gpu, outgoing, N):
+    """BF16 TriMul module (run_stable_trimul) forward + input / parameter
+    gradients vs the module's stock math in FP32 on the same bf16-representable
+    weights (LayerNorm affine perturbed from identity): output and input
+    gradient max-rel <= 2e-2, parameter gradients <= 3e-2; bitwise replay;
+    the stock math never runs on the stable route."""
+    from openfold3_triangle_kernel_amd import (
+        TriangleMultiplicationIncoming,
+        TriangleMultiplicationOutgoing,
+        stock_invocation_count,
+    )
+
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    torch.manual_seed(11)
+    m = cls(128, 128)
+    for name, p in m.named_parameters():
+        if p.dim() == 2:
+            p.data = (torch.randn_like(p) / math.sqrt(p.shape[1])).bfloat16().float()
+        else:
+            base = 1.0 if name.endswith("weight") else 0.0
+            p.data = (base + 0.1 * torch.randn_like(p)).bfloat16().float()
+    m = m.to(gpu)
+    x = torch.randn(1, N, N, 128, device=gpu).bfloat16().float()
+    mask = (torch.rand(1, N, N, device=gpu) > 0.1).float()
+    dout = torch.randn(1, N, N, 128, device=gpu).bfloat16().float()
+    xr = x.clone().requires_grad_(True)
+    ref = m(xr, mask, use_stable_triangle_multiplicative=False)
+    ref_grads = torch.autograd.grad(ref, [xr] + list(m.parameters()), dout)
+    mb = m.to(torch.bfloat16)
+    xb = x.bfloat16().requires_grad_(True)
+    before = stock_invocation_count()
+    out = mb(xb, mask.bfloat16())
+    grads = torch.autograd.grad(out, [xb] + list(mb.parameters()), dout.bfloat16())
+    out2 = mb(xb, mask.bfloat16())
+    grads2 = torch.autograd.grad(out2, [xb] + list(mb.parameters()), dout.bfloat16())
+    assert stock_invocation_count() == before
+    assert torch.equal(out, out2) and all(torch.equal(a, b) for a, b in zip(grads, grads2))
+    names = ["out", "x"] + [n for n, _ in mb.named_parameters()]
+    for name, a, b in zip(names, [out] + list(grads), [ref] + list(ref_grads)):
+        err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
+        print(f"trimul module out={outgoing} N={N} {name} max-rel {err:.3e}", flush=True)
         assert err <= (2e-2 if name in ("out", "x") else 3e-2), f"{name}: {err:.3e}"
