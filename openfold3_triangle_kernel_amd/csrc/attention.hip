@@ -454,14 +454,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   constexpr int QDE = 32 * DP;                 // elements of one Q (or dO) tile
   constexpr int QDI = QDE * 2 / 1024;          // 1 KB async loads per Q (or dO) tile
   constexpr int NISSUE = 2 + 2 * QDI + 1;      // async loads per wave per step
-  // Double buffers as distinct objects, so the compiler can tell the
-  // in-flight direct-to-LDS loads of one half from reads of the other.
-  __shared__ __attribute__((aligned(16))) float Bf0[2][1024];          // bias fragments [cb]
-  __shared__ __attribute__((aligned(16))) float Bf1[2][1024];
-  __shared__ __attribute__((aligned(16))) __bf16 QD0[4][2 * QDE];      // [wave] Q | dO rows
-  __shared__ __attribute__((aligned(16))) __bf16 QD1[4][2 * QDE];
-  __shared__ __attribute__((aligned(16))) float RS0[4][64];            // [wave] nl2 | nd
-  __shared__ __attribute__((aligned(16))) float RS1[4][64];
+  // Double buffers [parity]; one loop body serves both parities, so the
+  // resident accumulators keep one register assignment across steps.
+  __shared__ __attribute__((aligned(16))) float Bfb[2][2][1024];       // bias fragments [cb]
+  __shared__ __attribute__((aligned(16))) __bf16 QDb[2][4][2 * QDE];   // [wave] Q | dO rows
+  __shared__ __attribute__((aligned(16))) float RSb[2][4][64];         // [wave] nl2 | nd
   constexpr int SSE = 64 * (KT > SP ? KT : SP);  // dS^T tile, or the K tile at setup
   __shared__ __attribute__((aligned(16))) __bf16 dSs[4][SSE];
 
@@ -494,13 +491,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   __bf16* Ss = dSs[w];
 
   // Zero the Q / dO buffers once: chunks past D are never loaded.
-  for (int i = tid; i < 4 * 2 * QDE / 8; i += 256) {
-    reinterpret_cast<bf16x8*>(&QD0[0][0])[i] = zero8();
-    reinterpret_cast<bf16x8*>(&QD1[0][0])[i] = zero8();
-  }
+  for (int i = tid; i < 2 * 4 * 2 * QDE / 8; i += 256)
+    reinterpret_cast<bf16x8*>(&QDb[0][0][0])[i] = zero8();
   if (!active) {  // statistics of an idle wave: P = 0 everywhere
-    RS0[w][lane] = lane < 32 ? -INFINITY : 0.f;
-    RS1[w][lane] = lane < 32 ? -INFINITY : 0.f;
+    RSb[0][w][lane] = lane < 32 ? -INFINITY : 0.f;
+    RSb[1][w][lane] = lane < 32 ? -INFINITY : 0.f;
   }
 
   // Per-wave constant operands for this key block.
@@ -717,10 +712,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       for (int e = 0; e < 8; ++e) dst[(int64_t)e * N] = f2bf(acc[e]);
     }
   };
-  issue(0, Bf0, QD0, RS0);
-  for (int q0 = 0; q0 < N; q0 += 64) {
-    step(q0, Bf0, QD0, RS0, Bf1, QD1, RS1);
-    step(q0 + 32, Bf1, QD1, RS1, Bf0, QD0, RS0);
+  issue(0, Bfb[0], QDb[0], RSb[0]);
+#pragma unroll 1
+  for (int q0 = 0; q0 < N; q0 += 32) {
+    const int cur = (q0 >> 5) & 1;
+    step(q0, Bfb[cur], QDb[cur], RSb[cur], Bfb[cur ^ 1], QDb[cur ^ 1], RSb[cur ^ 1]);
   }
   if (!active) return;
   // dK (scaled) and dV, in Q/K/V storage order.
