@@ -336,27 +336,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
 
 // ---------------------------------------------------------------------------
 // delta[b,o,h,q] = sum_d f32(dO) * f32(O), both [B,O,N,H,D] contiguous.
-// One thread per (plane, q, h) row; rows of one (plane, q) are adjacent.
+// One thread per (row, 8-channel chunk), rows r = (plane, q, h): consecutive
+// lanes read consecutive 16 bytes.  A row's D/8 chunk products meet in LDS
+// (workgroup w takes items [w * per, (w + 1) * per), per a multiple of D/8)
+// and are added in chunk order.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void attn_delta_kernel(
     const __bf16* __restrict__ dout, const __bf16* __restrict__ out,
-    float* __restrict__ delta, int64_t rows, int H, int N, int D) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const __bf16* a = dout + r * D;
-  const __bf16* o = out + r * D;
+    float* __restrict__ delta, int64_t items, int per, int H, int N, int D) {
+  __shared__ float part[256];
+  const int tid = threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * per + tid;
+  const bool act = tid < per && t < items;
   float s = 0.f;
-  for (int d = 0; d < D; d += 8) {
-    bf16x8 x = ld8(a + d), y = ld8(o + d);
+  if (act) {
+    const bf16x8 x = ld8(dout + t * 8), y = ld8(out + t * 8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) s = fmaf(bf2f(x[e]), bf2f(y[e]), s);
   }
+  part[tid] = s;
+  __syncthreads();
+  const int d8 = D / 8;
+  if (!act || (t % d8) != 0) return;
+  float acc = 0.f;
+  for (int u = 0; u < d8; ++u) acc += part[tid + u];
   // r enumerates [plane][q][h]; delta is [plane][h][q].
+  const int64_t r = t / d8;
   const int hh = (int)(r % H);
   const int64_t pq = r / H;
   const int qq = (int)(pq % N);
   const int64_t plane = pq / N;
-  delta[(plane * H + hh) * N + qq] = s;
+  delta[(plane * H + hh) * N + qq] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -1156,10 +1166,11 @@ int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t
   if (!dout || !out || !delta) return set_error(TPF_ERR_ARG, "tpf_attn_delta_bf16: null pointer");
   if (B < 1 || O < 1 || H < 1 || N < 1 || D < 8 || D > 64 || D % 8)
     return set_error(TPF_ERR_SHAPE, "tpf_attn_delta_bf16: bad shape");
-  const int64_t rows = B * O * N * H;
-  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, (const __bf16*)dout, (const __bf16*)out, delta, rows,
-                     (int)H, (int)N, (int)D);
+  const int64_t items = B * O * N * H * (D / 8);
+  const int per = 256 - 256 % (int)(D / 8);
+  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((items + per - 1) / per)), dim3(256), 0,
+                     (hipStream_t)stream, (const __bf16*)dout, (const __bf16*)out, delta, items,
+                     per, (int)H, (int)N, (int)D);
   return check_launch("tpf_attn_delta_bf16");
 }
 
