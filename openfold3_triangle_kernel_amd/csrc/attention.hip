@@ -546,22 +546,43 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   typedef float BfT[2][1024];
   typedef __bf16 QDT[4][2 * QDE];
   typedef float RST[4][64];
+  // bf16 pair (1, 0) for the dBias sum, materialised in a register: as an
+  // operand of v_dot2c_f32_bf16 the compiler would encode it as the inline
+  // constant 1.0, which the hardware reads as the f32 pattern 0x3f800000,
+  // i.e. the pair (0, 1).
+  uint32_t sel_lo_bits;
+  asm volatile("v_mov_b32 %0, 0x3f80" : "=v"(sel_lo_bits));
+  // Buffer loads with per-lane byte offsets fixed for the whole walk; each
+  // step advances only a scalar offset.  Lanes past D and the lanes of an
+  // idle wave read zeros (kBufOOB).
+  const i32x4 rs_bias = buffer_rsrc(bfrag);
+  const i32x4 rs_q = buffer_rsrc(q + plane_off);
+  const i32x4 rs_do = buffer_rsrc(dout + do_plane);
+  uint32_t vb[2], vq[QDI], vdo[QDI];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int kbx = 2 * w + x, cb = kbx >> 2, j = kbx & 3;
+    vb[x] = (uint32_t)((cb * nb32 * 1024 + j * 256 + lane * 4) * 4);
+  }
+#pragma unroll
+  for (int n = 0; n < QDI; ++n) {
+    const int gc = n * 64 + lane, r = gc / (DP / 8), c = (gc % (DP / 8)) ^ qd_swz<DP>(r);
+    const bool ld = active && c * 8 < D;
+    vq[n] = ld ? (uint32_t)((r * g.s_row + c * 8) * 2) : kBufOOB;
+    vdo[n] = ld ? (uint32_t)((r * H * D + c * 8) * 2) : kBufOOB;
+  }
   auto issue = [&](int q0, BfT& Bf, QDT& QDs, RST& RS) {
     // Bias fragments: 8 KB per step, wave w loads kilobytes 2w and 2w+1.
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       const int kbx = 2 * w + x, cb = kbx >> 2, j = kbx & 3;
-      g2lds16(bfrag + ((int64_t)cb * nb32 + (q0 >> 5)) * 1024 + j * 256 + lane * 4,
-              &Bf[cb][j * 256]);
+      buf2lds16_so(rs_bias, vb[x], (uint32_t)q0 * 128u, &Bf[cb][j * 256]);
     }
-    // Q and dO rows, swizzled; lanes past D (or of an idle wave) do not load.
+    // Q and dO rows, swizzled.
 #pragma unroll
     for (int n = 0; n < QDI; ++n) {
-      const int gc = n * 64 + lane, r = gc / (DP / 8), c = (gc % (DP / 8)) ^ qd_swz<DP>(r);
-      if (active && c * 8 < D) {
-        g2lds16(q + plane_off + (int64_t)(q0 + r) * g.s_row + c * 8, &QDs[w][n * 512]);
-        g2lds16(dout + do_plane + (int64_t)(q0 + r) * H * D + c * 8, &QDs[w][QDE + n * 512]);
-      }
+      buf2lds16_so(rs_q, vq[n], (uint32_t)(q0 * g.s_row * 2), &QDs[w][n * 512]);
+      buf2lds16_so(rs_do, vdo[n], (uint32_t)(q0 * H * D * 2), &QDs[w][QDE + n * 512]);
     }
     // An idle wave keeps the -inf / 0 statistics written at setup, so its
     // P and dS are exactly zero and it adds nothing to the dBias sum.
@@ -705,17 +726,20 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     // consecutive keys of one query row (128 bytes).
     {
       const int key = tid & 63, qb = tid >> 6;
-      float acc[8];
+      // Each add is one v_dot2 with a one-hot selector: x * 1 + y * 0 + acc
+      // is the f32 sum acc + x (unpack and add in one instruction).
+      const bf16x2 sel[2] = {__builtin_bit_cast(bf16x2, sel_lo_bits),
+                             {static_cast<__bf16>(0.f), static_cast<__bf16>(1.f)}};
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
         const __bf16* src = &dSs[ww][key * SP + 8 * qb];
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(src);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(src + 4);
+        const bf16x2 pr[4] = {{lo[0], lo[1]}, {lo[2], lo[3]}, {hi[0], hi[1]}, {hi[2], hi[3]}};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = ww ? acc[e] + bf2f(lo[e]) : bf2f(lo[e]);
-          acc[4 + e] = ww ? acc[4 + e] + bf2f(hi[e]) : bf2f(hi[e]);
-        }
+        for (int e = 0; e < 8; ++e)
+          acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
       }
       __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0 + 8 * qb) * N + key_base + key;
 #pragma unroll

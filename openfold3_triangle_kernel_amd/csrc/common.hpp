@@ -175,6 +175,17 @@ __device__ __forceinline__ void buf2lds16(i32x4 rsrc, uint32_t voff, void* dst_b
                :: "s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
 
+// buf2lds16 with a uniform byte offset `soff` (an SGPR) added to every
+// lane's voff: a loop advances soff on the scalar unit while the per-lane
+// offsets stay fixed.  voff = kBufOOB still reads zeros.
+__device__ __forceinline__ void buf2lds16_so(i32x4 rsrc, uint32_t voff, uint32_t soff,
+                                             void* dst_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+
 // Division by a run-time invariant d (Granlund-Montgomery): for n < 2^31,
 // n / d = (umulhi(n, m) + n) >> s with s = ceil(log2 d),
 // m = floor(2^32 (2^s - d) / d) + 1.  Replaces 32/64-bit integer division
