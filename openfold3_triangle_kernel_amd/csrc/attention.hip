@@ -778,83 +778,99 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
 }
 
 // dQ = bf16(scale * sum_kb partial[kb]) in ascending key-block order; bf16
-// partials [kb][plane][h][q][D], output in Q's storage order.
+// partials [kb][plane][h][q][D], output in Q's storage order.  Grid: x =
+// (query, 8-channel chunk) inside one (plane, head) block, y = plane * H + h
+// (strided past the grid limit).  Up to 8 partial loads are in flight; they
+// are added in key-block order.
 __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
     const __bf16* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
   const int D8 = g.D / 8;
-  const int64_t total = (int64_t)g.B * g.O * g.H * g.N * D8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= total) return;
-  const int d0 = (int)(idx % D8) * 8;
-  int64_t r = idx / D8;                 // [plane][h][q]
-  const int qq = (int)(r % g.N); r /= g.N;
-  const int hh = (int)(r % g.H);
-  const int64_t plane = r / g.H;
-  const int64_t stride = (int64_t)g.B * g.O * g.H * g.N * g.D;
-  const __bf16* src = part + ((plane * g.H + hh) * g.N + qq) * g.D + d0;
-  float acc[8];
-  {
-    bf16x8 x = ld8(src);
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= g.N * D8) return;
+  const int qq = t / D8, d0 = (t - qq * D8) * 8;
+  const int64_t nph = (int64_t)g.B * g.O * g.H;
+  const int64_t stride = nph * g.N * g.D;
+  for (int64_t ph = blockIdx.y; ph < nph; ph += gridDim.y) {
+    const int64_t plane = ph / g.H;
+    const int hh = (int)(ph - plane * g.H);
+    const __bf16* src = part + (ph * g.N + qq) * g.D + d0;
+    float acc[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = bf2f(x[e]);
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int k0 = 0; k0 < nkb; k0 += 8) {
+      bf16x8 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < nkb) x[u] = ld8(src + (int64_t)(k0 + u) * stride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < nkb) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] = (k0 + u == 0) ? bf2f(x[u][e]) : acc[e] + bf2f(x[u][e]);
+        }
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
+    st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
   }
-  for (int kb = 1; kb < nkb; ++kb) {
-    bf16x8 x = ld8(src + kb * stride);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += bf2f(x[e]);
-  }
-  bf16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
-  st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
 }
 
-// dBias[bb,h,q,k] (f32) = ascending fold over the bf16 (b, outer group)
-// partials that share bias batch bb.  Bb == 1 folds every batch; Bb == B
-// folds per batch.
+// dBias[bb,h,q,k] (f32) = fold over the bf16 (b, outer group) partials that
+// share bias batch bb (Bb == 1 folds every batch; Bb == B folds per batch).
+// Workgroup = 64 chunks of 8 consecutive outputs x 4 ranges of partials:
+// thread (range s, chunk c) sums its range in ascending order (8 loads in
+// flight; each load instruction of a wave reads 1 KB contiguous), and the
+// four range sums are added in the fixed order ((s0 + s1) + s2) + s3.
 __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
     const __bf16* __restrict__ part, float* __restrict__ dbias, int B, int Bb,
     int groups, int H, int N) {
+  __shared__ float red[4][64][9];
+  const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
   const int64_t hnn8 = (int64_t)H * N * N / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)Bb * hnn8) return;
-  const int bb = (int)(idx / hnn8);
-  const int64_t e = (idx % hnn8) * 8;
+  const int64_t idx = (int64_t)blockIdx.x * 64 + c;
+  const bool act = idx < (int64_t)Bb * hnn8;
+  const int bb = act ? (int)(idx / hnn8) : 0;
+  const int64_t e = act ? (idx % hnn8) * 8 : 0;
   const int b_lo = (Bb == 1) ? 0 : bb, b_hi = (Bb == 1) ? B : bb + 1;
-  // Partials (bi, gi) in ascending order are consecutive slots
-  // b_lo*groups .. b_hi*groups - 1; 8 loads in flight, added in order.
+  const int n = (b_hi - b_lo) * groups;
+  const int per = (n + 3) / 4;
+  const int s0 = sl * per, s1 = min(n, s0 + per);
   const int64_t stride = (int64_t)H * N * N;
   const __bf16* src = part + (int64_t)b_lo * groups * stride + e;
-  const int n = (b_hi - b_lo) * groups;
   float acc[8];
-  {
-    const bf16x8 x = ld8(src);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = bf2f(x[i]);
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  if (act) {
+    for (int s = s0; s < s1; s += 8) {
+      bf16x8 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s + u < s1) x[u] = ld8(src + (int64_t)(s + u) * stride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s + u < s1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = (s + u == s0) ? bf2f(x[u][i]) : acc[i] + bf2f(x[u][i]);
+        }
+    }
   }
-  int s = 1;
-  for (; s + 8 <= n; s += 8) {
-    bf16x8 x[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = ld8(src + (int64_t)(s + u) * stride);
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += bf2f(x[u][i]);
-  }
-  for (; s < n; ++s) {
-    const bf16x8 x = ld8(src + (int64_t)s * stride);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += bf2f(x[i]);
-  }
+  for (int i = 0; i < 8; ++i) red[sl][c][i] = acc[i];
+  __syncthreads();
+  if (sl != 0 || !act) return;
   f32x4 lo, hi;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { lo[i] = acc[i]; hi[i] = acc[4 + i]; }
+  for (int i = 0; i < 8; ++i) {
+    float v = red[0][c][i];
+    for (int r = 1; r < 4; ++r)
+      if (r * per < n) v += red[r][c][i];
+    if (i < 4) lo[i] = v; else hi[i - 4] = v;
+  }
   float* d = dbias + (int64_t)bb * H * N * N + e;
   *reinterpret_cast<f32x4*>(d) = lo;
   *reinterpret_cast<f32x4*>(d + 4) = hi;
 }
-
 
 // ---------------------------------------------------------------------------
 // Output gate of the pair-row module core.  One thread per (pair row,
@@ -1148,13 +1164,14 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
   BwdParts pt;
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t dq_items = B * O * H * N * (D / 8);
-  hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
-                     0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
+  const int64_t nph = B * O * H;
+  hipLaunchKernelGGL(attn_dq_reduce_kernel,
+                     dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
+                     dim3(256), 0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
   int rc = check_launch(fn);
   if (rc) return rc;
   const int64_t db_items = bias_batches * H * N * N / 8;
-  hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 255) / 256)),
+  hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 63) / 64)),
                      dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
                      (int)H, (int)N);
   return check_launch(fn);
@@ -1364,9 +1381,10 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
     return rc;
   BwdParts pt;
   bwd_layout(B, N, H, N, D, (char*)workspace, &pt);
-  const int64_t dq_items = B * N * H * N * (D / 8);
-  hipLaunchKernelGGL(attn_dq_reduce_kernel, dim3((unsigned)((dq_items + 255) / 256)), dim3(256),
-                     0, s, pt.dq, dp, g, (int)(N / 64));
+  const int64_t nph = B * N * H;
+  hipLaunchKernelGGL(attn_dq_reduce_kernel,
+                     dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
+                     dim3(256), 0, s, pt.dq, dp, g, (int)(N / 64));
   if ((rc = check_launch(fn))) return rc;
   const int64_t groups = (N + kBwdGroup - 1) / kBwdGroup;
   const int64_t db_items = B * N * N / 8;
