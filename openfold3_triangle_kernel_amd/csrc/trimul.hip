@@ -29,6 +29,9 @@
 //             partials) -> GEMMs da, db -> tm_in_proj<bwd> (d a_p .. d b_g)
 //             -> tm_ln_bwd<rows> (dz, LN_in partials) -> split-K weight
 //             GEMMs -> fixed-order folds.
+// 32-deep k stages: every TriMul GEMM has K = C or 5H (small), and the
+// halved LDS ring lets the forward input projection run 4 workgroups per CU.
+#define TPF_GEMM_GK 32
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "tpf_gemm.hpp"
@@ -388,11 +391,11 @@ __device__ __forceinline__ void put_planes(__bf16* S, const RegTile& t, int nch)
 // d g = d * mask * p * s(g) (1 - s(g)) into dproj5, d = da / db.
 // ---------------------------------------------------------------------------
 template <bool BWD>
-__global__ __launch_bounds__(256, 2) void tm_in_proj_kernel(
+__global__ __launch_bounds__(256, BWD ? 2 : 4) void tm_in_proj_kernel(
     const __bf16* __restrict__ zln, const __bf16* __restrict__ wp, const float* __restrict__ mask,
     __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl,
     __bf16* __restrict__ dproj5, TmGeom g, int C) {
-  __shared__ __attribute__((aligned(1024))) char smem[kInProjLds];
+  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kInProjLds : lds_bytes(128 * kSP * 2)];
   __shared__ float mask_s[128];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
