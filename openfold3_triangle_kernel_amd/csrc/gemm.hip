@@ -83,6 +83,75 @@ __global__ __launch_bounds__(256) void fold_f32_kernel(const float* __restrict__
   dst[(int64_t)j * dst_stride + i] = acc;
 }
 
+// Several folds in one launch per pass: blockIdx.y runs over the (segment,
+// chunk) pairs.  Intermediate passes fold 64-split chunks in place (as
+// fold_launch does); the final pass writes element i of a segment to
+// dst[i / piece][i % piece], so one segment can land in up to 4 outputs.
+__global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f, int final_pass) {
+  int sg = 0;
+  while (sg + 1 < f.nseg && (int)blockIdx.y >= f.gbase[sg + 1]) ++sg;
+  const int j = (int)blockIdx.y - f.gbase[sg];
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= f.n[sg]) return;
+  const float* part = f.part[sg];
+  const int64_t stride = f.stride[sg];
+  const int chunk = final_pass ? f.splits[sg] : 64;
+  const int s0 = j * chunk, s1 = min(f.splits[sg], s0 + chunk);
+  float acc = part[(int64_t)s0 * stride + i];
+  int s = s0 + 1;
+  for (; s + 8 <= s1; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(s + e) * stride + i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += v[e];
+  }
+  for (; s < s1; ++s) acc += part[(int64_t)s * stride + i];
+  if (final_pass) {
+    const int64_t pc = i / f.piece[sg];
+    f.dst[sg][pc][i - pc * f.piece[sg]] = acc;
+  } else {
+    const_cast<float*>(part)[(int64_t)j * 64 * stride + i] = acc;
+  }
+}
+
+int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
+  if (f.nseg < 1 || f.nseg > kFoldMaxSegs) return set_error(TPF_ERR_ARG, "%s: bad fold segments", fn);
+  for (;;) {
+    // Segments with more than 64 splits take a 64-chunk pass; the others wait.
+    FoldSegs p = f;
+    p.nseg = 0;
+    int groups = 0;
+    int64_t maxn = 0;
+    for (int sg = 0; sg < f.nseg; ++sg) {
+      if (f.splits[sg] <= 64) continue;
+      const int k = p.nseg++;
+      p.part[k] = f.part[sg]; p.n[k] = f.n[sg]; p.stride[k] = f.stride[sg];
+      p.splits[k] = f.splits[sg]; p.gbase[k] = groups;
+      groups += (f.splits[sg] + 63) / 64;
+      maxn = f.n[sg] > maxn ? f.n[sg] : maxn;
+    }
+    if (p.nseg == 0) break;
+    hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)((maxn + 255) / 256), (unsigned)groups),
+                       dim3(256), 0, stream, p, 0);
+    int rc = check_launch(fn);
+    if (rc) return rc;
+    for (int sg = 0; sg < f.nseg; ++sg)
+      if (f.splits[sg] > 64) {
+        f.splits[sg] = (f.splits[sg] + 63) / 64;
+        f.stride[sg] *= 64;
+      }
+  }
+  int64_t maxn = 0;
+  for (int sg = 0; sg < f.nseg; ++sg) {
+    f.gbase[sg] = sg;
+    maxn = f.n[sg] > maxn ? f.n[sg] : maxn;
+  }
+  hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)((maxn + 255) / 256), (unsigned)f.nseg),
+                     dim3(256), 0, stream, f, 1);
+  return check_launch(fn);
+}
+
 int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
                 hipStream_t stream, const char* fn) {
   GemmArgs g = g0;

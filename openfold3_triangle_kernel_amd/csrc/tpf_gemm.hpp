@@ -41,4 +41,18 @@ int gemm_f32_launch(const GemmArgsF32& g, int a_kc, int b_kc, int batch, hipStre
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
                 hipStream_t stream, const char* fn);
 
+// Up to kFoldMaxSegs independent fixed-order folds (same order as
+// fold_launch) in one launch per pass.  Segment sg folds `splits` partial
+// vectors of n floats spaced `stride` apart (folded in place in its part
+// buffer when splits > 64) into dst[sg][i / piece][i % piece].
+constexpr int kFoldMaxSegs = 4;
+struct FoldSegs {
+  const float* part[kFoldMaxSegs];
+  float* dst[kFoldMaxSegs][4];
+  int64_t n[kFoldMaxSegs], stride[kFoldMaxSegs], piece[kFoldMaxSegs];
+  int splits[kFoldMaxSegs], gbase[kFoldMaxSegs];
+  int nseg;
+};
+int fold_multi(FoldSegs f, hipStream_t stream, const char* fn);
+
 }  // namespace tpf

@@ -869,7 +869,6 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   t += align256(R * 5 * C * 2);                    // dproj5
   t += 3 * align256(B * C * N * Np * 2);           // dx, da, db
   t += align256(tiles * 4 * C * 4);                // LN parameter partials
-  t += align256(4 * C * 4);                        // folded LN parameter grads
   t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
   t += align256((int64_t)tm_wz_splits(R) * C * C * 4);
   return t;
@@ -914,7 +913,6 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   __bf16* da = (__bf16*)take(plane_bytes);
   __bf16* db = (__bf16*)take(plane_bytes);
   float* lnp = (float*)take(tiles * 4 * C * 4);
-  float* lnf = (float*)take(4 * C * 4);
   float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
   float* wzp = (float*)take((int64_t)sz * C * C * 4);
   if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
@@ -964,14 +962,19 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gz.M = (int)C; gz.N = (int)H; gz.K = (int)R; gz.ksplit = sz;
   gz.k_chunk = (int)((R + sz - 1) / sz); gz.alpha = 1.f;
   if ((rc = gemm_launch(gz, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dWz)"))) return rc;
-  if ((rc = fold_launch(w5p, d_w5, 5 * C * C, 5 * C * C, s5, s, fn))) return rc;
-  if ((rc = fold_launch(wzp, d_w_z, C * H, C * H, sz, s, fn))) return rc;
-  if ((rc = fold_launch(lnp, lnf, 4 * C, 4 * C, (int)tiles, s, fn))) return rc;
-  float* outs[4] = {d_ln_out_w, d_ln_out_b, d_ln_in_w, d_ln_in_b};
-  for (int i = 0; i < 4; ++i)
-    if (hipMemcpyAsync(outs[i], lnf + i * C, C * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
-      return set_error(TPF_ERR_LAUNCH, "%s: copy of LN parameter gradients failed", fn);
-  return TPF_OK;
+  // The three weight-gradient folds in one launch per pass; the LayerNorm
+  // partials [tiles][ln_out_w | ln_out_b | ln_in_w | ln_in_b] land directly
+  // in the four parameter gradients.
+  FoldSegs f{};
+  f.nseg = 3;
+  f.part[0] = w5p; f.n[0] = 5 * C * C; f.stride[0] = 5 * C * C; f.splits[0] = s5;
+  f.piece[0] = 5 * C * C; f.dst[0][0] = d_w5;
+  f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = sz;
+  f.piece[1] = C * H; f.dst[1][0] = d_w_z;
+  f.part[2] = lnp; f.n[2] = 4 * C; f.stride[2] = 4 * C; f.splits[2] = (int)tiles;
+  f.piece[2] = C;
+  f.dst[2][0] = d_ln_out_w; f.dst[2][1] = d_ln_out_b; f.dst[2][2] = d_ln_in_w; f.dst[2][3] = d_ln_in_b;
+  return fold_multi(f, s, fn);
 }
 
 }  // extern "C"
