@@ -16,12 +16,11 @@
 
 namespace tpf {
 
+// Tile T of problem g (T < tiles of g, in (n-tile, m-tile, split, batch)
+// order) into C.
 template <bool A_KC, bool B_KC, bool OUT_F32>
-__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+__device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, char* smem) {
   const int tm = (g.M + kGM - 1) / kGM, tn = (g.N + kGN - 1) / kGN;
-  const int64_t T = xcd_order((int64_t)tm * tn * g.batch * g.ksplit);
-  if (T < 0) return;
   const int nt = (int)(T % tn);
   int64_t r = T / tn;
   const int mt = (int)(r % tm);
@@ -56,6 +55,36 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g) {
         }
       }
     }
+}
+
+__host__ __device__ inline int64_t gemm_tiles(const GemmArgs& g) {
+  return (int64_t)((g.M + kGM - 1) / kGM) * ((g.N + kGN - 1) / kGN) * g.batch * g.ksplit;
+}
+
+template <bool A_KC, bool B_KC, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  const int64_t T = xcd_order(gemm_tiles(g));
+  if (T < 0) return;
+  gemm_bf16_tile<A_KC, B_KC, OUT_F32>(g, T, smem);
+}
+
+// Two problems of one layout in one grid: workgroups [0, p0) take the
+// tiles of g0 and the rest those of g1 (p0 = g0's tiles rounded up to 8),
+// each in its own XCD-aware order, so both problems spread over all XCDs
+// and independent small GEMMs stay in flight together.
+template <bool AK0, bool BK0, bool AK1, bool BK1, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_pair_kernel(GemmArgs g0, GemmArgs g1) {
+  __shared__ __attribute__((aligned(1024))) char smem[kGMainLdsBytes];
+  const int64_t t0 = gemm_tiles(g0), p0 = (t0 + 7) / 8 * 8;
+  const int64_t L = blockIdx.x;
+  if (L < p0) {
+    const int64_t T = xcd_order_of(L, t0);
+    if (T >= 0) gemm_bf16_tile<AK0, BK0, OUT_F32>(g0, T, smem);
+  } else {
+    const int64_t T = xcd_order_of(L - p0, gemm_tiles(g1));
+    if (T >= 0) gemm_bf16_tile<AK1, BK1, OUT_F32>(g1, T, smem);
+  }
 }
 
 // Fixed-order fold of split partials: thread (i, j) sums splits
@@ -152,9 +181,7 @@ int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
   return check_launch(fn);
 }
 
-int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
-                hipStream_t stream, const char* fn) {
-  GemmArgs g = g0;
+static int gemm_prepare(GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch, const char* fn) {
   g.batch = batch;
   if (g.M < 1 || g.N < 1 || g.K < 1 || batch < 1 || g.ksplit < 1)
     return set_error(TPF_ERR_SHAPE, "%s: bad GEMM shape M=%d N=%d K=%d", fn, g.M, g.N, g.K);
@@ -183,10 +210,17 @@ int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
     return set_error(TPF_ERR_ARG, "%s: split-K needs f32 output", fn);
   if (g.k_chunk <= 0) g.k_chunk = g.K;
   g.k_chunk = ((g.k_chunk + kGK - 1) / kGK) * kGK;
-  const int64_t total = (int64_t)((g.M + kGM - 1) / kGM) * ((g.N + kGN - 1) / kGN) * batch * g.ksplit;
-  const int64_t blocks = (total + 7) / 8 * 8;
-  if (blocks > INT32_MAX) return set_error(TPF_ERR_SHAPE, "%s: GEMM grid too large", fn);
-  dim3 grid((unsigned)blocks);
+  if ((gemm_tiles(g) + 7) / 8 * 8 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: GEMM grid too large", fn);
+  return TPF_OK;
+}
+
+int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
+                hipStream_t stream, const char* fn) {
+  GemmArgs g = g0;
+  int rc = gemm_prepare(g, a_kc, b_kc, out_f32, batch, fn);
+  if (rc) return rc;
+  dim3 grid((unsigned)((gemm_tiles(g) + 7) / 8 * 8));
 #define TPF_GEMM_CASE(AK, BK, OF)                                                            \
   if (a_kc == AK && b_kc == BK && out_f32 == OF) {                                            \
     hipLaunchKernelGGL((gemm_bf16_kernel<AK, BK, OF>), grid, dim3(256), 0, stream, g);         \
@@ -202,6 +236,27 @@ int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
   TPF_GEMM_CASE(0, 0, 1)
 #undef TPF_GEMM_CASE
   return set_error(TPF_ERR_ARG, "%s: bad GEMM layout flags", fn);
+}
+
+int gemm_launch_pair(const GemmArgs& p0, int a_kc0, int b_kc0, const GemmArgs& p1, int a_kc1,
+                     int b_kc1, int out_f32, hipStream_t stream, const char* fn) {
+  GemmArgs g0 = p0, g1 = p1;
+  int rc = gemm_prepare(g0, a_kc0, b_kc0, out_f32, p0.batch > 0 ? p0.batch : 1, fn);
+  if (rc) return rc;
+  if ((rc = gemm_prepare(g1, a_kc1, b_kc1, out_f32, p1.batch > 0 ? p1.batch : 1, fn))) return rc;
+  const int64_t blocks = (gemm_tiles(g0) + 7) / 8 * 8 + (gemm_tiles(g1) + 7) / 8 * 8;
+  if (blocks > INT32_MAX) return set_error(TPF_ERR_SHAPE, "%s: GEMM grid too large", fn);
+  dim3 grid((unsigned)blocks);
+#define TPF_GEMM_PAIR_CASE(A0, B0, A1, B1, OF)                                                \
+  if (a_kc0 == A0 && b_kc0 == B0 && a_kc1 == A1 && b_kc1 == B1 && out_f32 == OF) {             \
+    hipLaunchKernelGGL((gemm_bf16_pair_kernel<A0, B0, A1, B1, OF>), grid, dim3(256), 0, stream,  \
+                       g0, g1);                                                               \
+    return check_launch(fn);                                                                  \
+  }
+  TPF_GEMM_PAIR_CASE(0, 0, 0, 0, 1)  // TriMul weight gradients
+  TPF_GEMM_PAIR_CASE(1, 0, 0, 0, 0)  // TriMul contraction backward (dA, dB)
+#undef TPF_GEMM_PAIR_CASE
+  return set_error(TPF_ERR_ARG, "%s: GEMM pair layout not instantiated", fn);
 }
 
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,

@@ -200,6 +200,14 @@ __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperan
 // XCD-aware tile order: workgroup L runs on XCD L % 8; consecutive logical
 // tiles T (which share operand rows) are placed on the same XCD so they hit
 // the same L2.  Returns -1 for the padding ids of the rounded-up grid.
+// XCD-aware order of workgroup L over `total` tiles (L from 0 in steps of
+// 8 per XCD round); -1 for the padding ids.
+__device__ __forceinline__ int64_t xcd_order_of(int64_t L, int64_t total) {
+  const int64_t per = (total + 7) / 8;
+  const int64_t T = (L % 8) * per + L / 8;
+  return T < total ? T : -1;
+}
+
 __device__ __forceinline__ int64_t xcd_order(int64_t total) {
   const int64_t L = blockIdx.x;
   const int64_t per = (total + 7) / 8;

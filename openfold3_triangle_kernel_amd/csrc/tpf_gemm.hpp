@@ -36,6 +36,10 @@ struct GemmArgsF32 {
 // a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).
 int gemm_launch(const GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch,
                 hipStream_t stream, const char* fn);
+// Two GEMMs in one launch (g.batch of each, 0 meaning 1), each with its own
+// operand layout; instantiated for the layout pairs TriMul uses.
+int gemm_launch_pair(const GemmArgs& g0, int a_kc0, int b_kc0, const GemmArgs& g1, int a_kc1,
+                     int b_kc1, int out_f32, hipStream_t stream, const char* fn);
 int gemm_f32_launch(const GemmArgsF32& g, int a_kc, int b_kc, int batch, hipStream_t stream,
                     const char* fn);
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,

@@ -932,13 +932,16 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   ga.B = (const __bf16*)b; ga.b_ld = g.Np; ga.b_bs = g.PS;
   ga.C = da; ga.c_ld = g.Np; ga.c_bs = g.PS;
   ga.M = (int)N; ga.N = (int)N; ga.K = g.Np; ga.ksplit = 1; ga.k_chunk = g.Np; ga.alpha = 1.f;
-  if ((rc = gemm_launch(ga, 1, 0, 0, (int)(B * C), s, "tpf_trimul_backward_bf16(dA)"))) return rc;
   GemmArgs gb{};
   gb.A = dx; gb.a_ld = g.Np; gb.a_bs = g.PS;
   gb.B = (const __bf16*)a; gb.b_ld = g.Np; gb.b_bs = g.PS;
   gb.C = db; gb.c_ld = g.Np; gb.c_bs = g.PS;
   gb.M = (int)N; gb.N = (int)N; gb.K = (int)N; gb.ksplit = 1; gb.k_chunk = (int)N; gb.alpha = 1.f;
-  if ((rc = gemm_launch(gb, 0, 0, 0, (int)(B * C), s, "tpf_trimul_backward_bf16(dB)"))) return rc;
+  // dA and dB in one launch (2 x B*C batched tiles keep the tail short).
+  ga.batch = (int)(B * C);
+  gb.batch = (int)(B * C);
+  if ((rc = gemm_launch_pair(ga, 1, 0, gb, 0, 0, 0, s, "tpf_trimul_backward_bf16(dA, dB)")))
+    return rc;
   hipLaunchKernelGGL(tm_in_proj_kernel<true>, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
                      (const __bf16*)zln, k.wp, mask, da, db, (__bf16*)nullptr, dproj5, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
@@ -954,14 +957,18 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gw.C = w5p; gw.c_ld = C; gw.c_bs = 0; gw.c_split = 5 * C * C;
   gw.M = (int)(5 * H); gw.N = (int)C; gw.K = (int)R; gw.ksplit = s5;
   gw.k_chunk = (int)((R + s5 - 1) / s5); gw.alpha = 1.f;
-  if ((rc = gemm_launch(gw, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dW5)"))) return rc;
   GemmArgs gz{};
   gz.A = dy; gz.a_ld = C; gz.a_bs = 0;
   gz.B = (const __bf16*)xln; gz.b_ld = H; gz.b_bs = 0;
   gz.C = wzp; gz.c_ld = H; gz.c_bs = 0; gz.c_split = C * H;
   gz.M = (int)C; gz.N = (int)H; gz.K = (int)R; gz.ksplit = sz;
   gz.k_chunk = (int)((R + sz - 1) / sz); gz.alpha = 1.f;
-  if ((rc = gemm_launch(gz, 0, 0, 1, 1, s, "tpf_trimul_backward_bf16(dWz)"))) return rc;
+  // dW5 and dWz are independent split-K GEMMs of ~300 tiles each: one
+  // launch keeps both in flight together.
+  gw.batch = 1;
+  gz.batch = 1;
+  if ((rc = gemm_launch_pair(gw, 0, 0, gz, 0, 0, 1, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
+    return rc;
   // The three weight-gradient folds in one launch per pass; the LayerNorm
   // partials [tiles][ln_out_w | ln_out_b | ln_in_w | ln_in_b] land directly
   // in the four parameter gradients.
