@@ -180,6 +180,128 @@ __global__ __launch_bounds__(256) void tm32_ln_planes_kernel(const float* __rest
   }
 }
 
+// Vector forms of the two LayerNorms (used when the shapes allow 16-byte
+// accesses).  Rows: 16 lanes per row, 16 rows per workgroup; lane l holds
+// the float4 chunks l, l + 16, ... of its row in registers (C <= 64 * NV).
+template <int NV>
+__global__ __launch_bounds__(256) void tm32_ln_rows_vec_kernel(const float* __restrict__ x,
+                                                               int64_t ld_in, int C,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ beta,
+                                                               float eps, float* __restrict__ y,
+                                                               int64_t ld_out, int64_t R) {
+  const int l = threadIdx.x & 15;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool ok = row < R;
+  const int n4 = C / 4;
+  f32x4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c4 = k * 16 + l;
+    v[k] = (ok && c4 < n4) ? *reinterpret_cast<const f32x4*>(x + row * ld_in + c4 * 4)
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
+  const float mean = s / C;
+  float v2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (k * 16 + l >= n4) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = v[k][e] - mean;
+      v2 = fmaf(d, d, v2);
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
+  const float rstd = 1.f / sqrtf(v2 / C + eps);
+  if (!ok) return;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c4 = k * 16 + l;
+    if (c4 >= n4) continue;
+    const f32x4 gm = gamma ? *reinterpret_cast<const f32x4*>(gamma + c4 * 4) : f32x4{1.f, 1.f, 1.f, 1.f};
+    const f32x4 bt = beta ? *reinterpret_cast<const f32x4*>(beta + c4 * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (v[k][e] - mean) * rstd * gm[e] + bt[e];
+    *reinterpret_cast<f32x4*>(y + row * ld_out + c4 * 4) = o;
+  }
+}
+
+// Planes: 64 positions per workgroup (N % 4 == 0, so 4 consecutive positions
+// share one row of the plane); float4 loads along positions, LDS
+// [channel][position] with pitch 65, 4 threads per position for the
+// statistics, float4 stores of 4 channels.
+__global__ __launch_bounds__(256) void tm32_ln_planes_vec_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ gamma,
+                                                                 const float* __restrict__ beta,
+                                                                 float eps, float* __restrict__ xln,
+                                                                 Tm32Geom g) {
+  constexpr int T = 64, XP = T + 1;
+  __shared__ float Xs[256 * XP];  // [channel][position], H <= 256
+  __shared__ float mu_s[T], rs_s[T];
+  const int tid = threadIdx.x, b = blockIdx.y;
+  const int64_t p0 = (int64_t)blockIdx.x * T;
+  for (int idx = tid; idx < g.H * (T / 4); idx += 256) {
+    const int c = idx / (T / 4), q4 = idx % (T / 4);
+    const int64_t p = p0 + 4 * q4;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (p < g.NN) {
+      const uint32_t i = fdiv((uint32_t)p, g.div_n);
+      v = *reinterpret_cast<const f32x4*>(
+          x + ((int64_t)b * g.H + c) * g.PS + (int64_t)i * g.Np + ((uint32_t)p - i * (uint32_t)g.N));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Xs[c * XP + 4 * q4 + e] = v[e];
+  }
+  __syncthreads();
+  {
+    const int pp = tid >> 2, part = tid & 3;
+    float s = 0.f;
+    for (int c = part; c < g.H; c += 4) s += Xs[c * XP + pp];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    const float mean = s / g.H;
+    float v2 = 0.f;
+    for (int c = part; c < g.H; c += 4) {
+      const float d = Xs[c * XP + pp] - mean;
+      v2 = fmaf(d, d, v2);
+    }
+    v2 += __shfl_xor(v2, 1);
+    v2 += __shfl_xor(v2, 2);
+    if (part == 0) {
+      mu_s[pp] = mean;
+      rs_s[pp] = 1.f / sqrtf(v2 / g.H + eps);
+    }
+  }
+  __syncthreads();
+  const int h4n = g.H4 / 4;
+  for (int idx = tid; idx < T * h4n; idx += 256) {
+    const int pp = idx / h4n, c0 = 4 * (idx % h4n);
+    const int64_t p = p0 + pp;
+    if (p >= g.NN) continue;
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = c0 + e;
+      float t = 0.f;
+      if (c < g.H) {
+        t = (Xs[c * XP + pp] - mu_s[pp]) * rs_s[pp];
+        if (gamma) t *= gamma[c];
+        if (beta) t += beta[c];
+      }
+      o[e] = t;
+    }
+    *reinterpret_cast<f32x4*>(xln + ((int64_t)b * g.NN + p) * g.H4 + c0) = o;
+  }
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf(-x)); }
 
 // Input projections in stored row order m (natural row = gather of m for
@@ -395,9 +517,23 @@ int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap,
     hipLaunchKernelGGL(tm32_zero_kernel, dim3(8192), dim3(256), 0, s, wk.a, (int64_t)(wk.x - wk.a));
     if ((rc = check_launch(fn))) return rc;
   }
-  hipLaunchKernelGGL(tm32_ln_rows_kernel, dim3((unsigned)((g.R + 3) / 4)), dim3(256), 0, s, z,
-                     (int64_t)C, (int)C, ln_in_w, ln_in_b, (float)ln_in_eps, wk.zln,
-                     (int64_t)g.C4, g.R);
+  const bool rows_vec = C % 4 == 0 && ((uintptr_t)z | (uintptr_t)ln_in_w | (uintptr_t)ln_in_b) % 16 == 0;
+  const int nv = (int)((C / 4 + 15) / 16);  // float4 chunks per lane (C <= 512: <= 8)
+  if (rows_vec) {
+    const dim3 grid((unsigned)((g.R + 15) / 16));
+#define TM32_LN_ROWS(NV)                                                                       \
+  hipLaunchKernelGGL(tm32_ln_rows_vec_kernel<NV>, grid, dim3(256), 0, s, z, (int64_t)C, (int)C,  \
+                     ln_in_w, ln_in_b, (float)ln_in_eps, wk.zln, (int64_t)g.C4, g.R)
+    if (nv <= 1) TM32_LN_ROWS(1);
+    else if (nv <= 2) TM32_LN_ROWS(2);
+    else if (nv <= 4) TM32_LN_ROWS(4);
+    else TM32_LN_ROWS(8);
+#undef TM32_LN_ROWS
+  } else {
+    hipLaunchKernelGGL(tm32_ln_rows_kernel, dim3((unsigned)((g.R + 3) / 4)), dim3(256), 0, s, z,
+                       (int64_t)C, (int)C, ln_in_w, ln_in_b, (float)ln_in_eps, wk.zln,
+                       (int64_t)g.C4, g.R);
+  }
   if ((rc = check_launch(fn))) return rc;
   const int64_t tiles = (g.R + 127) / 128;
   const int64_t ptiles = tiles * (2 * g.ntg + g.ntgo);
@@ -411,8 +547,12 @@ int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap,
   ga.M = g.N; ga.N = g.N; ga.K = g.Np; ga.alpha = 1.f; ga.bias = nullptr;
   if ((rc = gemm_f32_launch(ga, 1, 1, (int)(B * H), s, "tpf_trimul_forward_f32(contract)")))
     return rc;
-  hipLaunchKernelGGL(tm32_ln_planes_kernel, dim3((unsigned)((g.NN + 31) / 32), (unsigned)B),
-                     dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
+  if (N % 4 == 0 && g.Np % 4 == 0)
+    hipLaunchKernelGGL(tm32_ln_planes_vec_kernel, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
+                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
+  else
+    hipLaunchKernelGGL(tm32_ln_planes_kernel, dim3((unsigned)((g.NN + 31) / 32), (unsigned)B),
+                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
   if ((rc = check_launch(fn))) return rc;
   const int64_t otiles = tiles * ((C + 127) / 128);
   hipLaunchKernelGGL(tm32_out_proj_kernel, dim3((unsigned)((otiles + 7) / 8 * 8)), dim3(256), 0, s,
