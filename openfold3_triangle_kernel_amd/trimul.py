@@ -41,6 +41,17 @@ def _f32(t: torch.Tensor) -> torch.Tensor:
     return t.detach().to(torch.float32).contiguous()
 
 
+def _f32_all(ts) -> list:
+    """f32 contiguous versions of several parameters: no copy when all of them
+    already are, otherwise one concatenation and one cast for the group (the
+    kernels read weights element-wise, so split views need no alignment)."""
+    if all(t.dtype == torch.float32 and t.is_contiguous() for t in ts):
+        return [t.detach() for t in ts]
+    flat = torch.cat([t.detach().reshape(-1) for t in ts]).to(torch.float32)
+    parts = torch.split(flat, [t.numel() for t in ts])
+    return [p.view(t.shape) for p, t in zip(parts, ts)]
+
+
 def _check_op_inputs(z_bf, w_ap):
     if z_bf.dim() != 4 or z_bf.shape[1] != z_bf.shape[2]:
         raise ValueError(f"expected square pair input [B,N,N,C], got {tuple(z_bf.shape)}")
@@ -89,7 +100,8 @@ def _trimul_fwd_v1(
     mask_f = mask_f.to(torch.float32).contiguous()
     Np = int(_native.query("tpf_trimul_plane_pitch", N))
     rows = B * N * N
-    wts = [_f32(t) for t in (w_ap, w_ag, w_bp, w_bg, w_g, w_z)]
+    *wts, g_in32, b_in32, g_out32, b_out32 = _f32_all(
+        (w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_out))
     out = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
     z_ln = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
     gate = torch.empty((rows, C), device=dev, dtype=torch.bfloat16)
@@ -102,7 +114,7 @@ def _trimul_fwd_v1(
     f32 = dict(device=dev, dtype=torch.float32)
     mean_in, rstd_in = torch.empty(rows, **f32), torch.empty(rows, **f32)
     mean_out, rstd_out = torch.empty(rows, **f32), torch.empty(rows, **f32)
-    lnw = [_f32(t) for t in (g_in, b_in, g_out, b_out)]
+    lnw = [g_in32, b_in32, g_out32, b_out32]
     with _device_ctx(dev):
         _native.call(
             "tpf_trimul_forward_bf16",
@@ -177,8 +189,7 @@ def _trimul_bwd_v1(
     dev = z_bf.device
     grad = grad_out.to(torch.bfloat16).contiguous()
     mask_f = mask_f.to(torch.float32).contiguous()
-    wts = [_f32(t) for t in (w_ap, w_ag, w_bp, w_bg, w_g, w_z)]
-    gin, gout = _f32(g_in), _f32(g_out)
+    *wts, gin, gout = _f32_all((w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out))
     f32 = dict(device=dev, dtype=torch.float32)
     d_z = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
     d_w5 = torch.empty((5 * H, C), **f32)  # [ap; ag; bp; bg; g]
@@ -243,9 +254,14 @@ def _fwd_backward(ctx, grad_out, *unused_grads):
     )
     H = w_ap.shape[0]
     dts = ctx.weight_dtypes
-    grads = [d_w5[i * H:(i + 1) * H].to(dts[i]) for i in range(5)]
-    return (d_z, None, *grads, d_wz.to(dts[5]), d_gin.to(dts[6]), d_bin.to(dts[7]),
-            d_gout.to(dts[8]), d_bout.to(dts[9]), None, None)
+    parts = [d_w5[i * H:(i + 1) * H] for i in range(5)] + [d_wz, d_gin, d_bin, d_gout, d_bout]
+    if len(set(dts)) == 1 and dts[0] != torch.float32:
+        # One cast for all ten parameter gradients (views of one buffer).
+        flat = torch.cat([t.reshape(-1) for t in parts]).to(dts[0])
+        grads = [q.view(t.shape) for q, t in zip(torch.split(flat, [t.numel() for t in parts]), parts)]
+    else:
+        grads = [t.to(dt) for t, dt in zip(parts, dts)]
+    return (d_z, None, *grads, None, None)
 
 
 torch.library.register_autograd(
