@@ -412,9 +412,11 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 }
 
 // ---------------------------------------------------------------------------
-// Backward.  One workgroup = (64-key block, head, group of 4 outer rows); wave
-// w owns outer row o = 4*group + w and keeps its dK / dV accumulators for the
-// 64 keys in registers while streaming all queries in 32-row steps.  Scores are
+// Backward.  One workgroup = (key block of 64*KH keys, head, group of 4 outer
+// rows), KH = 2 for D <= 32 (8 waves) and 1 for D = 64 (4 waves, LDS-bound);
+// wave w owns outer row o = 4*group + (w % 4) and key half w / 4 and keeps its
+// dK / dV accumulators for those 64 keys in registers while streaming all
+// queries in 32-row steps.  Scores are
 // formed as S = Q K^T (lane = key column) so the C-layout P and dS tiles are
 // the B operands of dV^T += dO^T P and dK^T += Q^T dS without data movement;
 // the transposed A operands (dO^T, Q^T) and dS^T for dQ^T = K^T dS^T come
@@ -424,11 +426,20 @@ __global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf1
 // Inputs of step i+1 (the bias fragments shared by the 4 waves, each wave's
 // Q / dO rows and row statistics) stream into the other half of a double
 // buffer with direct global->LDS loads while step i computes.
-// dQ leaves as a bf16 partial per key block; dBias sums the 4 waves' bf16
-// dS^T tiles in LDS (fixed order) into a bf16 partial per outer group.  Fixed-order reducers
-// finish both.  Tiles are ordered XCD-aware by (head, outer group, key block).
+// The two key halves of an outer row add their f32 dQ tiles through LDS
+// (half 0 + half 1), and dQ leaves as one bf16 partial per key block; dBias
+// sums the 4 outer rows' bf16 dS^T tiles in LDS (fixed order) into a bf16
+// partial per outer group.  Fixed-order reducers finish both.  Tiles are
+// ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
+// Key halves per backward workgroup (keys per workgroup = 64 * KH).
+__host__ __device__ constexpr int bwd_kh(int dp) { return dp == 32 ? 2 : 1; }
+// Backward key blocks (= dQ partials) for head dimension D.
+static inline int64_t bwd_key_blocks(int64_t N, int64_t D) {
+  const int64_t kw = 64 * bwd_kh(D <= 32 ? 32 : 64);
+  return (N + kw - 1) / kw;
+}
 
 // Q / dO tile of 32 rows x DP bf16 stored unpadded, 16-byte chunks permuted
 // per row (phys = c ^ swz(r)) so transposing reads of 4 consecutive rows and
@@ -451,7 +462,7 @@ __device__ __forceinline__ bf16x4 qd_tr_col4(const __bf16* M, int rbase_lo, int 
 }
 
 template <int DP>
-__global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
+__global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const __bf16* __restrict__ dout,
     const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
@@ -461,21 +472,27 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
+  constexpr int KH = bwd_kh(DP);               // key halves of 64 keys
+  constexpr int NW = 4 * KH;                    // waves
+  constexpr int NT = 64 * NW;                   // threads
   constexpr int QDE = 32 * DP;                 // elements of one Q (or dO) tile
   constexpr int QDI = QDE * 2 / 1024;          // 1 KB async loads per Q (or dO) tile
-  constexpr int NISSUE = 2 + 2 * QDI + 1;      // async loads per wave per step
+  static_assert(QDI % KH == 0, "Q / dO loads split over the key halves");
   // Double buffers [parity]; one loop body serves both parities, so the
   // resident accumulators keep one register assignment across steps.
-  __shared__ __attribute__((aligned(16))) float Bfb[2][2][1024];       // bias fragments [cb]
-  __shared__ __attribute__((aligned(16))) __bf16 QDb[2][4][2 * QDE];   // [wave] Q | dO rows
-  __shared__ __attribute__((aligned(16))) float RSb[2][4][64];         // [wave] nl2 | nd
+  __shared__ __attribute__((aligned(16))) float Bfb[2][2 * KH][1024];  // bias fragments [32-key block]
+  __shared__ __attribute__((aligned(16))) __bf16 QDb[2][4][2 * QDE];   // [outer row] Q | dO rows
+  __shared__ __attribute__((aligned(16))) float RSb[2][4][64];         // [outer row] nl2 | nd
   constexpr int SSE = 64 * (KT > SP ? KT : SP);  // dS^T tile, or the K tile at setup
-  __shared__ __attribute__((aligned(16))) __bf16 dSs[4][SSE];
+  __shared__ __attribute__((aligned(16))) __bf16 dSs[NW][SSE];
+  // Key half 1's dQ^T tiles for key half 0 [outer row][d block][16 regs][lane].
+  __shared__ __attribute__((aligned(16))) float Xq[KH == 2 ? 4 : 1][DP / 32][16][64];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int pw = w & 3, kh = w >> 2;            // outer row in the group, key half
   const int kl = lane & 31, hl = lane >> 5;
   const int N = g.N, D = g.D, H = g.H;
-  const int nkb = N / 64;
+  const int nkb = (N + 64 * KH - 1) / (64 * KH);
   const int groups = (g.O + kBwdGroup - 1) / kBwdGroup;
   const int64_t total = (int64_t)H * nkb * g.B * groups;
   int64_t T;
@@ -491,21 +508,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   const int bog = (int)(hb % ((int64_t)g.B * groups));
   const int h = (int)(hb / ((int64_t)g.B * groups));
   const int b = bog / groups, og = bog % groups;
-  const int o = og * kBwdGroup + w;
-  const bool active = o < g.O;
-  const int plane = b * g.O + (active ? o : 0);
+  const int o = og * kBwdGroup + pw;
+  const bool plane_ok = o < g.O;
+  const int plane = b * g.O + (plane_ok ? o : 0);
   const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
-  const int key_base = kblk * 64;
+  const int key_base = kblk * 64 * KH + 64 * kh;
+  // A key half past N (N % 128 == 64) runs with every key masked: P = dS = 0.
+  const bool keys_ok = key_base < N;
+  const bool active = plane_ok && keys_ok;
   const float c2 = g.scale * kLog2e;
   const float inv_scale = 1.f / g.scale;
   __bf16* Ss = dSs[w];
 
   // Zero the Q / dO buffers once: chunks past D are never loaded.
-  for (int i = tid; i < 2 * 4 * 2 * QDE / 8; i += 256)
+  for (int i = tid; i < 2 * 4 * 2 * QDE / 8; i += NT)
     reinterpret_cast<bf16x8*>(&QDb[0][0][0])[i] = zero8();
-  if (!active) {  // statistics of an idle wave: P = 0 everywhere
-    RSb[0][w][lane] = lane < 32 ? -INFINITY : 0.f;
-    RSb[1][w][lane] = lane < 32 ? -INFINITY : 0.f;
+  if (!plane_ok && kh == 0) {  // statistics of an idle outer row: P = 0 everywhere
+    RSb[0][pw][lane] = lane < 32 ? -INFINITY : 0.f;
+    RSb[1][pw][lane] = lane < 32 ? -INFINITY : 0.f;
   }
 
   // Per-wave constant operands for this key block.
@@ -523,7 +543,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       vB[cb][s] = (active && d0 < D) ? ld8(v + off) : zero8();
       *reinterpret_cast<bf16x8*>(&Ss[(cb * 32 + kl) * KT + d0]) = kB[cb][s];
     }
-    mk2[cb] = active ? mask[(int64_t)plane * N + key] * inv_scale : 0.f;
+    mk2[cb] = active ? mask[(int64_t)plane * N + key] * inv_scale : (keys_ok ? 0.f : -INFINITY);
   }
   const bool wmask = __any(mk2[0] != 0.f || mk2[1] != 0.f);
   __syncthreads();
@@ -537,13 +557,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   const int64_t bb = (g.bias_bstride == 0) ? 0 : b;
   const int nb32 = N / 32;
   // Fragment blocks (kb32, qb) of this head: [(bb*H + h)*nb32 + kb32][qb][1024].
-  const float* bfrag = bias_f + ((bb * H + h) * nb32 + kblk * 2) * (int64_t)nb32 * 1024;
+  const float* bfrag = bias_f + ((bb * H + h) * nb32 + kblk * 2 * KH) * (int64_t)nb32 * 1024;
   const int64_t do_plane = (int64_t)plane * N * H * D + (int64_t)h * D;  // dO is [B,O,N,H,D]
   const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
   __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
+  const int key_blk0 = kblk * 64 * KH;  // first key of the workgroup
 
   // Issue the direct-to-LDS loads of step q0 into buffer `buf`.
-  typedef float BfT[2][1024];
+  typedef float BfT[2 * KH][1024];
   typedef __bf16 QDT[4][2 * QDE];
   typedef float RST[4][64];
   // bf16 pair (1, 0) for the dBias sum, materialised in a register: as an
@@ -558,21 +579,25 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
   const i32x4 rs_bias = buffer_rsrc(bfrag);
   const i32x4 rs_q = buffer_rsrc(q + plane_off);
   const i32x4 rs_do = buffer_rsrc(dout + do_plane);
-  uint32_t vb[2], vq[QDI], vdo[QDI];
+  // Bias: wave w loads kilobytes 2w and 2w+1 of the step's 8*KH KB (32-key
+  // blocks past N read zeros).  Q / dO: key half kh loads its share of its
+  // outer row's tiles.
+  constexpr int QDH = QDI / KH;
+  uint32_t vb[2], vq[QDH], vdo[QDH];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     const int kbx = 2 * w + x, cb = kbx >> 2, j = kbx & 3;
-    vb[x] = (uint32_t)((cb * nb32 * 1024 + j * 256 + lane * 4) * 4);
+    vb[x] = key_blk0 + 32 * cb < N ? (uint32_t)((cb * nb32 * 1024 + j * 256 + lane * 4) * 4)
+                                   : kBufOOB;
   }
 #pragma unroll
-  for (int n = 0; n < QDI; ++n) {
-    const int gc = n * 64 + lane, r = gc / (DP / 8), c = (gc % (DP / 8)) ^ qd_swz<DP>(r);
-    const bool ld = active && c * 8 < D;
+  for (int n = 0; n < QDH; ++n) {
+    const int gc = (kh * QDH + n) * 64 + lane, r = gc / (DP / 8), c = (gc % (DP / 8)) ^ qd_swz<DP>(r);
+    const bool ld = plane_ok && c * 8 < D;
     vq[n] = ld ? (uint32_t)((r * g.s_row + c * 8) * 2) : kBufOOB;
     vdo[n] = ld ? (uint32_t)((r * H * D + c * 8) * 2) : kBufOOB;
   }
   auto issue = [&](int q0, BfT& Bf, QDT& QDs, RST& RS) {
-    // Bias fragments: 8 KB per step, wave w loads kilobytes 2w and 2w+1.
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       const int kbx = 2 * w + x, cb = kbx >> 2, j = kbx & 3;
@@ -580,15 +605,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     }
     // Q and dO rows, swizzled.
 #pragma unroll
-    for (int n = 0; n < QDI; ++n) {
-      buf2lds16_so(rs_q, vq[n], (uint32_t)(q0 * g.s_row * 2), &QDs[w][n * 512]);
-      buf2lds16_so(rs_do, vdo[n], (uint32_t)(q0 * H * D * 2), &QDs[w][QDE + n * 512]);
+    for (int n = 0; n < QDH; ++n) {
+      const int nn = kh * QDH + n;
+      buf2lds16_so(rs_q, vq[n], (uint32_t)(q0 * g.s_row * 2), &QDs[pw][nn * 512]);
+      buf2lds16_so(rs_do, vdo[n], (uint32_t)(q0 * H * D * 2), &QDs[pw][QDE + nn * 512]);
     }
-    // An idle wave keeps the -inf / 0 statistics written at setup, so its
-    // P and dS are exactly zero and it adds nothing to the dBias sum.
-    if (active && lane < 16) {
+    // An idle outer row keeps the -inf / 0 statistics written at setup, so
+    // its P and dS are exactly zero and it adds nothing to the dBias sum.
+    if (plane_ok && kh == 0 && lane < 16) {
       const float* src = (lane < 8 ? nl2_g : nd_g) + st_plane + q0 + (lane & 7) * 4;
-      g2lds16(src, &RS[w][0]);
+      g2lds16(src, &RS[pw][0]);
     }
   };
 
@@ -613,23 +639,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        f32x4 x = *reinterpret_cast<const f32x4*>(&Bc[cb][j * 256 + lane * 4]);
+        f32x4 x = *reinterpret_cast<const f32x4*>(&Bc[2 * kh + cb][j * 256 + lane * 4]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sinit[cb][4 * j + i] = x[i];
       }
     f32x16 nl2v, ndv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      f32x4 a4 = *reinterpret_cast<const f32x4*>(&RSc[w][8 * j + 4 * hl]);
-      f32x4 d4 = *reinterpret_cast<const f32x4*>(&RSc[w][32 + 8 * j + 4 * hl]);
+      f32x4 a4 = *reinterpret_cast<const f32x4*>(&RSc[pw][8 * j + 4 * hl]);
+      f32x4 d4 = *reinterpret_cast<const f32x4*>(&RSc[pw][32 + 8 * j + 4 * hl]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         nl2v[4 * j + i] = a4[i];
         ndv[4 * j + i] = d4[i];
       }
     }
-    const __bf16* Qs = QDc[w];
-    const __bf16* dOs = QDc[w] + QDE;
+    const __bf16* Qs = QDc[pw];
+    const __bf16* dOs = QDc[pw] + QDE;
     bf16x8 qA[DP / 16], doA[DP / 16];
 #pragma unroll
     for (int s = 0; s < DP / 16; ++s) {
@@ -696,16 +722,33 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         for (int i = 0; i < 4; ++i) s4[i] = h[4 * (j & 1) + i];
         *reinterpret_cast<bf16x4*>(&Ss[(cb * 32 + kl) * SP + 8 * j + 4 * hl]) = s4;
       }
-    // dQ^T (d x 32 queries) = K^T dS^T over this block's 64 keys -> bf16 partial.
-    if (active) {
+    // dQ^T (d x 32 queries) = K^T dS^T over this wave's 64 keys; key half 1
+    // hands its tile to key half 0 through LDS (read after the barrier).
+    f32x16 dqacc[DP / 32];
+#pragma unroll
+    for (int db = 0; db < DP / 32; ++db) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16x8 sb = cat8(tr_col4(Ss, SP, 16 * t, 16 * t + 8, 0),
+                               tr_col4(Ss, SP, 16 * t + 4, 16 * t + 12, 0));
+        acc = mfma32(kA[db][t], sb, acc);
+      }
+      dqacc[db] = acc;
+      if (KH == 2 && kh == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Xq[pw][db][r][lane] = acc[r];
+      }
+    }
+    lds_barrier();
+    // dQ partial over the workgroup's keys: (half 0 + half 1) -> bf16.
+    if (kh == 0 && plane_ok) {
 #pragma unroll
       for (int db = 0; db < DP / 32; ++db) {
-        f32x16 acc = zero16();
+        f32x16 acc = dqacc[db];
+        if (KH == 2) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const bf16x8 sb = cat8(tr_col4(Ss, SP, 16 * t, 16 * t + 8, 0),
-                                 tr_col4(Ss, SP, 16 * t + 4, 16 * t + 12, 0));
-          acc = mfma32(kA[db][t], sb, acc);
+          for (int r = 0; r < 16; ++r) acc[r] += Xq[pw][db][r][lane];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -719,13 +762,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         }
       }
     }
-    lds_barrier();
-    // dBias partial: the 4 waves' bf16 dS^T tiles summed in the fixed order
-    // ((w0 + w1) + w2) + w3.  Thread = (key, 8-query block): 8-byte reads of
-    // each wave's row, and each store instruction of a wave writes 64
-    // consecutive keys of one query row (128 bytes).
+    // dBias partial: the 4 outer rows' bf16 dS^T tiles summed in the fixed
+    // order ((o0 + o1) + o2) + o3.  Thread = (key, 8-query block): 8-byte
+    // reads of each wave's row, and each store instruction of a wave writes
+    // 64 consecutive keys of one query row (128 bytes).
     {
-      const int key = tid & 63, qb = tid >> 6;
+      const int key = tid % (64 * KH), qb = tid / (64 * KH);
+      const int kw = 4 * (key >> 6);  // first wave of this key's half
       // Each add is one v_dot2 with a one-hot selector: x * 1 + y * 0 + acc
       // is the f32 sum acc + x (unpack and add in one instruction).
       const bf16x2 sel[2] = {__builtin_bit_cast(bf16x2, sel_lo_bits),
@@ -733,7 +776,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const __bf16* src = &dSs[ww][key * SP + 8 * qb];
+        const __bf16* src = &dSs[kw + ww][(key & 63) * SP + 8 * qb];
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(src);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(src + 4);
         const bf16x2 pr[4] = {{lo[0], lo[1]}, {lo[2], lo[3]}, {hi[0], hi[1]}, {hi[2], hi[3]}};
@@ -741,9 +784,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(
         for (int e = 0; e < 8; ++e)
           acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
       }
-      __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0 + 8 * qb) * N + key_base + key;
+      if (key_blk0 + key < N) {
+        __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0 + 8 * qb) * N + key_blk0 + key;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[(int64_t)e * N] = f2bf(acc[e]);
+        for (int e = 0; e < 8; ++e) dst[(int64_t)e * N] = f2bf(acc[e]);
+      }
     }
   };
   issue(0, Bfb[0], QDb[0], RSb[0]);
@@ -1092,7 +1137,7 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   return check_launch(fn);
 }
 
-// Backward workspace: bf16 dQ partials [N/64][B,O,H,N,D] | bf16 dBias
+// Backward workspace: bf16 dQ partials [key blocks][B,O,H,N,D] | bf16 dBias
 // partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
 // f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
 struct BwdParts {
@@ -1111,7 +1156,7 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   const int64_t rows = B * O * H * N;
   int64_t off = 0;
   auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
-  char* dq = take((N / 64) * rows * D * 2);
+  char* dq = take(bwd_key_blocks(N, D) * rows * D * 2);
   char* db = take(B * groups * H * N * N * 2);
   char* bf = take(B * H * N * N * 4);
   char* nl = take(rows * 4);
@@ -1130,7 +1175,7 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
                                    void* workspace, hipStream_t s, const char* fn) {
   const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  if ((H * (N / 64) * B * groups + 7) / 8 * 8 > INT32_MAX)
+  if ((H * bwd_key_blocks(N, D) * B * groups + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
   BwdParts pt;
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
@@ -1144,14 +1189,14 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
                      dim3(256), 0, s, (const __bf16*)bias, pt.bias_f, items, (int)N,
                      1.f / g.scale, bv);
   if ((rc = check_launch(fn))) return rc;
-  const int64_t total = H * (N / 64) * B * groups;
+  const int64_t total = H * bwd_key_blocks(N, D) * B * groups;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
-    hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
+    hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256 * bwd_kh(32)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
                        mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
   else
-    hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
+    hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256 * bwd_kh(64)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
                        mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
   return check_launch(fn);
@@ -1167,7 +1212,7 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
   const int64_t nph = B * O * H;
   hipLaunchKernelGGL(attn_dq_reduce_kernel,
                      dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
-                     dim3(256), 0, s, pt.dq, (__bf16*)dq, g, (int)(N / 64));
+                     dim3(256), 0, s, pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D));
   int rc = check_launch(fn);
   if (rc) return rc;
   const int64_t db_items = bias_batches * H * N * N / 8;
@@ -1384,7 +1429,7 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   const int64_t nph = B * N * H;
   hipLaunchKernelGGL(attn_dq_reduce_kernel,
                      dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
-                     dim3(256), 0, s, pt.dq, dp, g, (int)(N / 64));
+                     dim3(256), 0, s, pt.dq, dp, g, (int)bwd_key_blocks(N, D));
   if ((rc = check_launch(fn))) return rc;
   const int64_t groups = (N + kBwdGroup - 1) / kBwdGroup;
   const int64_t db_items = B * N * N / 8;

@@ -82,7 +82,7 @@ def test_workspace_sizes(lib):
     from openfold3_triangle_kernel_amd import _native
 
     ws = _native.query("tpf_attn_backward_workspace_bytes", 1, 384, 4, 384, 32)
-    dq = 6 * 384 * 4 * 384 * 32 * 2  # bf16 dQ partial per 64-key block
+    dq = 3 * 384 * 4 * 384 * 32 * 2  # bf16 dQ partial per 128-key block (D <= 32)
     assert ws >= dq + 96 * 4 * 384 * 384 * 2  # bf16 dBias partial per 4 outer rows
     assert _native.query("tpf_trimul_plane_pitch", 113) == 120
     assert _native.query("tpf_trimul_plane_pitch", 384) == 384
