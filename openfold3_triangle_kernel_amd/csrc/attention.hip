@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   // Key half 1's dQ^T tiles for key half 0 [outer row][d block][16 regs][lane].
   __shared__ __attribute__((aligned(16))) float Xq[KH == 2 ? 4 : 1][DP / 32][16][64];
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int pw = w & 3, kh = w >> 2;            // outer row in the group, key half
   const int kl = lane & 31, hl = lane >> 5;
   const int N = g.N, D = g.D, H = g.H;
@@ -562,6 +562,13 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
   __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
   const int key_blk0 = kblk * 64 * KH;  // first key of the workgroup
+  // Partial stores through buffer resources: per-lane offsets fixed for the
+  // walk, the step's offset in a scalar.  dQ: this wave's outer row and
+  // head; dBias: the (outer group, head) N x N block.
+  const __amdgpu_buffer_rsrc_t rs_dq = __builtin_amdgcn_make_buffer_rsrc(dqp, 0, 0x7FFFFFFF, 0x00020000);
+  const uint32_t vdq = (uint32_t)((kl * D + 4 * hl) * 2);
+  const __amdgpu_buffer_rsrc_t rs_db = __builtin_amdgcn_make_buffer_rsrc(
+      dbias_part + ((int64_t)bog * H + h) * N * N, 0, 0x7FFFFFFF, 0x00020000);
 
   // Issue the direct-to-LDS loads of step q0 into buffer `buf`.
   typedef float BfT[2 * KH][1024];
@@ -757,7 +764,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
             bf16x4 o4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[4 * j + i]);
-            *reinterpret_cast<bf16x4*>(dqp + (int64_t)(q0 + kl) * D + d0) = o4;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o4), rs_dq,
+                                                  vdq + (db * 32 + 8 * j) * 2, q0 * D * 2, 0);
           }
         }
       }
@@ -785,9 +793,10 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
           acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
       }
       if (key_blk0 + key < N) {
-        __bf16* dst = dbias_part + (((int64_t)bog * H + h) * N + q0 + 8 * qb) * N + key_blk0 + key;
+        const uint32_t voff = (uint32_t)((8 * qb * N + key_blk0 + key) * 2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dst[(int64_t)e * N] = f2bf(acc[e]);
+        for (int e = 0; e < 8; ++e)
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf_bits(acc[e]), rs_db, voff, (q0 + e) * N * 2, 0);
       }
     }
   };

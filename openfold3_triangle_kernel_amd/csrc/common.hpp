@@ -49,6 +49,7 @@ __device__ __forceinline__ float bf2f(__bf16 h) { return static_cast<float>(h); 
 
 // Round-to-nearest-even f32 -> bf16 (hardware v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ __bf16 f2bf(float f) { return static_cast<__bf16>(f); }
+typedef uint32_t u32x2 __attribute__((__vector_size__(8)));
 __device__ __forceinline__ u16 f2bf_bits(float f) {
   __bf16 h = static_cast<__bf16>(f);
   return *reinterpret_cast<u16*>(&h);
@@ -123,13 +124,19 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& c, int r0) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// LDS byte offset of a generic pointer into LDS: its low 32 bits (the flat
+// LDS aperture keeps the offset there).  Truncating the generic address
+// instead of an address-space cast avoids the cast's null-pointer select.
+__device__ __forceinline__ unsigned lds_offset(const void* p) {
+  return (unsigned)(uintptr_t)p;
+}
+
 // Direct 16-byte global -> LDS load (global_load_lds_dwordx4): lane i writes
 // dst_base + 16*i.  Issued through inline assembly so the compiler does not
 // guard every later LDS read with a full vmcnt wait; callers wait explicitly
 // (wait_vmcnt) before reading the destination.  dst_base must be uniform.
 __device__ __forceinline__ void g2lds16(const void* src, void* dst_base) {
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(lds_offset(dst_base));
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :: "v"(src), "s"(lds) : "memory", "m0");
 }
@@ -169,8 +176,7 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base) {
 // writes dst_base + 16*i with the 16 bytes at byte offset voff of the
 // buffer (zeros when voff is out of range).  Same waiting rules as g2lds16.
 __device__ __forceinline__ void buf2lds16(i32x4 rsrc, uint32_t voff, void* dst_base) {
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(lds_offset(dst_base));
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
@@ -180,8 +186,7 @@ __device__ __forceinline__ void buf2lds16(i32x4 rsrc, uint32_t voff, void* dst_b
 // offsets stay fixed.  voff = kBufOOB still reads zeros.
 __device__ __forceinline__ void buf2lds16_so(i32x4 rsrc, uint32_t voff, uint32_t soff,
                                              void* dst_base) {
-  const unsigned lds = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(lds_void*)dst_base);
+  const unsigned lds = __builtin_amdgcn_readfirstlane(lds_offset(dst_base));
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
