@@ -141,10 +141,14 @@ __device__ __forceinline__ bf16x8 tile_frag(const __bf16* T, int rbase, int s) {
   }
 }
 
-// Full k loop of one 128 x 128 tile.  smem holds kGMainLdsBytes; on return
-// every wave has finished reading it (callers may reuse it after a barrier).
-// kGNS - 1 stages are in flight while one is multiplied.
-template <bool A_KC, bool B_KC>
+// LDS bytes of an NS-stage ring.
+constexpr int gemm_ring_bytes(int ns) { return ns * kGStageBytes; }
+
+// Full k loop of one 128 x 128 tile.  smem holds gemm_ring_bytes(NS); on
+// return every wave has finished reading it (callers may reuse it after a
+// barrier).  NS - 1 stages are in flight while one is multiplied: deeper
+// rings hide more load latency per workgroup at the cost of LDS.
+template <bool A_KC, bool B_KC, int NS = kGNS>
 __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperand& B, int m0,
                                           int n0, int kbeg, int kend, char* smem,
                                           f32x16 (&acc)[2][2]) {
@@ -161,22 +165,22 @@ __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperan
   const int nk = (kend - kbeg + kGK - 1) / kGK;
   if (nk <= 0) return;
 #pragma unroll
-  for (int st = 0; st < kGNS - 1; ++st) {
+  for (int st = 0; st < NS - 1; ++st) {
     if (st < nk) {
       la.issue(kbeg + st * kGK, kend, smem + st * kGStageBytes);
       lb.issue(kbeg + st * kGK, kend, smem + st * kGStageBytes + kGTileBytes);
     }
   }
   for (int kt = 0; kt < nk; ++kt) {
-    char* cur = smem + (kt % kGNS) * kGStageBytes;
+    char* cur = smem + (kt % NS) * kGStageBytes;
     // Stage kt has landed once at most the later stages' loads are pending.
-    if (kt + kGNS - 2 < nk) wait_vmcnt<(kGNS - 2) * 2 * kGInstr>();
+    if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * 2 * kGInstr>();
     else wait_vmcnt<0>();
     lds_barrier();
-    if (kt + kGNS - 1 < nk) {
-      char* nxt = smem + ((kt + kGNS - 1) % kGNS) * kGStageBytes;
-      la.issue(kbeg + (kt + kGNS - 1) * kGK, kend, nxt);
-      lb.issue(kbeg + (kt + kGNS - 1) * kGK, kend, nxt + kGTileBytes);
+    if (kt + NS - 1 < nk) {
+      char* nxt = smem + ((kt + NS - 1) % NS) * kGStageBytes;
+      la.issue(kbeg + (kt + NS - 1) * kGK, kend, nxt);
+      lb.issue(kbeg + (kt + NS - 1) * kGK, kend, nxt + kGTileBytes);
     }
     const __bf16* As = reinterpret_cast<const __bf16*>(cur);
     const __bf16* Bs = reinterpret_cast<const __bf16*>(cur + kGTileBytes);

@@ -51,10 +51,17 @@ struct TmGeom {
 
 constexpr int kSP = 136;  // bf16 pitch of 128-wide LDS staging tiles
 // LDS of a kernel = max(main loop ring, epilogue staging).
-constexpr int lds_bytes(int epilogue) { return epilogue > kGMainLdsBytes ? epilogue : kGMainLdsBytes; }
-constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2);   // d tile + [dp | dg] tile
-constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2);     // gate + dout tiles
-constexpr int kLnBwdLds = lds_bytes(128 * kSP * 2);           // x tile
+// LDS of a kernel whose epilogue staging reuses its NS-stage GEMM ring.
+constexpr int lds_bytes(int epilogue, int ns = kGNS) {
+  return epilogue > gemm_ring_bytes(ns) ? epilogue : gemm_ring_bytes(ns);
+}
+// Ring depths per kernel (measured): the short-K projections keep two
+// stages (occupancy), the long-K / large-epilogue kernels take more.
+constexpr int kInProjFwdNS = 2, kInProjBwdNS = 3, kOutProjNS = 4;
+__host__ __device__ constexpr int ln_bwd_ns(bool planes) { return planes ? 2 : 4; }
+constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2, kInProjBwdNS);  // d tile + [dp | dg] tile
+constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2, kOutProjNS);  // gate + dout tiles
+constexpr int ln_bwd_lds(bool planes) { return lds_bytes(128 * kSP * 2, ln_bwd_ns(planes)); }  // x tile
 
 // Element offset of position p = i*N + j inside a channel-major plane.
 __device__ __forceinline__ int64_t tm_plane_off(const TmGeom& g, int64_t p) {
@@ -395,7 +402,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : 4) void tm_in_proj_kernel(
     const __bf16* __restrict__ zln, const __bf16* __restrict__ wp, const float* __restrict__ mask,
     __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl,
     __bf16* __restrict__ dproj5, TmGeom g, int C) {
-  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kInProjLds : lds_bytes(128 * kSP * 2)];
+  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kInProjLds : lds_bytes(128 * kSP * 2, kInProjFwdNS)];
   __shared__ float mask_s[128];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
@@ -416,7 +423,7 @@ __global__ __launch_bounds__(256, BWD ? 2 : 4) void tm_in_proj_kernel(
   RegTile dreg;
   if (BWD) fetch_planes(dreg, (nt / g.ntg) ? b_pl : a_pl, g, 64, m0, 64 * (nt % g.ntg));
   f32x16 acc[2][2];
-  gemm_tile<true, true>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
+  gemm_tile<true, true, BWD ? kInProjBwdNS : kInProjFwdNS>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
   const AccPos ap;
   __bf16* S0 = reinterpret_cast<__bf16*>(smem);
 
@@ -495,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
   fetch_rows(greg, gl, C, C, m0, g.R);
   if (BWD) fetch_rows(dreg, dout, C, C, m0, g.R);
   f32x16 acc[2][2];
-  gemm_tile<true, true>(A, W, (int)m0, 0, 0, H, smem, acc);
+  gemm_tile<true, true, kOutProjNS>(A, W, (int)m0, 0, 0, H, smem, acc);
   const AccPos ap;
   __bf16* Sg = reinterpret_cast<__bf16*>(smem);
   __bf16* Sd = reinterpret_cast<__bf16*>(smem + kStage);
@@ -583,7 +590,7 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
     const __bf16* __restrict__ xsrc, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gamma, __bf16* __restrict__ dst, float* __restrict__ lnp,
     int slot0, TmGeom g, int W) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLnBwdLds];
+  __shared__ __attribute__((aligned(1024))) char smem[ln_bwd_lds(PLANES)];
   __shared__ __attribute__((aligned(16))) float mean_s[128], rstd_s[128];
   __shared__ __attribute__((aligned(16))) float rsum[2][2][128];  // [quantity][wn][row]
   __shared__ float csum[2][2][128];                               // [quantity][wm][col]
@@ -605,7 +612,7 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
   if (PLANES) fetch_planes(xreg, xsrc, g, 128, m0, 0);
   else fetch_rows(xreg, xsrc, W, W, m0, g.R);
   f32x16 acc[2][2];
-  gemm_tile<true, false>(A, B, (int)m0, 0, 0, K, smem, acc);
+  gemm_tile<true, false, ln_bwd_ns(PLANES)>(A, B, (int)m0, 0, 0, K, smem, acc);
   __bf16* Xt = reinterpret_cast<__bf16*>(smem);  // [ch][row] (PLANES) or [row][ch]
   if (PLANES) put_planes(Xt, xreg, 128);
   else put_rows(Xt, xreg);
