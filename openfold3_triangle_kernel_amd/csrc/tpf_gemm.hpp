@@ -40,6 +40,11 @@ int gemm_launch(const GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch,
 // operand layout; instantiated for the layout pairs TriMul uses.
 int gemm_launch_pair(const GemmArgs& g0, int a_kc0, int b_kc0, const GemmArgs& g1, int a_kc1,
                      int b_kc1, int out_f32, hipStream_t stream, const char* fn);
+// Split-K weight-gradient products (both operands MN-contiguous, f32 output):
+// one problem, or two in one launch (gemm_wgrad.hip).
+int gemm_launch_wgrad(const GemmArgs& g, hipStream_t stream, const char* fn);
+int gemm_launch_pair_wgrad(const GemmArgs& g0, const GemmArgs& g1, hipStream_t stream,
+                           const char* fn);
 int gemm_f32_launch(const GemmArgsF32& g, int a_kc, int b_kc, int batch, hipStream_t stream,
                     const char* fn);
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,

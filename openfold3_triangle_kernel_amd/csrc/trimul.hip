@@ -974,7 +974,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   // launch keeps both in flight together.
   gw.batch = 1;
   gz.batch = 1;
-  if ((rc = gemm_launch_pair(gw, 0, 0, gz, 0, 0, 1, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
+  if ((rc = gemm_launch_pair_wgrad(gw, gz, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
     return rc;
   // The three weight-gradient folds in one launch per pass; the LayerNorm
   // partials [tiles][ln_out_w | ln_out_b | ln_in_w | ln_in_b] land directly
