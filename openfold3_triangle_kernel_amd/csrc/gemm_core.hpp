@@ -50,9 +50,15 @@ struct GemmOperand {
   FastDiv div_n, div_nn;  // division by gather_n and gather_n^2 (gather only)
 };
 
-// Slot of 16-byte chunk c in row r of a KC tile (conflict-free row reads).
+// Slot of 16-byte chunk c in row r of a KC tile.  gfx950's LDS serves 64
+// banks (256 bytes) per cycle, i.e. 16 lanes of a 16-byte read: with 64-byte
+// rows (kGK = 32) the 16 rows of one lane group fill all banks when the slot
+// varies with r / 4 (measured: no bank-conflict cycles).  The 128-byte rows
+// of kGK = 64 keep the row-parity swizzle (two-way conflicts remain; the
+// loader's per-lane chunk must not change between the 8-row groups of one
+// instruction, which excludes an (r / 2)-based slot).
 __device__ __forceinline__ int kc_slot(int r, int c) {
-  return kGK == 64 ? (c ^ (r & 7)) : (c ^ ((r >> 1) & 3));
+  return kGK == 64 ? (c ^ (r & 7)) : (c ^ ((r >> 2) & 3));
 }
 
 // Per-lane loader state of one operand (offsets fixed for the whole k loop).
