@@ -198,8 +198,15 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
 }
 
 // ---------------------------------------------------------------------------
-// LN_out over the channels of the channel-major product x: 64 positions per
-// workgroup (natural order), written as row-major xln.
+// LN_out over the channels of the channel-major product x, written as
+// row-major xln.  Workgroup = 128 positions (natural order) x all channels;
+// thread = (8-position group pg = tid % 16, 8-channel group cg = tid / 16):
+// it reads its 8 channels' 16-byte position runs (coalesced along pg) and
+// keeps the 8 x 8 block in registers, so no LDS transpose is needed.  Per-
+// position sums over channels: the 4 channel groups of a wave by shuffles,
+// the 4 waves through LDS in fixed order; mean first, then the centred
+// sum of squares (two passes, as before).  Each thread then writes its 8
+// channels of its 8 rows as 16-byte stores.
 // ---------------------------------------------------------------------------
 template <int H>
 __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restrict__ x,
@@ -209,63 +216,95 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
                                                            float* __restrict__ mean_out,
                                                            float* __restrict__ rstd_out,
                                                            TmGeom g) {
-  constexpr int T = 64, XP = T + 8;
-  __shared__ __attribute__((aligned(16))) __bf16 Xb[H * XP];
-  const int tid = threadIdx.x, b = blockIdx.y;
-  const int64_t p0 = (int64_t)blockIdx.x * T;
-  const bool vec = (g.Np == g.N) && (p0 + T <= g.NN);
-  for (int idx = tid; idx < H * (T / 8); idx += 256) {
-    const int c = idx / (T / 8), ch = idx % (T / 8);
-    const __bf16* plane = x + ((int64_t)b * H + c) * g.PS;
-    if (vec) {
-      *reinterpret_cast<bf16x8*>(&Xb[c * XP + ch * 8]) = ld8(plane + p0 + ch * 8);
-    } else {
+  constexpr int T = 128;  // positions per workgroup
+  __shared__ float red[4][16][8];
+  const int tid = threadIdx.x, wv = tid >> 6, b = blockIdx.y;
+  const int pg = tid & 15, cg = tid >> 4;
+  const bool chan = cg * 8 < H;
+  const int64_t pb = (int64_t)blockIdx.x * T + pg * 8;  // first position of this thread
+  bf16x8 v[8];  // v[c][e]: channel cg*8 + c, position pb + e
+  if (chan) {
+    const bool vec = (g.Np == g.N) && (pb + 8 <= g.NN);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int64_t p = p0 + ch * 8 + e;
-        Xb[c * XP + ch * 8 + e] = p < g.NN ? plane[tm_plane_off(g, p)] : static_cast<__bf16>(0.f);
+    for (int c = 0; c < 8; ++c) {
+      const __bf16* plane = x + ((int64_t)b * H + cg * 8 + c) * g.PS;
+      if (vec) {
+        v[c] = ld8(plane + pb);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[c][e] = pb + e < g.NN ? plane[tm_plane_off(g, pb + e)] : static_cast<__bf16>(0.f);
       }
     }
-  }
-  __syncthreads();
-  constexpr int CPT = H / 4;
-  const int row = tid >> 2, part = tid & 3;
-  const int64_t p = p0 + row;
-  float xv[CPT];
-  float s = 0.f;
+  } else {
 #pragma unroll
-  for (int e = 0; e < CPT; ++e) {
-    xv[e] = bf2f(Xb[(part * CPT + e) * XP + row]);
-    s += xv[e];
+    for (int c = 0; c < 8; ++c) v[c] = zero8();
   }
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  const float mean = s * (1.f / H);
-  float v2 = 0.f;
+  // Sum over all channels of q[e] (this thread's 8 channels already summed).
+  auto channel_sum = [&](float (&q)[8]) {
 #pragma unroll
-  for (int e = 0; e < CPT; ++e) {
-    const float d = xv[e] - mean;
-    v2 = fmaf(d, d, v2);
+    for (int e = 0; e < 8; ++e) {
+      q[e] += __shfl_xor(q[e], 16);
+      q[e] += __shfl_xor(q[e], 32);
+    }
+    if ((tid & 48) == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wv][pg][e] = q[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = ((red[0][pg][e] + red[1][pg][e]) + red[2][pg][e]) + red[3][pg][e];
+    __syncthreads();
+  };
+  float mean[8], rstd[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s += bf2f(v[c][e]);
+    mean[e] = s;
   }
-  v2 += __shfl_xor(v2, 1);
-  v2 += __shfl_xor(v2, 2);
-  const float rstd = rsqrtf(v2 * (1.f / H) + 1e-5f);
-  if (p < g.NN) {
-    const int64_t rho = (int64_t)b * g.NN + p;
+  channel_sum(mean);
 #pragma unroll
-    for (int c8 = 0; c8 < CPT / 8; ++c8) {
+  for (int e = 0; e < 8; ++e) mean[e] *= 1.f / H;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float s = 0.f;
+    if (chan) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float d = bf2f(v[c][e]) - mean[e];
+        s = fmaf(d, d, s);
+      }
+    }
+    rstd[e] = s;
+  }
+  channel_sum(rstd);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) rstd[e] = rsqrtf(rstd[e] * (1.f / H) + 1e-5f);
+  if (chan) {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + cg * 8);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + cg * 8 + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + cg * 8);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + cg * 8 + 4);
+    const float wc[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+    const float bc[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (pb + e >= g.NN) continue;
       bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int c = part * CPT + c8 * 8 + e;
-        o[e] = f2bf((xv[c8 * 8 + e] - mean) * rstd * w[c] + bias[c]);
+      for (int c = 0; c < 8; ++c) o[c] = f2bf((bf2f(v[c][e]) - mean[e]) * rstd[e] * wc[c] + bc[c]);
+      st8(xln + ((int64_t)b * g.NN + pb + e) * H + cg * 8, o);
+    }
+  }
+  if (cg == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (pb + e < g.NN) {
+        mean_out[(int64_t)b * g.NN + pb + e] = mean[e];
+        rstd_out[(int64_t)b * g.NN + pb + e] = rstd[e];
       }
-      st8(xln + rho * H + part * CPT + c8 * 8, o);
-    }
-    if (part == 0) {
-      mean_out[rho] = mean;
-      rstd_out[rho] = rstd;
-    }
   }
 }
 
@@ -845,7 +884,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
   ga.M = (int)N; ga.N = (int)N; ga.K = g.Np; ga.ksplit = 1; ga.k_chunk = g.Np; ga.alpha = 1.f;
   if ((rc = gemm_launch(ga, 1, 1, 0, (int)(B * C), s, "tpf_trimul_forward_bf16(contract)")))
     return rc;
-  TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
+  TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)((g.NN + 127) / 128), (unsigned)B),
                 (const __bf16*)x, ln_out_w, ln_out_b, (__bf16*)xln, mean_out, rstd_out, g);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_out)"))) return rc;
   hipLaunchKernelGGL(tm_out_proj_kernel<false>, dim3(tm_grid(tiles)), dim3(256), 0, s,
