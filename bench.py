@@ -340,8 +340,9 @@ def main():
             "ms_fwd_bwd": round(blk_ms, 3),
             "config": {"N": Np, "C": Cz, "blocks": ["trimul_out", "trimul_in", "tri_att_start",
                                                       "tri_att_end"], "H": 4, "D": 32},
-            "note": "config 5: residual pair block through the drop-in modules (bf16 params, "
-                    "LayerNorm / projections in torch, hot ops in the HIP kernels)",
+            "note": "config 5: residual pair block through the drop-in modules (bf16 params; "
+                    "LayerNorm, fused q/k/v/g/bias projection, attention core and TriMul in the "
+                    "HIP kernels, linear_o and the residual adds in torch)",
         }
         del zp, mods, params
 
