@@ -379,22 +379,25 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 //            h, [j][lane][i] holds (query 32*qb + 8*j + 4*hl + i,
 //            key 32*kb + (lane % 32)), hl = lane / 32.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_bwd_rowprep_kernel(const float* __restrict__ lse,
-                                                               const float* __restrict__ delta,
-                                                               float* __restrict__ nl2,
-                                                               float* __restrict__ nd, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float l = lse[i];
-  nl2[i] = (l == -INFINITY) ? -INFINITY : -l * kLog2e;
-  nd[i] = -delta[i];
-}
-
-__global__ __launch_bounds__(256) void attn_bias_bwd_prescale_kernel(const __bf16* __restrict__ bias,
-                                                                     float* __restrict__ out,
-                                                                     int64_t items, int N,
-                                                                     float inv_scale, BiasView bv) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
+// One launch for both: workgroups [0, row_blocks) take rowprep items, the
+// rest take bias items (256 items per workgroup each).
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ lse,
+                                                            const float* __restrict__ delta,
+                                                            float* __restrict__ nl2,
+                                                            float* __restrict__ nd, int64_t rows,
+                                                            int64_t row_blocks,
+                                                            const __bf16* __restrict__ bias,
+                                                            float* __restrict__ out, int64_t items,
+                                                            int N, float inv_scale, BiasView bv) {
+  if ((int64_t)blockIdx.x < row_blocks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows) return;
+    const float l = lse[i];
+    nl2[i] = (l == -INFINITY) ? -INFINITY : -l * kLog2e;
+    nd[i] = -delta[i];
+    return;
+  }
+  const int64_t i = ((int64_t)blockIdx.x - row_blocks) * 256 + threadIdx.x;  // (block, j, lane)
   if (i >= items) return;
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
   const int64_t blk = i >> 8;
@@ -1189,15 +1192,15 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
   BwdParts pt;
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
   const int64_t rows = B * O * H * N;
-  hipLaunchKernelGGL(attn_bwd_rowprep_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
-                     s, lse, delta, pt.nl2, pt.nd, rows);
+  const int64_t items = bias_batches * H * N * N / 4;
+  const int64_t row_blocks = (rows + 255) / 256;
+  if (row_blocks + (items + 255) / 256 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: backward preparation grid too large", fn);
+  hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)(row_blocks + (items + 255) / 256)),
+                     dim3(256), 0, s, lse, delta, pt.nl2, pt.nd, rows, row_blocks,
+                     (const __bf16*)bias, pt.bias_f, items, (int)N, 1.f / g.scale, bv);
   int rc = check_launch(fn);
   if (rc) return rc;
-  const int64_t items = bias_batches * H * N * N / 4;
-  hipLaunchKernelGGL(attn_bias_bwd_prescale_kernel, dim3((unsigned)((items + 255) / 256)),
-                     dim3(256), 0, s, (const __bf16*)bias, pt.bias_f, items, (int)N,
-                     1.f / g.scale, bv);
-  if ((rc = check_launch(fn))) return rc;
   const int64_t total = H * bwd_key_blocks(N, D) * B * groups;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
