@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-trimul", action="store_true")
     ap.add_argument("--no-fp32", action="store_true", help="skip the FP32 inference-mode timings")
+    ap.add_argument("--no-config5-attention", action="store_true",
+                    help="skip the config-5 attention timings (N=768: H=4 D=32 and H=8 D=64)")
     ap.add_argument("--pair-block", action="store_true",
                     help="also time the config-5 pair-stack block (N=768) through the modules")
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -193,6 +195,40 @@ def main():
         "avg_launch_us": round(bwd_kernel_ms * 1e3, 2),
         "flops_per_launch": bwd_flops,
     }
+
+    # ------------- config 5 attention shapes (starting node) -------------
+    config5_attention = None
+    if not args.no_config5_attention:
+        config5_attention = []
+        reps = max(3, args.steps // 4)
+        for H5, D5 in ((4, 32), (8, 64)):
+            N5 = 768
+            g5 = torch.Generator(device=dev).manual_seed(5)
+            qkv5 = [torch.randn(1, N5, H5, N5, D5, device=dev, generator=g5).to(torch.bfloat16)
+                    .requires_grad_(True) for _ in range(3)]
+            bias5 = torch.randn(1, 1, H5, N5, N5, device=dev, generator=g5).to(torch.bfloat16)
+            bias5.requires_grad_(True)
+            mask5 = torch.zeros(1, N5, 1, 1, N5, device=dev)
+            dout5 = torch.randn(1, N5, N5, H5, D5, device=dev, generator=g5).to(torch.bfloat16)
+
+            def step5():
+                o5 = turbopairformer_triangle_attention(*qkv5, mask5, bias5)
+                torch.autograd.grad(o5, (*qkv5, bias5), dout5)
+
+            for _ in range(2):
+                step5()
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                step5()
+            e1.record()
+            torch.cuda.synchronize()
+            ms5 = e0.elapsed_time(e1) / reps
+            fl5 = 14.0 * N5 * H5 * N5 * N5 * D5
+            config5_attention.append({"N": N5, "O": N5, "H": H5, "D": D5, "ms_fwd_bwd": round(ms5, 3),
+                                      "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2), "steps": reps})
+            del qkv5, bias5, mask5, dout5
+        torch.cuda.empty_cache()
 
     # --------------------------- TriMul ----------------------------------
     trimul = None
@@ -376,6 +412,7 @@ def main():
             "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         },
         "trimul": trimul,
+        "config5_attention": config5_attention,
         "fp32_inference": fp32,
         "pair_block": pair_block,
         "roofline": roofline,
