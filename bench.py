@@ -267,10 +267,21 @@ def main():
         R = TM_N * TM_N
         tm_fwd_flops = 2.0 * R * C * 5 * C + 2.0 * C * TM_N ** 3 + 2.0 * R * C * C
         tm_flops = 2 * 3 * tm_fwd_flops
+        # Per-stage roofline sum_s max(F_s / P_mfma, B_s / BW_hbm) with the
+        # minimum bytes of each direction (12 U forward, 20 U backward, U =
+        # rows * C * 2 B); at C = 128 every stage is HBM-bound (the
+        # contraction's 14.5 GFLOP take 5.8 us at the MFMA peak against 14 us
+        # for its 3 U), so the sum is the byte term.
+        U = TM_N * TM_N * C * 2
+        roof_ms = 2 * 32 * U / (HBM_PEAK_GBPS * 1e9) * 1e3
         trimul = {
             "ms_fwd_bwd_out_plus_in": round(tm_ms, 4),
             "tflops": round(tm_flops / (tm_ms * 1e-3) / 1e12, 2),
             "flops": tm_flops,
+            "roofline_ms": round(roof_ms, 4),
+            "roofline_frac": round(roof_ms / tm_ms, 4),
+            "roofline_basis": "sum over stages of max(F/P, B/BW); minimum bytes 12U fwd + 20U bwd "
+                              "per direction at 8 TB/s (all stages HBM-bound at C=128)",
             "config": {"N": TM_N, "C": C, "H": C, "directions": ["outgoing", "incoming"]},
         }
 
