@@ -122,8 +122,6 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& c, int r0) {
   return o;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // LDS byte offset of a generic pointer into LDS: its low 32 bits (the flat
 // LDS aperture keeps the offset there).  Truncating the generic address
 // instead of an address-space cast avoids the cast's null-pointer select.

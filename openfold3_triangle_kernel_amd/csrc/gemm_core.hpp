@@ -9,7 +9,8 @@
 //                            n = 64 wn + 32 j + lane % 32.
 //
 // Operands are read from HBM straight into LDS (buffer_load ... lds, 16 bytes
-// per lane, zeros outside the tensor) through a ring of kGNS stages.  Either
+// per lane, zeros outside the tensor) through a ring of NS stages (a
+// template parameter of gemm_tile, default kGNS).  Either
 // operand may be
 //   KC (K-contiguous): X[row * ld + k] -- LDS tile [128 rows][kGK k], the 16-
 //      byte chunk c of row r stored at slot kc_slot(r, c); fragments are plain
@@ -38,7 +39,6 @@ constexpr int kGK = TPF_GEMM_GK;                  // k depth of one stage (32 or
 constexpr int kGNS = TPF_GEMM_NS;                 // stages in the LDS ring
 constexpr int kGTileBytes = kGM * kGK * 2;        // one operand tile
 constexpr int kGStageBytes = 2 * kGTileBytes;     // A + B
-constexpr int kGMainLdsBytes = kGNS * kGStageBytes;
 constexpr int kGInstr = kGTileBytes / 1024 / 4;   // 1 KiB loads per wave per operand tile
 static_assert(kGK == 32 || kGK == 64, "stage depth");
 
@@ -210,19 +210,13 @@ __device__ __forceinline__ void gemm_tile(const GemmOperand& A, const GemmOperan
 // XCD-aware tile order: workgroup L runs on XCD L % 8; consecutive logical
 // tiles T (which share operand rows) are placed on the same XCD so they hit
 // the same L2.  Returns -1 for the padding ids of the rounded-up grid.
-// XCD-aware order of workgroup L over `total` tiles (L from 0 in steps of
-// 8 per XCD round); -1 for the padding ids.
 __device__ __forceinline__ int64_t xcd_order_of(int64_t L, int64_t total) {
   const int64_t per = (total + 7) / 8;
   const int64_t T = (L % 8) * per + L / 8;
   return T < total ? T : -1;
 }
 
-__device__ __forceinline__ int64_t xcd_order(int64_t total) {
-  const int64_t L = blockIdx.x;
-  const int64_t per = (total + 7) / 8;
-  const int64_t T = (L % 8) * per + L / 8;
-  return T < total ? T : -1;
-}
+// The same order for this workgroup.
+__device__ __forceinline__ int64_t xcd_order(int64_t total) { return xcd_order_of(blockIdx.x, total); }
 
 }  // namespace tpf
