@@ -939,7 +939,7 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
 // o / og / d_og / d_o are [B, N, N, H*D] rows; g and dg sit at the gate
 // columns (offset 3*H*D) of the projection rows (row pitch `pitch`).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float gate_sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+__device__ __forceinline__ float gate_sigmoid(float x) { return sigmoidf(x); }
 
 __global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __restrict__ o,
                                                             const __bf16* __restrict__ gate,

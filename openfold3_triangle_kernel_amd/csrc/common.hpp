@@ -71,7 +71,11 @@ __device__ __forceinline__ float xor32_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + __expf(-x)); }
+// Logistic function with the hardware reciprocal (v_rcp_f32, 1 ulp): the
+// IEEE division of 1 / (1 + e^-x) costs about ten VALU instructions, and every
+// consumer rounds the result (or its products) to bf16.  x = -inf gives
+// rcp(inf) = 0, x = +inf gives 1.
+__device__ __forceinline__ float sigmoidf(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // 16-byte global load/store of 8 bf16 values.
 __device__ __forceinline__ bf16x8 ld8(const __bf16* p) {
