@@ -865,9 +865,12 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
   const TmWeights w{w_ap, w_ag, w_bp, w_bg, w_g, w_z};
   if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
   if (g.Np != g.N) {
-    // The contraction reads whole rows of Np; pad columns must be zero.
+    // The contraction reads whole rows of Np; pad columns must be zero.  It
+    // stores only the N real columns of x, so x's pad is cleared too: the
+    // saved state is then a function of the inputs alone.
     if ((rc = zero_fill(a, B * C * g.PS * 2, s, fn))) return rc;
     if ((rc = zero_fill(b, B * C * g.PS * 2, s, fn))) return rc;
+    if ((rc = zero_fill(x, B * C * g.PS * 2, s, fn))) return rc;
   }
   TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)((g.R + 15) / 16)), (const __bf16*)z, ln_in_w,
                 ln_in_b, (__bf16*)zln, mean_in, rstd_in, g.R);
