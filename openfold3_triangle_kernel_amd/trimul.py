@@ -391,13 +391,61 @@ def turbo_trimul(
         raise ValueError("p_in_weight and g_in_weight must be [2*H, C] with H == C")
     if tuple(p_out_weight.shape) != (C, H) or tuple(g_out_weight.shape) != (C, C):
         raise ValueError("p_out_weight must be [C, H] and g_out_weight [C, C]")
-    return _run_trimul(
-        z, mask,
-        p_in_weight[:H], g_in_weight[:H], p_in_weight[H:], g_in_weight[H:],
-        g_out_weight, p_out_weight,
-        norm_in_weight, norm_in_bias, norm_out_weight, norm_out_bias,
-        direction == "outgoing",
-    )
+    if mask is None:
+        mask = z.new_ones(z.shape[:-1])
+    orig_shape = z.shape
+    N = int(z.shape[-2])
+    if z.shape[-3] != N:
+        raise ValueError(f"expected square pair input, got {tuple(z.shape)}")
+    batch = z.numel() // (N * N * C)
+    z_bf = z.reshape(batch, N, N, C).to(torch.bfloat16).contiguous()
+    mask_f = mask.expand(*orig_shape[:-1]).reshape(batch, N, N).to(torch.float32).contiguous()
+    out = _TurboTrimulFn.apply(z_bf, mask_f, p_in_weight, g_in_weight, g_out_weight, p_out_weight,
+                               norm_in_weight, norm_in_bias, norm_out_weight, norm_out_bias,
+                               direction == "outgoing")
+    return out.view(orig_shape).to(z.dtype)
+
+
+class _TurboTrimulFn(torch.autograd.Function):
+    """``turbo_trimul`` over its concatenated input weights.
+
+    The custom ops take the six projection weights separately; slicing
+    ``p_in`` / ``g_in`` into them under autograd would make every slice's
+    backward zero-fill and copy a full-size gradient and then sum the
+    pieces.  This node owns the concatenated weights instead and returns
+    their gradients as two row gathers of ``d_w5``.
+    """
+
+    @staticmethod
+    def forward(ctx, z_bf, mask_f, p_in, g_in, g_out_w, p_out_w, n_in_w, n_in_b, n_out_w,
+                n_out_b, outgoing):
+        H = int(p_in.shape[0]) // 2
+        ws = (p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w)
+        res = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(
+            z_bf, mask_f, *ws, n_in_w, n_in_b, n_out_w, n_out_b, bool(outgoing), True)
+        out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out = res
+        ctx.save_for_backward(z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
+                              rstd_out, p_in, g_in, g_out_w, p_out_w, n_in_w, n_out_w, out)
+        ctx.outgoing = bool(outgoing)
+        ctx.dtypes = tuple(t.dtype for t in (p_in, g_in, g_out_w, p_out_w, n_in_w, n_in_b,
+                                             n_out_w, n_out_b))
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out, p_in, g_in,
+         g_out_w, p_out_w, n_in_w, n_out_w, out) = ctx.saved_tensors
+        H = int(p_in.shape[0]) // 2
+        d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout = _trimul_bwd_v1(
+            grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
+            rstd_out, p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w, n_in_w, n_out_w,
+            out, ctx.outgoing)
+        # d_w5 rows: [a_p | a_g | b_p | b_g | g]; p_in = [a_p; b_p], g_in = [a_g; b_g].
+        pg = d_w5[:4 * H].view(2, 2, H, -1)
+        grads = (pg[:, 0].reshape(2 * H, -1), pg[:, 1].reshape(2 * H, -1), d_w5[4 * H:], d_wz,
+                 d_gin, d_bin, d_gout, d_bout)
+        grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
+        return (d_z, None, *grads, None)
 
 
 __all__ = ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]
