@@ -835,42 +835,48 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
 }
 
 // dQ = bf16(scale * sum_kb partial[kb]) in ascending key-block order; bf16
-// partials [kb][plane][h][q][D], output in Q's storage order.  Grid: x =
-// (query, 8-channel chunk) inside one (plane, head) block, y = plane * H + h
-// (strided past the grid limit).  Up to 8 partial loads are in flight; they
-// are added in key-block order.
-__global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
-    const __bf16* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
+// partials [kb][plane][h][q][D], output in Q's storage order.  One call
+// folds 256 (query, 8-channel chunk) items, chunk bx, of (plane, head) block
+// ph.  Up to 8 partial loads are in flight; they are added in key-block order.
+__device__ __forceinline__ void dq_fold_block(const __bf16* __restrict__ part,
+                                              __bf16* __restrict__ dq, const AttnGeom& g, int nkb,
+                                              int bx, int64_t ph) {
   const int D8 = g.D / 8;
-  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int t = bx * 256 + threadIdx.x;
   if (t >= g.N * D8) return;
   const int qq = t / D8, d0 = (t - qq * D8) * 8;
   const int64_t nph = (int64_t)g.B * g.O * g.H;
   const int64_t stride = nph * g.N * g.D;
-  for (int64_t ph = blockIdx.y; ph < nph; ph += gridDim.y) {
-    const int64_t plane = ph / g.H;
-    const int hh = (int)(ph - plane * g.H);
-    const __bf16* src = part + (ph * g.N + qq) * g.D + d0;
-    float acc[8];
+  const int64_t plane = ph / g.H;
+  const int hh = (int)(ph - plane * g.H);
+  const __bf16* src = part + (ph * g.N + qq) * g.D + d0;
+  float acc[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int k0 = 0; k0 < nkb; k0 += 8) {
-      bf16x8 x[8];
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int k0 = 0; k0 < nkb; k0 += 8) {
+    bf16x8 x[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k0 + u < nkb) x[u] = ld8(src + (int64_t)(k0 + u) * stride);
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u < nkb) x[u] = ld8(src + (int64_t)(k0 + u) * stride);
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k0 + u < nkb) {
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u < nkb) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] = (k0 + u == 0) ? bf2f(x[u][e]) : acc[e] + bf2f(x[u][e]);
-        }
-    }
-    bf16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
-    st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
+        for (int e = 0; e < 8; ++e) acc[e] = (k0 + u == 0) ? bf2f(x[u][e]) : acc[e] + bf2f(x[u][e]);
+      }
   }
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
+  st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
+}
+
+// Grid: x = 256-item chunk, y = plane * H + h (strided past the grid limit).
+__global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
+    const __bf16* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
+  const int64_t nph = (int64_t)g.B * g.O * g.H;
+  for (int64_t ph = blockIdx.y; ph < nph; ph += gridDim.y)
+    dq_fold_block(part, dq, g, nkb, blockIdx.x, ph);
 }
 
 // dBias[bb,h,q,k] (f32) = fold over the bf16 (b, outer group) partials that
@@ -879,13 +885,13 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
 // thread (range s, chunk c) sums its range in ascending order (8 loads in
 // flight; each load instruction of a wave reads 1 KB contiguous), and the
 // four range sums are added in the fixed order ((s0 + s1) + s2) + s3.
-__global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
-    const __bf16* __restrict__ part, float* __restrict__ dbias, int B, int Bb,
-    int groups, int H, int N) {
+__device__ __forceinline__ void dbias_fold_block(const __bf16* __restrict__ part,
+                                                 float* __restrict__ dbias, int B, int Bb,
+                                                 int groups, int H, int N, int64_t blk) {
   __shared__ float red[4][64][9];
   const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
   const int64_t hnn8 = (int64_t)H * N * N / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 64 + c;
+  const int64_t idx = blk * 64 + c;
   const bool act = idx < (int64_t)Bb * hnn8;
   const int bb = act ? (int)(idx / hnn8) : 0;
   const int64_t e = act ? (idx % hnn8) * 8 : 0;
@@ -927,6 +933,21 @@ __global__ __launch_bounds__(256) void attn_dbias_reduce_kernel(
   float* d = dbias + (int64_t)bb * H * N * N + e;
   *reinterpret_cast<f32x4*>(d) = lo;
   *reinterpret_cast<f32x4*>(d + 4) = hi;
+}
+
+// Both folds of the backward in one launch: blocks [0, n_db) fold dBias
+// (the longer blocks first), the rest fold dQ ((plane, head) major).
+__global__ __launch_bounds__(256) void attn_fold_kernel(
+    const __bf16* __restrict__ dq_part, __bf16* __restrict__ dq, AttnGeom g, int nkb, int dq_bx,
+    const __bf16* __restrict__ db_part, float* __restrict__ dbias, int Bb, int groups,
+    int64_t n_db) {
+  const int64_t b = blockIdx.x;
+  if (b < n_db) {
+    dbias_fold_block(db_part, dbias, g.B, Bb, groups, g.H, g.N, b);
+  } else {
+    const int64_t r = b - n_db;
+    dq_fold_block(dq_part, dq, g, nkb, (int)(r % dq_bx), r / dq_bx);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1006,7 +1027,7 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
 // Pair-bias gradient into the projection gradient rows: thread = (bias batch
 // bb, query q, 8 consecutive keys); for each head, the bf16 (b, outer group)
 // partials that share bb are folded in ascending order (as in
-// attn_dbias_reduce_kernel), then every key's row receives its H values and
+// dbias_fold_block), then every key's row receives its H values and
 // zeros over the rest of the row tail [4*H*D, pitch).
 template <int HMAX>
 __global__ __launch_bounds__(256) void attn_dbias_pair_kernel(
@@ -1222,15 +1243,13 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
   const int64_t nph = B * O * H;
-  hipLaunchKernelGGL(attn_dq_reduce_kernel,
-                     dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
-                     dim3(256), 0, s, pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D));
-  int rc = check_launch(fn);
-  if (rc) return rc;
-  const int64_t db_items = bias_batches * H * N * N / 8;
-  hipLaunchKernelGGL(attn_dbias_reduce_kernel, dim3((unsigned)((db_items + 63) / 64)),
-                     dim3(256), 0, s, pt.db, dbias, (int)B, (int)bias_batches, (int)groups,
-                     (int)H, (int)N);
+  const int64_t dq_bx = (N * (D / 8) + 255) / 256;
+  const int64_t n_db = (bias_batches * H * N * N / 8 + 63) / 64;
+  const int64_t blocks = n_db + dq_bx * nph;
+  if (blocks > 0x7fffffff) return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
+  hipLaunchKernelGGL(attn_fold_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pt.dq,
+                     (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
+                     (int)bias_batches, (int)groups, n_db);
   return check_launch(fn);
 }
 
