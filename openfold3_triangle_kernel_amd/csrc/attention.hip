@@ -109,7 +109,8 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  One workgroup = 4 waves = 128 queries of one plane; each wave owns
+// Forward.  One workgroup = NW waves = 32*NW queries of one plane (NW = 4:
+// 2, 3 and 6 measured slower at N = 384); each wave owns
 // 32 queries and walks all keys in 64-key tiles staged in LDS (double
 // buffered, fetched into registers one tile ahead).  Scores are produced
 // transposed (S^T = K Q^T) so each lane owns one query column: row max / sum
@@ -123,15 +124,17 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
 // running max is raised only when a block exceeds it by more than 8 in log2
 // units (p <= 256 otherwise), so the O rescale is rare.
 // ---------------------------------------------------------------------------
-template <int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 4 : 2, 8))) void attn_fwd_kernel(
+template <int DP, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 4 : 2, 8))) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
     const float* __restrict__ bias_s, __bf16* __restrict__ out,
     float* __restrict__ lse, AttnGeom g) {
   constexpr int KP = DP + 8;     // K tile pitch (bf16): conflict-free 16-byte reads
   constexpr int VP = 64 + 4;     // V^T tile pitch (bf16): conflict-free 8-byte reads
-  constexpr int KITEMS = 64 * DP / 8;   // 16-byte K chunks per tile (one per thread)
+  constexpr int NT = 64 * NW;           // threads
+  constexpr int QT = 32 * NW;           // queries per workgroup
+  constexpr int KITEMS = 64 * DP / 8;   // 16-byte K chunks per tile
   constexpr int VITEMS = 16 * DP / 8;   // (4-key group, 8-channel chunk) V items
   __shared__ __attribute__((aligned(16))) __bf16 Ks[2][64 * KP];
   __shared__ __attribute__((aligned(16))) __bf16 Vt[2][DP * VP];
@@ -140,11 +143,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
   const int ql = lane & 31, hl = lane >> 5;
   const int N = g.N, D = g.D;
   TileId tile;
-  const int qtiles = (N + 127) / 128;
+  const int qtiles = (N + QT - 1) / QT;
   if (!xcd_tile((int64_t)qtiles * g.H * g.B * g.O, qtiles, g.B * g.O, &tile)) return;
   const int h = tile.h, plane = tile.plane;
   const int b = plane / g.O;
-  const int q0 = tile.qt * 128 + w * 32;
+  const int q0 = tile.qt * QT + w * 32;
   const bool active = q0 < N;
   const int qi = q0 + ql;
 
@@ -170,7 +173,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
 
   // K: thread -> (key, 8-channel chunk) items; V: thread -> (4-key group,
   // chunk), transposed into Vt[d][key] with 8-byte stores.
-  constexpr int KPT = (KITEMS + 255) / 256;  // K items per thread
+  constexpr int KPT = (KITEMS + NT - 1) / NT;  // K items per thread
+  static_assert(VITEMS <= NT, "V items");
   const int vgrp = tid % 16, vc = tid / 16;
   const bool vthread = tid < VITEMS;
   const bool vload = vthread && vc * 8 < D;
@@ -178,7 +182,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
   auto load_kv = [&](int kt) {
 #pragma unroll
     for (int it = 0; it < KPT; ++it) {
-      const int idx = it * 256 + tid;
+      const int idx = it * NT + tid;
       const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
       kr[it] = (idx < KITEMS && kc * 8 < D) ? ld8(kb + (int64_t)(kt + kkey) * g.s_row + kc * 8) : zero8();
     }
@@ -189,7 +193,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 
   auto store_kv = [&](int buf) {
 #pragma unroll
     for (int it = 0; it < KPT; ++it) {
-      const int idx = it * 256 + tid;
+      const int idx = it * NT + tid;
       const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
       if (idx < KITEMS) *reinterpret_cast<bf16x8*>(&Ks[buf][kkey * KP + kc * 8]) = kr[it];
     }
@@ -1153,7 +1157,10 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
                              const float* mask, const void* bias, const BiasView& bv,
                              int64_t bias_batches, void* out, float* lse, void* workspace,
                              hipStream_t s, const char* fn) {
-  const int64_t total = ((g.N + 127) / 128) * (int64_t)g.H * g.B * g.O;
+  // Waves (32 queries each) per workgroup.
+  constexpr int kFwdWaves32 = 4, kFwdWaves64 = 4;
+  const int nw = g.D <= 32 ? kFwdWaves32 : kFwdWaves64;
+  const int64_t total = ((g.N + 32 * nw - 1) / (32 * nw)) * (int64_t)g.H * g.B * g.O;
   if ((total + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many query tiles", fn);
   float* bias_s = (float*)workspace;
@@ -1162,10 +1169,12 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   g.bias_bstride = (bias_batches == 1) ? 0 : (int64_t)g.H * g.N * g.N;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (g.D <= 32)
-    hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(256), 0, s, (const __bf16*)q,
+    hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves32>), grid, dim3(64 * kFwdWaves32), 0, s,
+                       (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
   else
-    hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(256), 0, s, (const __bf16*)q,
+    hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves64>), grid, dim3(64 * kFwdWaves64), 0, s,
+                       (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
   return check_launch(fn);
 }
