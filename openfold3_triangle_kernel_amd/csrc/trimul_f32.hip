@@ -302,6 +302,94 @@ __global__ __launch_bounds__(256) void tm32_ln_planes_vec_kernel(const float* __
   }
 }
 
+// Planes, register-resident: workgroup = 64 positions x all channels;
+// thread = (4-position group pg = tid % 16, channel group cg = tid / 16 of
+// CPT channels).  Each thread issues all of its CPT float4 loads at once and
+// keeps the CPT x 4 block in registers; per-position channel sums go through
+// the 4 channel groups of a wave by shuffles and the 4 waves through LDS in
+// fixed order (mean first, then the centred sum of squares).  Rows of xln
+// are written as float4 runs of the thread's channels (pad channels up to
+// H4 as zeros).  Needs N % 4 == 0 and H <= 16 * CPT.
+template <int CPT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void tm32_ln_planes_reg_kernel(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float eps, float* __restrict__ xln, Tm32Geom g) {
+  constexpr int T = 64;
+  __shared__ float red[2][4][16][4];  // [pass][wave][position group][position]
+  const int tid = threadIdx.x, wv = tid >> 6, b = blockIdx.y;
+  const int pg = tid & 15, cg = tid >> 4;
+  const int64_t pb = (int64_t)blockIdx.x * T + 4 * pg;  // first position of this thread
+  const bool pos_ok = pb < g.NN;                       // NN % 4 == 0: all 4 or none
+  const int c0 = cg * CPT;
+  int64_t off = 0;
+  if (pos_ok) {
+    const uint32_t i = fdiv((uint32_t)pb, g.div_n);
+    off = (int64_t)i * g.Np + ((uint32_t)pb - i * (uint32_t)g.N);
+  }
+  float v[CPT][4];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    if (pos_ok && c0 + c < g.H)
+      t = *reinterpret_cast<const f32x4*>(x + ((int64_t)b * g.H + c0 + c) * g.PS + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[c][e] = t[e];
+  }
+  const float invH = 1.f / g.H;
+  float mean[4], rstd[4];
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    float q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        if (pass == 0) {
+          a += v[c][e];
+        } else if (c0 + c < g.H) {
+          const float d = v[c][e] - mean[e];
+          a = fmaf(d, d, a);
+        }
+      }
+      a += __shfl_xor(a, 16);
+      a += __shfl_xor(a, 32);
+      q[e] = a;
+    }
+    if ((tid & 48) == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[pass][wv][pg][e] = q[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = ((red[pass][0][pg][e] + red[pass][1][pg][e]) + red[pass][2][pg][e]) +
+                      red[pass][3][pg][e];
+      if (pass == 0) mean[e] = t * invH;
+      else rstd[e] = 1.f / sqrtf(t * invH + eps);
+    }
+  }
+  if (!pos_ok || c0 >= g.H4) return;
+#pragma unroll
+  for (int c4 = 0; c4 < CPT / 4; ++c4) {
+    if (c0 + 4 * c4 >= g.H4) continue;
+    float gm[4], bt[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = c0 + 4 * c4 + k;
+      gm[k] = c < g.H ? (gamma ? gamma[c] : 1.f) : 0.f;
+      bt[k] = c < g.H ? (beta ? beta[c] : 0.f) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = (v[4 * c4 + k][e] - mean[e]) * rstd[e] * gm[k] + bt[k];
+      *reinterpret_cast<f32x4*>(xln + ((int64_t)b * g.NN + pb + e) * g.H4 + c0 + 4 * c4) = o;
+    }
+  }
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf(-x)); }
 
 // Input projections in stored row order m (natural row = gather of m for
@@ -547,7 +635,13 @@ int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap,
   ga.M = g.N; ga.N = g.N; ga.K = g.Np; ga.alpha = 1.f; ga.bias = nullptr;
   if ((rc = gemm_f32_launch(ga, 1, 1, (int)(B * H), s, "tpf_trimul_forward_f32(contract)")))
     return rc;
-  if (N % 4 == 0 && g.Np % 4 == 0)
+  if (N % 4 == 0 && g.Np % 4 == 0 && H <= 128)
+    hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<8>, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
+                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
+  else if (N % 4 == 0 && g.Np % 4 == 0 && H <= 256)
+    hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<16>, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
+                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
+  else if (N % 4 == 0 && g.Np % 4 == 0)
     hipLaunchKernelGGL(tm32_ln_planes_vec_kernel, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
                        dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
   else

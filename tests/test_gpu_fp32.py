@@ -156,6 +156,8 @@ TRIMUL_CASES = [
     (2, 40, 48, 40, False, True, True, True, "float"),
     (1, 17, 30, 22, True, False, False, False, "none"),
     (1, 96, 128, 96, False, True, False, True, "bool"),
+    (1, 36, 64, 150, True, False, False, True, "float"),   # 16 channels per thread, H4 pad
+    (1, 32, 48, 30, False, True, False, True, "float"),    # 8 channels per thread, H4 pad
 ]
 
 
