@@ -489,10 +489,24 @@ __global__ __launch_bounds__(256, 2) void tm32_out_proj_kernel(
   const int64_t m0 = (T / tn) * 128;
   GemmOperandF32 A{xln, g.H4, (int)g.R, 0, {}, {}};
   GemmOperandF32 W{wz, g.H4, g.C, 0, {}, {}};
-  f32x16 acc[2][2];
-  gemm_tile_f32<true, true>(A, W, (int)m0, nt * 128, 0, g.H4, smem, acc);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int rl = lane & 31, hl = lane >> 5, wm = w >> 1, wn = w & 1;
+  // The gate values of this lane's accumulator elements are loaded before
+  // the main loop, so their latency overlaps it.
+  float gv[2][2][16];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = nt * 128 + 64 * wn + 32 * j + rl;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t rho = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
+        gv[j][i][r] = (c < g.C && rho < g.R) ? gate[rho * g.C4 + c] : 0.f;
+      }
+  }
+  f32x16 acc[2][2];
+  gemm_tile_f32<true, true>(A, W, (int)m0, nt * 128, 0, g.H4, smem, acc);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int c = nt * 128 + 64 * wn + 32 * j + rl;
@@ -503,7 +517,7 @@ __global__ __launch_bounds__(256, 2) void tm32_out_proj_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t rho = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * hl + (r & 3);
-        if (rho < g.R) out[rho * g.C + c] = (acc[i][j][r] + bias) * gate[rho * g.C4 + c];
+        if (rho < g.R) out[rho * g.C + c] = (acc[i][j][r] + bias) * gv[j][i][r];
       }
   }
 }
