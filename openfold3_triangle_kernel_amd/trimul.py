@@ -440,9 +440,10 @@ class _TurboTrimulFn(torch.autograd.Function):
             grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
             rstd_out, p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w, n_in_w, n_out_w,
             out, ctx.outgoing)
-        # d_w5 rows: [a_p | a_g | b_p | b_g | g]; p_in = [a_p; b_p], g_in = [a_g; b_g].
-        pg = d_w5[:4 * H].view(2, 2, H, -1)
-        grads = (pg[:, 0].reshape(2 * H, -1), pg[:, 1].reshape(2 * H, -1), d_w5[4 * H:], d_wz,
+        # d_w5 rows: [a_p | a_g | b_p | b_g | g]; p_in = [a_p; b_p], g_in = [a_g; b_g]:
+        # one transposing copy to [p | g][branch], both gradients views of it.
+        pg = d_w5[:4 * H].view(2, 2, H, -1).transpose(0, 1).contiguous()
+        grads = (pg[0].view(2 * H, -1), pg[1].view(2 * H, -1), d_w5[4 * H:], d_wz,
                  d_gin, d_bin, d_gout, d_bout)
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
         return (d_z, None, *grads, None)
