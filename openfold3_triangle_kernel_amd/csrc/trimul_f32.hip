@@ -390,7 +390,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   }
 }
 
-__device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf(-x)); }
+// Hardware exp and reciprocal (each within a few ulp: far inside the FP32
+// mode's 1e-4 bound); the IEEE division made the gating epilogue VALU-bound.
+__device__ __forceinline__ float sigmoid_f32(float x) { return sigmoidf(x); }
 
 // Input projections in stored row order m (natural row = gather of m for
 // the incoming direction).  Gated tiles write a / b planes; output-gate
