@@ -400,9 +400,14 @@ def turbo_trimul(
     batch = z.numel() // (N * N * C)
     z_bf = z.reshape(batch, N, N, C).to(torch.bfloat16).contiguous()
     mask_f = mask.expand(*orig_shape[:-1]).reshape(batch, N, N).to(torch.float32).contiguous()
-    out = _TurboTrimulFn.apply(z_bf, mask_f, p_in_weight, g_in_weight, g_out_weight, p_out_weight,
-                               norm_in_weight, norm_in_bias, norm_out_weight, norm_out_bias,
-                               direction == "outgoing")
+    params = (p_in_weight, g_in_weight, g_out_weight, p_out_weight, norm_in_weight, norm_in_bias,
+              norm_out_weight, norm_out_bias)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (z_bf,) + params):
+        out = _TurboTrimulFn.apply(z_bf, mask_f, *params, direction == "outgoing")
+    else:  # no autograd: no saved state (the op's save_state rule)
+        out = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(
+            z_bf, mask_f, p_in_weight[:H], g_in_weight[:H], p_in_weight[H:], g_in_weight[H:],
+            g_out_weight, p_out_weight, *params[4:], direction == "outgoing", False)[0]
     return out.view(orig_shape).to(z.dtype)
 
 

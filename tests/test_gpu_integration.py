@@ -230,3 +230,27 @@ def test_attention_module_chunk_size_leaves_output_unchanged(gpu, chunk_size):
         ref = m(x, mask)
         out = m(x, mask, chunk_size=chunk_size, inplace_safe=chunk_size is not None)
     assert torch.equal(ref, out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_turbo_trimul_no_grad_matches_autograd_forward(gpu, direction):
+    """Without autograd the public operator skips the saved state; the output
+    is bitwise the one of the differentiable call."""
+    from openfold3_triangle_kernel_amd import turbo_trimul
+
+    g = torch.Generator(device=gpu).manual_seed(5)
+    C, N = 64, 40
+    z = torch.randn(1, N, N, C, device=gpu, generator=g).to(torch.bfloat16)
+    w = dict(p_in_weight=torch.randn(2 * C, C, device=gpu, generator=g) / 8,
+             g_in_weight=torch.randn(2 * C, C, device=gpu, generator=g) / 8,
+             p_out_weight=torch.randn(C, C, device=gpu, generator=g) / 8,
+             g_out_weight=torch.randn(C, C, device=gpu, generator=g) / 8)
+    mask = (torch.rand(1, N, N, device=gpu, generator=g) > 0.1).float()
+    with torch.no_grad():
+        ref = turbo_trimul(z, direction, mask, **w)
+    wg = {k: v.clone().requires_grad_(True) for k, v in w.items()}
+    out = turbo_trimul(z.clone().requires_grad_(True), direction, mask, **wg)
+    assert torch.equal(ref, out.detach())
+    out.float().sum().backward()
+    assert all(t.grad is not None for t in wg.values())
