@@ -146,8 +146,10 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
 }
 
 // ---------------------------------------------------------------------------
-// LN_in over rows of z (16 lanes per row, 8 channels per lane).
+// LN_in over rows of z (16 lanes per row, 8 channels per lane).  A thread
+// handles kLnRowsRPT rows 16 apart, their loads issued together.
 // ---------------------------------------------------------------------------
+constexpr int kLnRowsRPT = 2;
 template <int C>
 __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restrict__ z,
                                                          const float* __restrict__ w,
@@ -156,43 +158,47 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
                                                          float* __restrict__ mean_out,
                                                          float* __restrict__ rstd_out, int64_t R) {
   const int l16 = threadIdx.x & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool act = (row < R) && (l16 < C / 8);
-  float x[8];
-  if (act) {
-    const bf16x8 v = ld8(z + row * C + l16 * 8);
+  const int64_t row0 = (int64_t)blockIdx.x * 16 * kLnRowsRPT + (threadIdx.x >> 4);
+  float x[kLnRowsRPT][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = bf2f(v[e]);
-  } else {
+  for (int k = 0; k < kLnRowsRPT; ++k) {
+    const int64_t row = row0 + 16 * k;
+    bf16x8 v = zero8();
+    if (row < R && l16 < C / 8) v = ld8(z + row * C + l16 * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = 0.f;
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) s += x[e];
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
-  const float mean = s * (1.f / C);
-  float v2 = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float d = act ? x[e] - mean : 0.f;
-    v2 = fmaf(d, d, v2);
+    for (int e = 0; e < 8; ++e) x[k][e] = bf2f(v[e]);
   }
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
-  const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
-  if (act) {
-    bf16x8 o;
+  for (int k = 0; k < kLnRowsRPT; ++k) {
+    const int64_t row = row0 + 16 * k;
+    const bool act = (row < R) && (l16 < C / 8);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[k][e];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
+    const float mean = s * (1.f / C);
+    float v2 = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = l16 * 8 + e;
-      o[e] = f2bf((x[e] - mean) * rstd * w[c] + bias[c]);
+      const float d = act ? x[k][e] - mean : 0.f;
+      v2 = fmaf(d, d, v2);
     }
-    st8(out + row * C + l16 * 8, o);
-    if (l16 == 0) {
-      mean_out[row] = mean;
-      rstd_out[row] = rstd;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
+    const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
+    if (act) {
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = l16 * 8 + e;
+        o[e] = f2bf((x[k][e] - mean) * rstd * w[c] + bias[c]);
+      }
+      st8(out + row * C + l16 * 8, o);
+      if (l16 == 0) {
+        mean_out[row] = mean;
+        rstd_out[row] = rstd;
+      }
     }
   }
 }
@@ -872,7 +878,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
     if ((rc = zero_fill(b, B * C * g.PS * 2, s, fn))) return rc;
     if ((rc = zero_fill(x, B * C * g.PS * 2, s, fn))) return rc;
   }
-  TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)((g.R + 15) / 16)), (const __bf16*)z, ln_in_w,
+  TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)((g.R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT))), (const __bf16*)z, ln_in_w,
                 ln_in_b, (__bf16*)zln, mean_in, rstd_in, g.R);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_in)"))) return rc;
   const int64_t tiles = (g.R + 127) / 128;
