@@ -105,7 +105,7 @@ def main():
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported; this build measures one MI355X "
-            "(the hot path has no collectives; see DESIGN.md for how it would shard)",
+            "(the hot path has no collectives: one GPU's share is the whole kernel workload)",
             file=sys.stderr,
         )
         sys.exit(2)
