@@ -57,10 +57,11 @@ constexpr int lds_bytes(int epilogue, int ns = kGNS) {
 }
 // Ring depths per kernel (measured): the short-K projections keep two
 // stages (occupancy), the long-K / large-epilogue kernels take more.
-constexpr int kInProjFwdNS = 2, kInProjBwdNS = 3, kOutProjNS = 4;
+constexpr int kInProjFwdNS = 2, kInProjBwdNS = 3, kOutProjNS = 4, kOutProjFwdNS = 2;
 __host__ __device__ constexpr int ln_bwd_ns(bool planes) { return planes ? 2 : 4; }
 constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2, kInProjBwdNS);  // d tile + [dp | dg] tile
 constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2, kOutProjNS);  // gate + dout tiles
+constexpr int kOutProjFwdLds = lds_bytes(128 * kSP * 2, kOutProjFwdNS);  // gate tile
 constexpr int ln_bwd_lds(bool planes) { return lds_bytes(128 * kSP * 2, ln_bwd_ns(planes)); }  // x tile
 
 // Element offset of position p = i*N + j inside a channel-major plane.
@@ -534,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
     const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, __bf16* __restrict__ out,
     __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, TmGeom g, int C) {
   constexpr int kStage = 128 * kSP * 2;
-  __shared__ __attribute__((aligned(1024))) char smem[kOutProjLds];
+  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kOutProjLds : kOutProjFwdLds];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
   const int64_t T = xcd_order((g.R + 127) / 128);
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
   fetch_rows(greg, gl, C, C, m0, g.R);
   if (BWD) fetch_rows(dreg, dout, C, C, m0, g.R);
   f32x16 acc[2][2];
-  gemm_tile<true, true, kOutProjNS>(A, W, (int)m0, 0, 0, H, smem, acc);
+  gemm_tile<true, true, BWD ? kOutProjNS : kOutProjFwdNS>(A, W, (int)m0, 0, 0, H, smem, acc);
   const AccPos ap;
   __bf16* Sg = reinterpret_cast<__bf16*>(smem);
   __bf16* Sd = reinterpret_cast<__bf16*>(smem + kStage);
