@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (2). */
+/* ABI revision of this header (4). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -59,11 +59,30 @@ int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const flo
                           int64_t D, int seq_major, int64_t bias_batches, double scale,
                           void* stream);
 
+/* Forward that also writes the shadow residual: residual bf16 [B, O, N, H, D]
+ * = bf16(O_f32 - f32(out)), the part of the f32 output the bf16 store of out
+ * drops.  The backward's delta then pairs dO with out + residual
+ * (tpf_attn_delta_shadow_bf16).  Replaces turbopairformer_triangle_forward_shadow_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_forward.cu:1960-1990,
+ * selected by OPENFOLD3_SR_SHADOW, turbopairformer_triangle_attention.py:247-262). */
+int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, const float* mask,
+                                 const void* bias, void* out, float* lse, void* residual,
+                                 void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
+                                 int64_t H, int64_t N, int64_t D, int seq_major,
+                                 int64_t bias_batches, double scale, void* stream);
+
 /* delta = rowsum(f32(dout) * f32(out)) for dout/out bf16 [B, O, N, H, D].
  * Replaces turbopairformer_triangle_delta_out
  * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_delta.cu:292-342). */
 int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,
                         int64_t H, int64_t N, int64_t D, void* stream);
+
+/* delta = rowsum(f32(dout) * (f32(out) + f32(residual))), residual from
+ * tpf_attn_forward_shadow_bf16.  Replaces turbopairformer_triangle_delta_shadow_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_delta.cu:343-416). */
+int tpf_attn_delta_shadow_bf16(const void* dout, const void* out, const void* residual,
+                               float* delta, int64_t B, int64_t O, int64_t H, int64_t N,
+                               int64_t D, void* stream);
 
 /* Bytes of device workspace tpf_attn_backward_bf16 needs (dQ and dBias partials). */
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
@@ -243,19 +262,23 @@ int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64_t B, int64
  * instead of proj[b, q, k, 4HD + h].  Forward writes o [B, N, N, H*D], lse
  * [B, N, H, N] f32 and the gated og = o * sigmoid(gate).  Backward takes
  * d_og and writes the whole projection gradient row into dproj (same
- * layout as proj, pad columns zeroed).  Replaces the module glue around the
+ * layout as proj, pad columns zeroed).  residual (nullable, bf16 like o):
+ * when given, the forward writes o's shadow residual there and the backward
+ * forms delta from o + residual, as the standalone shadow entry points do.
+ * Replaces the module glue around the
  * kernel (openfold3/core/model/layers/triangular_attention.py:160-243 with
  * openfold3/core/model/primitives/attention.py:640-692: q/k/v/gate/bias
  * projections split into views, gating, and the gradient concatenation). */
 int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H);
 int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int transpose_bias, void* o, float* lse, void* og, void* workspace,
-                               int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
-                               int64_t D, double scale, void* stream);
+                               int transpose_bias, void* o, float* lse, void* og, void* residual,
+                               void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
+                               int64_t H, int64_t D, double scale, void* stream);
 int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D);
 int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
                                 int transpose_bias, const void* o, const float* lse,
-                                const void* d_og, void* dproj, void* workspace,
+                                const void* residual, const void* d_og, void* dproj,
+                                void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
                                 int64_t D, double scale, void* stream);
 

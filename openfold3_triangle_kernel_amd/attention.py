@@ -62,6 +62,23 @@ def validate_attention_policy() -> None:
         )
 
 
+def shadow_enabled() -> bool:
+    """Whether the forward saves the bf16 rounding residual of its output.
+
+    The reference's ``OPENFOLD3_SR_SHADOW`` policy (default ``1``,
+    ``openfold3/core/utils/distributed_contract.py:41-44``; read at forward
+    time, ``turbopairformer_triangle_attention.py:247-262``): with the
+    residual, the backward's row term delta = sum dO * O uses O's f32 value
+    instead of its bf16 rounding.  ``TURBOPAIRFORMER_SR_SHADOW`` takes
+    precedence over the legacy name; any value other than ``0`` / ``1``
+    raises.
+    """
+    value = _env_flag("TURBOPAIRFORMER_SR_SHADOW", "OPENFOLD3_SR_SHADOW")
+    if value not in ("0", "1"):
+        raise ValueError(f"OPENFOLD3_SR_SHADOW must be 0 or 1, got {value!r}")
+    return value == "1"
+
+
 def _is_gfx950(device: torch.device) -> bool:
     idx = device.index if device.index is not None else torch.cuda.current_device()
     arch = _ARCH_CACHE.get(idx)
@@ -107,6 +124,12 @@ def _supported_uncached(q, k, v, res_mask, pair_bias) -> tuple[bool, str]:
     named = {"q": q, "k": k, "v": v, "res_mask": res_mask, "pair_bias": pair_bias}
     if any(not isinstance(t, torch.Tensor) for t in named.values()):
         return False, "all inputs must be torch.Tensor instances"
+    if q.dtype == torch.float32:
+        # FP32 q selects the inference implementation and its own contract
+        # (reference ``turbopairformer_triangle_attention.py:144-150``).
+        from .attention_fp32 import is_attention_fp32_supported
+
+        return is_attention_fp32_supported(q, k, v, res_mask, pair_bias)
     ok, reason = _device_supported(q)
     if not ok:
         return False, reason
@@ -171,21 +194,33 @@ class _TriangleAttentionFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, mask, bias_k, source_bias, seq_major, scale, bias_reduce):
+    def forward(ctx, q, k, v, mask, bias_k, source_bias, seq_major, scale, bias_reduce, shadow):
         B, O, H, N, D = (int(x) for x in q.shape)
         out = torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype)
         lse = torch.empty((B, O, H, N), device=q.device, dtype=torch.float32)
         Bb = int(bias_k.shape[0])
         ws_bytes = int(_native.query("tpf_attn_forward_workspace_bytes", B, H, N, Bb))
         workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+        residual = torch.empty_like(out) if shadow else None
         with _device_ctx(q.device):
-            _native.call(
-                "tpf_attn_forward_bf16",
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
-                out.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ws_bytes, B, O, H, N, D,
-                int(seq_major), Bb, float(scale), _native.stream_of(q),
-            )
-        ctx.save_for_backward(q, k, v, mask, bias_k, out, lse)
+            if residual is None:
+                _native.call(
+                    "tpf_attn_forward_bf16",
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
+                    out.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ws_bytes, B, O, H, N,
+                    D, int(seq_major), Bb, float(scale), _native.stream_of(q),
+                )
+            else:
+                _native.call(
+                    "tpf_attn_forward_shadow_bf16",
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
+                    out.data_ptr(), lse.data_ptr(), residual.data_ptr(), workspace.data_ptr(),
+                    ws_bytes, B, O, H, N, D, int(seq_major), Bb, float(scale),
+                    _native.stream_of(q),
+                )
+        # The residual fixes the delta path for this autograd context; the
+        # backward never rereads the environment.
+        ctx.save_for_backward(q, k, v, mask, bias_k, out, lse, residual)
         ctx.seq_major = bool(seq_major)
         ctx.scale = float(scale)
         ctx.bias_reduce = bias_reduce
@@ -195,7 +230,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_out):
-        q, k, v, mask, bias_k, out, lse = ctx.saved_tensors
+        q, k, v, mask, bias_k, out, lse, residual = ctx.saved_tensors
         B, O, H, N, D = (int(x) for x in q.shape)
         d_out = d_out.contiguous()
         if d_out.dtype != torch.bfloat16:
@@ -203,10 +238,16 @@ class _TriangleAttentionFn(torch.autograd.Function):
         with _device_ctx(q.device):
             stream = _native.stream_of(q)
             delta = torch.empty_like(lse)
-            _native.call(
-                "tpf_attn_delta_bf16", d_out.data_ptr(), out.data_ptr(), delta.data_ptr(),
-                B, O, H, N, D, stream,
-            )
+            if residual is None:
+                _native.call(
+                    "tpf_attn_delta_bf16", d_out.data_ptr(), out.data_ptr(), delta.data_ptr(),
+                    B, O, H, N, D, stream,
+                )
+            else:
+                _native.call(
+                    "tpf_attn_delta_shadow_bf16", d_out.data_ptr(), out.data_ptr(),
+                    residual.data_ptr(), delta.data_ptr(), B, O, H, N, D, stream,
+                )
             if ctx.seq_major:
                 dq, dk, dv = (
                     torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype).transpose(2, 3)
@@ -230,7 +271,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
         if ctx.bias_reduce is not None:
             d_bias = ctx.bias_reduce(d_bias)
         d_bias = d_bias.reshape(ctx.bias_shape).to(ctx.bias_dtype)
-        return dq, dk, dv, None, None, d_bias, None, None, None
+        return dq, dk, dv, None, None, d_bias, None, None, None, None
 
 
 def turbopairformer_triangle_attention(q, k, v, res_mask, pair_bias):
@@ -247,6 +288,12 @@ def turbopairformer_triangle_attention(q, k, v, res_mask, pair_bias):
         raise ValueError(f"unsupported TurboPairFormer case: {reason}")
     global _INVOCATIONS
     _INVOCATIONS += 1
+    if q.dtype == torch.float32:
+        # FP32 inference keeps FP32 storage end to end (reference ``:362-370``).
+        from .attention_fp32 import turbopairformer_attention_fp32
+
+        return turbopairformer_attention_fp32(q, k, v, res_mask, pair_bias)
+    shadow = shadow_enabled()
 
     if pair_bias.dtype == torch.float32:
         pair_bias = pair_bias.to(torch.bfloat16)
@@ -323,7 +370,7 @@ def turbopairformer_triangle_attention(q, k, v, res_mask, pair_bias):
             qf, kf, vf = (t.contiguous() for t in (qf, kf, vf))
             seq_major = False
     out = _TriangleAttentionFn.apply(
-        qf, kf, vf, mask_f, bias_k, pair_bias, seq_major, scale, bias_reduce
+        qf, kf, vf, mask_f, bias_k, pair_bias, seq_major, scale, bias_reduce, shadow
     )
     if seq_pad:
         out = out[:, :, :sequence]
@@ -350,6 +397,7 @@ def turbo_attention(q, k, v, pair_bias, res_mask=None):
 __all__ = [
     "invocation_count",
     "is_turbopairformer_supported",
+    "shadow_enabled",
     "turbo_attention",
     "turbopairformer_triangle_attention",
     "validate_attention_policy",

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
     const float* __restrict__ bias_s, __bf16* __restrict__ out,
-    float* __restrict__ lse, AttnGeom g) {
+    float* __restrict__ lse, __bf16* __restrict__ res, AttnGeom g) {
   constexpr int KP = DP + 8;     // K tile pitch (bf16): conflict-free 16-byte reads
   constexpr int VP = 64 + 4;     // V^T tile pitch (bf16): conflict-free 8-byte reads
   constexpr int NT = 64 * NW;           // threads
@@ -319,17 +319,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
 
   const float l_tot = xor32_sum(l);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  __bf16* orow = out + (((int64_t)plane * N + qi) * g.H + h) * D;
+  const int64_t orow_off = (((int64_t)plane * N + qi) * g.H + h) * D;
+  __bf16* orow = out + orow_off;
 #pragma unroll
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = db * 32 + 8 * j + 4 * hl;
       if (d0 < D) {
-        bf16x4 o4;
+        bf16x4 o4, r4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[db][4 * j + i] * inv);
+        for (int i = 0; i < 4; ++i) {
+          const float of = acc[db][4 * j + i] * inv;
+          o4[i] = f2bf(of);
+          // Shadow residual: the part of the f32 output the bf16 store drops.
+          r4[i] = f2bf(of - bf2f(o4[i]));
+        }
         *reinterpret_cast<bf16x4*>(orow + d0) = o4;
+        if (res) *reinterpret_cast<bf16x4*>(res + orow_off + d0) = r4;
       }
     }
   if (hl == 0) {
@@ -339,15 +346,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
 }
 
 // ---------------------------------------------------------------------------
-// delta[b,o,h,q] = sum_d f32(dO) * f32(O), both [B,O,N,H,D] contiguous.
+// delta[b,o,h,q] = sum_d f32(dO) * f32(O), both [B,O,N,H,D] contiguous; with
+// SHADOW, sum_d f32(dO) * (f32(O) + f32(res)) where res is the forward's bf16
+// rounding residual of O (reference: turbopairformer_triangle_delta.cu:343-416).
 // One thread per (row, 8-channel chunk), rows r = (plane, q, h): consecutive
 // lanes read consecutive 16 bytes.  A row's D/8 chunk products meet in LDS
 // (workgroup w takes items [w * per, (w + 1) * per), per a multiple of D/8)
 // and are added in chunk order.
 // ---------------------------------------------------------------------------
+template <bool SHADOW>
 __global__ __launch_bounds__(256) void attn_delta_kernel(
     const __bf16* __restrict__ dout, const __bf16* __restrict__ out,
-    float* __restrict__ delta, int64_t items, int per, int H, int N, int D) {
+    const __bf16* __restrict__ res, float* __restrict__ delta, int64_t items, int per, int H,
+    int N, int D) {
   __shared__ float part[256];
   const int tid = threadIdx.x;
   const int64_t t = (int64_t)blockIdx.x * per + tid;
@@ -355,8 +366,15 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
   float s = 0.f;
   if (act) {
     const bf16x8 x = ld8(dout + t * 8), y = ld8(out + t * 8);
+    if (SHADOW) {
+      // O_f32 ~ O_bf16 + residual, summed in f32 before the product.
+      const bf16x8 r = ld8(res + t * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s = fmaf(bf2f(x[e]), bf2f(y[e]), s);
+      for (int e = 0; e < 8; ++e) s = fmaf(bf2f(x[e]), bf2f(y[e]) + bf2f(r[e]), s);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = fmaf(bf2f(x[e]), bf2f(y[e]), s);
+    }
   }
   part[tid] = s;
   __syncthreads();
@@ -435,8 +453,9 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restr
 // buffer with direct global->LDS loads while step i computes.
 // The two key halves of an outer row add their f32 dQ tiles through LDS
 // (half 0 + half 1), and dQ leaves as one bf16 partial per key block; dBias
-// sums the 4 outer rows' bf16 dS^T tiles in LDS (fixed order) into a bf16
-// partial per outer group.  Fixed-order reducers finish both.  Tiles are
+// sums the 4 outer rows' bf16 dS^T tiles in LDS (fixed order) into an f32
+// partial per outer group (one bf16 rounding fewer than a bf16 partial: the
+// reference's error envelope on dBias needs it).  Fixed-order reducers finish both.  Tiles are
 // ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
@@ -475,7 +494,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dq_part, __bf16* __restrict__ dbias_part, AttnGeom g) {
+    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
@@ -777,7 +796,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         }
       }
     }
-    // dBias partial: the 4 outer rows' bf16 dS^T tiles summed in the fixed
+    // dBias partial (f32): the 4 outer rows' bf16 dS^T tiles summed in the fixed
     // order ((o0 + o1) + o2) + o3.  Thread = (key, 8-query block): 8-byte
     // reads of each wave's row, and each store instruction of a wave writes
     // 64 consecutive keys of one query row (128 bytes).
@@ -800,10 +819,11 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
           acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
       }
       if (key_blk0 + key < N) {
-        const uint32_t voff = (uint32_t)((8 * qb * N + key_blk0 + key) * 2);
+        const uint32_t voff = (uint32_t)((8 * qb * N + key_blk0 + key) * 4);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          __builtin_amdgcn_raw_buffer_store_b16(f2bf_bits(acc[e]), rs_db, voff, (q0 + e) * N * 2, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[e]), rs_db, voff,
+                                                (q0 + e) * N * 4, 0);
       }
     }
   };
@@ -883,13 +903,13 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
     dq_fold_block(part, dq, g, nkb, blockIdx.x, ph);
 }
 
-// dBias[bb,h,q,k] (f32) = fold over the bf16 (b, outer group) partials that
+// dBias[bb,h,q,k] (f32) = fold over the f32 (b, outer group) partials that
 // share bias batch bb (Bb == 1 folds every batch; Bb == B folds per batch).
 // Workgroup = 64 chunks of 8 consecutive outputs x 4 ranges of partials:
-// thread (range s, chunk c) sums its range in ascending order (8 loads in
-// flight; each load instruction of a wave reads 1 KB contiguous), and the
+// thread (range s, chunk c) sums its range in ascending order (4 partials,
+// 8 loads in flight; each load instruction of a wave reads 1 KB contiguous), and the
 // four range sums are added in the fixed order ((s0 + s1) + s2) + s3.
-__device__ __forceinline__ void dbias_fold_block(const __bf16* __restrict__ part,
+__device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
                                                  float* __restrict__ dbias, int B, int Bb,
                                                  int groups, int H, int N, int64_t blk) {
   __shared__ float red[4][64][9];
@@ -904,21 +924,28 @@ __device__ __forceinline__ void dbias_fold_block(const __bf16* __restrict__ part
   const int per = (n + 3) / 4;
   const int s0 = sl * per, s1 = min(n, s0 + per);
   const int64_t stride = (int64_t)H * N * N;
-  const __bf16* src = part + (int64_t)b_lo * groups * stride + e;
+  const float* src = part + (int64_t)b_lo * groups * stride + e;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   if (act) {
-    for (int s = s0; s < s1; s += 8) {
-      bf16x8 x[8];
+    for (int s = s0; s < s1; s += 4) {
+      f32x4 x[4][2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (s + u < s1) x[u] = ld8(src + (int64_t)(s + u) * stride);
+      for (int u = 0; u < 4; ++u)
+        if (s + u < s1) {
+          const float* p = src + (int64_t)(s + u) * stride;
+          x[u][0] = *reinterpret_cast<const f32x4*>(p);
+          x[u][1] = *reinterpret_cast<const f32x4*>(p + 4);
+        }
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 4; ++u)
         if (s + u < s1) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = (s + u == s0) ? bf2f(x[u][i]) : acc[i] + bf2f(x[u][i]);
+          for (int i = 0; i < 8; ++i) {
+            const float xv = x[u][i >> 2][i & 3];
+            acc[i] = (s + u == s0) ? xv : acc[i] + xv;
+          }
         }
     }
   }
@@ -943,7 +970,7 @@ __device__ __forceinline__ void dbias_fold_block(const __bf16* __restrict__ part
 // (the longer blocks first), the rest fold dQ ((plane, head) major).
 __global__ __launch_bounds__(256) void attn_fold_kernel(
     const __bf16* __restrict__ dq_part, __bf16* __restrict__ dq, AttnGeom g, int nkb, int dq_bx,
-    const __bf16* __restrict__ db_part, float* __restrict__ dbias, int Bb, int groups,
+    const float* __restrict__ db_part, float* __restrict__ dbias, int Bb, int groups,
     int64_t n_db) {
   const int64_t b = blockIdx.x;
   if (b < n_db) {
@@ -960,7 +987,8 @@ __global__ __launch_bounds__(256) void attn_fold_kernel(
 //   forward   og = o * sigmoid(g)
 //   backward  d_o = d_og * sigmoid(g),  dg = d_og * o * s * (1 - s), and
 //             delta[b,i,h,j] = sum_d d_o * o (the softmax backward's row term;
-//             the D/8 chunk partials of a head meet in LDS).
+//             the D/8 chunk partials of a head meet in LDS), with o + res when
+//             the forward saved the shadow residual res of o.
 // o / og / d_og / d_o are [B, N, N, H*D] rows; g and dg sit at the gate
 // columns (offset 3*H*D) of the projection rows (row pitch `pitch`).
 // ---------------------------------------------------------------------------
@@ -984,9 +1012,11 @@ __global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __rest
 
 // Workgroup w takes items [w * per, (w + 1) * per) with per a multiple of
 // D/8, so a head's chunks never straddle two workgroups.
+template <bool SHADOW>
 __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     const __bf16* __restrict__ d_og, const __bf16* __restrict__ o,
-    const __bf16* __restrict__ gate, int64_t pitch, __bf16* __restrict__ d_o,
+    const __bf16* __restrict__ res, const __bf16* __restrict__ gate, int64_t pitch,
+    __bf16* __restrict__ d_o,
     float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, int N, int H,
     int D) {
   __shared__ float part[256];
@@ -1000,6 +1030,8 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     const int c = (int)(t - row * hc8);
     const bf16x8 dv = ld8(d_og + t * 8), ov = ld8(o + t * 8),
                  gv = ld8(gate + row * pitch + c * 8);
+    bf16x8 rv;
+    if (SHADOW) rv = ld8(res + t * 8);
     bf16x8 r_do, r_dg;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1007,8 +1039,9 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
       const float dd = bf2f(dv[e]), oo = bf2f(ov[e]);
       r_do[e] = f2bf(dd * sg);
       r_dg[e] = f2bf(dd * oo * sg * (1.f - sg));
-      // delta pairs the bf16 dO that the backward kernel reads with O.
-      sdot = fmaf(bf2f(r_do[e]), oo, sdot);
+      // delta pairs the bf16 dO that the backward kernel reads with O (with
+      // SHADOW, with O + its rounding residual, summed in f32).
+      sdot = fmaf(bf2f(r_do[e]), SHADOW ? oo + bf2f(rv[e]) : oo, sdot);
     }
     st8(d_o + t * 8, r_do);
     st8(dgate + row * pitch + c * 8, r_dg);
@@ -1029,13 +1062,13 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
 }
 
 // Pair-bias gradient into the projection gradient rows: thread = (bias batch
-// bb, query q, 8 consecutive keys); for each head, the bf16 (b, outer group)
+// bb, query q, 8 consecutive keys); for each head, the f32 (b, outer group)
 // partials that share bb are folded in ascending order (as in
 // dbias_fold_block), then every key's row receives its H values and
 // zeros over the rest of the row tail [4*H*D, pitch).
 template <int HMAX>
 __global__ __launch_bounds__(256) void attn_dbias_pair_kernel(
-    const __bf16* __restrict__ part, int B, int Bb, int groups, int H, int N,
+    const float* __restrict__ part, int B, int Bb, int groups, int H, int N,
     __bf16* __restrict__ dproj, int64_t pitch, int64_t tail_off, int transpose_bias) {
   const int64_t nn8 = (int64_t)N * N / 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1052,27 +1085,32 @@ __global__ __launch_bounds__(256) void attn_dbias_pair_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i][h] = 0.f;
     if (h >= H) continue;
-    const __bf16* src = part + (int64_t)b_lo * groups * stride + (int64_t)h * N * N + e;
+    const float* src = part + (int64_t)b_lo * groups * stride + (int64_t)h * N * N + e;
+    auto ld = [&](int s, int i) { return src[(int64_t)s * stride + i]; };
     float a[8];
     {
-      const bf16x8 x = ld8(src);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = bf2f(x[i]);
+      for (int i = 0; i < 4; ++i) { a[i] = x0[i]; a[4 + i] = x1[i]; }
     }
     int s = 1;
     for (; s + 4 <= n; s += 4) {
-      bf16x8 x[4];
+      f32x4 x[4][2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) x[u] = ld8(src + (int64_t)(s + u) * stride);
+      for (int u = 0; u < 4; ++u) {
+        const float* p = src + (int64_t)(s + u) * stride;
+        x[u][0] = *reinterpret_cast<const f32x4*>(p);
+        x[u][1] = *reinterpret_cast<const f32x4*>(p + 4);
+      }
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] += bf2f(x[u][i]);
+        for (int i = 0; i < 8; ++i) a[i] += x[u][i >> 2][i & 3];
     }
     for (; s < n; ++s) {
-      const bf16x8 x = ld8(src + (int64_t)s * stride);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] += bf2f(x[i]);
+      for (int i = 0; i < 8; ++i) a[i] += ld(s, i);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i][h] = a[i];
@@ -1155,8 +1193,8 @@ static int attn_prescale_bias(const AttnGeom& g, const void* bias, const BiasVie
 
 static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const void* v,
                              const float* mask, const void* bias, const BiasView& bv,
-                             int64_t bias_batches, void* out, float* lse, void* workspace,
-                             hipStream_t s, const char* fn) {
+                             int64_t bias_batches, void* out, float* lse, void* res,
+                             void* workspace, hipStream_t s, const char* fn) {
   // Waves (32 queries each) per workgroup.
   constexpr int kFwdWaves32 = 4, kFwdWaves64 = 4;
   const int nw = g.D <= 32 ? kFwdWaves32 : kFwdWaves64;
@@ -1171,20 +1209,22 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   if (g.D <= 32)
     hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves32>), grid, dim3(64 * kFwdWaves32), 0, s,
                        (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
+                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
+                       (__bf16*)res, g);
   else
     hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves64>), grid, dim3(64 * kFwdWaves64), 0, s,
                        (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse, g);
+                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
+                       (__bf16*)res, g);
   return check_launch(fn);
 }
 
-// Backward workspace: bf16 dQ partials [key blocks][B,O,H,N,D] | bf16 dBias
+// Backward workspace: bf16 dQ partials [key blocks][B,O,H,N,D] | f32 dBias
 // partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
 // f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
 struct BwdParts {
   __bf16* dq;
-  __bf16* db;
+  float* db;
   float* bias_f;
   float* nl2;
   float* nd;
@@ -1199,12 +1239,12 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   int64_t off = 0;
   auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
   char* dq = take(bwd_key_blocks(N, D) * rows * D * 2);
-  char* db = take(B * groups * H * N * N * 2);
+  char* db = take(B * groups * H * N * N * 4);
   char* bf = take(B * H * N * N * 4);
   char* nl = take(rows * 4);
   char* nd = take(rows * 4);
   if (parts) {
-    parts->dq = (__bf16*)dq; parts->db = (__bf16*)db; parts->bias_f = (float*)bf;
+    parts->dq = (__bf16*)dq; parts->db = (float*)db; parts->bias_f = (float*)bf;
     parts->nl2 = (float*)nl; parts->nd = (float*)nd;
   }
   return off;
@@ -1284,20 +1324,58 @@ int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const flo
   if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
   return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
-                           out, lse, workspace, (hipStream_t)stream, fn);
+                           out, lse, nullptr, workspace, (hipStream_t)stream, fn);
+}
+
+int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, const float* mask,
+                                 const void* bias, void* out, float* lse, void* residual,
+                                 void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
+                                 int64_t H, int64_t N, int64_t D, int seq_major,
+                                 int64_t bias_batches, double scale, void* stream) {
+  const char* fn = "tpf_attn_forward_shadow_bf16";
+  AttnGeom g;
+  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  if (rc) return rc;
+  if (!q || !k || !v || !mask || !bias || !out || !lse || !residual || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+                           out, lse, residual, workspace, (hipStream_t)stream, fn);
+}
+
+static int attn_delta_launch(const void* dout, const void* out, const void* res, float* delta,
+                             int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                             void* stream, const char* fn) {
+  if (!dout || !out || !delta) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 8 || D > 64 || D % 8)
+    return set_error(TPF_ERR_SHAPE, "%s: bad shape", fn);
+  const int64_t items = B * O * N * H * (D / 8);
+  const int per = 256 - 256 % (int)(D / 8);
+  const dim3 grid((unsigned)((items + per - 1) / per));
+  if (res)
+    hipLaunchKernelGGL(attn_delta_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const __bf16*)dout, (const __bf16*)out, (const __bf16*)res, delta, items,
+                       per, (int)H, (int)N, (int)D);
+  else
+    hipLaunchKernelGGL(attn_delta_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const __bf16*)dout, (const __bf16*)out, (const __bf16*)nullptr, delta,
+                       items, per, (int)H, (int)N, (int)D);
+  return check_launch(fn);
 }
 
 int tpf_attn_delta_bf16(const void* dout, const void* out, float* delta, int64_t B, int64_t O,
                         int64_t H, int64_t N, int64_t D, void* stream) {
-  if (!dout || !out || !delta) return set_error(TPF_ERR_ARG, "tpf_attn_delta_bf16: null pointer");
-  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 8 || D > 64 || D % 8)
-    return set_error(TPF_ERR_SHAPE, "tpf_attn_delta_bf16: bad shape");
-  const int64_t items = B * O * N * H * (D / 8);
-  const int per = 256 - 256 % (int)(D / 8);
-  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((items + per - 1) / per)), dim3(256), 0,
-                     (hipStream_t)stream, (const __bf16*)dout, (const __bf16*)out, delta, items,
-                     per, (int)H, (int)N, (int)D);
-  return check_launch("tpf_attn_delta_bf16");
+  return attn_delta_launch(dout, out, nullptr, delta, B, O, H, N, D, stream,
+                           "tpf_attn_delta_bf16");
+}
+
+int tpf_attn_delta_shadow_bf16(const void* dout, const void* out, const void* residual,
+                               float* delta, int64_t B, int64_t O, int64_t H, int64_t N,
+                               int64_t D, void* stream) {
+  if (!residual) return set_error(TPF_ERR_ARG, "tpf_attn_delta_shadow_bf16: null pointer");
+  return attn_delta_launch(dout, out, residual, delta, B, O, H, N, D, stream,
+                           "tpf_attn_delta_shadow_bf16");
 }
 
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
@@ -1399,9 +1477,9 @@ int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H) {
 }
 
 int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int transpose_bias, void* o, float* lse, void* og, void* workspace,
-                               int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
-                               int64_t D, double scale, void* stream) {
+                               int transpose_bias, void* o, float* lse, void* og, void* residual,
+                               void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
+                               int64_t H, int64_t D, double scale, void* stream) {
   const char* fn = "tpf_attn_pair_forward_bf16";
   AttnGeom g;
   BiasView bv;
@@ -1416,8 +1494,10 @@ int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mas
   const int64_t hc = H * D;
   const __bf16* p = (const __bf16*)proj;
   hipStream_t s = (hipStream_t)stream;
+  if (residual && (uintptr_t)residual % 16)
+    return set_error(TPF_ERR_ARG, "%s: residual must be 16-byte aligned", fn);
   if ((rc = attn_forward_impl(g, p, p + hc, p + 2 * hc, mask, p + 4 * hc, bv, B, o, lse,
-                              workspace, s, fn)))
+                              residual, workspace, s, fn)))
     return rc;
   const int64_t items = B * N * N * (hc / 8);
   hipLaunchKernelGGL(attn_gate_fwd_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
@@ -1434,7 +1514,8 @@ int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, 
 
 int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
                                 int transpose_bias, const void* o, const float* lse,
-                                const void* d_og, void* dproj, void* workspace,
+                                const void* residual, const void* d_og, void* dproj,
+                                void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
                                 int64_t D, double scale, void* stream) {
   const char* fn = "tpf_attn_pair_backward_bf16";
@@ -1457,9 +1538,15 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   hipStream_t s = (hipStream_t)stream;
   const int64_t items = B * N * N * (hc / 8);
   const int per = 256 - 256 % (int)(D / 8);
-  hipLaunchKernelGGL(attn_gate_bwd_kernel, dim3((unsigned)((items + per - 1) / per)), dim3(256), 0,
-                     s, (const __bf16*)d_og, (const __bf16*)o, p + 3 * hc, pitch, d_o, delta,
-                     dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
+  const dim3 ggrid((unsigned)((items + per - 1) / per));
+  if (residual)
+    hipLaunchKernelGGL(attn_gate_bwd_kernel<true>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
+                       (const __bf16*)o, (const __bf16*)residual, p + 3 * hc, pitch, d_o, delta,
+                       dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
+  else
+    hipLaunchKernelGGL(attn_gate_bwd_kernel<false>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
+                       (const __bf16*)o, (const __bf16*)nullptr, p + 3 * hc, pitch, d_o, delta,
+                       dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
   if ((rc = check_launch(fn))) return rc;
   if ((rc = attn_backward_main_impl(g, p, p + hc, p + 2 * hc, d_o, lse, delta, mask, p + 4 * hc,
                                     bv, B, dp + hc, dp + 2 * hc, workspace, s, fn)))

@@ -42,7 +42,12 @@ import torch
 from torch import nn
 
 from . import _native, routing
-from .attention import _device_ctx, is_turbopairformer_supported, turbopairformer_triangle_attention
+from .attention import (
+    _device_ctx,
+    is_turbopairformer_supported,
+    shadow_enabled,
+    turbopairformer_triangle_attention,
+)
 from .attention_fp32 import turbopairformer_attention_fp32
 from .layernorm import layer_norm_bf16
 from .trimul import check_stable_trimul_support, run_stable_trimul
@@ -129,12 +134,16 @@ class _PairAttentionCore(torch.autograd.Function):
         ws_bytes = int(_native.query("tpf_attn_pair_forward_workspace_bytes", B, N, H))
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         scale = 1.0 / math.sqrt(D)
+        # Shadow residual of o (the facade's OPENFOLD3_SR_SHADOW policy): the
+        # backward's delta then sees o's f32 value.
+        res = torch.empty_like(o) if shadow_enabled() else None
         with _device_ctx(dev):
             _native.call("tpf_attn_pair_forward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
                          int(transpose_bias), o.data_ptr(), lse.data_ptr(), og.data_ptr(),
-                         ws.data_ptr(), ws_bytes, B, N, H, D, scale, _native.stream_of(proj))
+                         _native.ptr(res), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
+                         _native.stream_of(proj))
         out = og @ wo.t()
-        ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add)
+        ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add, res)
         ctx.dims = (B, N, H, D, C, P, bool(transpose_bias), scale)
         ctx.w_dtypes = (w_all.dtype, w_o.dtype)
         ctx.set_materialize_grads(False)
@@ -144,7 +153,7 @@ class _PairAttentionCore(torch.autograd.Function):
     def backward(ctx, dout):
         if dout is None:
             return (None,) * 7
-        x2, wa, wo, proj, o, og, lse, mask_add = ctx.saved_tensors
+        x2, wa, wo, proj, o, og, lse, mask_add, res = ctx.saved_tensors
         B, N, H, D, C, P, transpose_bias, scale = ctx.dims
         R = B * N * N
         dev = x2.device
@@ -156,8 +165,9 @@ class _PairAttentionCore(torch.autograd.Function):
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         with _device_ctx(dev):
             _native.call("tpf_attn_pair_backward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
-                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), d_og.data_ptr(),
-                         dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
+                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), _native.ptr(res),
+                         d_og.data_ptr(), dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D,
+                         scale,
                          _native.stream_of(dproj))
         dx = (dproj @ wa).view(B, N, N, C) if ctx.needs_input_grad[0] else None
         dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None

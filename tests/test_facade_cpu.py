@@ -46,18 +46,31 @@ class FakeBackend:
 
     def __call__(self, name, *a):
         self.calls.append(name)
-        if name == "tpf_attn_forward_bf16":
-            q, k, v, mask, bias, out, lse, ws, wsb, B, O, H, N, D, sm, Bb, scale, _ = a
+        if name in ("tpf_attn_forward_bf16", "tpf_attn_forward_shadow_bf16"):
+            if name == "tpf_attn_forward_bf16":
+                q, k, v, mask, bias, out, lse, ws, wsb, B, O, H, N, D, sm, Bb, scale, _ = a
+                res = None
+            else:
+                q, k, v, mask, bias, out, lse, res, ws, wsb, B, O, H, N, D, sm, Bb, scale, _ = a
             Q, K, V = (self._qkv(p, B, O, H, N, D, sm) for p in (q, k, v))
             M = _arr(mask, (B, O, N), np.float32).reshape(B, O, 1, 1, N)
             Bi = _bf2f(_arr(bias, (Bb, H, N, N), np.uint16))[:, None]
             o, l, _ = attention_forward(Q, K, V, M, Bi, scale=scale)
-            _arr(out, (B, O, N, H, D), np.uint16)[...] = _f2bf(o)
+            ob = _f2bf(o)
+            _arr(out, (B, O, N, H, D), np.uint16)[...] = ob
             _arr(lse, (B, O, H, N), np.float32)[...] = l
-        elif name == "tpf_attn_delta_bf16":
-            do, out, delta, B, O, H, N, D, _ = a
+            if res is not None:
+                _arr(res, (B, O, N, H, D), np.uint16)[...] = _f2bf(o.astype(np.float32) - _bf2f(ob))
+        elif name in ("tpf_attn_delta_bf16", "tpf_attn_delta_shadow_bf16"):
+            if name == "tpf_attn_delta_bf16":
+                do, out, delta, B, O, H, N, D, _ = a
+                res = None
+            else:
+                do, out, res, delta, B, O, H, N, D, _ = a
             dO = _bf2f(_arr(do, (B, O, N, H, D), np.uint16))
             Ov = _bf2f(_arr(out, (B, O, N, H, D), np.uint16))
+            if res is not None:
+                Ov = Ov + _bf2f(_arr(res, (B, O, N, H, D), np.uint16))
             _arr(delta, (B, O, H, N), np.float32)[...] = np.swapaxes((dO * Ov).sum(-1), 2, 3)
         elif name == "tpf_attn_backward_bf16":
             (q, k, v, do, lse, delta, mask, bias, dq, dk, dv, dbias, ws, wsb, B, O, H, N, D, sm,
@@ -158,7 +171,8 @@ def test_invocation_count_and_turbo_attention_defaults(fake):
 
 
 @pytest.mark.parametrize("mutate,msg", [
-    (lambda a: a.update(q=a["q"].float()), "BF16"),
+    (lambda a: a.update(q=a["q"].half()), "BF16"),
+    (lambda a: a.update(q=a["q"].float()), "FP32"),
     (lambda a: a.update(q=a["q"][..., :1, :, :]), "k shape must match q"),
     (lambda a: a.update(q=torch.zeros(1, 2, 2, 64, 72, dtype=torch.bfloat16),
                         k=torch.zeros(1, 2, 2, 64, 72, dtype=torch.bfloat16),
@@ -198,3 +212,64 @@ def test_product_path_fails_loudly_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_LIB", None)
     with pytest.raises(RuntimeError, match="not built"):
         _native.library()
+
+
+@pytest.mark.parametrize("canonical,legacy,expect_shadow", [
+    (None, None, True),          # reference default: OPENFOLD3_SR_SHADOW=1
+    (None, "0", False),
+    ("1", "0", True),            # canonical name takes precedence
+    ("0", None, False),
+])
+def test_shadow_residual_policy_routes_entry_points(fake, monkeypatch, canonical, legacy,
+                                                    expect_shadow):
+    """The shadow flag selects the residual-saving forward and the residual
+    delta, as the reference's OPENFOLD3_SR_SHADOW does
+    (turbopairformer_triangle_attention.py:247-262)."""
+    for name, value in (("TURBOPAIRFORMER_SR_SHADOW", canonical), ("OPENFOLD3_SR_SHADOW", legacy)):
+        if value is None:
+            monkeypatch.delenv(name, raising=False)
+        else:
+            monkeypatch.setenv(name, value)
+    case = attention_case(1, 2, 2, 64, 16, mask_frac=0.1, seed=9)
+    got = _grads(*case)
+    shadow_calls = {"tpf_attn_forward_shadow_bf16", "tpf_attn_delta_shadow_bf16"}
+    plain_calls = {"tpf_attn_forward_bf16", "tpf_attn_delta_bf16"}
+    used = set(fake.calls)
+    assert (shadow_calls <= used) == expect_shadow
+    assert (plain_calls <= used) == (not expect_shadow)
+    q, k, v, mask, bias, dout = (t.numpy() for t in case)
+    ref = attention_backward(q, k, v, mask, bias, dout)
+    for g, r in zip(got[1:], ref):
+        assert max_rel(g, r) <= 2e-2
+
+
+def test_shadow_flag_rejects_other_values(fake, monkeypatch):
+    monkeypatch.setenv("TURBOPAIRFORMER_SR_SHADOW", "yes")
+    case = attention_case(1, 2, 2, 64, 16, seed=1)
+    with pytest.raises(ValueError, match="SR_SHADOW"):
+        _grads(*case)
+
+
+def test_fp32_q_delegates_to_fp32_inference(monkeypatch):
+    """FP32 q routes the verdict and the call to the FP32 implementation
+    (reference turbopairformer_triangle_attention.py:144-150, 362-370)."""
+    from openfold3_triangle_kernel_amd import attention, attention_fp32
+
+    attention._SUPPORT_CACHE.clear()
+    seen = {}
+    monkeypatch.setattr(attention_fp32, "is_attention_fp32_supported",
+                        lambda *a: (True, "fp32 verdict"))
+
+    def fake_fp32(q, k, v, m, b):
+        seen["called"] = True
+        return torch.zeros(q.shape[:-3] + (q.shape[-2], q.shape[-3], q.shape[-1]))
+
+    monkeypatch.setattr(attention_fp32, "turbopairformer_attention_fp32", fake_fp32)
+    q = torch.randn(1, 2, 2, 8, 4)
+    mask = torch.zeros(1, 2, 1, 1, 8)
+    bias = torch.zeros(1, 1, 2, 8, 8)
+    with torch.no_grad():
+        assert attention.is_turbopairformer_supported(q, q, q, mask, bias) == (True, "fp32 verdict")
+        out = attention.turbopairformer_triangle_attention(q, q, q, mask, bias)
+    assert seen["called"] and out.shape == (1, 2, 8, 2, 4)
+    attention._SUPPORT_CACHE.clear()

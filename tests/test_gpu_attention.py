@@ -81,3 +81,90 @@ def test_attention_bitwise_replay(gpu):
     b = _run(case, gpu)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+@pytest.mark.gpu
+def test_config2_readme_shape(gpu):
+    """Config 2 exactly: q/k/v [1,128,4,128,32], bias [1,1,4,128,128] N(0,1),
+    the last 13 keys masked, every output and gradient against the FP64
+    oracle (dBias folds all 128 outer rows)."""
+    print("[attn parity] config 2 [1,128,4,128,32] mask tail 13", flush=True)
+    case = attention_case(1, 128, 4, 128, 32, mask_tail=13, seed=2)
+    q, k, v, mask, bias, dout = (t.numpy() for t in case)
+    ref_out, _, _ = attention_forward(q, k, v, mask, bias)
+    ref = [ref_out, *attention_backward(q, k, v, mask, bias, dout)]
+    got = _run(case, gpu)
+    for n, g_, r in zip(["out", "dq", "dk", "dv", "dbias"], got, ref):
+        e = max_rel(g_, r)
+        print(n, f"{e:.3e}", flush=True)
+        assert e <= TOL, f"config 2: {n} max-rel {e:.3e} > {TOL}"
+
+
+def _bias_variant(gpu, B, O, H, N, D, bias_shape, bias_dtype, seed):
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    q, k, v, mask, _, dout = attention_case(B, O, H, N, D, mask_frac=0.15, seed=seed)
+    g = torch.Generator().manual_seed(seed + 100)
+    bias = torch.randn(bias_shape, generator=g).to(torch.bfloat16).float()
+    tq, tk, tv = (t.to(gpu, torch.bfloat16).requires_grad_(True) for t in (q, k, v))
+    tb = bias.to(gpu, bias_dtype).requires_grad_(True)
+    out = turbopairformer_triangle_attention(tq, tk, tv, mask.to(gpu), tb)
+    out.backward(dout.to(gpu, torch.bfloat16))
+    torch.cuda.synchronize()
+    assert tb.grad.dtype == bias_dtype and tuple(tb.grad.shape) == tuple(bias_shape)
+    ref_out, _, _ = attention_forward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), bias.numpy())
+    ref = [ref_out, *attention_backward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(),
+                                        bias.numpy(), dout.numpy())]
+    got = [t.detach().float().cpu().numpy() for t in (out, tq.grad, tk.grad, tv.grad, tb.grad)]
+    for n, g_, r in zip(["out", "dq", "dk", "dv", "dbias"], got, ref):
+        assert g_.shape == r.shape, (n, g_.shape, r.shape)
+        e = max_rel(g_, r)
+        print(n, f"{e:.3e}", flush=True)
+        assert e <= TOL, f"{n} max-rel {e:.3e} > {TOL}"
+
+
+@pytest.mark.gpu
+def test_per_batch_bf16_bias_backward(gpu):
+    """A bias per batch element ([B,1,H,N,N], Bb = B): each batch's dBias is
+    folded over its own outer rows only."""
+    print("[attn parity] per-batch bias B=2", flush=True)
+    _bias_variant(gpu, 2, 6, 2, 128, 32, (2, 1, 2, 128, 128), torch.bfloat16, seed=11)
+
+
+@pytest.mark.gpu
+def test_partially_broadcast_bias_backward(gpu):
+    """Prefix [2, 3] with a bias prefix [1, 3]: per-batch gradients summed over
+    the broadcast dimension (reference dq_dbias.py:326-376)."""
+    print("[attn parity] partial broadcast bias prefix (1,3) of (2,3)", flush=True)
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    P0, P1, O, H, N, D = 2, 3, 4, 2, 64, 16
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(P0, P1, O, H, N, D, generator=g).to(torch.bfloat16).float()
+               for _ in range(3))
+    mask = torch.zeros(P0, P1, O, 1, 1, N)
+    mask[torch.rand(P0, P1, O, 1, 1, N, generator=g) < 0.2] = float("-inf")
+    bias = torch.randn(1, P1, 1, H, N, N, generator=g).to(torch.bfloat16).float()
+    dout = torch.randn(P0, P1, O, N, H, D, generator=g).to(torch.bfloat16).float()
+    tq, tk, tv = (t.to(gpu, torch.bfloat16).requires_grad_(True) for t in (q, k, v))
+    tb = bias.to(gpu, torch.bfloat16).requires_grad_(True)
+    out = turbopairformer_triangle_attention(tq, tk, tv, mask.to(gpu), tb)
+    out.backward(dout.to(gpu, torch.bfloat16))
+    torch.cuda.synchronize()
+    ref_out, _, _ = attention_forward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), bias.numpy())
+    ref = [ref_out, *attention_backward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(),
+                                        bias.numpy(), dout.numpy())]
+    got = [t.detach().float().cpu().numpy() for t in (out, tq.grad, tk.grad, tv.grad, tb.grad)]
+    for n, g_, r in zip(["out", "dq", "dk", "dv", "dbias"], got, ref):
+        assert g_.shape == r.shape, (n, g_.shape, r.shape)
+        e = max_rel(g_, r)
+        print(n, f"{e:.3e}", flush=True)
+        assert e <= TOL, f"{n} max-rel {e:.3e} > {TOL}"
+
+
+@pytest.mark.gpu
+def test_fp32_pair_bias_gets_fp32_gradient(gpu):
+    """An FP32 pair_bias is rounded to bf16 for the kernels and its gradient
+    comes back in FP32 (reference turbopairformer_triangle_attention.py:371-377)."""
+    print("[attn parity] fp32 pair bias", flush=True)
+    _bias_variant(gpu, 1, 8, 4, 192, 32, (1, 1, 4, 192, 192), torch.float32, seed=12)

@@ -131,11 +131,10 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
     The reference's module check (scripts/benchmarks/
     turbopairformer_module_wiring_smoke.py:90-130) gates the output and the
     input gradient (absolute gap < 0.1) and bitwise replay, and only reports
-    the parameter gradients.  Here: output and input gradient max-rel <= 2e-2;
-    parameter gradients max-rel <= 3e-2 (a weight gradient sums B*N^2 rows of
-    signed terms, so the bf16 roundings of dQ / dK / dS stand out against a
-    largely cancelled total: linear_q's lands at 1e-2 .. 2.1e-2 on both
-    routes); a second pass is bitwise identical."""
+    the parameter gradients.  Here the output, the input gradient and every
+    parameter gradient are gated at max-rel <= 2e-2,
+    under the default shadow-residual policy; a second pass is bitwise
+    identical."""
     from openfold3_triangle_kernel_amd import TriangleAttention
 
     torch.manual_seed(7)
@@ -171,7 +170,7 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
         err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
         print(f"module starting={starting} N={N} tb={transpose_bias} {name} max-rel {err:.3e}",
               flush=True)
-        assert err <= (2e-2 if name in ("out", "x") else 3e-2), f"{name}: {err:.3e}"
+        assert err <= 2e-2, f"{name}: {err:.3e}"
 
 
 @pytest.mark.gpu
@@ -180,8 +179,8 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
 def test_trimul_module_backward(gpu, outgoing, N):
     """BF16 TriMul module (run_stable_trimul) forward + input / parameter
     gradients vs the module's stock math in FP32 on the same bf16-representable
-    weights (LayerNorm affine perturbed from identity): output and input
-    gradient max-rel <= 2e-2, parameter gradients <= 3e-2; bitwise replay;
+    weights (LayerNorm affine perturbed from identity): output, input and
+    parameter gradients max-rel <= 2e-2; bitwise replay;
     the stock math never runs on the stable route."""
     from openfold3_triangle_kernel_amd import (
         TriangleMultiplicationIncoming,
@@ -218,4 +217,4 @@ def test_trimul_module_backward(gpu, outgoing, N):
     for name, a, b in zip(names, [out] + list(grads), [ref] + list(ref_grads)):
         err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
         print(f"trimul module out={outgoing} N={N} {name} max-rel {err:.3e}", flush=True)
-        assert err <= (2e-2 if name in ("out", "x") else 3e-2), f"{name}: {err:.3e}"
+        assert err <= 2e-2, f"{name}: {err:.3e}"

@@ -1,0 +1,142 @@
+"""The reference's numeric qualification gate for triangle attention, on MI355X.
+
+Restates the release smoke of the reference (tools/aot_numeric_smoke.py:94-140
+for the seven production cases, :174-180 for the rule): every output and
+gradient of the kernels, measured as relative L2 error against an FP64
+oracle, must satisfy
+
+    rel_L2(ours) <= 1.1 * rel_L2(stock) + 1e-6
+
+where "stock" is the BF16-matmul / FP32-softmax PyTorch attention of the
+stock OpenFold3 route (:50-60), run here on the same GPU through torch.
+The FP64 oracle is ``oracle.attention`` (closed-form forward and backward,
+pinned in tests/test_oracle_attention.py); the smoke tool's finite mask
+(-inf -> -1e4, :30-36) only differs on fully masked rows, whose outputs are
+cropped as the tool does and whose gradients are zero either way.
+
+Besides the gate, each case checks what the tool checks: finite values,
+bitwise self-replay and exact zeros on fully masked planes.  The production
+flags of the tool keep the shadow residual on (``PROD_FLAGS``, :31), and the
+rule gates that policy; the same cases also run with it off (the reference's
+ablation setting), held to 1.3 * stock.
+
+Published H100 values (release_artifacts/turbopairformer-h100-20260918/
+single_h100_numerics.json:130-412) are printed beside ours for reference.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import attention_backward, attention_forward
+
+LABELS = ("out", "dq", "dk", "dv", "dbias")
+
+# (name, B, O, H, N, D, mask_frac, full_planes), aot_numeric_smoke.py:94-140
+CASES = [
+    ("prod N=128 D=32", 1, 8, 4, 128, 32, 0.0, 0),
+    ("prod N=100 pad D=32 masked", 1, 8, 4, 100, 32, 0.3, 0),
+    ("prod N=384 D=24", 1, 4, 4, 384, 24, 0.2, 0),
+    ("prod N=200 D=20 padD", 2, 4, 4, 200, 20, 0.2, 0),
+    ("prod N=256 D=64 full planes", 1, 6, 4, 256, 64, 0.2, 2),
+    ("prod N=384 D=48", 1, 2, 4, 384, 48, 0.1, 0),
+    ("prod N=768 D=16 H=8", 1, 2, 8, 768, 16, 0.1, 0),
+]
+
+# H100 rel-L2 of the reference kernels per case (out, dq, dk, dv, dbias).
+H100 = {
+    "prod N=128 D=32": (1.83e-3, 2.94e-3, 2.38e-3, 2.36e-3, 2.46e-3),
+    "prod N=100 pad D=32 masked": (1.80e-3, 2.95e-3, 2.41e-3, 2.32e-3, 2.44e-3),
+    "prod N=384 D=24": (1.82e-3, 2.90e-3, 2.35e-3, 2.35e-3, 1.65e-3),
+    "prod N=200 D=20 padD": (2.20e-3, 3.62e-3, 3.18e-3, 2.64e-3, 2.73e-3),
+    "prod N=256 D=64 full planes": (1.81e-3, 2.91e-3, 2.36e-3, 2.35e-3, 2.42e-3),
+    "prod N=384 D=48": (1.82e-3, 2.91e-3, 2.38e-3, 2.34e-3, 1.67e-3),
+    "prod N=768 D=16 H=8": (1.83e-3, 2.97e-3, 2.35e-3, 2.35e-3, 1.67e-3),
+}
+
+
+def _inputs(B, O, H, N, D, mask_frac, full_planes, seed=0):
+    """Same distributions as the tool's ``_case`` (:78-91), seeded on the host."""
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, O, H, N, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    mask = torch.zeros(B, O, 1, 1, N)
+    if mask_frac:
+        mask[torch.rand(B, O, 1, 1, N, generator=g) < mask_frac] = float("-inf")
+    if full_planes:
+        mask[:, :full_planes] = float("-inf")
+    bias = (torch.randn(1, 1, H, N, N, generator=g) * 2).to(torch.bfloat16)
+    dout = torch.randn(B, O, N, H, D, generator=g).to(torch.bfloat16)
+    if full_planes:
+        dout[:, :full_planes] = 0
+    return q, k, v, mask, bias, dout
+
+
+def _stock(q, k, v, mask, bias, dout):
+    """BF16 matmuls, FP32 softmax, autograd in those dtypes (tool :50-60)."""
+    q_, k_, v_ = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    b_ = bias.detach().clone().requires_grad_(True)
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    finite = torch.where(torch.isinf(mask), torch.full_like(mask, -1e4), mask)
+    s = torch.matmul(q_, k_.transpose(-1, -2)).float() * scale
+    s = s + finite + b_.float()
+    out = torch.matmul(torch.softmax(s, dim=-1).to(torch.bfloat16), v_).transpose(-2, -3)
+    out.backward(dout)
+    return [t.detach().double().cpu().numpy() for t in (out, q_.grad, k_.grad, v_.grad, b_.grad)]
+
+
+def _ours(q, k, v, mask, bias, dout):
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    q_, k_, v_ = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    b_ = bias.detach().clone().requires_grad_(True)
+    out = turbopairformer_triangle_attention(q_, k_, v_, mask, b_)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    return [t.detach() for t in (out, q_.grad, k_.grad, v_.grad, b_.grad)]
+
+
+def _rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shadow", ["1", "0"], ids=["shadow", "no-shadow"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_release_numeric_gate(gpu, monkeypatch, case, shadow):
+    name, B, O, H, N, D, frac, full = case
+    print(f"[numeric gate] {name} shadow={shadow}", flush=True)
+    monkeypatch.setenv("TURBOPAIRFORMER_SR_SHADOW", shadow)
+    inputs = _inputs(B, O, H, N, D, frac, full)
+    dev_inputs = [t.to(gpu) for t in inputs]
+    got = _ours(*dev_inputs)
+    replay = _ours(*dev_inputs)
+    for a, b in zip(got, replay):
+        assert torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)), \
+            f"{name}: not bitwise replayable"
+    got = [t.double().cpu().numpy() for t in got]
+    assert all(np.isfinite(t).all() for t in got), f"{name}: non-finite values"
+    stock = _stock(*dev_inputs)
+    q, k, v, mask, bias, dout = (t.float().numpy() for t in inputs)
+    ref_out, _, _ = attention_forward(q, k, v, mask, bias)
+    ref = [ref_out, *attention_backward(q, k, v, mask, bias, dout)]
+    if full:
+        for t in got[:4]:
+            assert np.all(t[:, :full] == 0), f"{name}: fully masked planes must be zero"
+        got[0], stock[0], ref[0] = got[0][:, full:], stock[0][:, full:], ref[0][:, full:]
+    rows = []
+    for i, label in enumerate(LABELS):
+        e, es = _rel(got[i], ref[i]), _rel(stock[i], ref[i])
+        rows.append((label, e, es, 1.1 * es + 1e-6))
+    print("  " + "  ".join(f"{l}: {e:.2e}/{es:.2e} (H100 {H100[name][i]:.2e})"
+                           for i, (l, e, es, _) in enumerate(rows)), flush=True)
+    # The rule applies to the production policy (shadow on).  Shadow off is
+    # the reference's accuracy-ablation setting: reported, and held to a
+    # looser 1.3 * stock (its delta pairs dO with the bf16-rounded output).
+    factor = 1.1 if shadow == "1" else 1.3
+    for label, e, es, _ in rows:
+        limit = factor * es + 1e-6
+        assert e <= limit, f"{name} {label}: rel-L2 {e:.3e} exceeds {factor}*stock+1e-6 = {limit:.3e}"
