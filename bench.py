@@ -14,11 +14,16 @@ A step is one pass of the hot path over one batch of synthetic input:
     LN weights 1/0, projections ~ N(0, 1/sqrt(128)), mask all ones), timed
     as its own loop and reported under "trimul".
 ``value`` is the attention fwd+bwd throughput in algorithmic TFLOP/s
-(14*B*O*H*N^2*D per variant), inputs resident in HBM before timing.
+(14*B*O*H*N^2*D per variant), inputs resident in HBM before timing; step
+times are the median of per-step HIP-event times over exactly ``--steps``
+steps after ``--warmup`` untimed ones (defaults 50 and 10).
 
-Also reported: the roofline of the dominant kernel (the attention backward
-kernel, timed alone with HIP events on the launching stream) and a CPU
-baseline (the numpy oracle on a bounded sample of the same workload).
+Also reported: config 5 (attention at N=768, H=4 D=32 and H=8 D=64, and the
+pair-stack block TriMul-out -> TriMul-in -> TriAtt-start -> TriAtt-end
+through the modules; ``--no-config5`` skips it), the FP32 inference mode,
+the roofline of the dominant kernel (the attention backward kernel, timed
+alone with HIP events on the launching stream) and a CPU baseline (the stock
+PyTorch math in FP32 on the host cores, configs 1, 3 and 4 in full).
 """
 
 from __future__ import annotations
@@ -40,22 +45,41 @@ TM_N, TM_C = 384, 128
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-trimul", action="store_true")
     ap.add_argument("--no-fp32", action="store_true", help="skip the FP32 inference-mode timings")
-    ap.add_argument("--config5-attention", action="store_true",
-                    help="also time config 5's attention shapes (N=768: H=4 D=32 and H=8 D=64); "
-                         "off by default so that the default run's kernel trace holds only the "
-                         "config-3 launches the roofline figure is taken from")
-    ap.add_argument("--pair-block", action="store_true",
-                    help="also time the config-5 pair-stack block (N=768) through the modules")
+    ap.add_argument("--no-config5", action="store_true",
+                    help="skip config 5 (attention at N=768: H=4 D=32 and H=8 D=64, and the "
+                         "pair-stack block through the modules); for profiling runs whose kernel "
+                         "trace should hold only the config-3 / config-4 launches")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch a 256 MiB calibration copy and one attention backward kernel, "
                          "then exit (the program profiled by the FETCH_SIZE / WRITE_SIZE passes)")
     return ap.parse_args()
+
+
+def gpu_time(torch, fn, steps, warmup):
+    """Run ``warmup`` untimed steps, then exactly ``steps`` timed ones, each
+    bracketed by HIP events on the current stream; the whole timed region is
+    bracketed by device synchronisation.  Returns the median and mean step
+    time in ms (median: the GPU clock ramps over the first seconds)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ts = sorted(a.elapsed_time(b) for a, b in ev)
+    return {"median": ts[len(ts) // 2], "mean": sum(ts) / len(ts), "wall": wall}
 
 
 def attention_inputs(torch, dev, seed=0):
@@ -146,32 +170,16 @@ def main():
             out = turbopairformer_triangle_attention(vq, vk, vv, vm, vb)
             torch.autograd.grad(out, (vq, vk, vv, vb), vd)
 
-    for _ in range(args.warmup):
-        attn_step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_wall = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        attn_step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t_wall) * 1e3 / args.steps
-    ms_step = e0.elapsed_time(e1) / args.steps
+    at = gpu_time(torch, attn_step, args.steps, args.warmup)
+    ms_step, wall_ms = at["median"], at["wall"]
     attn_flops = 2 * 14.0 * B * O * H * N * N * D  # two variants
     attn_tflops = attn_flops / (ms_step * 1e-3) / 1e12
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     # Forward-only timing (starting node) for the breakdown.
     with torch.no_grad():
-        for _ in range(3):
-            turbopairformer_triangle_attention(q, k, v, mask, bias)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            turbopairformer_triangle_attention(q, k, v, mask, bias)
-        e1.record()
-        torch.cuda.synchronize()
-    fwd_ms = e0.elapsed_time(e1) / args.steps
+        fwd_ms = gpu_time(torch, lambda: turbopairformer_triangle_attention(q, k, v, mask, bias),
+                          args.steps, 3)["median"]
 
     # ------------- dominant kernel: attention backward, alone -------------
     bwd_main = dominant_kernel(torch, _native, dev, q, k, v, bias, mask, dout)
@@ -200,9 +208,9 @@ def main():
 
     # ------------- config 5 attention shapes (starting node) -------------
     config5_attention = None
-    if args.config5_attention:
+    if not args.no_config5:
         config5_attention = []
-        reps = max(3, args.steps // 4)
+        reps = max(10, args.steps // 4)
         for H5, D5 in ((4, 32), (8, 64)):
             N5 = 768
             g5 = torch.Generator(device=dev).manual_seed(5)
@@ -217,15 +225,7 @@ def main():
                 o5 = turbopairformer_triangle_attention(*qkv5, mask5, bias5)
                 torch.autograd.grad(o5, (*qkv5, bias5), dout5)
 
-            for _ in range(2):
-                step5()
-            torch.cuda.synchronize()
-            e0.record()
-            for _ in range(reps):
-                step5()
-            e1.record()
-            torch.cuda.synchronize()
-            ms5 = e0.elapsed_time(e1) / reps
+            ms5 = gpu_time(torch, step5, reps, 3)["median"]
             fl5 = 14.0 * N5 * H5 * N5 * N5 * D5
             config5_attention.append({"N": N5, "O": N5, "H": H5, "D": D5, "ms_fwd_bwd": round(ms5, 3),
                                       "tflops": round(fl5 / (ms5 * 1e-3) / 1e12, 2), "steps": reps})
@@ -257,15 +257,7 @@ def main():
                 o = turbo_trimul(z, direction, tm_mask, **wts)
                 torch.autograd.grad(o, params, tm_dout)
 
-        for _ in range(args.warmup):
-            tm_step()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            tm_step()
-        e1.record()
-        torch.cuda.synchronize()
-        tm_ms = e0.elapsed_time(e1) / args.steps
+        tm_ms = gpu_time(torch, tm_step, args.steps, args.warmup)["median"]
         R = TM_N * TM_N
         tm_fwd_flops = 2.0 * R * C * 5 * C + 2.0 * C * TM_N ** 3 + 2.0 * R * C * C
         tm_flops = 2 * 3 * tm_fwd_flops
@@ -350,7 +342,7 @@ def main():
 
     # ------------- config 5: pair-stack block at N=768 (modules) -----------
     pair_block = None
-    if args.pair_block:
+    if not args.no_config5:
         from openfold3_triangle_kernel_amd import (
             TriangleAttention,
             TriangleMultiplicationIncoming,
@@ -376,15 +368,7 @@ def main():
                 h = h + mo(h, mp)
             torch.autograd.grad(h.float().square().mean(), params)
 
-        for _ in range(2):
-            block_step()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(max(1, args.steps // 4)):
-            block_step()
-        e1.record()
-        torch.cuda.synchronize()
-        blk_ms = e0.elapsed_time(e1) / max(1, args.steps // 4)
+        blk_ms = gpu_time(torch, block_step, max(10, args.steps // 4), 3)["median"]
         pair_block = {
             "ms_fwd_bwd": round(blk_ms, 3),
             "config": {"N": Np, "C": Cz, "blocks": ["trimul_out", "trimul_in", "tri_att_start",
@@ -420,6 +404,8 @@ def main():
         },
         "attention": {
             "ms_fwd_bwd_start_plus_end": round(ms_step, 4),
+            "ms_mean": round(at["mean"], 4),
+            "timing": "median of per-step HIP-event times",
             "ms_fwd_start": round(fwd_ms, 4),
             "host_wall_ms_per_step": round(wall_ms, 4),
             "mfma_frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -451,45 +437,105 @@ def traffic_bytes():
         return None
 
 
+def _cpu_threads() -> int:
+    """Host cores this process may run on (the cgroup / affinity share)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def _median_time(fn, reps, warmup):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2] * 1e3, ts
+
+
 def cpu_baseline():
-    """The numpy oracle (fp32) on a bounded sample of the attention workload:
-    the same N=384, H=4, D=32 planes, fwd+bwd, on a subset of outer rows."""
-    import numpy as np
+    """The stock PyTorch math in FP32 on the host cores (oracle/stock_torch.py,
+    a restatement of OpenFold3's ``_attention`` and TriMul forward with
+    autograd for the backward), on the same seeded workloads:
+
+    * config 1 in full: attention fwd+bwd [1,64,4,64,32], mask zeros;
+    * config 3 in full: attention fwd+bwd, starting + ending node
+      [1,384,4,384,32], chunked over the outer rows (the stock chunked path);
+    * config 4 in full: TriMul outgoing + incoming fwd+bwd [1,384,384,128].
+
+    Median of 5 timed runs after 2 warm-ups each; ``value`` is config 3 in
+    the headline unit (TFLOP/s), so it sits beside the GPU figure.
+    """
+    import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle.attention import attention_backward, attention_forward
+    from oracle.stock_torch import attention_stock_train_step, trimul_stock
 
-    try:
-        from threadpoolctl import threadpool_info
+    cores = _cpu_threads()
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    reps, warm = 5, 2
 
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = 1
-    o_sample = 16
-    rng = np.random.default_rng(0)
-    q, k, v = (rng.standard_normal((1, o_sample, H, N, D)).astype(np.float32) for _ in range(3))
-    bias = (2 * rng.standard_normal((1, 1, H, N, N))).astype(np.float32)
-    mask = np.zeros((1, o_sample, 1, 1, N), np.float32)
-    dout = rng.standard_normal((1, o_sample, N, H, D)).astype(np.float32)
-    flops = 14.0 * o_sample * H * N * N * D
-    attention_forward(q, k, v, mask, bias, dtype=np.float32)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        attention_forward(q, k, v, mask, bias, dtype=np.float32)
-        attention_backward(q, k, v, mask, bias, dout, dtype=np.float32)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 12.0:
-            break
-    sec = el / reps
+    def attn_case(O_, N_, bias_scale, tail):
+        q_, k_, v_ = (torch.randn(1, O_, H, N_, D, generator=g) for _ in range(3))
+        b_ = torch.randn(1, 1, H, N_, N_, generator=g) * bias_scale
+        m_ = torch.zeros(1, O_, 1, 1, N_)
+        if tail:
+            tails = torch.randint(0, tail + 1, (O_,), generator=g)
+            for o_ in range(O_):
+                if int(tails[o_]):
+                    m_[0, o_, ..., N_ - int(tails[o_]):] = float("-inf")
+        d_ = torch.randn(1, O_, N_, H, D, generator=g)
+        return q_, k_, v_, m_, b_, d_
+
+    # Config 1.
+    c1 = attn_case(64, 64, 1.0, 0)
+    c1_ms, _ = _median_time(lambda: attention_stock_train_step(*c1), reps, warm)
+    # Config 3: starting node and ending node (transposed pair, transposed bias).
+    q3, k3, v3, m3, b3, d3 = attn_case(O, N, 2.0, 32)
+    q3e, k3e, v3e = (t.transpose(1, 3).contiguous() for t in (q3, k3, v3))
+    b3e = b3.transpose(-1, -2).contiguous()
+
+    def c3_step():
+        attention_stock_train_step(q3, k3, v3, m3, b3, d3, chunk=64)
+        attention_stock_train_step(q3e, k3e, v3e, m3, b3e, d3, chunk=64)
+
+    c3_ms, _ = _median_time(c3_step, reps, warm)
+    c3_flops = 2 * 14.0 * B * O * H * N * N * D
+    # Config 4: TriMul out + in.
+    C = TM_C
+    z = torch.randn(1, TM_N, TM_N, C, generator=g).requires_grad_(True)
+    sd = 1.0 / math.sqrt(C)
+    w = {n: (torch.randn(C, C, generator=g) * sd).requires_grad_(True)
+         for n in ("w_ap", "w_ag", "w_bp", "w_bg", "w_g", "w_z")}
+    w.update({n: (torch.ones(C) if n.startswith("g") else torch.zeros(C)).requires_grad_(True)
+              for n in ("g_in", "b_in", "g_out", "b_out")})
+    tm_mask = torch.ones(1, TM_N, TM_N)
+    tm_dout = torch.randn(1, TM_N, TM_N, C, generator=g)
+    params = [z] + list(w.values())
+
+    def c4_step():
+        for outgoing in (True, False):
+            out = trimul_stock(z, tm_mask, w, outgoing)
+            torch.autograd.grad(out, params, tm_dout)
+
+    c4_ms, _ = _median_time(c4_step, reps, warm)
     return {
-        "value": round(flops / sec / 1e12, 5),
+        "value": round(c3_flops / (c3_ms * 1e-3) / 1e12, 5),
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": int(cores),
         "kind": "port",
-        "sample": f"numpy fp32 oracle, attention fwd+bwd, {o_sample} of 384 outer rows at N=384 H=4 D=32, "
-                  f"{reps} reps in {el:.1f} s ({sec * 1e3:.1f} ms/rep)",
-        "ms_full_step_extrapolated": round(sec * (O / o_sample) * 2 * 1e3, 1),
+        "sample": "stock OpenFold3 math in FP32 on the host (oracle/stock_torch.py), config 3 in "
+                  "full: attention fwd+bwd, starting + ending node, chunked over 64 outer rows; "
+                  f"median of {reps} after {warm} warm-ups",
+        "config1_attention_ms": round(c1_ms, 3),
+        "config3_attention_ms": round(c3_ms, 1),
+        "config4_trimul_out_plus_in_ms": round(c4_ms, 1),
+        "torch_threads": torch.get_num_threads(),
     }
 
 
