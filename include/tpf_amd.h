@@ -222,6 +222,16 @@ int tpf_gemm_bf16(const void* A, int a_kc, int64_t a_ld, int64_t a_bs, const voi
                   int64_t b_ld, int64_t b_bs, void* C, int out_f32, int64_t c_ld, int64_t c_bs,
                   int64_t M, int64_t N, int64_t K, int64_t batch, double alpha, void* stream);
 
+/* Fixed-order FP32 fold of weight-gradient partials [chunks, elements]:
+ * accumulator[e] = (((init + p[0][e]) + p[1][e]) + ...) + p[chunks-1][e],
+ * each add rounded to nearest, init = 0 when initialize != 0 else the
+ * accumulator's current value (bitwise equal to an ascending FP32 add_ over
+ * the chunks).  The accumulator must not overlap the partials.  Replaces
+ * trimul_wgrad_fixed_fold
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_trimul_cuda.cu:200-217, 2050-2089). */
+int tpf_trimul_wgrad_fixed_fold(const float* partials, int64_t chunks, int64_t elements,
+                                float* accumulator, int initialize, void* stream);
+
 /* Batched FP32 MFMA GEMM C[z] = alpha * A[z] B[z]^T + bias (bias per column,
  * nullable), operands K- or MN-contiguous as tpf_gemm_bf16, C row-major f32.
  * The strict-FP32 products of the reference's FP32 TriMul

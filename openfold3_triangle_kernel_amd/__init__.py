@@ -20,9 +20,15 @@ __all__ = [
     "turbopairformer_triangle_attention",
 ]
 
-from .trimul import check_stable_trimul_support, run_stable_trimul, turbo_trimul  # noqa: E402
+from .trimul import (  # noqa: E402
+    check_stable_trimul_support,
+    run_stable_trimul,
+    trimul_wgrad_fixed_fold,
+    turbo_trimul,
+)
 
-__all__ += ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]
+__all__ += ["check_stable_trimul_support", "run_stable_trimul", "trimul_wgrad_fixed_fold",
+            "turbo_trimul"]
 
 from .attention_fp32 import is_attention_fp32_supported, turbopairformer_attention_fp32  # noqa: E402
 

@@ -78,6 +78,29 @@ __global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f, int final_p
   }
 }
 
+// The weight-gradient fold contract of the reference
+// (trimul_wgrad_fixed_fold, turbopairformer_trimul_cuda.cu:200-217, 2050-2089):
+// accumulator[e] = (((init + p[0][e]) + p[1][e]) + ...) + p[chunks-1][e] in
+// round-to-nearest FP32, init = 0 (initialize) or the accumulator's value.
+template <bool INIT>
+__global__ __launch_bounds__(256) void wgrad_fixed_fold_kernel(const float* __restrict__ part,
+                                                               int chunks, int64_t n,
+                                                               float* __restrict__ acc) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float sum = INIT ? 0.f : acc[i];
+  int c = 0;
+  for (; c + 8 <= chunks; c += 8) {  // 8 loads in flight, added in ascending order
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(c + e) * n + i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum = __fadd_rn(sum, v[e]);
+  }
+  for (; c < chunks; ++c) sum = __fadd_rn(sum, part[(int64_t)c * n + i]);
+  acc[i] = sum;
+}
+
 int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
   if (f.nseg < 1 || f.nseg > kFoldMaxSegs) return set_error(TPF_ERR_ARG, "%s: bad fold segments", fn);
   for (;;) {
@@ -196,3 +219,25 @@ extern "C" int tpf_gemm_bf16(const void* A, int a_kc, int64_t a_ld, int64_t a_bs
   return tpf::gemm_launch(g, a_kc, b_kc, out_f32, (int)batch, (hipStream_t)stream, "tpf_gemm_bf16");
 }
 
+
+extern "C" int tpf_trimul_wgrad_fixed_fold(const float* partials, int64_t chunks, int64_t elements,
+                                           float* accumulator, int initialize, void* stream) {
+  const char* fn = "tpf_trimul_wgrad_fixed_fold";
+  if (!partials || !accumulator) return tpf::set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (chunks < 1 || chunks > INT32_MAX || elements < 1)
+    return tpf::set_error(TPF_ERR_SHAPE, "%s: chunks and elements must be positive", fn);
+  if ((elements + 255) / 256 > INT32_MAX)
+    return tpf::set_error(TPF_ERR_SHAPE, "%s: too many elements", fn);
+  const char* pa = (const char*)partials;
+  const char* ac = (const char*)accumulator;
+  if (ac < pa + chunks * elements * 4 && pa < ac + elements * 4)
+    return tpf::set_error(TPF_ERR_ARG, "%s: accumulator overlaps the partials", fn);
+  const dim3 grid((unsigned)((elements + 255) / 256));
+  if (initialize)
+    hipLaunchKernelGGL(tpf::wgrad_fixed_fold_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
+                       partials, (int)chunks, elements, accumulator);
+  else
+    hipLaunchKernelGGL(tpf::wgrad_fixed_fold_kernel<false>, grid, dim3(256), 0,
+                       (hipStream_t)stream, partials, (int)chunks, elements, accumulator);
+  return tpf::check_launch(fn);
+}

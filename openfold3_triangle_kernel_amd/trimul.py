@@ -90,7 +90,11 @@ def _trimul_fwd_v1(
 
     ``a``/``b`` are the channel-major stored matrices [B*H, N*Np] and ``x`` the
     product [B*H, N, Np] (Np = N rounded up to 8); ``gate`` holds the
-    output-gate logits [B*N*N, C].
+    output-gate logits [B*N*N, C].  With ``save_state=False`` (inference) the
+    backward-only state ``z_ln``, ``xln``, ``mean_out`` and ``rstd_out`` comes
+    back with zero rows, as the reference's schema contract has it
+    (turbopairformer_trimul.py:532-546); the kernels then use scratch buffers
+    for them that are freed on return.
     """
     _check_op_inputs(z_bf, w_ap)
     B, N, _, C = (int(s) for s in z_bf.shape)
@@ -115,6 +119,7 @@ def _trimul_fwd_v1(
     mean_in, rstd_in = torch.empty(rows, **f32), torch.empty(rows, **f32)
     mean_out, rstd_out = torch.empty(rows, **f32), torch.empty(rows, **f32)
     lnw = [g_in32, b_in32, g_out32, b_out32]
+    state = (z_ln, xln, mean_out, rstd_out)
     with _device_ctx(dev):
         _native.call(
             "tpf_trimul_forward_bf16",
@@ -126,6 +131,12 @@ def _trimul_fwd_v1(
             mean_out.data_ptr(), rstd_out.data_ptr(), ws.data_ptr(), ws_bytes,
             _native.stream_of(z_bf),
         )
+    if not save_state:
+        # The scratch state dies here (its memory returns to the caching
+        # allocator in stream order); only zero-row tensors leave the op.
+        del state
+        z_ln, xln = z_bf.new_empty((0, C)), z_bf.new_empty((0, H))
+        mean_out, rstd_out = torch.empty(0, **f32), torch.empty(0, **f32)
     return (out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out)
 
 
@@ -136,18 +147,19 @@ def _trimul_fwd_v1_fake(z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_
     H = w_ap.shape[0]
     Np = (N + 7) // 8 * 8
     rows = B * N * N
+    saved = rows if save_state else 0
     return (
         z_bf.new_empty((B, N, N, C)),
-        z_bf.new_empty((rows, C)),
+        z_bf.new_empty((saved, C)),
         z_bf.new_empty((rows, C)),
         z_bf.new_empty((B * H, N * Np)),
         z_bf.new_empty((B * H, N * Np)),
         z_bf.new_empty((B * H, N, Np)),
-        z_bf.new_empty((rows, H)),
+        z_bf.new_empty((saved, H)),
         g_in.new_empty((rows,), dtype=torch.float32),
         g_in.new_empty((rows,), dtype=torch.float32),
-        g_in.new_empty((rows,), dtype=torch.float32),
-        g_in.new_empty((rows,), dtype=torch.float32),
+        g_in.new_empty((saved,), dtype=torch.float32),
+        g_in.new_empty((saved,), dtype=torch.float32),
     )
 
 
@@ -233,6 +245,10 @@ def _trimul_bwd_v1_fake(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_
 def _fwd_setup_context(ctx, inputs, output):
     (z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_out, outgoing,
      save_state) = inputs
+    if not save_state and any(ctx.needs_input_grad):
+        # Reference turbopairformer_trimul.py:689-692.
+        raise RuntimeError(
+            "TurboPairFormer TriMul requires save_state=True when gradients are enabled")
     out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out = output
     ctx.save_for_backward(z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
                           rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, out)
@@ -454,4 +470,31 @@ class _TurboTrimulFn(torch.autograd.Function):
         return (d_z, None, *grads, None)
 
 
-__all__ = ["check_stable_trimul_support", "run_stable_trimul", "turbo_trimul"]
+def trimul_wgrad_fixed_fold(partials: torch.Tensor, accumulator: torch.Tensor,
+                            initialize: bool) -> torch.Tensor:
+    """Fold FP32 weight-gradient partials ``[chunks, M, C]`` into
+    ``accumulator [M, C]`` in ascending chunk order (starting from zero when
+    ``initialize``, else from the accumulator) and return the accumulator.
+
+    The reference's native ``trimul_wgrad_fixed_fold``
+    (turbopairformer_trimul_cuda.cu:2050-2089, contract checked by
+    tools/aot_numeric_smoke.py:201-222): bitwise equal to an ascending FP32
+    ``add_`` over the chunks.
+    """
+    if partials.dtype != torch.float32 or accumulator.dtype != torch.float32:
+        raise RuntimeError("trimul_wgrad_fixed_fold: partials and accumulator must be FP32")
+    if partials.dim() != 3 or not partials.is_contiguous():
+        raise RuntimeError("trimul_wgrad_fixed_fold: partials must be contiguous [chunks, M, C]")
+    if tuple(accumulator.shape) != tuple(partials.shape[1:]) or not accumulator.is_contiguous():
+        raise RuntimeError("trimul_wgrad_fixed_fold: accumulator must be contiguous [M, C]")
+    if accumulator.device != partials.device or partials.device.type != "cuda":
+        raise RuntimeError("trimul_wgrad_fixed_fold: tensors must share one GPU")
+    with _device_ctx(partials.device):
+        _native.call("tpf_trimul_wgrad_fixed_fold", partials.data_ptr(), partials.shape[0],
+                     accumulator.numel(), accumulator.data_ptr(), int(bool(initialize)),
+                     _native.stream_of(partials))
+    return accumulator
+
+
+__all__ = ["check_stable_trimul_support", "run_stable_trimul", "trimul_wgrad_fixed_fold",
+           "turbo_trimul"]

@@ -27,54 +27,81 @@ def invocation_count() -> int:
     return _INVOCATIONS
 
 
-def _check_parameter(tensor, shape, device, name, *, optional=False):
-    if tensor is None and optional:
-        return
-    if not isinstance(tensor, torch.Tensor):
-        raise TypeError(f"{name} must be a tensor")
-    if tensor.dtype != torch.float32 or tensor.device != device:
-        raise ValueError(f"{name} must be FP32 on {device}")
-    if tuple(tensor.shape) != tuple(shape):
-        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(tensor.shape)}")
+class _ParamError(ValueError):
+    """A module parameter that the FP32 kernels cannot take as it is."""
 
 
-def _linear_parts(layer, rows, channels, device, name):
-    _check_parameter(layer.weight, (rows, channels), device, name + ".weight")
-    bias = getattr(layer, "bias", None)
-    _check_parameter(bias, (rows,), device, name + ".bias", optional=True)
+def _fp32_param(owner, attr, shape, device, label, required):
+    """``owner.attr`` as an FP32 tensor of ``shape`` on ``device`` (None when
+    it is absent and not ``required``); anything else raises _ParamError
+    naming ``label``."""
+    value = getattr(owner, attr, None)
+    if value is None:
+        if required:
+            raise _ParamError(f"{label} is required")
+        return None
+    if not isinstance(value, torch.Tensor):
+        raise TypeError(f"{label} must be a tensor")
+    problems = []
+    if value.dtype != torch.float32:
+        problems.append(f"dtype {value.dtype}")
+    if value.device != device:
+        problems.append(f"device {value.device}")
+    if problems:
+        raise _ParamError(f"{label} must be FP32 on {device} ({', '.join(problems)})")
+    if tuple(value.shape) != tuple(shape):
+        raise _ParamError(f"{label} must have shape {tuple(shape)}, got {tuple(value.shape)}")
+    return value
+
+
+# The FP32 kernels take six projections: a_p, a_g, b_p, b_g [H, C],
+# g [C, C], z [C, H], each with an optional bias.  OpenFold3 modules expose
+# the four input projections either as separate layers or as two fused
+# [2H, C] layers (a rows first, then b).
+_UNFUSED = ("linear_a_p", "linear_a_g", "linear_b_p", "linear_b_g")
+_FUSED = ("linear_ab_p", "linear_ab_g")
+
+
+def _layer(module, name, out_rows, in_cols, device):
+    """(weight, bias) of a linear layer, with the FP32-only precision check."""
+    layer = getattr(module, name)
+    weight = _fp32_param(layer, "weight", (out_rows, in_cols), device, f"{name}.weight", True)
+    bias = _fp32_param(layer, "bias", (out_rows,), device, f"{name}.bias", False)
     if getattr(layer, "precision", None) not in (None, torch.float32):
-        raise ValueError(f"{name}.precision requests a non-FP32 computation")
-    return layer.weight, bias
+        raise _ParamError(f"{name}.precision requests a non-FP32 computation")
+    return weight, bias
 
 
-def _normalization_parts(layer, channels, device, name):
-    weight = getattr(layer, "weight", None)
-    bias = getattr(layer, "bias", None)
-    _check_parameter(weight, (channels,), device, name + ".weight", optional=True)
-    _check_parameter(bias, (channels,), device, name + ".bias", optional=True)
+def _projections(module, channels, hidden, device):
+    """[(weight, bias)] in kernel order a_p, a_g, b_p, b_g, g, z."""
+    layouts = [all(hasattr(module, n) for n in names) for names in (_UNFUSED, _FUSED)]
+    if layouts.count(True) != 1:
+        raise _ParamError("TriMul module must expose exactly one fused or unfused projection layout")
+    if layouts[0]:
+        inputs = [_layer(module, n, hidden, channels, device) for n in _UNFUSED]
+    else:
+        (pw, pb), (gw, gb) = (_layer(module, n, 2 * hidden, channels, device) for n in _FUSED)
+        rows = (slice(0, hidden), slice(hidden, 2 * hidden))
+
+        def cut(t, r):
+            return None if t is None else t[r]
+
+        # Kernel order interleaves projection and gate per branch.
+        inputs = [(cut(w, r), cut(b, r)) for r in rows for w, b in ((pw, pb), (gw, gb))]
+    return inputs + [_layer(module, "linear_g", channels, channels, device),
+                     _layer(module, "linear_z", channels, hidden, device)]
+
+
+def _norm(module, name, width, device):
+    """(weight, bias, eps) of a LayerNorm whose affine parameters may be absent."""
+    layer = getattr(module, name)
+    weight = _fp32_param(layer, "weight", (width,), device, f"{name}.weight", False)
+    bias = _fp32_param(layer, "bias", (width,), device, f"{name}.bias", False)
     eps = getattr(layer, "eps", None)
-    if isinstance(eps, bool) or not isinstance(eps, (int, float)) or not 0 < eps < float("inf"):
-        raise ValueError(f"{name}.eps must be finite and positive")
+    ok = isinstance(eps, (int, float)) and not isinstance(eps, bool) and 0 < eps < float("inf")
+    if not ok:
+        raise _ParamError(f"{name}.eps must be finite and positive")
     return weight, bias, float(eps)
-
-
-def _input_parameters(module, channels, hidden, device):
-    """[(weight, bias)] for a_p, a_g, b_p, b_g from either projection layout."""
-    unfused = ("linear_a_p", "linear_a_g", "linear_b_p", "linear_b_g")
-    has_unfused = all(hasattr(module, n) for n in unfused)
-    has_fused = all(hasattr(module, n) for n in ("linear_ab_p", "linear_ab_g"))
-    if has_unfused == has_fused:
-        raise ValueError("TriMul module must expose exactly one fused or unfused projection layout")
-    if has_unfused:
-        return [_linear_parts(getattr(module, n), hidden, channels, device, n) for n in unfused]
-    p, pb = _linear_parts(module.linear_ab_p, 2 * hidden, channels, device, "linear_ab_p")
-    g, gb = _linear_parts(module.linear_ab_g, 2 * hidden, channels, device, "linear_ab_g")
-
-    def half(t, lo):
-        return None if t is None else (t[:hidden] if lo else t[hidden:])
-
-    return [(p[:hidden], half(pb, True)), (g[:hidden], half(gb, True)),
-            (p[hidden:], half(pb, False)), (g[hidden:], half(gb, False))]
 
 
 def run_trimul_fp32(module, z, mask=None, *, output_row_chunk_size=None,
@@ -118,11 +145,9 @@ def run_trimul_fp32(module, z, mask=None, *, output_row_chunk_size=None,
         except RuntimeError as error:
             raise ValueError("mask must broadcast exactly to z.shape[:-1]") from error
     dev = z.device
-    norm_in = _normalization_parts(module.layer_norm_in, channels, dev, "layer_norm_in")
-    norm_out = _normalization_parts(module.layer_norm_out, hidden, dev, "layer_norm_out")
-    parts = _input_parameters(module, channels, hidden, dev)
-    parts.append(_linear_parts(module.linear_g, channels, channels, dev, "linear_g"))
-    parts.append(_linear_parts(module.linear_z, channels, hidden, dev, "linear_z"))
+    norm_in = _norm(module, "layer_norm_in", channels, dev)
+    norm_out = _norm(module, "layer_norm_out", hidden, dev)
+    parts = _projections(module, channels, hidden, dev)
 
     prefix = tuple(int(x) for x in z.shape[:-3])
     batch = 1

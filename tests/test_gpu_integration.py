@@ -98,8 +98,27 @@ def test_trimul_fake_forward_metadata_matches_real(gpu, save_state):
     assert len(real) == len(fake) == 11
     for r, f in zip(real, fake):
         assert (r.shape, r.dtype, r.device, r.stride()) == (f.shape, f.dtype, f.device, f.stride())
-    ptrs = [t.data_ptr() for t in real]
+    ptrs = [t.data_ptr() for t in real if t.numel()]
     assert len(set(ptrs)) == len(ptrs), "forward outputs must not alias"
+    # save_state=False keeps the schema but returns the backward-only state
+    # (z_ln, xln, mean_out, rstd_out) with zero rows (reference
+    # turbopairformer_trimul.py:532-546).
+    saved_rows = 17 * 17 if save_state else 0
+    for i in (1, 6, 9, 10):
+        assert real[i].shape[0] == saved_rows, (i, tuple(real[i].shape))
+    if not save_state:
+        with_state = trimul._trimul_fwd_v1(*tensors, True, True)
+        assert torch.equal(real[0], with_state[0]), "inference output must not depend on save_state"
+
+
+@pytest.mark.gpu
+def test_trimul_save_state_false_rejects_gradients(gpu):
+    """Reference turbopairformer_trimul.py:689-692: no saved state, no backward."""
+    m = _trimul_module(32, True, gpu, 77)
+    z = torch.randn(1, 16, 16, 32, device=gpu, dtype=torch.bfloat16, requires_grad=True)
+    mask = torch.ones(1, 16, 16, device=gpu)
+    with pytest.raises(RuntimeError, match="save_state=True"):
+        torch.ops.openfold3_turbopairformer._trimul_fwd_v1(*_fwd_inputs(m, z, mask, True, False))
 
 
 class _Route(torch.nn.Module):
