@@ -71,6 +71,20 @@ int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, co
                                  int64_t H, int64_t N, int64_t D, int seq_major,
                                  int64_t bias_batches, double scale, void* stream);
 
+/* Forward that allocates nothing: the same kernels as tpf_attn_forward_bf16,
+ * with the prescaled-bias scratch in a static per-GPU device array of 16 MiB
+ * (bias_batches * H * N * N <= 4,194,304; larger problems are rejected with
+ * TPF_ERR_SHAPE) instead of a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams) race and must be serialised by the caller.  The
+ * array's address is looked up once per device on that device's first call. */
+int tpf_attn_forward_noalloc_bf16(const void* q, const void* k, const void* v, const float* mask,
+                                  const void* bias, void* out, float* lse, int64_t B, int64_t O,
+                                  int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t bias_batches, double scale, void* stream);
+
 /* delta = rowsum(f32(dout) * f32(out)) for dout/out bf16 [B, O, N, H, D].
  * Replaces turbopairformer_triangle_delta_out
  * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_delta.cu:292-342). */

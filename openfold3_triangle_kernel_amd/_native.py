@@ -38,6 +38,10 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P] * 9 + [_I64] * 6 + [_I32, _I64, _F64, _P],
     ),
+    "tpf_attn_forward_noalloc_bf16": (
+        _I32,
+        [_P] * 7 + [_I64] * 5 + [_I32, _I64, _F64, _P],
+    ),
     "tpf_attn_delta_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "tpf_attn_delta_shadow_bf16": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "tpf_attn_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),

@@ -24,6 +24,8 @@
 //   mask   [B, O, N] f32 additive.    bias [Bb, H, N, N] bf16, Bb in {1, B}.
 //   out    [B, O, N, H, D] bf16.      lse / delta [B, O, H, N] f32.
 // N must be a multiple of 64 (the host pads) and D a multiple of 8, D <= 64.
+#include <mutex>
+
 #include "common.hpp"
 #include "tpf_status.hpp"
 
@@ -1325,6 +1327,65 @@ int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const flo
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
   return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
                            out, lse, nullptr, workspace, (hipStream_t)stream, fn);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward: the prescaled-bias scratch lives in a file-scope
+// device array instead of a caller workspace.  Each GPU holds its own copy
+// of the array (at its own address) until the process ends; its address is
+// looked up once per device with that device current and kept per device.
+// Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+// (two streams) race on it.  The prescale kernel writes every scratch word
+// the forward kernel then reads, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+static constexpr int64_t kNoAllocScratchBytes = 16ll << 20;  // 4M f32 bias values
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / 4];
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int noalloc_scratch(void** out, const char* fn) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(TPF_ERR_LAUNCH, "%s: no current HIP device (or device index >= %d)", fn,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(TPF_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       fn, dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TPF_OK;
+}
+
+extern "C" {
+
+int tpf_attn_forward_noalloc_bf16(const void* q, const void* k, const void* v, const float* mask,
+                                  const void* bias, void* out, float* lse, int64_t B, int64_t O,
+                                  int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t bias_batches, double scale, void* stream) {
+  const char* fn = "tpf_attn_forward_noalloc_bf16";
+  AttnGeom g;
+  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  if (rc) return rc;
+  if (!q || !k || !v || !mask || !bias || !out || !lse)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  const int64_t need = tpf_attn_forward_workspace_bytes(B, H, N, bias_batches);
+  if (need > kNoAllocScratchBytes)
+    return set_error(TPF_ERR_SHAPE,
+                     "%s: bias_batches*H*N*N = %lld exceeds the static scratch of %lld f32 values "
+                     "(use tpf_attn_forward_bf16 with a workspace)",
+                     fn, (long long)(need / 4), (long long)(kNoAllocScratchBytes / 4));
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(&ws, fn))) return rc;
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+                           out, lse, nullptr, ws, (hipStream_t)stream, fn);
 }
 
 int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, const float* mask,
