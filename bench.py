@@ -40,6 +40,7 @@ HBM_PEAK_GBPS = 8000.0           # MI355X HBM3E
 
 B, O, H, N, D = 1, 384, 4, 384, 32
 TM_N, TM_C = 384, 128
+PROBE_PASSES = 6
 
 
 def parse():
@@ -55,6 +56,11 @@ def parse():
                          "pair-stack block through the modules); for profiling runs whose kernel "
                          "trace should hold only the config-3 / config-4 launches")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--probe", choices=("attention", "trimul"),
+                    help="launch a 256 MiB calibration copy, then two fwd+bwd passes of one path "
+                         "(attention: config 3 starting node; trimul: config 4 outgoing + incoming) "
+                         "six times and exit: the program that the per-kernel rocprofv3 counter passes "
+                         "profile (the last pass is the steady-state one)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch a 256 MiB calibration copy and one attention backward kernel, "
                          "then exit (the program profiled by the FETCH_SIZE / WRITE_SIZE passes)")
@@ -80,6 +86,56 @@ def gpu_time(torch, fn, steps, warmup):
     wall = (time.perf_counter() - t0) * 1e3 / steps
     ts = sorted(a.elapsed_time(b) for a, b in ev)
     return {"median": ts[len(ts) // 2], "mean": sum(ts) / len(ts), "wall": wall}
+
+
+def trimul_inputs(torch, dev, seed=1):
+    """Config 4: z [1,384,384,128] ~ N(0,1) bf16, LN weights 1 / 0, projections
+    ~ N(0, 1/sqrt(128)) in the named-argument layout, mask all ones."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    C = TM_C
+    z = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    sd = 1.0 / math.sqrt(C)
+    wts = dict(
+        norm_in_weight=torch.ones(C, device=dev), norm_in_bias=torch.zeros(C, device=dev),
+        p_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
+        g_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
+        norm_out_weight=torch.ones(C, device=dev), norm_out_bias=torch.zeros(C, device=dev),
+        p_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
+        g_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
+    )
+    wts = {kk: vv.requires_grad_(True) for kk, vv in wts.items()}
+    mask = torch.ones(1, TM_N, TM_N, device=dev)
+    dout = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16)
+    return z, wts, mask, dout
+
+
+def probe(torch, dev, target):
+    """Calibration copy (256 MiB read + 256 MiB written), then six fwd+bwd
+    passes of one path, for per-kernel counter passes (the last pass runs
+    with warm clocks and caches)."""
+    from openfold3_triangle_kernel_amd import turbo_trimul, turbopairformer_triangle_attention
+
+    src = torch.ones(64 * 1024 * 1024, device=dev, dtype=torch.float32)  # 256 MiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    if target == "attention":
+        q, k, v, bias, mask, dout = attention_inputs(torch, dev)
+        xs = [t.detach().requires_grad_(True) for t in (q, k, v, bias)]
+        for _ in range(PROBE_PASSES):
+            out = turbopairformer_triangle_attention(xs[0], xs[1], xs[2], mask, xs[3])
+            torch.autograd.grad(out, xs, dout)
+    else:
+        z, wts, mask, dout = trimul_inputs(torch, dev)
+        params = [z] + list(wts.values())
+        for _ in range(PROBE_PASSES):
+            for direction in ("outgoing", "incoming"):
+                o = turbo_trimul(z, direction, mask, **wts)
+                torch.autograd.grad(o, params, dout)
+    torch.cuda.synchronize()
+    print(f"probe {target}: copy 268435456 B read + 268435456 B written; {PROBE_PASSES} fwd+bwd "
+          "passes", flush=True)
 
 
 def attention_inputs(torch, dev, seed=0):
@@ -141,6 +197,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.probe:
+        probe(torch, dev, args.probe)
+        return
+
     # ---------------- attention: starting + ending node -----------------
     q, k, v, bias, mask, dout = attention_inputs(torch, dev)
     if args.traffic_probe:
@@ -195,7 +255,7 @@ def main():
     bwd_flops = 10.0 * B * O * H * N * N * D
     achieved = bwd_flops / (bwd_kernel_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "attn_bwd_kernel<32>",
+        "kernel": "attn_bwd_kernel<32> (timed with its attn_bwd_prep_kernel launch)",
         "bound": "mfma",
         "achieved": round(achieved, 2),
         "peak": MFMA_BF16_PEAK_TFLOPS,
@@ -235,21 +295,8 @@ def main():
     # --------------------------- TriMul ----------------------------------
     trimul = None
     if not args.no_trimul:
-        g = torch.Generator(device=dev).manual_seed(1)
         C = TM_C
-        z = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
-        sd = 1.0 / math.sqrt(C)
-        wts = dict(
-            norm_in_weight=torch.ones(C, device=dev), norm_in_bias=torch.zeros(C, device=dev),
-            p_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
-            g_in_weight=torch.randn(2 * C, C, device=dev, generator=g) * sd,
-            norm_out_weight=torch.ones(C, device=dev), norm_out_bias=torch.zeros(C, device=dev),
-            p_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
-            g_out_weight=torch.randn(C, C, device=dev, generator=g) * sd,
-        )
-        wts = {kk: vv.requires_grad_(True) for kk, vv in wts.items()}
-        tm_mask = torch.ones(1, TM_N, TM_N, device=dev)
-        tm_dout = torch.randn(1, TM_N, TM_N, C, device=dev, generator=g).to(torch.bfloat16)
+        z, wts, tm_mask, tm_dout = trimul_inputs(torch, dev)
         params = [z] + list(wts.values())
 
         def tm_step():
@@ -276,6 +323,8 @@ def main():
             "roofline_frac": round(roof_ms / tm_ms, 4),
             "roofline_basis": "sum over stages of max(F/P, B/BW); minimum bytes 12U fwd + 20U bwd "
                               "per direction at 8 TB/s (all stages HBM-bound at C=128)",
+            "traffic": trimul_traffic_bytes(),
+            "min_bytes": int(2 * 32 * U),
             "config": {"N": TM_N, "C": C, "H": C, "directions": ["outgoing", "incoming"]},
         }
 
@@ -431,6 +480,22 @@ def traffic_bytes():
     summary is absent)."""
     try:
         with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(t["fetch_bytes_calibrated"] + t["write_bytes_calibrated"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+TRIMUL_TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                   "trimul_N384_C128_traffic.json")
+
+
+def trimul_traffic_bytes():
+    """HBM bytes of one TriMul out + in fwd + bwd step, summed over the
+    library's kernels from the committed FETCH_SIZE / WRITE_SIZE passes over
+    ``bench.py --probe trimul`` (None when the summary is absent)."""
+    try:
+        with open(TRIMUL_TRAFFIC_FILE) as f:
             t = json.load(f)
         return int(t["fetch_bytes_calibrated"] + t["write_bytes_calibrated"])
     except (OSError, KeyError, ValueError):
