@@ -35,16 +35,25 @@ int tpf_abi_version(void);
 /* ------------------------------------------------------------------------
  * Triangle attention with pair bias.
  *
- * q, k, v: bf16 [B, O, H, N, D] in one shared storage order: head-major
- *   (contiguous, seq_major = 0) or sequence-major (a contiguous
- *   [B, O, N, H, D] buffer viewed as [B, O, H, N, D], seq_major = 1).
+ * layout: bit flags.  q, k, v: bf16 [B, O, H, N, D] in one shared storage
+ *   order: head-major (contiguous) or, with TPF_QKV_SEQ_MAJOR, sequence-major
+ *   (a contiguous [B, O, N, H, D] buffer viewed as [B, O, H, N, D]).
  * mask: f32 [B, O, N] additive (0 keeps, -inf drops).
- * bias: bf16 [bias_batches, H, N, N], bias_batches in {1, B} (1 = shared).
+ * bias: bf16 [bias_batches, H, N, N], bias_batches in {1, B} (1 = shared),
+ *   contiguous or, with TPF_BIAS_TRANSPOSED, the transpose over its last two
+ *   axes of a contiguous one (bias[bb, h, q, k] stored at
+ *   ((bb * H + h) * N + k) * N + q: the ending node's transposed pair bias,
+ *   read in place).
  * out: bf16 [B, O, N, H, D].  lse, delta: f32 [B, O, H, N].
  * Requirements: N % 64 == 0 (pad on the host with -inf mask entries),
  * D % 8 == 0 and 8 <= D <= 64, B*O <= 65535.  scale = 1/sqrt(D_true): when
  * the host zero-pads D it passes the unpadded D's scale.
  * ---------------------------------------------------------------------- */
+
+enum {
+  TPF_QKV_SEQ_MAJOR = 1,   /* q, k, v (and dq, dk, dv) in sequence-major storage */
+  TPF_BIAS_TRANSPOSED = 2, /* bias given as the transpose of a contiguous tensor */
+};
 
 /* Bytes of device workspace tpf_attn_forward_bf16 needs (the bias in f32,
  * prescaled by 1/scale). */
@@ -56,7 +65,7 @@ int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N, int64_
 int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
                           const void* bias, void* out, float* lse, void* workspace,
                           int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                          int64_t D, int seq_major, int64_t bias_batches, double scale,
+                          int64_t D, int layout, int64_t bias_batches, double scale,
                           void* stream);
 
 /* Forward that also writes the shadow residual: residual bf16 [B, O, N, H, D]
@@ -68,7 +77,7 @@ int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const flo
 int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, const float* mask,
                                  const void* bias, void* out, float* lse, void* residual,
                                  void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
-                                 int64_t H, int64_t N, int64_t D, int seq_major,
+                                 int64_t H, int64_t N, int64_t D, int layout,
                                  int64_t bias_batches, double scale, void* stream);
 
 /* Forward that allocates nothing: the same kernels as tpf_attn_forward_bf16,
@@ -82,7 +91,7 @@ int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, co
  * array's address is looked up once per device on that device's first call. */
 int tpf_attn_forward_noalloc_bf16(const void* q, const void* k, const void* v, const float* mask,
                                   const void* bias, void* out, float* lse, int64_t B, int64_t O,
-                                  int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream);
 
 /* delta = rowsum(f32(dout) * f32(out)) for dout/out bf16 [B, O, N, H, D].
@@ -113,7 +122,7 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
                            const float* lse, const float* delta, const float* mask,
                            const void* bias, void* dq, void* dk, void* dv, float* dbias,
                            void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
-                           int64_t H, int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                           int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
                            double scale, void* stream);
 
 /* The two stages of tpf_attn_backward_bf16, for callers that time or
@@ -125,13 +134,14 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                                 const float* lse, const float* delta, const float* mask,
                                 const void* bias, void* dk, void* dv, void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
-                                int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                                int64_t N, int64_t D, int layout, int64_t bias_batches,
                                 double scale, void* stream);
 int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
-                                  int64_t O, int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t O, int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream);
 
-/* FP32 forward (inference): q, k, v, bias f32 in the layouts above, out f32
+/* FP32 forward (inference): q, k, v, bias f32 in the layouts above (layout:
+ * TPF_QKV_SEQ_MAJOR only; the bias is contiguous), out f32
  * [B, O, N, H, D], lse (nullable) f32 [B, O, H, N].  Requirements: N % 64 == 0,
  * D % 4 == 0 and 4 <= D <= 64.  Products and sums in FP32 MFMA.
  * Replaces turbopairformer_attention_fp32_forward
@@ -141,7 +151,7 @@ int64_t tpf_attn_forward_f32_workspace_bytes(int64_t B, int64_t H, int64_t N,
 int tpf_attn_forward_f32(const float* q, const float* k, const float* v, const float* mask,
                          const float* bias, float* out, float* lse, void* workspace,
                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                         int64_t D, int seq_major, int64_t bias_batches, double scale,
+                         int64_t D, int layout, int64_t bias_batches, double scale,
                          void* stream);
 
 /* ------------------------------------------------------------------------

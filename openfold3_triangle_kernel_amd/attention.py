@@ -29,6 +29,9 @@ import torch
 from . import _native
 
 _PAD_QUANTUM = 64  # kernels tile the sequence in 64-key blocks
+# Layout bits of the C ABI (include/tpf_amd.h TPF_QKV_SEQ_MAJOR, TPF_BIAS_TRANSPOSED).
+_QKV_SEQ_MAJOR = 1
+_BIAS_TRANSPOSED = 2
 _MAX_HEAD_DIM = 64
 _MAX_GRID_YZ = 65_535
 _SUPPORT_CACHE: dict = {}
@@ -194,7 +197,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, mask, bias_k, source_bias, seq_major, scale, bias_reduce, shadow):
+    def forward(ctx, q, k, v, mask, bias_k, source_bias, layout, scale, bias_reduce, shadow):
         B, O, H, N, D = (int(x) for x in q.shape)
         out = torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype)
         lse = torch.empty((B, O, H, N), device=q.device, dtype=torch.float32)
@@ -208,20 +211,21 @@ class _TriangleAttentionFn(torch.autograd.Function):
                     "tpf_attn_forward_bf16",
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
                     out.data_ptr(), lse.data_ptr(), workspace.data_ptr(), ws_bytes, B, O, H, N,
-                    D, int(seq_major), Bb, float(scale), _native.stream_of(q),
+                    D, int(layout), Bb, float(scale), _native.stream_of(q),
                 )
             else:
                 _native.call(
                     "tpf_attn_forward_shadow_bf16",
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), bias_k.data_ptr(),
                     out.data_ptr(), lse.data_ptr(), residual.data_ptr(), workspace.data_ptr(),
-                    ws_bytes, B, O, H, N, D, int(seq_major), Bb, float(scale),
+                    ws_bytes, B, O, H, N, D, int(layout), Bb, float(scale),
                     _native.stream_of(q),
                 )
         # The residual fixes the delta path for this autograd context; the
         # backward never rereads the environment.
         ctx.save_for_backward(q, k, v, mask, bias_k, out, lse, residual)
-        ctx.seq_major = bool(seq_major)
+        ctx.layout = int(layout)
+        ctx.seq_major = bool(layout & _QKV_SEQ_MAJOR)
         ctx.scale = float(scale)
         ctx.bias_reduce = bias_reduce
         ctx.bias_shape = tuple(source_bias.shape)
@@ -265,7 +269,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), lse.data_ptr(),
                 delta.data_ptr(), mask.data_ptr(), bias_k.data_ptr(), dq.data_ptr(),
                 dk.data_ptr(), dv.data_ptr(), dbias.data_ptr(), workspace.data_ptr(), ws_bytes,
-                B, O, H, N, D, int(ctx.seq_major), Bb, ctx.scale, stream,
+                B, O, H, N, D, ctx.layout, Bb, ctx.scale, stream,
             )
         d_bias = dbias
         if ctx.bias_reduce is not None:
@@ -340,10 +344,17 @@ def turbopairformer_triangle_attention(q, k, v, res_mask, pair_bias):
     bias_prefix = tuple(int(x) for x in pair_bias.shape[:-4])
     aligned = (1,) * (len(prefix) - len(bias_prefix)) + bias_prefix
     bias_reduce = None
-    if all(x == 1 for x in aligned):
-        bias_k = pair_bias.reshape(1, heads, n_k, n_k).detach().contiguous()
-    elif aligned == prefix:
-        bias_k = pair_bias.reshape(batch, heads, n_k, n_k).detach().contiguous()
+    bias_transposed = False
+    if all(x == 1 for x in aligned) or aligned == prefix:
+        nbb = 1 if all(x == 1 for x in aligned) else batch
+        bias_t = pair_bias.transpose(-1, -2)
+        if not pair_bias.is_contiguous() and bias_t.is_contiguous():
+            # The ending node's bias.transpose(-1, -2) of a contiguous tensor:
+            # the kernels read it in place (TPF_BIAS_TRANSPOSED).
+            bias_k = bias_t.reshape(nbb, heads, n_k, n_k).detach()
+            bias_transposed = True
+        else:
+            bias_k = pair_bias.reshape(nbb, heads, n_k, n_k).detach().contiguous()
     else:
         # Partial broadcast: per-batch gradients, then a sum over the
         # broadcast prefix dimensions (reference ``dq_dbias.py:326-376``).
@@ -369,8 +380,9 @@ def turbopairformer_triangle_attention(q, k, v, res_mask, pair_bias):
         if len({_storage_order(t) for t in (qf, kf, vf)}) != 1:
             qf, kf, vf = (t.contiguous() for t in (qf, kf, vf))
             seq_major = False
+    layout = (_QKV_SEQ_MAJOR if seq_major else 0) | (_BIAS_TRANSPOSED if bias_transposed else 0)
     out = _TriangleAttentionFn.apply(
-        qf, kf, vf, mask_f, bias_k, pair_bias, seq_major, scale, bias_reduce, shadow
+        qf, kf, vf, mask_f, bias_k, pair_bias, layout, scale, bias_reduce, shadow
     )
     if seq_pad:
         out = out[:, :, :sequence]

@@ -1158,9 +1158,12 @@ static int check_geom(const AttnGeom& g, const char* fn) {
 }
 
 static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
-                     int seq_major, int64_t bias_batches, double scale, const char* fn) {
+                     int layout, int64_t bias_batches, double scale, const char* fn) {
   if (B > INT32_MAX || O > INT32_MAX || N > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: dimension exceeds int32", fn);
+  if (layout & ~(TPF_QKV_SEQ_MAJOR | TPF_BIAS_TRANSPOSED))
+    return set_error(TPF_ERR_ARG, "%s: unknown layout flags 0x%x", fn, layout);
+  const bool seq_major = layout & TPF_QKV_SEQ_MAJOR;
   g->B = (int)B; g->O = (int)O; g->H = (int)H; g->N = (int)N; g->D = (int)D;
   g->s_row = seq_major ? H * D : D;
   g->s_head = seq_major ? D : N * D;
@@ -1173,13 +1176,16 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
   return check_geom(*g, fn);
 }
 
-// Contiguous [Bb, H, N, N] bias.
-static BiasView dense_bias(int64_t H, int64_t N, int64_t bias_batches) {
+// Contiguous [Bb, H, N, N] bias, or (TPF_BIAS_TRANSPOSED in layout) the
+// transpose over its last two axes of a contiguous one: bias[bb, h, q, k]
+// stored at bb*H*N*N + h*N*N + k*N + q.
+static BiasView dense_bias(int64_t H, int64_t N, int64_t bias_batches, int layout = 0) {
+  const bool t = layout & TPF_BIAS_TRANSPOSED;
   BiasView bv;
   bv.s_bb = bias_batches == 1 ? 0 : H * N * N;
   bv.s_h = N * N;
-  bv.s_q = N;
-  bv.s_k = 1;
+  bv.s_q = t ? 1 : N;
+  bv.s_k = t ? N : 1;
   bv.H = (int)H;
   return bv;
 }
@@ -1296,10 +1302,10 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
   const int64_t nph = B * O * H;
   const int64_t dq_bx = (N * (D / 8) + 255) / 256;
   const int64_t n_db = (bias_batches * H * N * N / 8 + 63) / 64;
-  const int64_t blocks = n_db + dq_bx * nph;
-  if (blocks > 0x7fffffff) return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
-  hipLaunchKernelGGL(attn_fold_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pt.dq,
-                     (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
+  if (n_db + dq_bx * nph > 0x7fffffff)
+    return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
+  hipLaunchKernelGGL(attn_fold_kernel, dim3((unsigned)(n_db + dq_bx * nph)), dim3(256), 0, s,
+                     pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
                      (int)bias_batches, (int)groups, n_db);
   return check_launch(fn);
 }
@@ -1315,17 +1321,17 @@ int64_t tpf_attn_forward_workspace_bytes(int64_t B, int64_t H, int64_t N,
 int tpf_attn_forward_bf16(const void* q, const void* k, const void* v, const float* mask,
                           const void* bias, void* out, float* lse, void* workspace,
                           int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                          int64_t D, int seq_major, int64_t bias_batches, double scale,
+                          int64_t D, int layout, int64_t bias_batches, double scale,
                           void* stream) {
   const char* fn = "tpf_attn_forward_bf16";
   AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!q || !k || !v || !mask || !bias || !out || !lse || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
-  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches, layout), bias_batches,
                            out, lse, nullptr, workspace, (hipStream_t)stream, fn);
 }
 
@@ -1368,11 +1374,11 @@ extern "C" {
 
 int tpf_attn_forward_noalloc_bf16(const void* q, const void* k, const void* v, const float* mask,
                                   const void* bias, void* out, float* lse, int64_t B, int64_t O,
-                                  int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream) {
   const char* fn = "tpf_attn_forward_noalloc_bf16";
   AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!q || !k || !v || !mask || !bias || !out || !lse)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
@@ -1384,24 +1390,24 @@ int tpf_attn_forward_noalloc_bf16(const void* q, const void* k, const void* v, c
                      fn, (long long)(need / 4), (long long)(kNoAllocScratchBytes / 4));
   void* ws = nullptr;
   if ((rc = noalloc_scratch(&ws, fn))) return rc;
-  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches, layout), bias_batches,
                            out, lse, nullptr, ws, (hipStream_t)stream, fn);
 }
 
 int tpf_attn_forward_shadow_bf16(const void* q, const void* k, const void* v, const float* mask,
                                  const void* bias, void* out, float* lse, void* residual,
                                  void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
-                                 int64_t H, int64_t N, int64_t D, int seq_major,
+                                 int64_t H, int64_t N, int64_t D, int layout,
                                  int64_t bias_batches, double scale, void* stream) {
   const char* fn = "tpf_attn_forward_shadow_bf16";
   AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!q || !k || !v || !mask || !bias || !out || !lse || !residual || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   if (workspace_bytes < tpf_attn_forward_workspace_bytes(B, H, N, bias_batches))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
-  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches), bias_batches,
+  return attn_forward_impl(g, q, k, v, mask, bias, dense_bias(H, N, bias_batches, layout), bias_batches,
                            out, lse, residual, workspace, (hipStream_t)stream, fn);
 }
 
@@ -1448,8 +1454,8 @@ static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const vo
                             const void* v, const void* dout, const float* lse, const float* delta,
                             const float* mask, const void* bias, const void* workspace,
                             int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                            int64_t D, int seq_major, int64_t bias_batches, double scale) {
-  int rc = make_geom(g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+                            int64_t D, int layout, int64_t bias_batches, double scale) {
+  int rc = make_geom(g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!q || !k || !v || !dout || !lse || !delta || !mask || !bias || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
@@ -1466,26 +1472,26 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                                 const float* lse, const float* delta, const float* mask,
                                 const void* bias, void* dk, void* dv, void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
-                                int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                                int64_t N, int64_t D, int layout, int64_t bias_batches,
                                 double scale, void* stream) {
   const char* fn = "tpf_attn_backward_main_bf16";
   AttnGeom g;
   int rc = attn_bwd_prepare(&g, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
-                            workspace_bytes, B, O, H, N, D, seq_major, bias_batches, scale);
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale);
   if (rc) return rc;
   if (!dk || !dv) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   return attn_backward_main_impl(g, q, k, v, dout, lse, delta, mask, bias,
-                                 dense_bias(H, N, bias_batches), bias_batches, dk, dv, workspace,
+                                 dense_bias(H, N, bias_batches, layout), bias_batches, dk, dv, workspace,
                                  (hipStream_t)stream, fn);
 }
 
 // Stage 2 of the backward: fixed-order folds of the dQ and dBias partials.
 int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
-                                  int64_t O, int64_t H, int64_t N, int64_t D, int seq_major,
+                                  int64_t O, int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream) {
   const char* fn = "tpf_attn_backward_finish_bf16";
   AttnGeom g;
-  int rc = make_geom(&g, B, O, H, N, D, seq_major, bias_batches, scale, fn);
+  int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, (hipStream_t)stream,
@@ -1496,14 +1502,14 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
                            const float* lse, const float* delta, const float* mask,
                            const void* bias, void* dq, void* dk, void* dv, float* dbias,
                            void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
-                           int64_t H, int64_t N, int64_t D, int seq_major, int64_t bias_batches,
+                           int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
                            double scale, void* stream) {
   if (!dq || !dbias) return set_error(TPF_ERR_ARG, "tpf_attn_backward_bf16: null pointer");
   int rc = tpf_attn_backward_main_bf16(q, k, v, dout, lse, delta, mask, bias, dk, dv, workspace,
-                                       workspace_bytes, B, O, H, N, D, seq_major, bias_batches,
+                                       workspace_bytes, B, O, H, N, D, layout, bias_batches,
                                        scale, stream);
   if (rc) return rc;
-  return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, seq_major,
+  return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, layout,
                                        bias_batches, scale, stream);
 }
 

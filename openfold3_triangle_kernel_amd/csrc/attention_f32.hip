@@ -253,9 +253,13 @@ int64_t tpf_attn_forward_f32_workspace_bytes(int64_t B, int64_t H, int64_t N,
 int tpf_attn_forward_f32(const float* q, const float* k, const float* v, const float* mask,
                          const float* bias, float* out, float* lse, void* workspace,
                          int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                         int64_t D, int seq_major, int64_t bias_batches, double scale,
+                         int64_t D, int layout, int64_t bias_batches, double scale,
                          void* stream) {
   const char* fn = "tpf_attn_forward_f32";
+  if (layout & ~TPF_QKV_SEQ_MAJOR)
+    return set_error(TPF_ERR_ARG, "%s: layout flags 0x%x: only TPF_QKV_SEQ_MAJOR is supported", fn,
+                     layout);
+  const bool seq_major = layout & TPF_QKV_SEQ_MAJOR;
   if (!q || !k || !v || !mask || !bias || !out || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   if (B < 1 || O < 1 || H < 1 || N < 1)

@@ -38,6 +38,13 @@ class FakeBackend:
 
     def __init__(self):
         self.calls = []
+        self.layouts = []
+
+    def _bias(self, ptr, Bb, H, N, layout):
+        b = _bf2f(_arr(ptr, (Bb, H, N, N), np.uint16))
+        if layout & 2:  # TPF_BIAS_TRANSPOSED: storage holds bias[..., k, q]
+            b = np.swapaxes(b, -1, -2)
+        return b[:, None]
 
     def _qkv(self, ptr, B, O, H, N, D, seq_major):
         if seq_major:
@@ -52,9 +59,9 @@ class FakeBackend:
                 res = None
             else:
                 q, k, v, mask, bias, out, lse, res, ws, wsb, B, O, H, N, D, sm, Bb, scale, _ = a
-            Q, K, V = (self._qkv(p, B, O, H, N, D, sm) for p in (q, k, v))
+            Q, K, V = (self._qkv(p, B, O, H, N, D, sm & 1) for p in (q, k, v))
             M = _arr(mask, (B, O, N), np.float32).reshape(B, O, 1, 1, N)
-            Bi = _bf2f(_arr(bias, (Bb, H, N, N), np.uint16))[:, None]
+            Bi = self._bias(bias, Bb, H, N, sm)
             o, l, _ = attention_forward(Q, K, V, M, Bi, scale=scale)
             ob = _f2bf(o)
             _arr(out, (B, O, N, H, D), np.uint16)[...] = ob
@@ -75,13 +82,14 @@ class FakeBackend:
         elif name == "tpf_attn_backward_bf16":
             (q, k, v, do, lse, delta, mask, bias, dq, dk, dv, dbias, ws, wsb, B, O, H, N, D, sm,
              Bb, scale, _) = a
-            Q, K, V = (self._qkv(p, B, O, H, N, D, sm) for p in (q, k, v))
+            Q, K, V = (self._qkv(p, B, O, H, N, D, sm & 1) for p in (q, k, v))
             M = _arr(mask, (B, O, N), np.float32).reshape(B, O, 1, 1, N)
-            Bi = _bf2f(_arr(bias, (Bb, H, N, N), np.uint16))[:, None]
+            Bi = self._bias(bias, Bb, H, N, sm)
+            self.layouts.append(sm)
             dO = _bf2f(_arr(do, (B, O, N, H, D), np.uint16))
             gq, gk, gv, gb = attention_backward(Q, K, V, M, Bi, dO, scale=scale)
             for ptr, g in ((dq, gq), (dk, gk), (dv, gv)):
-                if sm:
+                if sm & 1:
                     _arr(ptr, (B, O, N, H, D), np.uint16)[...] = _f2bf(np.swapaxes(g, 2, 3))
                 else:
                     _arr(ptr, (B, O, H, N, D), np.uint16)[...] = _f2bf(g)
@@ -273,3 +281,25 @@ def test_fp32_q_delegates_to_fp32_inference(monkeypatch):
         out = attention.turbopairformer_triangle_attention(q, q, q, mask, bias)
     assert seen["called"] and out.shape == (1, 2, 8, 2, 4)
     attention._SUPPORT_CACHE.clear()
+
+
+def test_transposed_bias_view_is_read_in_place(fake):
+    """The ending node passes bias.transpose(-1, -2) of a contiguous tensor: the
+    facade hands its storage to the kernels with TPF_BIAS_TRANSPOSED instead of
+    copying it, and the gradient comes back in the view's shape."""
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    q, k, v, mask, bias, dout = attention_case(1, 3, 2, 64, 16, mask_frac=0.1, seed=17)
+    base = bias.transpose(-1, -2).contiguous().to(torch.bfloat16).requires_grad_(True)
+    view = base.transpose(-1, -2)
+    assert not view.is_contiguous()
+    tq, tk, tv = (t.to(torch.bfloat16).requires_grad_(True) for t in (q, k, v))
+    out = turbopairformer_triangle_attention(tq, tk, tv, mask, view)
+    out.backward(dout.to(torch.bfloat16))
+    assert fake.layouts and fake.layouts[-1] & 2
+    ref_out, _, _ = attention_forward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(),
+                                      view.detach().float().numpy())
+    ref = attention_backward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(),
+                             view.detach().float().numpy(), dout.numpy())
+    assert max_rel(out.detach().float().numpy(), ref_out) <= 2e-2
+    assert max_rel(base.grad.float().numpy(), np.swapaxes(ref[3], -1, -2)) <= 2e-2

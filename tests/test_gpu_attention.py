@@ -168,3 +168,30 @@ def test_fp32_pair_bias_gets_fp32_gradient(gpu):
     comes back in FP32 (reference turbopairformer_triangle_attention.py:371-377)."""
     print("[attn parity] fp32 pair bias", flush=True)
     _bias_variant(gpu, 1, 8, 4, 192, 32, (1, 1, 4, 192, 192), torch.float32, seed=12)
+
+
+@pytest.mark.gpu
+def test_transposed_bias_in_place_matches_copy(gpu):
+    """bias.transpose(-1, -2) of a contiguous bias (the ending node) is read in
+    place (TPF_BIAS_TRANSPOSED); outputs and gradients equal, bit for bit,
+    those of the same values passed as a contiguous tensor."""
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    print("[attn parity] transposed bias view vs contiguous copy", flush=True)
+    q, k, v, mask, bias, dout = attention_case(1, 8, 4, 192, 32, mask_frac=0.1, seed=23)
+    base = bias.transpose(-1, -2).contiguous().to(gpu, torch.bfloat16)
+    res = []
+    for contiguous in (False, True):
+        b0 = base.clone().requires_grad_(True)
+        view = b0.transpose(-1, -2)
+        if contiguous:
+            view = view.contiguous()
+        tq, tk, tv = (t.to(gpu, torch.bfloat16).requires_grad_(True) for t in (q, k, v))
+        out = turbopairformer_triangle_attention(tq, tk, tv, mask.to(gpu), view)
+        out.backward(dout.to(gpu, torch.bfloat16))
+        torch.cuda.synchronize()
+        res.append([t.detach().float().cpu() for t in (out, tq.grad, tk.grad, tv.grad, b0.grad)])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    ref_out, _, _ = attention_forward(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), bias.numpy())
+    assert max_rel(res[0][0].numpy(), ref_out) <= TOL
