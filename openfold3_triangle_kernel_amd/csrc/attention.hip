@@ -110,6 +110,9 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
 }
 
+// Longest mask row the forward stages in LDS (128 KiB of dynamic LDS).
+constexpr int kFwdMaskLdsMaxN = 32768;
+
 // ---------------------------------------------------------------------------
 // Forward.  One workgroup = NW waves = 32*NW queries of one plane (NW = 4:
 // 2, 3 and 6 measured slower at N = 384); each wave owns
@@ -140,6 +143,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
   constexpr int VITEMS = 16 * DP / 8;   // (4-key group, 8-channel chunk) V items
   __shared__ __attribute__((aligned(16))) __bf16 Ks[2][64 * KP];
   __shared__ __attribute__((aligned(16))) __bf16 Vt[2][DP * VP];
+  // This plane's mask row divided by the scale (dynamic LDS of N floats).
+  extern __shared__ __attribute__((aligned(16))) float Ms[];
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int ql = lane & 31, hl = lane >> 5;
@@ -214,6 +219,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
   // is per plane, so the flag is uniform); computed up front so no wait on
   // the mask sits inside the pipelined loop.
   const int ntiles = N / 64;
+  for (int i = tid; i < N; i += NT) Ms[i] = mrow[i] * inv_scale;
   uint64_t mbits = ~0ull;
   if (ntiles <= 64) {
     mbits = 0ull;
@@ -265,9 +271,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
       if (masked) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          f32x4 mv = *reinterpret_cast<const f32x4*>(mrow + kt + sb * 32 + 8 * j + 4 * hl);
+          const f32x4 mv = *reinterpret_cast<const f32x4*>(&Ms[kt + sb * 32 + 8 * j + 4 * hl]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s[4 * j + i] = fmaf(mv[i], inv_scale, s[4 * j + i]);
+          for (int i = 0; i < 4; ++i) s[4 * j + i] += mv[i];
         }
       }
       float mx = s[0];
@@ -1209,18 +1215,22 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   const int64_t total = ((g.N + 32 * nw - 1) / (32 * nw)) * (int64_t)g.H * g.B * g.O;
   if ((total + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many query tiles", fn);
+  if (g.N > kFwdMaskLdsMaxN)
+    return set_error(TPF_ERR_SHAPE, "%s: N=%d exceeds the forward's mask staging limit %d", fn, g.N,
+                     kFwdMaskLdsMaxN);
   float* bias_s = (float*)workspace;
   int rc = attn_prescale_bias(g, bias, bv, bias_s, bias_batches, s, fn);
   if (rc) return rc;
   g.bias_bstride = (bias_batches == 1) ? 0 : (int64_t)g.H * g.N * g.N;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
+  const unsigned mask_lds = (unsigned)g.N * 4u;
   if (g.D <= 32)
-    hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves32>), grid, dim3(64 * kFwdWaves32), 0, s,
+    hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves32>), grid, dim3(64 * kFwdWaves32), mask_lds, s,
                        (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
                        (__bf16*)res, g);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves64>), grid, dim3(64 * kFwdWaves64), 0, s,
+    hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves64>), grid, dim3(64 * kFwdWaves64), mask_lds, s,
                        (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
                        (__bf16*)res, g);

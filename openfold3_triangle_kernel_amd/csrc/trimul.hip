@@ -23,15 +23,16 @@
 // the transposed position (incoming), read through the GEMM's row gather.
 //
 // Kernels of one direction:
-//   forward:  tm_ln_rows (LN_in) -> tm_in_proj<fwd> (a, b, gl) -> GEMM x ->
+//   forward:  tm_ln_rows (LN_in) -> tm_in_proj_fwd (a, b, gl) -> GEMM x ->
 //             tm_ln_planes (LN_out) -> tm_out_proj<fwd> (out)
 //   backward: tm_out_proj<bwd> (dy, d gl) -> tm_ln_bwd<planes> (dx, LN_out
-//             partials) -> GEMMs da, db -> tm_in_proj<bwd> (d a_p .. d b_g)
+//             partials) -> GEMMs da, db -> tm_in_proj_bwd (d a_p .. d b_g)
 //             -> tm_ln_bwd<rows> (dz, LN_in partials) -> split-K weight
 //             GEMMs -> fixed-order folds.
-// 32-deep k stages: every TriMul GEMM has K = C or 5H (small), and the
-// halved LDS ring lets the forward input projection run 4 workgroups per CU.
+// 32-deep k stages: every TriMul GEMM has K = C or 5H (small).
 #define TPF_GEMM_GK 32
+#include <atomic>
+
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "tpf_gemm.hpp"
@@ -57,7 +58,7 @@ constexpr int lds_bytes(int epilogue, int ns = kGNS) {
 }
 // Ring depths per kernel (measured): the short-K projections keep two
 // stages (occupancy), the long-K / large-epilogue kernels take more.
-constexpr int kInProjFwdNS = 2, kInProjBwdNS = 3, kOutProjNS = 4, kOutProjFwdNS = 2;
+constexpr int kInProjBwdNS = 3, kOutProjNS = 4, kOutProjFwdNS = 2;
 __host__ __device__ constexpr int ln_bwd_ns(bool planes) { return planes ? 2 : 4; }
 constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2, kInProjBwdNS);  // d tile + [dp | dg] tile
 constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2, kOutProjNS);  // gate + dout tiles
@@ -91,8 +92,10 @@ __device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
 //   Wp tile t < 2*ntg (branch t / ntg, channel block q = t % ntg): rows
 //   [p c0..c0+31 | g c0..c0+31 | p c0+32..c0+63 | g c0+32..c0+63], c0 = 64q,
 //   so the wave holding output columns 64wn.. sees p and g of the same 32
-//   channels in its two accumulator columns; tile 2*ntg holds W_g.
-//   W5 = [W_ap; W_ag; W_bp; W_bg; W_g] [5H][C] (the reference's d_w5 order);
+//   channels in its two accumulator columns (the projection backward's B
+//   operand).
+//   W5 = [W_ap; W_ag; W_bp; W_bg; W_g] [5H][C] (the reference's d_w5 order;
+//   also the forward projections' stationary operand);
 //   Wz = W_z [C][H].  Missing channels are zero rows.
 // ---------------------------------------------------------------------------
 struct TmWeights {
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
                                                               __bf16* __restrict__ wz, int C,
                                                               int ntg) {
   const int cpr = C / 8;
-  const int wp_rows = (2 * ntg + 1) * 128;
+  const int wp_rows = 2 * ntg * 128;
   const int64_t total = (int64_t)(wp_rows + 6 * C) * cpr;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * 256) {
@@ -119,14 +122,10 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
     if (row < wp_rows) {
       dst = wp + (int64_t)row * C + ch * 8;
       const int t = row / 128, rr = row % 128;
-      if (t < 2 * ntg) {
-        const int br = t / ntg, q = t % ntg;
-        const int c = 64 * q + 32 * (rr / 64) + (rr & 31);
-        const bool isg = (rr >> 5) & 1;
-        if (c < C) src = (br ? (isg ? w.bg : w.bp) : (isg ? w.ag : w.ap)) + (int64_t)c * C;
-      } else if (rr < C) {
-        src = w.g + (int64_t)rr * C;
-      }
+      const int br = t / ntg, q = t % ntg;
+      const int c = 64 * q + 32 * (rr / 64) + (rr & 31);
+      const bool isg = (rr >> 5) & 1;
+      if (c < C) src = (br ? (isg ? w.bg : w.bp) : (isg ? w.ag : w.ap)) + (int64_t)c * C;
     } else if (row < wp_rows + 5 * C) {
       const int j = row - wp_rows, blk = j / C, c = j % C;
       dst = w5 + (int64_t)j * C + ch * 8;
@@ -437,22 +436,237 @@ __device__ __forceinline__ void put_planes(__bf16* S, const RegTile& t, int nch)
 }
 
 // ---------------------------------------------------------------------------
-// Input projections (stored row order).  Forward: tiles nt < 2*ntg produce
-// a / b = mask * sigmoid(g) * p for 64 channels (channel-major stores);
-// tile 2*ntg produces the output-gate logits gl (row-major).  Backward
-// (BWD): recompute p, g and write d p = d * mask * s(g),
+// Forward input projections, weight-stationary.  One wave per 16 channels
+// (C / 16 waves) holds the bf16 rows of W_ap, W_ag, W_bp, W_bg and W_g for
+// its channels in registers (the B operands of v_mfma_f32_16x16x32_bf16) for
+// the whole kernel; workgroups are persistent and walk 32-row blocks of zln
+// in stored row order.
+//   * loads: the first half of the waves stream each block's rows straight
+//     into a 4-deep LDS ring (buffer_load ... lds, three blocks ahead; the
+//     chunk order within a row is rotated by the row so the A-fragment
+//     reads are conflict-free) and the block's mask values beside them;
+//     these waves issue no stores, so their vmcnt waits cover loads only;
+//   * stores: the second half of the waves copy each block's staged outputs
+//     (a and b as [channel][32 positions], gl as [32 rows][channel], double
+//     buffered in LDS) to HBM as 64-byte plane segments and 2C-byte rows.
+// One barrier per block.
+//   16x16x32 layouts: A lane l holds A[l % 16][8 (l / 16) ..+8]; B lane l
+//   holds B[8 (l / 16) ..+8][l % 16]; C register r of lane l is
+//   C[4 (l / 16) + r][l % 16].
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// Direct 4-byte buffer -> LDS load: lane i writes dst_base + 4 i.
+__device__ __forceinline__ void buf2lds4(i32x4 rsrc, uint32_t voff, void* dst_base) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(lds_offset(dst_base));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+
+// Depth of the zln block ring (blocks in flight: kInFwdDepth - 2).
+constexpr int kInFwdDepth = 4;
+template <int C, bool PAD>
+__global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
+    const __bf16* __restrict__ zln, const __bf16* __restrict__ w5, const float* __restrict__ mask,
+    __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl, TmGeom g,
+    int64_t nblocks) {
+  constexpr int NW = C / 16;         // waves
+  constexpr int CPR = C / 8;         // 16-byte chunks per row
+  constexpr int KS = C / 32;         // 32-deep k steps
+  constexpr int PP = 40;             // plane staging pitch (bf16): 32 positions + pad
+  constexpr int GP = C + 8;          // gl staging pitch (bf16)
+  __shared__ __attribute__((aligned(1024))) __bf16 As[kInFwdDepth][32 * C];
+  __shared__ __attribute__((aligned(256))) float Ms[kInFwdDepth][64];
+  __shared__ __attribute__((aligned(16))) __bf16 Sp[2][2][C * PP];  // [buf][a | b][ch][pos]
+  __shared__ __attribute__((aligned(16))) __bf16 Sg[2][32 * GP];    // [buf][pos][ch]
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int ch = 16 * w + l16;  // this lane's output channel
+  const bool loader = w < NW / 2;
+
+  // Stationary B operands: W5 rows (proj * C + ch), k chunk 4 ks + lg.
+  bf16x8 wf[5][KS];
+#pragma unroll
+  for (int p = 0; p < 5; ++p)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) wf[p][ks] = ld8(w5 + ((int64_t)p * C + ch) * C + 8 * (4 * ks + lg));
+
+  const i32x4 rs_z = buffer_rsrc(zln);
+  const i32x4 rs_m = buffer_rsrc(mask);
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(a_pl, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(b_pl, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_g = __builtin_amdgcn_make_buffer_rsrc(gl, 0, 0x7FFFFFFF, 0x00020000);
+  // Workgroup c takes the contiguous blocks [c per, (c + 1) per).
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loader: instruction j of wave w fills LDS chunks (2 w + j) * 64 + lane
+  // (row ci / CPR, slot ci % CPR) with global chunk (slot - row) mod CPR.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % kInFwdDepth);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ci = (2 * w + j) * 64 + lane;
+      const int r = ci / CPR, slot = ci % CPR;
+      const int gc = (slot - r % CPR + CPR) % CPR;
+      const int64_t m = blk * 32 + r;
+      const bool ok = blk < bend && m < g.R;
+      const uint32_t off = ok ? (uint32_t)((tm_phys_row(g, m) * C + 8 * gc) * 2) : kBufOOB;
+      buf2lds16(rs_z, off, &As[stage][(2 * w + j) * 512]);
+    }
+    if (w == 0) {
+      const int64_t m = blk * 32 + lane;
+      const bool ok = lane < 32 && blk < bend && m < g.R;
+      buf2lds4(rs_m, ok ? (uint32_t)(tm_phys_row(g, m) * 4) : kBufOOB, &Ms[stage][0]);
+    }
+  };
+  auto mma = [&](int64_t blk, f32x4 (&acc)[5][2]) {
+#pragma unroll
+    for (int p = 0; p < 5; ++p)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) acc[p][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const __bf16* A = As[blk % kInFwdDepth];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 16 * rt + l16;
+        const bf16x8 af =
+            *reinterpret_cast<const bf16x8*>(&A[row * C + 8 * ((4 * ks + lg + row) % CPR)]);
+#pragma unroll
+        for (int p = 0; p < 5; ++p) acc[p][rt] = mfma16(af, wf[p][ks], acc[p][rt]);
+      }
+  };
+  // Epilogue of block blk: a = mask s(g_a) p_a, b likewise, gl -> staging.
+  auto epilogue = [&](int64_t blk, const f32x4 (&acc)[5][2]) {
+    const int sb = (int)(blk & 1);
+    __bf16* Sa = Sp[sb][0];
+    __bf16* Sb = Sp[sb][1];
+    __bf16* G = Sg[sb];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r0 = 16 * rt + 4 * lg;
+      const f32x4 mk = *reinterpret_cast<const f32x4*>(&Ms[blk % kInFwdDepth][r0]);
+      bf16x4 va, vb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        va[e] = f2bf(mk[e] * sigmoidf(acc[1][rt][e]) * acc[0][rt][e]);
+        vb[e] = f2bf(mk[e] * sigmoidf(acc[3][rt][e]) * acc[2][rt][e]);
+        G[(r0 + e) * GP + ch] = f2bf(acc[4][rt][e]);
+      }
+      *reinterpret_cast<bf16x4*>(&Sa[ch * PP + r0]) = va;
+      *reinterpret_cast<bf16x4*>(&Sb[ch * PP + r0]) = vb;
+    }
+  };
+  auto stores = [&](int64_t blk) {
+    // 12 C 16-byte chunks per block over the 2 C storing threads: all LDS
+    // reads first, then the stores (buffer stores; rows past the end are
+    // dropped through an out-of-range offset, so there are no branches).
+    const int sb = (int)(blk & 1);
+    const __bf16* G = Sg[sb];
+    const int st = tid - 2 * C;
+    const int64_t mb0 = blk * 32;
+    bf16x8 v[6];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int q = st + 2 * C * it;
+      const int t = it >> 1, c = (q - 4 * C * t) >> 2, part = q & 3;
+      v[it] = *reinterpret_cast<const bf16x8*>(&Sp[sb][t][c * PP + 8 * part]);
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int q = st + 2 * C * it, row = q / CPR, c8 = q % CPR;
+      v[4 + it] = *reinterpret_cast<const bf16x8*>(&G[row * GP + 8 * c8]);
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int q = st + 2 * C * it;       // < 8C: a then b, (channel, 8-position part)
+      const int t = it >> 1;
+      const int c = (q - 4 * C * t) >> 2, part = q & 3;
+      const int64_t mb = mb0 + 8 * part;
+      if (!PAD) {
+        // N % 8 == 0: the 8 positions are contiguous in one plane row.
+        int64_t bb, pp;
+        tm_bp(g, mb < g.R ? mb : 0, bb, pp);
+        const uint32_t off = mb < g.R ? (uint32_t)((((int64_t)bb * g.H + c) * g.PS + pp) * 2) : kBufOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), t ? rs_b : rs_a, off, 0, 0);
+      } else {
+        __bf16* planes = t ? b_pl : a_pl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t m = mb + e;
+          if (m < g.R) {
+            int64_t bb, pp;
+            tm_bp(g, m, bb, pp);
+            planes[((int64_t)bb * g.H + c) * g.PS + tm_plane_off(g, pp)] = v[it][e];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int q = st + 2 * C * it;       // < 4C: (row, chunk)
+      const int row = q / CPR, c8 = q % CPR;
+      const int64_t m = mb0 + row;
+      const uint32_t off = m < g.R ? (uint32_t)((tm_phys_row(g, m) * C + 8 * c8) * 2) : kBufOOB;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[4 + it]), rs_g, off, 0, 0);
+    }
+  };
+  // Pipeline: iteration blk issues the loads of blk + 3, multiplies blk + 1
+  // while finishing blk's epilogue, waits for blk + 2's loads, then the
+  // storing waves write blk's outputs.
+  if (loader) {
+#pragma unroll
+    for (int d = 0; d < kInFwdDepth - 1; ++d) issue(bbeg + d);
+    // blocks bbeg, bbeg + 1 landed
+    if (w == 0) wait_vmcnt<3 * (kInFwdDepth - 3)>(); else wait_vmcnt<2 * (kInFwdDepth - 3)>();
+  }
+  __syncthreads();
+  f32x4 acc0[5][2], acc1[5][2];
+  mma(bbeg, acc0);
+  int64_t blk = bbeg;
+  auto iter = [&](f32x4 (&cur)[5][2], f32x4 (&nxt)[5][2]) {
+    if (loader) issue(blk + kInFwdDepth - 1);
+    // The two waves sharing a SIMD (w, w + NW / 2) take the two halves in
+    // opposite order, so one's MFMAs overlap the other's epilogue VALU.
+    if (loader) {
+      if (blk + 1 < bend) mma(blk + 1, nxt);
+      epilogue(blk, cur);
+    } else {
+      epilogue(blk, cur);
+      if (blk + 1 < bend) mma(blk + 1, nxt);
+    }
+    if (loader) {
+      if (w == 0) wait_vmcnt<3 * (kInFwdDepth - 3)>(); else wait_vmcnt<2 * (kInFwdDepth - 3)>();   // block blk + 2 landed
+    }
+    __syncthreads();
+    if (!loader) stores(blk);
+    ++blk;
+  };
+#pragma unroll 1
+  while (blk < bend) {
+    iter(acc0, acc1);
+    if (blk >= bend) break;
+    iter(acc1, acc0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Input projections, backward (stored row order): recompute p, g for 64
+// channels of branch a or b and write d p = d * mask * s(g),
 // d g = d * mask * p * s(g) (1 - s(g)) into dproj5, d = da / db.
 // ---------------------------------------------------------------------------
-template <bool BWD>
-__global__ __launch_bounds__(256, BWD ? 2 : 4) void tm_in_proj_kernel(
+__global__ __launch_bounds__(256, 2) void tm_in_proj_bwd_kernel(
     const __bf16* __restrict__ zln, const __bf16* __restrict__ wp, const float* __restrict__ mask,
-    __bf16* __restrict__ a_pl, __bf16* __restrict__ b_pl, __bf16* __restrict__ gl,
+    const __bf16* __restrict__ a_pl, const __bf16* __restrict__ b_pl,
     __bf16* __restrict__ dproj5, TmGeom g, int C) {
-  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kInProjLds : lds_bytes(128 * kSP * 2, kInProjFwdNS)];
+  __shared__ __attribute__((aligned(1024))) char smem[kInProjLds];
   __shared__ float mask_s[128];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
-  const int tn = 2 * g.ntg + (BWD ? 0 : 1);
+  const int tn = 2 * g.ntg;
   const int64_t tm = (g.R + 127) / 128;
   const int64_t T = xcd_order(tm * tn);
   if (T < 0) return;
@@ -465,39 +679,15 @@ __global__ __launch_bounds__(256, BWD ? 2 : 4) void tm_in_proj_kernel(
     mask_s[threadIdx.x] = rho >= 0 ? mask[rho] : 0.f;
   }
   GemmOperand A{zln, C, (int)g.R, g.outgoing ? 0 : g.N, g.div_n, g.div_nn};
-  GemmOperand W{wp, C, (2 * g.ntg + 1) * 128, 0, {}, {}};
+  GemmOperand W{wp, C, 2 * g.ntg * 128, 0, {}, {}};
   RegTile dreg;
-  if (BWD) fetch_planes(dreg, (nt / g.ntg) ? b_pl : a_pl, g, 64, m0, 64 * (nt % g.ntg));
+  fetch_planes(dreg, (nt / g.ntg) ? b_pl : a_pl, g, 64, m0, 64 * (nt % g.ntg));
   f32x16 acc[2][2];
-  gemm_tile<true, true, BWD ? kInProjBwdNS : kInProjFwdNS>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
+  gemm_tile<true, true, kInProjBwdNS>(A, W, (int)m0, nt * 128, 0, C, smem, acc);
   const AccPos ap;
   __bf16* S0 = reinterpret_cast<__bf16*>(smem);
-
-  if (!BWD && nt == 2 * g.ntg) {  // output-gate logits, row-major
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) S0[ap.row(i, r) * kSP + ap.col(j)] = f2bf(acc[i][j][r]);
-    __syncthreads();
-    tm_store_rows(S0, C, rho_s, gl, C, 0);
-    return;
-  }
   const int br = nt / g.ntg, q = nt % g.ntg;
   const int cl = 32 * ap.wn + ap.rl;  // channel 64q + cl
-  if (!BWD) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = ap.row(i, r);
-        S0[cl * kSP + row] = f2bf(mask_s[row] * sigmoidf(acc[i][1][r]) * acc[i][0][r]);
-      }
-    __syncthreads();
-    tm_store_planes(S0, 64, br ? b_pl : a_pl, g, m0, 64 * q);
-    return;
-  }
   // Backward: d tile [64 ch][128 pos] in S0, outputs [128 rows][dp 64 | dg 64] in So.
   __bf16* So = S0 + 64 * kSP;
   put_planes(S0, dreg, 64);
@@ -802,7 +992,7 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
 }
 
 static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
-static int64_t tm_wp_rows(int64_t C) { return (2 * ((C + 63) / 64) + 1) * 128; }
+static int64_t tm_wp_rows(int64_t C) { return 2 * ((C + 63) / 64) * 128; }
 static int64_t tm_weights_bytes(int64_t C) {
   return align256(tm_wp_rows(C) * C * 2) + align256(5 * C * C * 2) + align256(C * C * 2);
 }
@@ -833,6 +1023,20 @@ static int tm_pack(const TmWeights& w, const TmPacked& k, int C, int ntg, hipStr
 }
 
 static unsigned tm_grid(int64_t tiles) { return (unsigned)((tiles + 7) / 8 * 8); }
+
+// Compute units of the current device (cached per device; 256 if unknown).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 #define TM_DISPATCH_C(C, KERNEL, GRID, ...)                                                   \
   switch (C) {                                                                               \
@@ -883,9 +1087,27 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
                 ln_in_b, (__bf16*)zln, mean_in, rstd_in, g.R);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_in)"))) return rc;
   const int64_t tiles = (g.R + 127) / 128;
-  hipLaunchKernelGGL(tm_in_proj_kernel<false>, dim3(tm_grid(tiles * (2 * g.ntg + 1))), dim3(256), 0,
-                     s, (const __bf16*)zln, k.wp, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate,
-                     (__bf16*)nullptr, g, (int)C);
+  {
+    // Persistent: one workgroup of C / 16 waves per CU share at C = 128.
+    const int64_t nblk = (g.R + 31) / 32;
+    const int64_t cap = (int64_t)device_cus() * (128 / C);
+    const unsigned grid = (unsigned)(nblk < cap ? nblk : cap);
+    switch (C) {
+#define TM_IN_FWD(CC)                                                                           \
+  case CC:                                                                                      \
+    if (g.Np == g.N)                                                                            \
+      hipLaunchKernelGGL((tm_in_proj_fwd_kernel<CC, false>), dim3(grid), dim3(4 * CC), 0, s,    \
+                         (const __bf16*)zln, k.w5, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate, \
+                         g, nblk);                                                              \
+    else                                                                                        \
+      hipLaunchKernelGGL((tm_in_proj_fwd_kernel<CC, true>), dim3(grid), dim3(4 * CC), 0, s,     \
+                         (const __bf16*)zln, k.w5, mask, (__bf16*)a, (__bf16*)b, (__bf16*)gate, \
+                         g, nblk);                                                              \
+    break;
+      TM_IN_FWD(32) TM_IN_FWD(64) TM_IN_FWD(96) TM_IN_FWD(128)
+#undef TM_IN_FWD
+    }
+  }
   if ((rc = check_launch("tpf_trimul_forward_bf16(in_proj)"))) return rc;
   GemmArgs ga{};
   ga.A = (const __bf16*)a; ga.a_ld = g.Np; ga.a_bs = g.PS;
@@ -998,8 +1220,8 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gb.batch = (int)(B * C);
   if ((rc = gemm_launch_pair(ga, 1, 0, gb, 0, 0, 0, s, "tpf_trimul_backward_bf16(dA, dB)")))
     return rc;
-  hipLaunchKernelGGL(tm_in_proj_kernel<true>, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
-                     (const __bf16*)zln, k.wp, mask, da, db, (__bf16*)nullptr, dproj5, g, (int)C);
+  hipLaunchKernelGGL(tm_in_proj_bwd_kernel, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
+                     (const __bf16*)zln, k.wp, mask, da, db, dproj5, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
   hipLaunchKernelGGL(tm_ln_bwd_kernel<false>, dim3(grid_rows), dim3(256), 0, s,
                      (const __bf16*)dproj5, 5 * H, k.w5, (int)(5 * H),
