@@ -654,6 +654,197 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Input projections, backward, weight-stationary (N % 8 == 0).  The same
+// persistent walk over 32-row blocks as the forward, with W_ap, W_ag, W_bp,
+// W_bg rows of the wave's 16 channels in registers as the A operand, so the
+// accumulators come out transposed (register r of lane l: channel
+// 16 w + 4 (l / 16) + r, row l % 16) and each lane owns 4 consecutive
+// channels of one row: the dproj5 row segments are 8-byte LDS writes.  Per
+// block the loading waves stream zln rows, the da / db plane segments
+// ([channel][32 positions], 64 bytes each) and the mask into a 4-deep LDS
+// ring; d is read back transposed (ds_read_b64_tr_b16).  Outputs
+// d a_p = d s(g_a), d a_g = d p_a s (1 - s), likewise for b, go through one
+// LDS staging tile [32 rows][4C] and are stored as 8C-byte row segments of
+// dproj5 by the storing waves.  Two barriers per block (staging reuse).
+// ---------------------------------------------------------------------------
+// 32-bit forms of the row / plane index helpers (R < 2^30 rows and plane
+// tensors below 2^30 elements, both checked by tm_geom).
+__device__ __forceinline__ uint32_t tm_phys_row32(const TmGeom& g, uint32_t m) {
+  if (g.outgoing) return m;
+  const uint32_t b = fdiv(m, g.div_nn), p = m - b * (uint32_t)g.NN;
+  const uint32_t i = fdiv(p, g.div_n), k = p - i * (uint32_t)g.N;
+  return b * (uint32_t)g.NN + k * (uint32_t)g.N + i;
+}
+// Element offset of stored row m in channel plane c (N % 8 == 0: Np == N).
+__device__ __forceinline__ uint32_t tm_plane_elem32(const TmGeom& g, uint32_t m, int c) {
+  const uint32_t b = fdiv(m, g.div_nn), p = m - b * (uint32_t)g.NN;
+  return (b * (uint32_t)g.H + (uint32_t)c) * (uint32_t)g.PS + p;
+}
+
+constexpr int kInBwdDepth = 4;
+template <int C>
+__global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
+    const __bf16* __restrict__ zln, const __bf16* __restrict__ w5, const float* __restrict__ mask,
+    const __bf16* __restrict__ da, const __bf16* __restrict__ db, __bf16* __restrict__ dproj5,
+    TmGeom g, int64_t nblocks) {
+  constexpr int NW = C / 16;         // waves
+  constexpr int CPR = C / 8;         // 16-byte chunks per zln row
+  constexpr int KS = C / 32;         // 32-deep k steps
+  constexpr int SOP = 4 * C + 8;     // staging pitch (bf16)
+  __shared__ __attribute__((aligned(1024))) __bf16 As[kInBwdDepth][32 * C];
+  __shared__ __attribute__((aligned(1024))) __bf16 Ds[kInBwdDepth][2 * C * 32];  // [t][ch][pos]
+  __shared__ __attribute__((aligned(256))) float Ms[kInBwdDepth][64];
+  __shared__ __attribute__((aligned(16))) __bf16 So[32 * SOP];                   // [row][4C]
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const bool loader = w < NW / 2;
+
+  // Stationary A operands: W5 rows (proj * C + 16 w + l16), k chunk 4 ks + lg.
+  bf16x8 wf[4][KS];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      wf[p][ks] = ld8(w5 + ((int64_t)p * C + 16 * w + l16) * C + 8 * (4 * ks + lg));
+
+  const i32x4 rs_z = buffer_rsrc(zln);
+  const i32x4 rs_m = buffer_rsrc(mask);
+  const i32x4 rs_da = buffer_rsrc(da);
+  const i32x4 rs_db = buffer_rsrc(db);
+  const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(dproj5, 0, 0x7FFFFFFF, 0x00020000);
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loads of a block per loading wave: 2 zln, 4 plane-segment, (wave 0) 1 mask.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % kInBwdDepth);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ci = (2 * w + j) * 64 + lane;
+      const int r = ci / CPR, slot = ci % CPR;
+      const int gc = (slot - r % CPR + CPR) % CPR;
+      const uint32_t m = (uint32_t)blk * 32 + r;
+      const bool ok = blk < bend && m < (uint32_t)g.R;
+      const uint32_t off = ok ? (tm_phys_row32(g, m) * C + 8 * gc) * 2 : kBufOOB;
+      buf2lds16(rs_z, off, &As[stage][(2 * w + j) * 512]);
+    }
+    // Plane chunks gi = (4 w + j) * 64 + lane over [t][channel][4 parts].
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gi = (4 * w + j) * 64 + lane;
+      const int t = (4 * w + j) * 64 / (4 * C), rem = gi - t * 4 * C;  // t wave-uniform
+      const int c = rem >> 2, part = rem & 3;
+      const uint32_t mb = (uint32_t)blk * 32 + 8 * part;
+      const bool ok = blk < bend && mb < (uint32_t)g.R;
+      const uint32_t off = ok ? tm_plane_elem32(g, mb, c) * 2 : kBufOOB;
+      // The first 4C chunks are da, the rest db (each wave's 4 instructions
+      // stay within one tensor: 4C is a multiple of 256).
+      buf2lds16(t ? rs_db : rs_da, off, &Ds[stage][(4 * w + j) * 512]);
+    }
+    if (w == 0) {
+      const uint32_t m = (uint32_t)blk * 32 + lane;
+      const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
+      buf2lds4(rs_m, ok ? tm_phys_row32(g, m) * 4 : kBufOOB, &Ms[stage][0]);
+    }
+  };
+  auto mma = [&](int64_t blk, f32x4 (&acc)[4][2]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) acc[p][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const __bf16* A = As[blk % kInBwdDepth];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 16 * rt + l16;
+        const bf16x8 zf =
+            *reinterpret_cast<const bf16x8*>(&A[row * C + 8 * ((4 * ks + lg + row) % CPR)]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) acc[p][rt] = mfma16(wf[p][ks], zf, acc[p][rt]);
+      }
+  };
+  // d for (channels 16 w + 4 lg + e, row 16 rt + l16) from the [ch][pos]
+  // plane tile: lane L of a 16-lane group supplies row 16 w + 4 lg + L / 4,
+  // columns 16 rt + 4 (L % 4) .. + 3.
+  auto epilogue = [&](int64_t blk, const f32x4 (&acc)[4][2]) {
+    const int stage = (int)(blk % kInBwdDepth);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const __bf16* src = &Ds[stage][(t * C + 16 * w + 4 * lg + (l16 >> 2)) * 32 + 16 * rt + 4 * (l16 & 3)];
+        const bf16x4 dv = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)src);
+        const int row = 16 * rt + l16;
+        const float mk = Ms[stage][row];
+        bf16x4 dp, dg;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float d = bf2f(dv[e]) * mk;
+          const float p = acc[2 * t][rt][e];
+          const float sg = sigmoidf(acc[2 * t + 1][rt][e]);
+          dp[e] = f2bf(d * sg);
+          dg[e] = f2bf(d * p * sg * (1.f - sg));
+        }
+        const int col = 16 * w + 4 * lg;
+        *reinterpret_cast<bf16x4*>(&So[row * SOP + (2 * t) * C + col]) = dp;
+        *reinterpret_cast<bf16x4*>(&So[row * SOP + (2 * t + 1) * C + col]) = dg;
+      }
+  };
+  auto stores = [&](int64_t blk) {
+    // 16 C chunks (32 rows x C / 2) over the 2 C storing threads, four LDS
+    // reads ahead of their stores.
+    const int st = tid - 2 * C;
+    const int64_t mb0 = blk * 32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 v[4];
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int q = st + 2 * C * (4 * h + it), row = q / (C / 2), k = q % (C / 2);
+        v[it] = *reinterpret_cast<const bf16x8*>(&So[row * SOP + 8 * k]);
+      }
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int q = st + 2 * C * (4 * h + it), row = q / (C / 2), k = q % (C / 2);
+        const uint32_t m = (uint32_t)mb0 + row;
+        const uint32_t off = m < (uint32_t)g.R ? (tm_phys_row32(g, m) * 5 * C + 8 * k) * 2 : kBufOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o, off, 0, 0);
+      }
+    }
+  };
+  if (loader) {
+#pragma unroll
+    for (int d = 0; d < kInBwdDepth - 1; ++d) issue(bbeg + d);
+    // blocks bbeg, bbeg + 1 landed
+    if (w == 0) wait_vmcnt<7 * (kInBwdDepth - 3)>(); else wait_vmcnt<6 * (kInBwdDepth - 3)>();
+  }
+  __syncthreads();
+  f32x4 acc0[4][2], acc1[4][2];
+  mma(bbeg, acc0);
+  int64_t blk = bbeg;
+  auto iter = [&](f32x4 (&cur)[4][2], f32x4 (&nxt)[4][2]) {
+    if (loader) issue(blk + kInBwdDepth - 1);
+    if (blk + 1 < bend) mma(blk + 1, nxt);
+    __syncthreads();  // the staging tile of blk - 1 has been read
+    epilogue(blk, cur);
+    if (loader) {     // block blk + 2 landed
+      if (w == 0) wait_vmcnt<7 * (kInBwdDepth - 3)>(); else wait_vmcnt<6 * (kInBwdDepth - 3)>();
+    }
+    __syncthreads();
+    if (!loader) stores(blk);
+    ++blk;
+  };
+#pragma unroll 1
+  while (blk < bend) {
+    iter(acc0, acc1);
+    if (blk >= bend) break;
+    iter(acc1, acc0);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Input projections, backward (stored row order): recompute p, g for 64
 // channels of branch a or b and write d p = d * mask * s(g),
 // d g = d * mask * p * s(g) (1 - s(g)) into dproj5, d = da / db.
@@ -1220,8 +1411,24 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gb.batch = (int)(B * C);
   if ((rc = gemm_launch_pair(ga, 1, 0, gb, 0, 0, 0, s, "tpf_trimul_backward_bf16(dA, dB)")))
     return rc;
-  hipLaunchKernelGGL(tm_in_proj_bwd_kernel, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
-                     (const __bf16*)zln, k.wp, mask, da, db, dproj5, g, (int)C);
+  if (g.Np == g.N) {
+    const int64_t nblk = (R + 31) / 32;
+    const int64_t cap = (int64_t)device_cus() * (128 / C);
+    const unsigned grid = (unsigned)(nblk < cap ? nblk : cap);
+    switch (C) {
+#define TM_IN_BWD(CC)                                                                            \
+  case CC:                                                                                       \
+    hipLaunchKernelGGL(tm_in_proj_bwd_ws_kernel<CC>, dim3(grid), dim3(4 * CC), 0, s,             \
+                       (const __bf16*)zln, k.w5, mask, (const __bf16*)da, (const __bf16*)db,     \
+                       dproj5, g, nblk);                                                         \
+    break;
+      TM_IN_BWD(32) TM_IN_BWD(64) TM_IN_BWD(96) TM_IN_BWD(128)
+#undef TM_IN_BWD
+    }
+  } else {
+    hipLaunchKernelGGL(tm_in_proj_bwd_kernel, dim3(tm_grid(tiles * 2 * g.ntg)), dim3(256), 0, s,
+                       (const __bf16*)zln, k.wp, mask, da, db, dproj5, g, (int)C);
+  }
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
   hipLaunchKernelGGL(tm_ln_bwd_kernel<false>, dim3(grid_rows), dim3(256), 0, s,
                      (const __bf16*)dproj5, 5 * H, k.w5, (int)(5 * H),
