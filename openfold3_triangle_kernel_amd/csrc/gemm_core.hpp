@@ -48,6 +48,7 @@ struct GemmOperand {
   int rows;         // extent of the m (or n) dimension
   int gather_n;     // KC row gather (0 = none); nn = gather_n^2
   FastDiv div_n, div_nn;  // division by gather_n and gather_n^2 (gather only)
+  int kmax = 0x7fffffff;  // MN: k rows that exist (rows past it read zeros)
 };
 
 // Slot of 16-byte chunk c in row r of a KC tile.  gfx950's LDS serves 64
@@ -68,6 +69,7 @@ struct TileLoader {
   uint32_t row_off[kGInstr];  // KC: byte offset of the row start (kBufOOB if absent)
   int col_ok;                 // MN: column chunk inside the tensor
   uint32_t col_off;           // MN: byte offset of the column chunk
+  int kmax;                   // MN: k rows that exist
   int sub;                    // KC: k offset of this lane; MN: k-row in instruction
   int64_t ld;
 
@@ -102,6 +104,7 @@ struct TileLoader {
       const int col = r0 + 8 * chunk;
       col_ok = col < op.rows;
       col_off = (uint32_t)col * 2;
+      kmax = op.kmax;
     }
   }
 
@@ -117,7 +120,7 @@ struct TileLoader {
         off = (row_off[t] != kBufOOB && k < kend) ? row_off[t] + (uint32_t)k * 2 : kBufOOB;
       } else {
         const int k = k0 + 4 * j + sub;
-        off = (col_ok && k < kend) ? (uint32_t)((int64_t)k * ld * 2) + col_off : kBufOOB;
+        off = (col_ok && k < kend && k < kmax) ? (uint32_t)((int64_t)k * ld * 2) + col_off : kBufOOB;
       }
       buf2lds16(rsrc, off, tile + j * 1024);
     }

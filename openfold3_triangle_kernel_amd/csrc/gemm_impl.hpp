@@ -31,7 +31,7 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
   const int kbeg = split * g.k_chunk;
   const int kend = min(g.K, kbeg + g.k_chunk);
   GemmOperand A{g.A + (int64_t)z * g.a_bs, g.a_ld, g.M, g.a_gather_n, g.a_div_n, g.a_div_nn};
-  GemmOperand B{g.B + (int64_t)z * g.b_bs, g.b_ld, g.N, 0, {}, {}};
+  GemmOperand B{g.B + (int64_t)z * g.b_bs, g.b_ld, g.N, 0, {}, {}, g.b_kmax > 0 ? g.b_kmax : 0x7fffffff};
   f32x16 acc[2][2];
   gemm_tile<A_KC, B_KC>(A, B, m0, n0, kbeg, kend, smem, acc);
 

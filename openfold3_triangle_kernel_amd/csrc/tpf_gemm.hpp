@@ -18,6 +18,7 @@ struct GemmArgs {
   int a_gather_n;                        // KC row gather of A (0 = none), see gemm_core.hpp
   FastDiv a_div_n, a_div_nn;             // set by gemm_launch when a_gather_n > 0
   int batch;                             // set by gemm_launch
+  int b_kmax;                            // MN B: k rows that exist (0 = all K)
 };
 
 // FP32 variant (gemm_core_f32.hpp); bias (nullable) is added per column n.

@@ -59,11 +59,11 @@ constexpr int lds_bytes(int epilogue, int ns = kGNS) {
 // Ring depths per kernel (measured): the short-K projections keep two
 // stages (occupancy), the long-K / large-epilogue kernels take more.
 constexpr int kInProjBwdNS = 3, kOutProjNS = 4, kOutProjFwdNS = 2;
-__host__ __device__ constexpr int ln_bwd_ns(bool planes) { return planes ? 2 : 4; }
+constexpr int kLnOutBwdNS = 2;
 constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2, kInProjBwdNS);  // d tile + [dp | dg] tile
 constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2, kOutProjNS);  // gate + dout tiles
 constexpr int kOutProjFwdLds = lds_bytes(128 * kSP * 2, kOutProjFwdNS);  // gate tile
-constexpr int ln_bwd_lds(bool planes) { return lds_bytes(128 * kSP * 2, ln_bwd_ns(planes)); }  // x tile
+constexpr int kLnOutBwdLds = lds_bytes(128 * kSP * 2, kLnOutBwdNS);  // x tile
 
 // Element offset of position p = i*N + j inside a channel-major plane.
 __device__ __forceinline__ int64_t tm_plane_off(const TmGeom& g, int64_t p) {
@@ -96,7 +96,8 @@ __device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
 //   operand).
 //   W5 = [W_ap; W_ag; W_bp; W_bg; W_g] [5H][C] (the reference's d_w5 order;
 //   also the forward projections' stationary operand);
-//   Wz = W_z [C][H].  Missing channels are zero rows.
+//   Wz = W_z [C][H]; W5t = W5^T [C][5H] (the LN_in backward's stationary
+//   operand).  Missing channels are zero rows.
 // ---------------------------------------------------------------------------
 struct TmWeights {
   const float* ap;
@@ -109,13 +110,28 @@ struct TmWeights {
 
 __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf16* __restrict__ wp,
                                                               __bf16* __restrict__ w5,
-                                                              __bf16* __restrict__ wz, int C,
+                                                              __bf16* __restrict__ wz,
+                                                              __bf16* __restrict__ w5t, int C,
                                                               int ntg) {
   const int cpr = C / 8;
   const int wp_rows = 2 * ntg * 128;
   const int64_t total = (int64_t)(wp_rows + 6 * C) * cpr;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+  const float* const mats[5] = {w.ap, w.ag, w.bp, w.bg, w.g};
+  // W5^T [C][5C]: chunk j of the C x 5C / 8 chunks after the row-copied part.
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total + (int64_t)C * 5 * cpr;
        idx += (int64_t)gridDim.x * 256) {
+    if (idx >= total) {
+      const int64_t j = idx - total;
+      const int c = (int)(j / (5 * cpr)), k0 = 8 * (int)(j % (5 * cpr));
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = k0 + e;
+        o[e] = f2bf(mats[k / C][(int64_t)(k % C) * C + c]);
+      }
+      st8(w5t + (int64_t)c * 5 * C + k0, o);
+      continue;
+    }
     const int row = (int)(idx / cpr), ch = (int)(idx % cpr);
     const float* src = nullptr;
     __bf16* dst;
@@ -129,7 +145,6 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
     } else if (row < wp_rows + 5 * C) {
       const int j = row - wp_rows, blk = j / C, c = j % C;
       dst = w5 + (int64_t)j * C + ch * 8;
-      const float* const mats[5] = {w.ap, w.ag, w.bp, w.bg, w.g};
       src = mats[blk] + (int64_t)c * C;
     } else {
       const int c = row - wp_rows - 5 * C;
@@ -651,6 +666,9 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
     if (blk >= bend) break;
     iter(acc1, acc0);
   }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -842,6 +860,9 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
     if (blk >= bend) break;
     iter(acc1, acc0);
   }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -966,32 +987,24 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// LayerNorm backward fused onto d_xhat-producing GEMMs (natural rows):
-//   PLANES (LN_out):  G = dy Wz  (A = dy [R][C], B = Wz read MN), x from the
-//                     channel-major planes, dx written to planes;
-//   rows   (LN_in):   G = dproj5 W5 (A = dproj5 [R][5H], B = W5 read MN),
-//                     x = z rows, dz written row-major.
+// LN_out backward fused onto the GEMM that produces its input gradient
+// (natural rows): G = dy Wz (A = dy [R][C], B = Wz read MN), x from the
+// channel-major planes, dx written to planes;
 //   g = G * gamma;  dx = rstd (g - mean(g) - xhat mean(g xhat));
 //   per-tile partials d gamma = sum G xhat, d beta = sum G into
-//   lnp[tile][slot0 | slot0 + 1][W] (W channels).
+//   lnp[tile][2][W] (W channels).
 // The epilogue works on the accumulators in registers: the x tile sits in
-// LDS in a layout whose reads give each lane the 4 consecutive rows of one
-// accumulator column (plain 8-byte reads for [channel][row], transposing
-// reads for [row][channel]); row sums are reduced across the 32 columns of
+// LDS as [channel][row], so 8-byte reads give each lane the 4 consecutive
+// rows of one accumulator column; row sums are reduced across the 32 columns of
 // a wave with a transposing butterfly and across the two column waves in
 // LDS, column sums across the two row halves with a lane swap and across
 // the row waves in LDS.  All reductions run in a fixed order.
 // ---------------------------------------------------------------------------
 
 // x values of acc[i][j] rows 4*rq .. 4*rq+3 (of this lane's 16 registers).
-template <bool PLANES>
 __device__ __forceinline__ bf16x4 tm_x4(const __bf16* Xt, const AccPos& ap, int i, int j, int rq) {
-  const int rbase = 64 * ap.wm + 32 * i + 8 * rq;
-  if (PLANES) {
-    const int row = rbase + 4 * ap.hl;
-    return *reinterpret_cast<const bf16x4*>(Xt + ap.col(j) * kSP + row);
-  }
-  return tr_col4(Xt, kSP, rbase, rbase + 4, 64 * ap.wn + 32 * j);
+  const int row = 64 * ap.wm + 32 * i + 8 * rq + 4 * ap.hl;
+  return *reinterpret_cast<const bf16x4*>(Xt + ap.col(j) * kSP + row);
 }
 
 // One level of the transposing butterfly: lanes exchange half of their
@@ -1011,17 +1024,15 @@ __device__ __forceinline__ void tm_butterfly(float* a, float* b, int lane) {
   }
 }
 
-template <bool PLANES>
-__global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
+__global__ __launch_bounds__(256, 2) void tm_ln_out_bwd_kernel(
     const __bf16* __restrict__ a_op, int64_t a_ld, const __bf16* __restrict__ w_op, int K,
     const __bf16* __restrict__ xsrc, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gamma, __bf16* __restrict__ dst, float* __restrict__ lnp,
-    int slot0, TmGeom g, int W) {
-  __shared__ __attribute__((aligned(1024))) char smem[ln_bwd_lds(PLANES)];
+    TmGeom g, int W) {
+  __shared__ __attribute__((aligned(1024))) char smem[kLnOutBwdLds];
   __shared__ __attribute__((aligned(16))) float mean_s[128], rstd_s[128];
   __shared__ __attribute__((aligned(16))) float rsum[2][2][128];  // [quantity][wn][row]
   __shared__ float csum[2][2][128];                               // [quantity][wm][col]
-  __shared__ int64_t rho_s[128];
   const int tid = threadIdx.x;
   const int64_t T = xcd_order((g.R + 127) / 128);
   if (T < 0) return;
@@ -1029,20 +1040,17 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
   if (tid < 128) {
     const int64_t m = m0 + tid;
     const bool ok = m < g.R;
-    rho_s[tid] = ok ? m : -1;
     mean_s[tid] = ok ? mean[m] : 0.f;
     rstd_s[tid] = ok ? rstd[m] : 0.f;
   }
   GemmOperand A{a_op, a_ld, (int)g.R, 0, {}, {}};
   GemmOperand B{w_op, W, W, 0, {}, {}};
   RegTile xreg;
-  if (PLANES) fetch_planes(xreg, xsrc, g, 128, m0, 0);
-  else fetch_rows(xreg, xsrc, W, W, m0, g.R);
+  fetch_planes(xreg, xsrc, g, 128, m0, 0);
   f32x16 acc[2][2];
-  gemm_tile<true, false, ln_bwd_ns(PLANES)>(A, B, (int)m0, 0, 0, K, smem, acc);
-  __bf16* Xt = reinterpret_cast<__bf16*>(smem);  // [ch][row] (PLANES) or [row][ch]
-  if (PLANES) put_planes(Xt, xreg, 128);
-  else put_rows(Xt, xreg);
+  gemm_tile<true, false, kLnOutBwdNS>(A, B, (int)m0, 0, 0, K, smem, acc);
+  __bf16* Xt = reinterpret_cast<__bf16*>(smem);  // [ch][row]
+  put_planes(Xt, xreg, 128);
   __syncthreads();
   const AccPos ap;
   const int lane = tid & 63;
@@ -1064,7 +1072,7 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
       const f32x4 rs = *reinterpret_cast<const f32x4*>(&rstd_s[row0]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const bf16x4 xv = tm_x4<PLANES>(Xt, ap, i, j, rq);
+        const bf16x4 xv = tm_x4(Xt, ap, i, j, rq);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * rq + e;
@@ -1101,9 +1109,9 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
   }
   __syncthreads();
   if (tid < W) {
-    float* part = lnp + T * 4 * W;
-    part[slot0 * W + tid] = csum[1][0][tid] + csum[1][1][tid];
-    part[(slot0 + 1) * W + tid] = csum[0][0][tid] + csum[0][1][tid];
+    float* part = lnp + T * 2 * W;
+    part[tid] = csum[1][0][tid] + csum[1][1][tid];
+    part[W + tid] = csum[0][0][tid] + csum[0][1][tid];
   }
   // Pass 2: dx in place of x (each element is read and written by one lane).
   const float invW = 1.f / W;
@@ -1120,7 +1128,7 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
       const f32x4 sx1 = *reinterpret_cast<const f32x4*>(&rsum[1][1][row0]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const bf16x4 xv = tm_x4<PLANES>(Xt, ap, i, j, rq);
+        const bf16x4 xv = tm_x4(Xt, ap, i, j, rq);
         bf16x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1129,17 +1137,206 @@ __global__ __launch_bounds__(256, 2) void tm_ln_bwd_kernel(
           const float gv = acc[i][j][4 * rq + e] * gam[j];
           o[e] = f2bf(rs[e] * (gv - mg - xh * mgx));
         }
-        if (PLANES) {
-          *reinterpret_cast<bf16x4*>(Xt + ap.col(j) * kSP + row0) = o;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) Xt[(row0 + e) * kSP + ap.col(j)] = o[e];
-        }
+        *reinterpret_cast<bf16x4*>(Xt + ap.col(j) * kSP + row0) = o;
       }
     }
   __syncthreads();
-  if (PLANES) tm_store_planes(Xt, 128, dst, g, m0, 0);
-  else tm_store_rows(Xt, W, rho_s, dst, W, 0);
+  tm_store_planes(Xt, 128, dst, g, m0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// LN_in backward, weight-stationary: G = dproj5 W5 (K = 5H) and the LayerNorm
+// backward of LN_in, per 32-row block of natural rows, persistent workgroups
+// of C / 16 waves.  Wave w holds the W5^T rows of channels 16 w .. 16 w + 15
+// (B operands of v_mfma_f32_16x16x32_bf16) for the whole kernel; the loading
+// waves stream each block's dproj5 rows (chunks rotated by row, so A-fragment
+// reads are conflict-free), z rows and the row statistics into a 3-deep LDS
+// ring.  Accumulator register r of lane l holds G[row 4 (l / 16) + r][channel
+// 16 w + l % 16] (+ 16 per row tile); z is read back transposed to match.
+// Row sums of g = G gamma and g xhat are reduced across a wave's 16 channels
+// with a transposing butterfly and across the waves in LDS (fixed order);
+// dz = rstd (g - mean(g) - xhat mean(g xhat)) is staged in LDS and stored as
+// full rows by the storing waves.  The d gamma / d beta column sums of each
+// lane stay in registers over all of a workgroup's blocks and are written
+// once per workgroup to lnp [workgroup][2][C] (d gamma, d beta).
+// ---------------------------------------------------------------------------
+constexpr int kLnInDepth = 3;
+template <int C>
+__global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
+    const __bf16* __restrict__ dproj5, const __bf16* __restrict__ w5t,
+    const __bf16* __restrict__ z, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gamma, __bf16* __restrict__ dz, float* __restrict__ lnp, TmGeom g,
+    int64_t nblocks) {
+  constexpr int NW = C / 16;         // waves
+  constexpr int K = 5 * C;           // contraction depth
+  constexpr int KC = K / 8;          // 16-byte chunks per dproj5 row
+  constexpr int CPR = C / 8;         // 16-byte chunks per z row
+  constexpr int KS = K / 32;         // 32-deep k steps
+  constexpr int SP = C + 8;          // dz staging pitch (bf16)
+  constexpr int PI = 32 * KC / 64 / (NW / 2);  // dproj5 load instructions per loading wave
+  __shared__ __attribute__((aligned(1024))) __bf16 Ps[kLnInDepth][32 * K];
+  __shared__ __attribute__((aligned(1024))) __bf16 Zs[kLnInDepth][32 * C];
+  __shared__ __attribute__((aligned(256))) float Ss[kLnInDepth][2][64];  // mean | rstd
+  __shared__ __attribute__((aligned(16))) float Rs[2][NW][32];           // row sums [q][wave][row]
+  __shared__ __attribute__((aligned(16))) __bf16 So[32 * SP];
+  static_assert(PI * 64 * (NW / 2) == 32 * KC, "dproj5 loads split evenly");
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int ch = 16 * w + l16;
+  const bool loader = w < NW / 2;
+
+  bf16x8 wf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) wf[ks] = ld8(w5t + (int64_t)ch * K + 8 * (4 * ks + lg));
+  const float gam = gamma[ch];
+
+  const i32x4 rs_p = buffer_rsrc(dproj5);
+  const i32x4 rs_z = buffer_rsrc(z);
+  const i32x4 rs_mu = buffer_rsrc(mean);
+  const i32x4 rs_rs = buffer_rsrc(rstd);
+  const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(dz, 0, 0x7FFFFFFF, 0x00020000);
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loads per block: PI dproj5 + 2 z instructions per loading wave, and the
+  // two statistics rows by wave 0.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % kLnInDepth);
+#pragma unroll
+    for (int j = 0; j < PI; ++j) {
+      const int ci = (PI * w + j) * 64 + lane;
+      const int r = ci / KC, slot = ci % KC;
+      const int gc = (slot - r % KC + KC) % KC;
+      const uint32_t m = (uint32_t)blk * 32 + r;
+      const bool ok = blk < bend && m < (uint32_t)g.R;
+      buf2lds16(rs_p, ok ? (m * K + 8 * gc) * 2 : kBufOOB, &Ps[stage][(PI * w + j) * 512]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ci = (2 * w + j) * 64 + lane;
+      const int r = ci / CPR, slot = ci % CPR;
+      const int gc = (slot - r % CPR + CPR) % CPR;
+      const uint32_t m = (uint32_t)blk * 32 + r;
+      const bool ok = blk < bend && m < (uint32_t)g.R;
+      buf2lds16(rs_z, ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Zs[stage][(2 * w + j) * 512]);
+    }
+    if (w == 0) {
+      const uint32_t m = (uint32_t)blk * 32 + lane;
+      const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
+      buf2lds4(rs_mu, ok ? m * 4 : kBufOOB, &Ss[stage][0][0]);
+      buf2lds4(rs_rs, ok ? m * 4 : kBufOOB, &Ss[stage][1][0]);
+    }
+  };
+  float cg = 0.f, cgx = 0.f;  // this lane's channel: sum G, sum G xhat over its rows
+  if (loader) {
+    issue(bbeg);
+    issue(bbeg + 1);
+  }
+#pragma unroll 1
+  for (int64_t blk = bbeg; blk < bend; ++blk) {
+    const int stage = (int)(blk % kLnInDepth);
+    if (loader) {  // block blk landed (block blk + 1 may be in flight)
+      if (w == 0) wait_vmcnt<PI + 4>(); else wait_vmcnt<PI + 2>();
+    }
+    __syncthreads();
+    if (loader) issue(blk + 2);
+    // G for rows 16 rt + 4 lg + r, channel ch.
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const __bf16* P = Ps[stage];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 16 * rt + l16;
+        const bf16x8 pf =
+            *reinterpret_cast<const bf16x8*>(&P[row * K + 8 * ((4 * ks + lg + row) % KC)]);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, wf[ks], acc[rt], 0, 0, 0);
+      }
+    // x for the same (row, channel) pairs: lane L of a 16-lane group reads
+    // row 16 rt + 4 lg + L / 4, channels 16 w + 4 (L % 4) .. + 3 (rotated chunk).
+    float xh[2][4], gv[2][4], a[8], b[8];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int rr = 16 * rt + 4 * lg + (l16 >> 2);
+      const int cc = 16 * w + 4 * (l16 & 3);
+      const __bf16* src = &Zs[stage][rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)];
+      const bf16x4 xv = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)src);
+      const f32x4 mu = *reinterpret_cast<const f32x4*>(&Ss[stage][0][16 * rt + 4 * lg]);
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][16 * rt + 4 * lg]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[rt][e] = (bf2f(xv[e]) - mu[e]) * rsd[e];
+        const float G = acc[rt][e];
+        gv[rt][e] = G * gam;
+        a[4 * rt + e] = gv[rt][e];
+        b[4 * rt + e] = gv[rt][e] * xh[rt][e];
+        cg += G;
+        cgx = fmaf(G, xh[rt][e], cgx);
+      }
+    }
+    // Row sums over the 16 channels of this wave: lane ends with row
+    // t = l16 & 7 of its lane group, summed over the 16 lanes.
+    tm_butterfly<4>(a, b, lane);
+    tm_butterfly<2>(a, b, lane);
+    tm_butterfly<1>(a, b, lane);
+    a[0] += __shfl_xor(a[0], 8);
+    b[0] += __shfl_xor(b[0], 8);
+    if (l16 < 8) {
+      const int t = l16, row = 16 * (t >> 2) + 4 * lg + (t & 3);
+      Rs[0][w][row] = a[0];
+      Rs[1][w][row] = b[0];
+    }
+    __syncthreads();
+    const float invC = 1.f / C;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r0 = 16 * rt + 4 * lg;
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][r0]);
+      f32x4 sg = *reinterpret_cast<const f32x4*>(&Rs[0][0][r0]);
+      f32x4 sx = *reinterpret_cast<const f32x4*>(&Rs[1][0][r0]);
+#pragma unroll
+      for (int v = 1; v < NW; ++v) {
+        sg += *reinterpret_cast<const f32x4*>(&Rs[0][v][r0]);
+        sx += *reinterpret_cast<const f32x4*>(&Rs[1][v][r0]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float o = rsd[e] * (gv[rt][e] - sg[e] * invC - xh[rt][e] * (sx[e] * invC));
+        So[(r0 + e) * SP + ch] = f2bf(o);
+      }
+    }
+    __syncthreads();
+    if (!loader) {
+      // 4 C chunks (32 rows x C / 8) over the 2 C storing threads.
+      const int st = tid - 2 * C;
+      bf16x8 v[2];
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        v[it] = *reinterpret_cast<const bf16x8*>(&So[row * SP + 8 * k]);
+      }
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        const uint32_t m = (uint32_t)blk * 32 + row;
+        const uint32_t off = m < (uint32_t)g.R ? (m * C + 8 * k) * 2 : kBufOOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o, off, 0, 0);
+      }
+    }
+  }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
+  // Column sums: the 4 lane groups of each channel, then one lane writes.
+  cg += __shfl_xor(cg, 16);
+  cgx += __shfl_xor(cgx, 16);
+  cg += __shfl_xor(cg, 32);
+  cgx += __shfl_xor(cgx, 32);
+  if (lg == 0) {
+    lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx;
+    lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cg;
+  }
 }
 
 // Zero-fill (used instead of hipMemsetAsync so callers may capture graphs).
@@ -1185,7 +1382,7 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
 static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 static int64_t tm_wp_rows(int64_t C) { return 2 * ((C + 63) / 64) * 128; }
 static int64_t tm_weights_bytes(int64_t C) {
-  return align256(tm_wp_rows(C) * C * 2) + align256(5 * C * C * 2) + align256(C * C * 2);
+  return align256(tm_wp_rows(C) * C * 2) + 2 * align256(5 * C * C * 2) + align256(C * C * 2);
 }
 
 // Packed bf16 weights at the start of a workspace.
@@ -1193,6 +1390,7 @@ struct TmPacked {
   __bf16* wp;
   __bf16* w5;
   __bf16* wz;
+  __bf16* w5t;
 };
 static TmPacked tm_packed(void* ws, int64_t C) {
   char* p = (char*)ws;
@@ -1202,14 +1400,16 @@ static TmPacked tm_packed(void* ws, int64_t C) {
   k.w5 = (__bf16*)p;
   p += align256(5 * C * C * 2);
   k.wz = (__bf16*)p;
+  p += align256(C * C * 2);
+  k.w5t = (__bf16*)p;
   return k;
 }
 
 static int tm_pack(const TmWeights& w, const TmPacked& k, int C, int ntg, hipStream_t s,
                    const char* fn) {
-  const int64_t chunks = (tm_wp_rows(C) + 6 * C) * (C / 8);
+  const int64_t chunks = (tm_wp_rows(C) + 11 * C) * (C / 8);
   hipLaunchKernelGGL(tm_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
-                     s, w, k.wp, k.w5, k.wz, C, ntg);
+                     s, w, k.wp, k.w5, k.wz, k.w5t, C, ntg);
   return check_launch(fn);
 }
 
@@ -1318,9 +1518,9 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
 }
 
 // Backward workspace (each region 256-byte aligned): packed weights, dy
-// [R][C], dproj5 [R][5H], dx / da / db channel-major planes, LayerNorm
-// parameter partials [tiles][4][C] and their fold, split-K partials of dW5
-// and dWz.
+// [R][C], dproj5 [R][5H], dx / da / db channel-major planes, LN_out
+// parameter partials [tiles][2][C], LN_in parameter partials [<= R/32][2][C],
+// split-K partials of dW5 and dWz.
 static int tm_split(int64_t R, int64_t per, int cap) {
   int64_t s = R / per;
   if (s < 1) s = 1;
@@ -1337,7 +1537,8 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   t += align256(R * C * 2);                        // dy
   t += align256(R * 5 * C * 2);                    // dproj5
   t += 3 * align256(B * C * N * Np * 2);           // dx, da, db
-  t += align256(tiles * 4 * C * 4);                // LN parameter partials
+  t += align256(tiles * 2 * C * 4);                // LN_out parameter partials
+  t += align256((R + 31) / 32 * 2 * C * 4);        // LN_in parameter partials (per workgroup)
   t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
   t += align256((int64_t)tm_wz_splits(R) * C * C * 4);
   return t;
@@ -1381,7 +1582,8 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   __bf16* dx = (__bf16*)take(plane_bytes);
   __bf16* da = (__bf16*)take(plane_bytes);
   __bf16* db = (__bf16*)take(plane_bytes);
-  float* lnp = (float*)take(tiles * 4 * C * 4);
+  float* lnp = (float*)take(tiles * 2 * C * 4);
+  float* lnin = (float*)take((R + 31) / 32 * 2 * C * 4);
   float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
   float* wzp = (float*)take((int64_t)sz * C * C * 4);
   if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
@@ -1391,9 +1593,9 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
                      (const __bf16*)xln, k.wz, (const __bf16*)gate, (const __bf16*)grad_out, (__bf16*)nullptr, dy, dproj5, g, (int)C);
   if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
-  hipLaunchKernelGGL(tm_ln_bwd_kernel<true>, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
+  hipLaunchKernelGGL(tm_ln_out_bwd_kernel, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
                      (int64_t)C, k.wz, (int)C, (const __bf16*)x, mean_out,
-                     rstd_out, ln_out_w, dx, lnp, 0, g, (int)H);
+                     rstd_out, ln_out_w, dx, lnp, g, (int)H);
   if ((rc = check_launch("tpf_trimul_backward_bf16(ln_out_bwd)"))) return rc;
   // Contraction backward: dA_c = dX_c B_c, dB_c = dX_c^T A_c (stored layouts).
   GemmArgs ga{};
@@ -1401,6 +1603,9 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   ga.B = (const __bf16*)b; ga.b_ld = g.Np; ga.b_bs = g.PS;
   ga.C = da; ga.c_ld = g.Np; ga.c_bs = g.PS;
   ga.M = (int)N; ga.N = (int)N; ga.K = g.Np; ga.ksplit = 1; ga.k_chunk = g.Np; ga.alpha = 1.f;
+  // K = Np runs over dX's zero pad columns; the matching rows of B_c past N
+  // do not exist (past the last plane they are past the tensor): read zeros.
+  ga.b_kmax = (int)N;
   GemmArgs gb{};
   gb.A = dx; gb.a_ld = g.Np; gb.a_bs = g.PS;
   gb.B = (const __bf16*)a; gb.b_ld = g.Np; gb.b_bs = g.PS;
@@ -1430,9 +1635,19 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
                        (const __bf16*)zln, k.wp, mask, da, db, dproj5, g, (int)C);
   }
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
-  hipLaunchKernelGGL(tm_ln_bwd_kernel<false>, dim3(grid_rows), dim3(256), 0, s,
-                     (const __bf16*)dproj5, 5 * H, k.w5, (int)(5 * H),
-                     (const __bf16*)z, mean_in, rstd_in, ln_in_w, (__bf16*)dz, lnp, 2, g, (int)C);
+  const int64_t ln_blk = (R + 31) / 32;
+  const int64_t ln_cap = (int64_t)device_cus() * (128 / C);
+  const int ln_grid = (int)(ln_blk < ln_cap ? ln_blk : ln_cap);
+  switch (C) {
+#define TM_LN_IN(CC)                                                                            \
+  case CC:                                                                                      \
+    hipLaunchKernelGGL(tm_ln_in_bwd_ws_kernel<CC>, dim3(ln_grid), dim3(4 * CC), 0, s,           \
+                       (const __bf16*)dproj5, k.w5t, (const __bf16*)z, mean_in, rstd_in,        \
+                       ln_in_w, (__bf16*)dz, lnin, g, ln_blk);                                  \
+    break;
+    TM_LN_IN(32) TM_LN_IN(64) TM_LN_IN(96) TM_LN_IN(128)
+#undef TM_LN_IN
+  }
   if ((rc = check_launch("tpf_trimul_backward_bf16(ln_in_bwd)"))) return rc;
   // Weight gradients over all rows: MN operands straight from the row-major
   // tensors, split-K + fixed-order fold.
@@ -1454,18 +1669,21 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gz.batch = 1;
   if ((rc = gemm_launch_pair_wgrad(gw, gz, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
     return rc;
-  // The three weight-gradient folds in one launch per pass; the LayerNorm
-  // partials [tiles][ln_out_w | ln_out_b | ln_in_w | ln_in_b] land directly
-  // in the four parameter gradients.
+  // The four weight-gradient folds in one launch per pass; the LayerNorm
+  // partials ([tiles][ln_out_w | ln_out_b] and [workgroups][ln_in_w |
+  // ln_in_b]) land directly in the four parameter gradients.
   FoldSegs f{};
-  f.nseg = 3;
+  f.nseg = 4;
   f.part[0] = w5p; f.n[0] = 5 * C * C; f.stride[0] = 5 * C * C; f.splits[0] = s5;
   f.piece[0] = 5 * C * C; f.dst[0][0] = d_w5;
   f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = sz;
   f.piece[1] = C * H; f.dst[1][0] = d_w_z;
-  f.part[2] = lnp; f.n[2] = 4 * C; f.stride[2] = 4 * C; f.splits[2] = (int)tiles;
+  f.part[2] = lnp; f.n[2] = 2 * C; f.stride[2] = 2 * C; f.splits[2] = (int)tiles;
   f.piece[2] = C;
-  f.dst[2][0] = d_ln_out_w; f.dst[2][1] = d_ln_out_b; f.dst[2][2] = d_ln_in_w; f.dst[2][3] = d_ln_in_b;
+  f.dst[2][0] = d_ln_out_w; f.dst[2][1] = d_ln_out_b;
+  f.part[3] = lnin; f.n[3] = 2 * C; f.stride[3] = 2 * C; f.splits[3] = ln_grid;
+  f.piece[3] = C;
+  f.dst[3][0] = d_ln_in_w; f.dst[3][1] = d_ln_in_b;
   return fold_multi(f, s, fn);
 }
 

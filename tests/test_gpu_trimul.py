@@ -80,3 +80,53 @@ def test_trimul_bitwise_replay(gpu):
     b = run_turbo(z, mask, w, dout, True, gpu)
     for k in a:
         assert np.array_equal(a[k], b[k]), k
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("outgoing", [1, 0], ids=["outgoing", "incoming"])
+def test_trimul_backward_ignores_memory_past_the_planes(gpu, outgoing):
+    """N % 8 != 0: the dA contraction runs K over the plane pitch Np (dX's zero
+    pad columns), whose rows of B_c past N do not exist -- past the last plane
+    they lie outside the tensor.  Here the memory right after a and b holds
+    non-finite values: every gradient must stay finite and equal the run with
+    clean memory (the kernels must not read there)."""
+    from openfold3_triangle_kernel_amd import _native
+
+    B, N, C = 1, 50, 128
+    print(f"[trimul pad tail] N={N} outgoing={outgoing}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    z = torch.randn(B, N, N, C, device=gpu, generator=g).bfloat16()
+    mask = (torch.rand(B, N, N, device=gpu, generator=g) > 0.1).float()
+    w = [torch.randn(C, C, device=gpu, generator=g) / C ** 0.5 for _ in range(6)]
+    ln = [torch.ones(C, device=gpu), torch.zeros(C, device=gpu)] * 2
+    dout = torch.randn(B, N, N, C, device=gpu, generator=g).bfloat16()
+    Np = int(_native.query("tpf_trimul_plane_pitch", N))
+    rows, pn = B * N * N, B * C * N * Np
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def run(tail):
+        E = lambda *s, dt=torch.bfloat16: torch.empty(*s, device=gpu, dtype=dt)  # noqa: E731
+        # a and b at the start of buffers whose remainder holds `tail`.
+        ab = torch.full((2, pn + 8 * Np), tail, device=gpu, dtype=torch.bfloat16)
+        a, b = ab[0], ab[1]
+        out, zln, gate, x, xln = E(rows, C), E(rows, C), E(rows, C), E(pn), E(rows, C)
+        st = [E(rows, dt=torch.float32) for _ in range(4)]
+        wsf = E(int(_native.query("tpf_trimul_forward_workspace_bytes", C)), dt=torch.uint8)
+        wsb = E(int(_native.query("tpf_trimul_backward_workspace_bytes", B, N, C)), dt=torch.uint8)
+        grads = [E(rows, C), E(5 * C, C, dt=torch.float32), E(C, C, dt=torch.float32)]
+        grads += [E(C, dt=torch.float32) for _ in range(4)]
+        s = torch.cuda.current_stream().cuda_stream
+        _native.call("tpf_trimul_forward_bf16", P(z), P(mask), *map(P, w), *map(P, ln), outgoing,
+                     B, N, C, P(out), P(zln), P(gate), P(a), P(b), P(x), P(xln), *map(P, st),
+                     P(wsf), wsf.numel(), s)
+        _native.call("tpf_trimul_backward_bf16", P(dout), P(z), P(mask), *map(P, w), P(ln[0]),
+                     P(ln[2]), P(zln), P(gate), P(a), P(b), P(x), P(xln), *map(P, st), outgoing,
+                     B, N, C, *map(P, grads), P(wsb), wsb.numel(), s)
+        torch.cuda.synchronize()
+        return grads
+
+    clean = run(0.0)
+    dirty = run(float("inf"))
+    for c, d in zip(clean, dirty):
+        assert torch.isfinite(d.float()).all()
+        assert torch.equal(c, d)
