@@ -96,8 +96,9 @@ __device__ __forceinline__ int64_t tm_phys_row(const TmGeom& g, int64_t m) {
 //   operand).
 //   W5 = [W_ap; W_ag; W_bp; W_bg; W_g] [5H][C] (the reference's d_w5 order;
 //   also the forward projections' stationary operand);
-//   Wz = W_z [C][H]; W5t = W5^T [C][5H] (the LN_in backward's stationary
-//   operand).  Missing channels are zero rows.
+//   Wz = W_z [C][H]; W5t = W5^T [C][5H] and Wzt = W_z^T [H][C] (stationary
+//   operands of the LN_in / LN_out backward kernels).  Missing channels are
+//   zero rows.
 // ---------------------------------------------------------------------------
 struct TmWeights {
   const float* ap;
@@ -111,15 +112,27 @@ struct TmWeights {
 __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf16* __restrict__ wp,
                                                               __bf16* __restrict__ w5,
                                                               __bf16* __restrict__ wz,
-                                                              __bf16* __restrict__ w5t, int C,
+                                                              __bf16* __restrict__ w5t,
+                                                              __bf16* __restrict__ wzt, int C,
                                                               int ntg) {
   const int cpr = C / 8;
   const int wp_rows = 2 * ntg * 128;
   const int64_t total = (int64_t)(wp_rows + 6 * C) * cpr;
   const float* const mats[5] = {w.ap, w.ag, w.bp, w.bg, w.g};
-  // W5^T [C][5C]: chunk j of the C x 5C / 8 chunks after the row-copied part.
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total + (int64_t)C * 5 * cpr;
+  // W5^T [C][5C] (C x 5C / 8 chunks) and Wz^T [H][C] (H x C / 8 chunks)
+  // after the row-copied part.
+  const int64_t t5 = total + (int64_t)C * 5 * cpr;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < t5 + (int64_t)C * cpr;
        idx += (int64_t)gridDim.x * 256) {
+    if (idx >= t5) {
+      const int64_t j = idx - t5;
+      const int h = (int)(j / cpr), c0 = 8 * (int)(j % cpr);
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f2bf(w.z[(int64_t)(c0 + e) * C + h]);
+      st8(wzt + (int64_t)h * C + c0, o);
+      continue;
+    }
     if (idx >= total) {
       const int64_t j = idx - total;
       const int c = (int)(j / (5 * cpr)), k0 = 8 * (int)(j % (5 * cpr));
@@ -1339,6 +1352,247 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Output projection backward and LN_out backward in one persistent,
+// weight-stationary kernel (N % 8 == 0), per 32-row block of natural rows:
+//   y = xln Wz^T (recomputed), s = s(gl):  dy = dout s,  d gl = dout y s (1 - s);
+//   G = dy Wz, then the LN_out backward of x (planes) into dx (planes).
+// Wave w owns channels 16 w .. 16 w + 15 of both products: its rows of Wz
+// (B operand of the first) and of Wz^T (B operand of the second) stay in
+// registers.  Accumulator register r of lane l holds row 4 (l / 16) + r
+// (+ 16 per row tile), channel 16 w + l % 16.  The loading waves stream each
+// block's xln, gl and dout rows (chunk-rotated) and x plane segments
+// ([channel][32 positions]) and the LN_out statistics into a 3-deep LDS ring;
+// gl and dout are read back transposed to match the accumulators.  dy (the
+// second product's A operand), d gl and dx are staged in LDS and stored by
+// the storing waves: dy rows, d gl into the last block of dproj5, dx plane
+// segments.  Row sums of the LayerNorm backward are reduced across each
+// wave's 16 channels with a transposing butterfly and across the waves in
+// LDS (fixed order); the d gamma / d beta column sums stay in registers for
+// all of a workgroup's blocks and go to lnp [workgroup][2][C].
+// ---------------------------------------------------------------------------
+constexpr int kOutBwdDepth = 3;
+template <int C>
+__global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
+    const __bf16* __restrict__ xln, const __bf16* __restrict__ wz, const __bf16* __restrict__ wzt,
+    const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, const __bf16* __restrict__ x,
+    const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
+    __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, __bf16* __restrict__ dx,
+    float* __restrict__ lnp, TmGeom g, int64_t nblocks) {
+  constexpr int NW = C / 16;         // waves
+  constexpr int CPR = C / 8;         // 16-byte chunks per row
+  constexpr int KS = C / 32;         // 32-deep k steps
+  constexpr int RP = C + 8;          // row staging pitch (bf16)
+  constexpr int PP = 40;             // plane staging pitch (bf16)
+  constexpr int TILE = 32 * C;       // elements of one [32][C] (or [C][32]) tile
+  __shared__ __attribute__((aligned(1024))) __bf16 Rg[kOutBwdDepth][4][TILE];  // xln | gl | dout | x
+  __shared__ __attribute__((aligned(256))) float Ss[kOutBwdDepth][2][64];      // mean | rstd
+  __shared__ __attribute__((aligned(16))) float Rs[2][NW][32];
+  __shared__ __attribute__((aligned(16))) __bf16 Dy[32 * RP];
+  __shared__ __attribute__((aligned(16))) __bf16 Dg[32 * RP];
+  __shared__ __attribute__((aligned(16))) __bf16 Dx[C * PP];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int ch = 16 * w + l16;
+  const bool loader = w < NW / 2;
+
+  bf16x8 wf[KS], wtf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    wf[ks] = ld8(wz + (int64_t)ch * C + 8 * (4 * ks + lg));
+    wtf[ks] = ld8(wzt + (int64_t)ch * C + 8 * (4 * ks + lg));
+  }
+  const float gam = gamma[ch];
+
+  const i32x4 rs_in[3] = {buffer_rsrc(xln), buffer_rsrc(gl), buffer_rsrc(dout)};
+  const i32x4 rs_x = buffer_rsrc(x);
+  const i32x4 rs_mu = buffer_rsrc(mean);
+  const i32x4 rs_rs = buffer_rsrc(rstd);
+  const __amdgpu_buffer_rsrc_t rs_dy = __builtin_amdgcn_make_buffer_rsrc(dy, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_dp = __builtin_amdgcn_make_buffer_rsrc(dproj5, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_dx = __builtin_amdgcn_make_buffer_rsrc(dx, 0, 0x7FFFFFFF, 0x00020000);
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loads per block and loading wave: 2 instructions for each of xln, gl,
+  // dout (rows, chunk-rotated) and x (plane segments); wave 0 also loads the
+  // two statistics rows.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % kOutBwdDepth);
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ci = (2 * w + j) * 64 + lane;
+        const int r = ci / CPR, slot = ci % CPR;
+        const int gc = (slot - r % CPR + CPR) % CPR;
+        const uint32_t m = (uint32_t)blk * 32 + r;
+        const bool ok = blk < bend && m < (uint32_t)g.R;
+        buf2lds16(rs_in[t], ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Rg[stage][t][(2 * w + j) * 512]);
+      }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ci = (2 * w + j) * 64 + lane;  // (channel ci / 4, 8-position part ci % 4)
+      const int c = ci >> 2, part = ci & 3;
+      const uint32_t mb = (uint32_t)blk * 32 + 8 * part;
+      const bool ok = blk < bend && mb < (uint32_t)g.R;
+      buf2lds16(rs_x, ok ? tm_plane_elem32(g, mb, c) * 2 : kBufOOB, &Rg[stage][3][(2 * w + j) * 512]);
+    }
+    if (w == 0) {
+      const uint32_t m = (uint32_t)blk * 32 + lane;
+      const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
+      buf2lds4(rs_mu, ok ? m * 4 : kBufOOB, &Ss[stage][0][0]);
+      buf2lds4(rs_rs, ok ? m * 4 : kBufOOB, &Ss[stage][1][0]);
+    }
+  };
+  // Rows 16 rt + 4 lg + e, channel ch of a chunk-rotated [32][C] tile: lane
+  // L of a 16-lane group reads row 16 rt + 4 lg + L / 4, channels
+  // 16 w + 4 (L % 4) .. + 3 (transposing read).
+  auto col4 = [&](const __bf16* T, int rt) {
+    const int rr = 16 * rt + 4 * lg + (l16 >> 2);
+    const int cc = 16 * w + 4 * (l16 & 3);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)&T[rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)]);
+  };
+  float cg = 0.f, cgx = 0.f;
+  if (loader) {
+    issue(bbeg);
+    issue(bbeg + 1);
+  }
+#pragma unroll 1
+  for (int64_t blk = bbeg; blk < bend; ++blk) {
+    const int stage = (int)(blk % kOutBwdDepth);
+    if (loader) {  // block blk landed (block blk + 1 may be in flight)
+      if (w == 0) wait_vmcnt<10>(); else wait_vmcnt<8>();
+    }
+    __syncthreads();
+    if (loader) issue(blk + 2);
+    // y = xln Wz^T for rows 16 rt + 4 lg + r, channel ch.
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const __bf16* Xl = Rg[stage][0];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 16 * rt + l16;
+        const bf16x8 af =
+            *reinterpret_cast<const bf16x8*>(&Xl[row * C + 8 * ((4 * ks + lg + row) % CPR)]);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[ks], acc[rt], 0, 0, 0);
+      }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const bf16x4 gv4 = col4(Rg[stage][1], rt);
+      const bf16x4 go4 = col4(Rg[stage][2], rt);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * rt + 4 * lg + e;
+        const float sg = sigmoidf(bf2f(gv4[e]));
+        const float go = bf2f(go4[e]);
+        Dy[row * RP + ch] = f2bf(go * sg);
+        Dg[row * RP + ch] = f2bf(go * acc[rt][e] * sg * (1.f - sg));
+      }
+    }
+    __syncthreads();
+    // G = dy Wz, then the LayerNorm backward (channel ch of LN_out).
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(&Dy[(16 * rt + l16) * RP + 8 * (4 * ks + lg)]);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wtf[ks], acc[rt], 0, 0, 0);
+      }
+    float xh[2][4], gv[2][4], a[8], b[8];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r0 = 16 * rt + 4 * lg;
+      const bf16x4 xv = *reinterpret_cast<const bf16x4*>(&Rg[stage][3][ch * 32 + r0]);
+      const f32x4 mu = *reinterpret_cast<const f32x4*>(&Ss[stage][0][r0]);
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][r0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[rt][e] = (bf2f(xv[e]) - mu[e]) * rsd[e];
+        const float G = acc[rt][e];
+        gv[rt][e] = G * gam;
+        a[4 * rt + e] = gv[rt][e];
+        b[4 * rt + e] = gv[rt][e] * xh[rt][e];
+        cg += G;
+        cgx = fmaf(G, xh[rt][e], cgx);
+      }
+    }
+    tm_butterfly<4>(a, b, lane);
+    tm_butterfly<2>(a, b, lane);
+    tm_butterfly<1>(a, b, lane);
+    a[0] += __shfl_xor(a[0], 8);
+    b[0] += __shfl_xor(b[0], 8);
+    if (l16 < 8) {
+      const int t = l16, row = 16 * (t >> 2) + 4 * lg + (t & 3);
+      Rs[0][w][row] = a[0];
+      Rs[1][w][row] = b[0];
+    }
+    __syncthreads();
+    const float invC = 1.f / C;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r0 = 16 * rt + 4 * lg;
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][r0]);
+      f32x4 sg = *reinterpret_cast<const f32x4*>(&Rs[0][0][r0]);
+      f32x4 sx = *reinterpret_cast<const f32x4*>(&Rs[1][0][r0]);
+#pragma unroll
+      for (int v = 1; v < NW; ++v) {
+        sg += *reinterpret_cast<const f32x4*>(&Rs[0][v][r0]);
+        sx += *reinterpret_cast<const f32x4*>(&Rs[1][v][r0]);
+      }
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = f2bf(rsd[e] * (gv[rt][e] - sg[e] * invC - xh[rt][e] * (sx[e] * invC)));
+      *reinterpret_cast<bf16x4*>(&Dx[ch * PP + r0]) = o;
+    }
+    __syncthreads();
+    if (!loader) {
+      // dy rows, d gl rows (into dproj5's last block), dx plane segments:
+      // 4 C chunks each over the 2 C storing threads.
+      const int st = tid - 2 * C;
+      bf16x8 v[6];
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        v[it] = *reinterpret_cast<const bf16x8*>(&Dy[row * RP + 8 * k]);
+        v[2 + it] = *reinterpret_cast<const bf16x8*>(&Dg[row * RP + 8 * k]);
+        v[4 + it] = *reinterpret_cast<const bf16x8*>(&Dx[(q >> 2) * PP + 8 * (q & 3)]);
+      }
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        const uint32_t m = (uint32_t)blk * 32 + row;
+        const bool ok = m < (uint32_t)g.R;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_dy,
+                                               ok ? (m * C + 8 * k) * 2 : kBufOOB, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[2 + it]), rs_dp,
+                                               ok ? (m * 5 * C + 4 * C + 8 * k) * 2 : kBufOOB, 0, 0);
+        const uint32_t mb = (uint32_t)blk * 32 + 8 * (q & 3);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, v[4 + it]), rs_dx,
+            mb < (uint32_t)g.R ? tm_plane_elem32(g, mb, q >> 2) * 2 : kBufOOB, 0, 0);
+      }
+    }
+  }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
+  cg += __shfl_xor(cg, 16);
+  cgx += __shfl_xor(cgx, 16);
+  cg += __shfl_xor(cg, 32);
+  cgx += __shfl_xor(cgx, 32);
+  if (lg == 0) {
+    lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx;
+    lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cg;
+  }
+}
+
 // Zero-fill (used instead of hipMemsetAsync so callers may capture graphs).
 __global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
@@ -1382,7 +1636,7 @@ static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, con
 static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
 static int64_t tm_wp_rows(int64_t C) { return 2 * ((C + 63) / 64) * 128; }
 static int64_t tm_weights_bytes(int64_t C) {
-  return align256(tm_wp_rows(C) * C * 2) + 2 * align256(5 * C * C * 2) + align256(C * C * 2);
+  return align256(tm_wp_rows(C) * C * 2) + 2 * align256(5 * C * C * 2) + 2 * align256(C * C * 2);
 }
 
 // Packed bf16 weights at the start of a workspace.
@@ -1391,6 +1645,7 @@ struct TmPacked {
   __bf16* w5;
   __bf16* wz;
   __bf16* w5t;
+  __bf16* wzt;
 };
 static TmPacked tm_packed(void* ws, int64_t C) {
   char* p = (char*)ws;
@@ -1402,14 +1657,16 @@ static TmPacked tm_packed(void* ws, int64_t C) {
   k.wz = (__bf16*)p;
   p += align256(C * C * 2);
   k.w5t = (__bf16*)p;
+  p += align256(5 * C * C * 2);
+  k.wzt = (__bf16*)p;
   return k;
 }
 
 static int tm_pack(const TmWeights& w, const TmPacked& k, int C, int ntg, hipStream_t s,
                    const char* fn) {
-  const int64_t chunks = (tm_wp_rows(C) + 11 * C) * (C / 8);
+  const int64_t chunks = (tm_wp_rows(C) + 12 * C) * (C / 8);
   hipLaunchKernelGGL(tm_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
-                     s, w, k.wp, k.w5, k.wz, k.w5t, C, ntg);
+                     s, w, k.wp, k.w5, k.wz, k.w5t, k.wzt, C, ntg);
   return check_launch(fn);
 }
 
@@ -1537,7 +1794,7 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   t += align256(R * C * 2);                        // dy
   t += align256(R * 5 * C * 2);                    // dproj5
   t += 3 * align256(B * C * N * Np * 2);           // dx, da, db
-  t += align256(tiles * 2 * C * 4);                // LN_out parameter partials
+  t += align256((R + 31) / 32 * 2 * C * 4);        // LN_out parameter partials (tiles or workgroups)
   t += align256((R + 31) / 32 * 2 * C * 4);        // LN_in parameter partials (per workgroup)
   t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
   t += align256((int64_t)tm_wz_splits(R) * C * C * 4);
@@ -1582,7 +1839,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   __bf16* dx = (__bf16*)take(plane_bytes);
   __bf16* da = (__bf16*)take(plane_bytes);
   __bf16* db = (__bf16*)take(plane_bytes);
-  float* lnp = (float*)take(tiles * 2 * C * 4);
+  float* lnp = (float*)take((R + 31) / 32 * 2 * C * 4);
   float* lnin = (float*)take((R + 31) / 32 * 2 * C * 4);
   float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
   float* wzp = (float*)take((int64_t)sz * C * C * 4);
@@ -1590,13 +1847,34 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   // Pad columns of dx are read by the dA GEMM (K = Np) and must be zero.
   if (g.Np != g.N && (rc = zero_fill(dx, plane_bytes, s, fn))) return rc;
   const unsigned grid_rows = tm_grid(tiles);
-  hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
-                     (const __bf16*)xln, k.wz, (const __bf16*)gate, (const __bf16*)grad_out, (__bf16*)nullptr, dy, dproj5, g, (int)C);
-  if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
-  hipLaunchKernelGGL(tm_ln_out_bwd_kernel, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
-                     (int64_t)C, k.wz, (int)C, (const __bf16*)x, mean_out,
-                     rstd_out, ln_out_w, dx, lnp, g, (int)H);
-  if ((rc = check_launch("tpf_trimul_backward_bf16(ln_out_bwd)"))) return rc;
+  int lnp_splits = (int)tiles;  // LN_out parameter partials
+  if (g.Np == g.N) {
+    // Output projection backward + LN_out backward in one pass.
+    const int64_t nblk = (R + 31) / 32;
+    const int64_t cap = (int64_t)device_cus() * (128 / C);
+    lnp_splits = (int)(nblk < cap ? nblk : cap);
+    switch (C) {
+#define TM_OUT_BWD(CC)                                                                          \
+  case CC:                                                                                      \
+    hipLaunchKernelGGL(tm_out_bwd_ws_kernel<CC>, dim3(lnp_splits), dim3(4 * CC), 0, s,          \
+                       (const __bf16*)xln, k.wz, k.wzt, (const __bf16*)gate,                    \
+                       (const __bf16*)grad_out, (const __bf16*)x, mean_out, rstd_out, ln_out_w, \
+                       dy, dproj5, dx, lnp, g, nblk);                                           \
+    break;
+      TM_OUT_BWD(32) TM_OUT_BWD(64) TM_OUT_BWD(96) TM_OUT_BWD(128)
+#undef TM_OUT_BWD
+    }
+    if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj + ln_out_bwd)"))) return rc;
+  } else {
+    hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
+                       (const __bf16*)xln, k.wz, (const __bf16*)gate, (const __bf16*)grad_out,
+                       (__bf16*)nullptr, dy, dproj5, g, (int)C);
+    if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
+    hipLaunchKernelGGL(tm_ln_out_bwd_kernel, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
+                       (int64_t)C, k.wz, (int)C, (const __bf16*)x, mean_out,
+                       rstd_out, ln_out_w, dx, lnp, g, (int)H);
+    if ((rc = check_launch("tpf_trimul_backward_bf16(ln_out_bwd)"))) return rc;
+  }
   // Contraction backward: dA_c = dX_c B_c, dB_c = dX_c^T A_c (stored layouts).
   GemmArgs ga{};
   ga.A = dx; ga.a_ld = g.Np; ga.a_bs = g.PS;
@@ -1678,7 +1956,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   f.piece[0] = 5 * C * C; f.dst[0][0] = d_w5;
   f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = sz;
   f.piece[1] = C * H; f.dst[1][0] = d_w_z;
-  f.part[2] = lnp; f.n[2] = 2 * C; f.stride[2] = 2 * C; f.splits[2] = (int)tiles;
+  f.part[2] = lnp; f.n[2] = 2 * C; f.stride[2] = 2 * C; f.splits[2] = lnp_splits;
   f.piece[2] = C;
   f.dst[2][0] = d_ln_out_w; f.dst[2][1] = d_ln_out_b;
   f.part[3] = lnin; f.n[3] = 2 * C; f.stride[3] = 2 * C; f.splits[3] = ln_grid;
