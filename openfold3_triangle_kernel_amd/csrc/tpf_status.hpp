@@ -19,6 +19,9 @@ inline int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int device_cus();
+
 inline int check_launch(const char* fn) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(TPF_ERR_LAUNCH, "%s: %s", fn, hipGetErrorString(e));

@@ -31,8 +31,6 @@
 //             GEMMs -> fixed-order folds.
 // 32-deep k stages: every TriMul GEMM has K = C or 5H (small).
 #define TPF_GEMM_GK 32
-#include <atomic>
-
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "tpf_gemm.hpp"
@@ -1672,19 +1670,6 @@ static int tm_pack(const TmWeights& w, const TmPacked& k, int C, int ntg, hipStr
 
 static unsigned tm_grid(int64_t tiles) { return (unsigned)((tiles + 7) / 8 * 8); }
 
-// Compute units of the current device (cached per device; 256 if unknown).
-static int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
 
 #define TM_DISPATCH_C(C, KERNEL, GRID, ...)                                                   \
   switch (C) {                                                                               \
