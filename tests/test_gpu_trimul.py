@@ -53,7 +53,11 @@ def run_turbo(z, mask, w, dout, outgoing, dev):
     return {k: v.detach().float().cpu().numpy() for k, v in got.items()}
 
 
-CASES = [(1, 64, 128), (1, 128, 128), (2, 33, 64), (1, 101, 32), (1, 113, 96), (1, 17, 128)]
+# N % 8 == 0 runs the persistent weight-stationary kernels (B = 2 crosses a
+# batch item inside the walk; N = 200 gives workgroups several 32-row blocks
+# and an uneven last share), other N the tile kernels.
+CASES = [(1, 64, 128), (1, 128, 128), (2, 33, 64), (1, 101, 32), (1, 113, 96), (1, 17, 128),
+         (2, 48, 64), (1, 72, 96), (1, 40, 32), (1, 200, 128)]
 
 
 @pytest.mark.gpu
