@@ -1591,6 +1591,114 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Output projection forward, weight-stationary (N % 8 == 0 not required:
+// rows are natural, row-major): out = (xln Wz^T) s(gl), persistent
+// workgroups of C / 16 waves over 32-row blocks.  Wave w holds the Wz rows of
+// channels 16 w .. 16 w + 15 (B operands of v_mfma_f32_16x16x32_bf16); the
+// loading waves stream xln and gl rows (chunk-rotated) into a 4-deep LDS
+// ring; gl is read back transposed to match the accumulators; out is staged
+// as [row][channel] and stored as full rows by the storing waves.
+// ---------------------------------------------------------------------------
+constexpr int kOutFwdDepth = 4;
+template <int C>
+__global__ __launch_bounds__(4 * C) void tm_out_proj_fwd_ws_kernel(
+    const __bf16* __restrict__ xln, const __bf16* __restrict__ wz, const __bf16* __restrict__ gl,
+    __bf16* __restrict__ out, TmGeom g, int64_t nblocks) {
+  constexpr int NW = C / 16;         // waves
+  constexpr int CPR = C / 8;         // 16-byte chunks per row
+  constexpr int KS = C / 32;         // 32-deep k steps
+  constexpr int RP = C + 8;          // staging pitch (bf16)
+  __shared__ __attribute__((aligned(1024))) __bf16 Rg[kOutFwdDepth][2][32 * C];  // xln | gl
+  __shared__ __attribute__((aligned(16))) __bf16 Or[2][32 * RP];
+
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int ch = 16 * w + l16;
+  const bool loader = w < NW / 2;
+
+  bf16x8 wf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) wf[ks] = ld8(wz + (int64_t)ch * C + 8 * (4 * ks + lg));
+  const i32x4 rs_in[2] = {buffer_rsrc(xln), buffer_rsrc(gl)};
+  const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(out, 0, 0x7FFFFFFF, 0x00020000);
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loads per block and loading wave: 2 instructions each for xln and gl.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % kOutFwdDepth);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ci = (2 * w + j) * 64 + lane;
+        const int r = ci / CPR, slot = ci % CPR;
+        const int gc = (slot - r % CPR + CPR) % CPR;
+        const uint32_t m = (uint32_t)blk * 32 + r;
+        const bool ok = blk < bend && m < (uint32_t)g.R;
+        buf2lds16(rs_in[t], ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Rg[stage][t][(2 * w + j) * 512]);
+      }
+  };
+  if (loader) {
+#pragma unroll
+    for (int d = 0; d < kOutFwdDepth - 1; ++d) issue(bbeg + d);
+    wait_vmcnt<4 * (kOutFwdDepth - 2)>();  // block bbeg landed
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int64_t blk = bbeg; blk < bend; ++blk) {
+    const int stage = (int)(blk % kOutFwdDepth);
+    const int sb = (int)(blk & 1);
+    if (loader) issue(blk + kOutFwdDepth - 1);
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const __bf16* Xl = Rg[stage][0];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int row = 16 * rt + l16;
+        const bf16x8 af =
+            *reinterpret_cast<const bf16x8*>(&Xl[row * C + 8 * ((4 * ks + lg + row) % CPR)]);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[ks], acc[rt], 0, 0, 0);
+      }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      // gl for rows 16 rt + 4 lg + e, channel ch: lane L of a 16-lane group
+      // reads row 16 rt + 4 lg + L / 4, channels 16 w + 4 (L % 4) .. + 3.
+      const int rr = 16 * rt + 4 * lg + (l16 >> 2);
+      const int cc = 16 * w + 4 * (l16 & 3);
+      const bf16x4 gv4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (lds_bf16x4*)&Rg[stage][1][rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        Or[sb][(16 * rt + 4 * lg + e) * RP + ch] = f2bf(acc[rt][e] * sigmoidf(bf2f(gv4[e])));
+    }
+    if (loader) wait_vmcnt<4 * (kOutFwdDepth - 2)>();  // block blk + 1 landed
+    __syncthreads();
+    if (!loader) {
+      // 4 C chunks (32 rows x C / 8) over the 2 C storing threads.
+      const int st = tid - 2 * C;
+      bf16x8 v[2];
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        v[it] = *reinterpret_cast<const bf16x8*>(&Or[sb][row * RP + 8 * k]);
+      }
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        const uint32_t m = (uint32_t)blk * 32 + row;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o,
+                                               m < (uint32_t)g.R ? (m * C + 8 * k) * 2 : kBufOOB, 0, 0);
+      }
+    }
+  }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
+}
+
 // Zero-fill (used instead of hipMemsetAsync so callers may capture graphs).
 __global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
@@ -1752,10 +1860,20 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
   TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)((g.NN + 127) / 128), (unsigned)B),
                 (const __bf16*)x, ln_out_w, ln_out_b, (__bf16*)xln, mean_out, rstd_out, g);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_out)"))) return rc;
-  hipLaunchKernelGGL(tm_out_proj_kernel<false>, dim3(tm_grid(tiles)), dim3(256), 0, s,
-                     (const __bf16*)xln, k.wz, (const __bf16*)gate,
-                     (const __bf16*)nullptr, (__bf16*)out, (__bf16*)nullptr, (__bf16*)nullptr, g,
-                     (int)C);
+  {
+    const int64_t nblk = (g.R + 31) / 32;
+    const int64_t cap = (int64_t)device_cus() * (128 / C);
+    const unsigned grid = (unsigned)(nblk < cap ? nblk : cap);
+    switch (C) {
+#define TM_OUT_FWD(CC)                                                                          \
+  case CC:                                                                                      \
+    hipLaunchKernelGGL(tm_out_proj_fwd_ws_kernel<CC>, dim3(grid), dim3(4 * CC), 0, s,           \
+                       (const __bf16*)xln, k.wz, (const __bf16*)gate, (__bf16*)out, g, nblk);   \
+    break;
+      TM_OUT_FWD(32) TM_OUT_FWD(64) TM_OUT_FWD(96) TM_OUT_FWD(128)
+#undef TM_OUT_FWD
+    }
+  }
   return check_launch("tpf_trimul_forward_bf16(out_proj)");
 }
 
