@@ -56,11 +56,10 @@ constexpr int lds_bytes(int epilogue, int ns = kGNS) {
 }
 // Ring depths per kernel (measured): the short-K projections keep two
 // stages (occupancy), the long-K / large-epilogue kernels take more.
-constexpr int kInProjBwdNS = 3, kOutProjNS = 4, kOutProjFwdNS = 2;
+constexpr int kInProjBwdNS = 3, kOutProjNS = 4;
 constexpr int kLnOutBwdNS = 2;
 constexpr int kInProjLds = lds_bytes((64 + 128) * kSP * 2, kInProjBwdNS);  // d tile + [dp | dg] tile
 constexpr int kOutProjLds = lds_bytes(2 * 128 * kSP * 2, kOutProjNS);  // gate + dout tiles
-constexpr int kOutProjFwdLds = lds_bytes(128 * kSP * 2, kOutProjFwdNS);  // gate tile
 constexpr int kLnOutBwdLds = lds_bytes(128 * kSP * 2, kLnOutBwdNS);  // x tile
 
 // Element offset of position p = i*N + j inside a channel-major plane.
@@ -938,17 +937,17 @@ __global__ __launch_bounds__(256, 2) void tm_in_proj_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Output projection y = xln Wz^T (natural rows).  Forward: out = y s(gl).
-// Backward (BWD): dy = dout s(gl) (row-major) and
-// d gl = dout y s(gl) (1 - s(gl)) into the last block of dproj5.
+// Output projection backward, tile GEMM (N % 8 != 0; otherwise the fused
+// tm_out_bwd_ws_kernel runs): y = xln Wz^T recomputed (natural rows),
+// dy = dout s(gl) (row-major) and d gl = dout y s(gl) (1 - s(gl)) into the
+// last block of dproj5.
 // ---------------------------------------------------------------------------
-template <bool BWD>
-__global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
+__global__ __launch_bounds__(256, 2) void tm_out_proj_bwd_kernel(
     const __bf16* __restrict__ xln, const __bf16* __restrict__ p_out,
-    const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, __bf16* __restrict__ out,
+    const __bf16* __restrict__ gl, const __bf16* __restrict__ dout,
     __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, TmGeom g, int C) {
   constexpr int kStage = 128 * kSP * 2;
-  __shared__ __attribute__((aligned(1024))) char smem[BWD ? kOutProjLds : kOutProjFwdLds];
+  __shared__ __attribute__((aligned(1024))) char smem[kOutProjLds];
   __shared__ int64_t rho_s[128];
   const int H = g.H;
   const int64_t T = xcd_order((g.R + 127) / 128);
@@ -959,14 +958,14 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
   GemmOperand W{p_out, H, C, 0, {}, {}};
   RegTile greg, dreg;
   fetch_rows(greg, gl, C, C, m0, g.R);
-  if (BWD) fetch_rows(dreg, dout, C, C, m0, g.R);
+  fetch_rows(dreg, dout, C, C, m0, g.R);
   f32x16 acc[2][2];
-  gemm_tile<true, true, BWD ? kOutProjNS : kOutProjFwdNS>(A, W, (int)m0, 0, 0, H, smem, acc);
+  gemm_tile<true, true, kOutProjNS>(A, W, (int)m0, 0, 0, H, smem, acc);
   const AccPos ap;
   __bf16* Sg = reinterpret_cast<__bf16*>(smem);
   __bf16* Sd = reinterpret_cast<__bf16*>(smem + kStage);
   put_rows(Sg, greg);
-  if (BWD) put_rows(Sd, dreg);
+  put_rows(Sd, dreg);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -979,22 +978,14 @@ __global__ __launch_bounds__(256, 2) void tm_out_proj_kernel(
         const int o = ap.row(i, r) * kSP + col;
         const float s = sigmoidf(bf2f(Sg[o]));
         const float y = acc[i][j][r];
-        if (!BWD) {
-          Sg[o] = f2bf(y * s);
-        } else {
-          const float go = bf2f(Sd[o]);
-          Sd[o] = f2bf(go * s);
-          Sg[o] = f2bf(go * y * s * (1.f - s));
-        }
+        const float go = bf2f(Sd[o]);
+        Sd[o] = f2bf(go * s);
+        Sg[o] = f2bf(go * y * s * (1.f - s));
       }
     }
   __syncthreads();
-  if (!BWD) {
-    tm_store_rows(Sg, C, rho_s, out, C, 0);
-  } else {
-    tm_store_rows(Sd, C, rho_s, dy, C, 0);
-    tm_store_rows(Sg, C, rho_s, dproj5, 5 * H, 4 * H);
-  }
+  tm_store_rows(Sd, C, rho_s, dy, C, 0);
+  tm_store_rows(Sg, C, rho_s, dproj5, 5 * H, 4 * H);
 }
 
 // ---------------------------------------------------------------------------
@@ -1969,9 +1960,9 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
     }
     if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj + ln_out_bwd)"))) return rc;
   } else {
-    hipLaunchKernelGGL(tm_out_proj_kernel<true>, dim3(grid_rows), dim3(256), 0, s,
+    hipLaunchKernelGGL(tm_out_proj_bwd_kernel, dim3(grid_rows), dim3(256), 0, s,
                        (const __bf16*)xln, k.wz, (const __bf16*)gate, (const __bf16*)grad_out,
-                       (__bf16*)nullptr, dy, dproj5, g, (int)C);
+                       dy, dproj5, g, (int)C);
     if ((rc = check_launch("tpf_trimul_backward_bf16(out_proj)"))) return rc;
     hipLaunchKernelGGL(tm_ln_out_bwd_kernel, dim3(grid_rows), dim3(256), 0, s, (const __bf16*)dy,
                        (int64_t)C, k.wz, (int)C, (const __bf16*)x, mean_out,
