@@ -889,7 +889,7 @@ __device__ __forceinline__ void dq_fold_block(const __bf16* __restrict__ part,
     bf16x8 x[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (k0 + u < nkb) x[u] = ld8(src + (int64_t)(k0 + u) * stride);
+      if (k0 + u < nkb) x[u] = ld8_nt(src + (int64_t)(k0 + u) * stride);
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (k0 + u < nkb) {
@@ -943,8 +943,8 @@ __device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
       for (int u = 0; u < 4; ++u)
         if (s + u < s1) {
           const float* p = src + (int64_t)(s + u) * stride;
-          x[u][0] = *reinterpret_cast<const f32x4*>(p);
-          x[u][1] = *reinterpret_cast<const f32x4*>(p + 4);
+          x[u][0] = ld4f_nt(p);
+          x[u][1] = ld4f_nt(p + 4);
         }
 #pragma unroll
       for (int u = 0; u < 4; ++u)
@@ -1069,79 +1069,67 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
   delta[(plane * H + h) * N + j] = s;
 }
 
-// Pair-bias gradient into the projection gradient rows: thread = (bias batch
-// bb, query q, 8 consecutive keys); for each head, the f32 (b, outer group)
-// partials that share bb are folded in ascending order (as in
-// dbias_fold_block), then every key's row receives its H values and
-// zeros over the rest of the row tail [4*H*D, pitch).
-template <int HMAX>
+// Pair-bias gradient into the projection gradient rows.  Workgroup = 512
+// consecutive (query, key) elements of one bias batch bb x 4 head slots:
+// thread (slot s, lane c) owns elements 4c..4c+3 and 256+4c..256+4c+3 (each
+// load instruction of a wave reads 1 KB contiguous) and folds heads s, s + 4,
+// ... < H, each over the f32 (b, outer group) partials that share bb in
+// ascending order (8 partials' loads in flight, nontemporal: the partials are
+// read once).  The H sums of an element meet in LDS, and the workgroup then
+// writes the row tails [4*H*D, pitch) of its 512 key rows (H values, zeros
+// after them) in 16-byte chunks, consecutive lanes on consecutive chunks.
 __global__ __launch_bounds__(256) void attn_dbias_pair_kernel(
     const float* __restrict__ part, int B, int Bb, int groups, int H, int N,
     __bf16* __restrict__ dproj, int64_t pitch, int64_t tail_off, int transpose_bias) {
-  const int64_t nn8 = (int64_t)N * N / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)Bb * nn8) return;
-  const int bb = (int)(idx / nn8);
-  const int64_t e = (idx % nn8) * 8;
-  const int q = (int)(e / N), k0 = (int)(e % N);
+  __shared__ float red[16][516];
+  const int tid = threadIdx.x, c = tid & 63, slot = tid >> 6;
+  const int64_t nn = (int64_t)N * N;  // a multiple of 512 (N % 64 == 0)
+  const int64_t el0 = (int64_t)blockIdx.x * 512;  // over Bb * nn
+  const int bb = (int)(el0 / nn);
+  const int64_t e = el0 - (int64_t)bb * nn;
   const int b_lo = (Bb == 1) ? 0 : bb, b_hi = (Bb == 1) ? B : bb + 1;
-  const int64_t stride = (int64_t)H * N * N;
+  const int64_t stride = (int64_t)H * nn;
   const int n = (b_hi - b_lo) * groups;
-  float acc[8][HMAX];
-#pragma unroll
-  for (int h = 0; h < HMAX; ++h) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i][h] = 0.f;
-    if (h >= H) continue;
-    const float* src = part + (int64_t)b_lo * groups * stride + (int64_t)h * N * N + e;
-    auto ld = [&](int s, int i) { return src[(int64_t)s * stride + i]; };
-    float a[8];
-    {
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { a[i] = x0[i]; a[4 + i] = x1[i]; }
-    }
+  const int o0 = 4 * c, o1 = 256 + 4 * c;
+  for (int h = slot; h < H; h += 4) {
+    const float* src = part + (int64_t)b_lo * groups * stride + (int64_t)h * nn + e;
+    f32x4 a0 = ld4f_nt(src + o0), a1 = ld4f_nt(src + o1);
     int s = 1;
-    for (; s + 4 <= n; s += 4) {
-      f32x4 x[4][2];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float* p = src + (int64_t)(s + u) * stride;
-        x[u][0] = *reinterpret_cast<const f32x4*>(p);
-        x[u][1] = *reinterpret_cast<const f32x4*>(p + 4);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] += x[u][i >> 2][i & 3];
-    }
-    for (; s < n; ++s) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] += ld(s, i);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i][h] = a[i];
-  }
-  const int tail8 = (int)((pitch - tail_off) / 8);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int k = k0 + i;
-    const int64_t r = (int64_t)bb * N * N + (transpose_bias ? (int64_t)k * N + q : (int64_t)q * N + k);
-    __bf16* dst = dproj + r * pitch + tail_off;
-    for (int c = 0; c < tail8; ++c) {
-      bf16x8 v;
+    for (; s + 8 <= n; s += 8) {
+      f32x4 x[8][2];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int h = c * 8 + u;
-        float val = 0.f;
-#pragma unroll
-        for (int hh = 0; hh < HMAX; ++hh)
-          if (hh == h) val = acc[i][hh];
-        v[u] = f2bf(val);
+        const float* p = src + (int64_t)(s + u) * stride;
+        x[u][0] = ld4f_nt(p + o0);
+        x[u][1] = ld4f_nt(p + o1);
       }
-      st8(dst + c * 8, v);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) { a0 += x[u][0]; a1 += x[u][1]; }
     }
+    for (; s < n; ++s) {
+      const float* p = src + (int64_t)s * stride;
+      a0 += ld4f_nt(p + o0);
+      a1 += ld4f_nt(p + o1);
+    }
+    *reinterpret_cast<f32x4*>(&red[h][o0]) = a0;
+    *reinterpret_cast<f32x4*>(&red[h][o1]) = a1;
+  }
+  __syncthreads();
+  // Row tails: 512 key rows x tail8 chunks of 8 bf16 (chunk u of a row holds
+  // heads 8u .. 8u+7).
+  const int tail8 = (int)((pitch - tail_off) / 8);
+  for (int t = tid; t < 512 * tail8; t += 256) {
+    const int j = t / tail8, ch = t - j * tail8;
+    const int64_t el = e + j;
+    const int q = (int)(el / N), k = (int)(el % N);
+    const int64_t r = (int64_t)bb * nn + (transpose_bias ? (int64_t)k * N + q : (int64_t)q * N + k);
+    bf16x8 v;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int h = ch * 8 + u;
+      v[u] = f2bf(h < H ? red[h][j] : 0.f);
+    }
+    st8(dproj + r * pitch + tail_off + ch * 8, v);
   }
 }
 
@@ -1636,17 +1624,9 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
                      dim3(256), 0, s, pt.dq, dp, g, (int)bwd_key_blocks(N, D));
   if ((rc = check_launch(fn))) return rc;
   const int64_t groups = (N + kBwdGroup - 1) / kBwdGroup;
-  const int64_t db_items = B * N * N / 8;
-  const dim3 db_grid((unsigned)((db_items + 255) / 256));
-  if (H <= 4)
-    hipLaunchKernelGGL(attn_dbias_pair_kernel<4>, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
-                       (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
-  else if (H <= 8)
-    hipLaunchKernelGGL(attn_dbias_pair_kernel<8>, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
-                       (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
-  else
-    hipLaunchKernelGGL(attn_dbias_pair_kernel<16>, db_grid, dim3(256), 0, s, pt.db, (int)B,
-                       (int)B, (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
+  const dim3 db_grid((unsigned)(B * N * N / 512));
+  hipLaunchKernelGGL(attn_dbias_pair_kernel, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
+                     (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
   return check_launch(fn);
 }
 

@@ -81,6 +81,14 @@ __device__ __forceinline__ float sigmoidf(float x) { return __builtin_amdgcn_rcp
 __device__ __forceinline__ bf16x8 ld8(const __bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
+// Streaming loads of data read once (fold partials): nontemporal, so they do
+// not displace reused lines from the caches.
+__device__ __forceinline__ bf16x8 ld8_nt(const __bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+}
+__device__ __forceinline__ f32x4 ld4f_nt(const float* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+}
 __device__ __forceinline__ void st8(__bf16* p, bf16x8 v) {
   *reinterpret_cast<bf16x8*>(p) = v;
 }

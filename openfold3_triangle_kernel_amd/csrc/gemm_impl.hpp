@@ -32,29 +32,65 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
   const int kend = min(g.K, kbeg + g.k_chunk);
   GemmOperand A{g.A + (int64_t)z * g.a_bs, g.a_ld, g.M, g.a_gather_n, g.a_div_n, g.a_div_nn};
   GemmOperand B{g.B + (int64_t)z * g.b_bs, g.b_ld, g.N, 0, {}, {}, g.b_kmax > 0 ? g.b_kmax : 0x7fffffff};
-  f32x16 acc[2][2];
-  gemm_tile<A_KC, B_KC>(A, B, m0, n0, kbeg, kend, smem, acc);
-
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int rl = lane & 31, hl = lane >> 5, wm = w >> 1, wn = w & 1;
   char* Cb = (char*)g.C + ((int64_t)z * g.c_bs + (int64_t)split * g.c_split) * (OUT_F32 ? 4 : 2);
+  f32x16 acc[2][2];
+  if constexpr (OUT_F32) {
+    gemm_tile<A_KC, B_KC>(A, B, m0, n0, kbeg, kend, smem, acc);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + rl;
-      if (col >= g.N) continue;
+      for (int j = 0; j < 2; ++j) {
+        const int col = n0 + wn * 64 + j * 32 + rl;
+        if (col >= g.N) continue;
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (rr >> 2) + 4 * hl + (rr & 3);
-        if (row < g.M) {
-          const float val = acc[i][j][rr] * g.alpha;
-          const int64_t off = (int64_t)row * g.c_ld + col;
-          if (OUT_F32) reinterpret_cast<float*>(Cb)[off] = val;
-          else reinterpret_cast<__bf16*>(Cb)[off] = f2bf(val);
+        for (int rr = 0; rr < 16; ++rr) {
+          const int row = m0 + wm * 64 + i * 32 + 8 * (rr >> 2) + 4 * hl + (rr & 3);
+          if (row < g.M)
+            reinterpret_cast<float*>(Cb)[(int64_t)row * g.c_ld + col] = acc[i][j][rr] * g.alpha;
         }
       }
+  } else {
+    // bf16 output: the tile is formed transposed (C^T = B A^T), so each lane's
+    // four consecutive accumulator registers are four consecutive columns of
+    // C; wave w stages its 64 x 64 sub-tile (rows 64 (w & 1), columns
+    // 64 (w >> 1)) in LDS as bf16 rows and writes it back with 16-byte stores,
+    // eight full 128-byte row segments per store instruction.
+    gemm_tile<B_KC, A_KC>(B, A, n0, m0, kbeg, kend, smem, acc);
+    constexpr int EP = 72;  // staged row pitch (bf16)
+    static_assert(4 * 64 * EP * 2 <= gemm_ring_bytes(kGNS), "epilogue staging fits the ring");
+    __bf16* Ls = reinterpret_cast<__bf16*>(smem) + w * 64 * EP;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = f2bf(acc[i][j][4 * r4 + e] * g.alpha);
+          *reinterpret_cast<bf16x4*>(&Ls[(32 * j + rl) * EP + 32 * i + 8 * r4 + 4 * hl]) = v;
+        }
+    __syncthreads();
+    const bool vec = ((g.c_ld | g.c_bs) % 8 == 0) && ((uintptr_t)g.C % 16 == 0);
+    __bf16* Cw = reinterpret_cast<__bf16*>(Cb);
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int rr = 8 * it + (lane >> 3), ch = lane & 7;
+      const int row = m0 + 64 * wn + rr, col = n0 + 64 * wm + 8 * ch;
+      if (row >= g.M || col >= g.N) continue;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(&Ls[rr * EP + 8 * ch]);
+      __bf16* dst = Cw + (int64_t)row * g.c_ld + col;
+      if (vec && col + 8 <= g.N) {
+        st8(dst, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (col + e < g.N) dst[e] = v[e];
+      }
     }
+  }
 }
 
 __host__ __device__ inline int64_t gemm_tiles(const GemmArgs& g) {
