@@ -21,61 +21,47 @@ namespace tpf {
 
 using namespace gk32;
 
-// Fixed-order fold of split partials: thread (i, j) sums splits
-// [j*chunk, min((j+1)*chunk, splits)) in ascending order and writes the
-// result to dst + j*dst_stride + i.  Repeated passes (chunk 64) reduce any
-// number of splits; the order depends only on the shapes (deterministic).
-__global__ __launch_bounds__(256) void fold_f32_kernel(const float* __restrict__ part,
-                                                       float* __restrict__ dst, int64_t n,
-                                                       int64_t stride, int splits, int chunk,
-                                                       int64_t dst_stride) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int j = blockIdx.y;
-  if (i >= n) return;
-  const int s0 = j * chunk, s1 = min(splits, s0 + chunk);
-  float acc = part[(int64_t)s0 * stride + i];
-  int s = s0 + 1;
-  for (; s + 8 <= s1; s += 8) {  // 8 loads in flight, added in ascending order
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(s + e) * stride + i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += v[e];
-  }
-  for (; s < s1; ++s) acc += part[(int64_t)s * stride + i];
-  dst[(int64_t)j * dst_stride + i] = acc;
-}
-
-// Several folds in one launch per pass: blockIdx.y runs over the (segment,
-// chunk) pairs.  Intermediate passes fold 64-split chunks in place (as
-// fold_launch does); the final pass writes element i of a segment to
-// dst[i / piece][i % piece], so one segment can land in up to 4 outputs.
-__global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f, int final_pass) {
+// Several fixed-order folds in one launch.  Segment sg owns workgroups
+// [gbase[sg], gbase[sg + 1]); a workgroup covers 256 / RC consecutive
+// elements x RC ranges of splits (RC = ranges[sg], a power of two chosen so
+// that a range holds at most about 16 splits): thread (range r, element i)
+// sums splits [r * per, min((r + 1) * per, splits)) in ascending order with
+// 8 loads in flight, and the ranges meet in LDS in the fixed order
+// ((r0 + r1) + r2) + ...; element i of the segment lands in
+// dst[i / piece][i % piece].  The order depends only on the shapes.
+__global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
+  __shared__ float red[256];
   int sg = 0;
-  while (sg + 1 < f.nseg && (int)blockIdx.y >= f.gbase[sg + 1]) ++sg;
-  const int j = (int)blockIdx.y - f.gbase[sg];
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= f.n[sg]) return;
+  while (sg + 1 < f.nseg && (int)blockIdx.x >= f.gbase[sg + 1]) ++sg;
+  const int rc = f.ranges[sg], epw = 256 / rc;
+  const int r = threadIdx.x / epw, el = threadIdx.x - r * epw;
+  const int64_t i = (int64_t)((int)blockIdx.x - f.gbase[sg]) * epw + el;
+  const bool act = i < f.n[sg];
+  const int splits = f.splits[sg];
+  const int per = (splits + rc - 1) / rc;
+  const int s0 = r * per, s1 = min(splits, s0 + per);
   const float* part = f.part[sg];
   const int64_t stride = f.stride[sg];
-  const int chunk = final_pass ? f.splits[sg] : 64;
-  const int s0 = j * chunk, s1 = min(f.splits[sg], s0 + chunk);
-  float acc = part[(int64_t)s0 * stride + i];
-  int s = s0 + 1;
-  for (; s + 8 <= s1; s += 8) {
-    float v[8];
+  float acc = 0.f;
+  if (act && s0 < s1) {
+    acc = part[(int64_t)s0 * stride + i];
+    int s = s0 + 1;
+    for (; s + 8 <= s1; s += 8) {
+      float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(s + e) * stride + i];
+      for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(s + e) * stride + i];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += v[e];
+      for (int e = 0; e < 8; ++e) acc += v[e];
+    }
+    for (; s < s1; ++s) acc += part[(int64_t)s * stride + i];
   }
-  for (; s < s1; ++s) acc += part[(int64_t)s * stride + i];
-  if (final_pass) {
-    const int64_t pc = i / f.piece[sg];
-    f.dst[sg][pc][i - pc * f.piece[sg]] = acc;
-  } else {
-    const_cast<float*>(part)[(int64_t)j * 64 * stride + i] = acc;
-  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (r != 0 || !act) return;
+  for (int q = 1; q < rc; ++q)
+    if (q * per < splits) acc += red[q * epw + el];
+  const int64_t pc = i / f.piece[sg];
+  f.dst[sg][pc][i - pc * f.piece[sg]] = acc;
 }
 
 // The weight-gradient fold contract of the reference
@@ -103,38 +89,18 @@ __global__ __launch_bounds__(256) void wgrad_fixed_fold_kernel(const float* __re
 
 int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
   if (f.nseg < 1 || f.nseg > kFoldMaxSegs) return set_error(TPF_ERR_ARG, "%s: bad fold segments", fn);
-  for (;;) {
-    // Segments with more than 64 splits take a 64-chunk pass; the others wait.
-    FoldSegs p = f;
-    p.nseg = 0;
-    int groups = 0;
-    int64_t maxn = 0;
-    for (int sg = 0; sg < f.nseg; ++sg) {
-      if (f.splits[sg] <= 64) continue;
-      const int k = p.nseg++;
-      p.part[k] = f.part[sg]; p.n[k] = f.n[sg]; p.stride[k] = f.stride[sg];
-      p.splits[k] = f.splits[sg]; p.gbase[k] = groups;
-      groups += (f.splits[sg] + 63) / 64;
-      maxn = f.n[sg] > maxn ? f.n[sg] : maxn;
-    }
-    if (p.nseg == 0) break;
-    hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)((maxn + 255) / 256), (unsigned)groups),
-                       dim3(256), 0, stream, p, 0);
-    int rc = check_launch(fn);
-    if (rc) return rc;
-    for (int sg = 0; sg < f.nseg; ++sg)
-      if (f.splits[sg] > 64) {
-        f.splits[sg] = (f.splits[sg] + 63) / 64;
-        f.stride[sg] *= 64;
-      }
-  }
-  int64_t maxn = 0;
+  int64_t blocks = 0;
   for (int sg = 0; sg < f.nseg; ++sg) {
-    f.gbase[sg] = sg;
-    maxn = f.n[sg] > maxn ? f.n[sg] : maxn;
+    if (f.splits[sg] < 1 || f.n[sg] < 1 || f.piece[sg] < 1)
+      return set_error(TPF_ERR_ARG, "%s: bad fold segment", fn);
+    int rc = 1;
+    while (rc < 64 && (f.splits[sg] + rc - 1) / rc > 16) rc *= 2;
+    f.ranges[sg] = rc;
+    f.gbase[sg] = (int)blocks;
+    blocks += (f.n[sg] + 256 / rc - 1) / (256 / rc);
   }
-  hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)((maxn + 255) / 256), (unsigned)f.nseg),
-                     dim3(256), 0, stream, f, 1);
+  if (blocks > 0x7fffffff) return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
+  hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, f);
   return check_launch(fn);
 }
 
@@ -183,22 +149,11 @@ int gemm_launch_pair(const GemmArgs& p0, int a_kc0, int b_kc0, const GemmArgs& p
 
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
                 hipStream_t stream, const char* fn) {
-  // Passes of 64-way chunks, written in place into each chunk's first slot.
-  constexpr int kChunk = 64;
-  float* buf = const_cast<float*>(part);
-  int64_t st = stride;
-  while (splits > kChunk) {
-    const int groups = (splits + kChunk - 1) / kChunk;
-    hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)groups),
-                       dim3(256), 0, stream, buf, buf, n, st, splits, kChunk, st * kChunk);
-    int rc = check_launch(fn);
-    if (rc) return rc;
-    splits = groups;
-    st *= kChunk;
-  }
-  hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256), 1), dim3(256), 0, stream,
-                     buf, out, n, st, splits, splits, (int64_t)0);
-  return check_launch(fn);
+  FoldSegs f{};
+  f.nseg = 1;
+  f.part[0] = part; f.n[0] = n; f.stride[0] = stride; f.splits[0] = splits;
+  f.piece[0] = n; f.dst[0][0] = out;
+  return fold_multi(f, stream, fn);
 }
 
 }  // namespace tpf

@@ -51,16 +51,17 @@ int gemm_f32_launch(const GemmArgsF32& g, int a_kc, int b_kc, int batch, hipStre
 int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int splits,
                 hipStream_t stream, const char* fn);
 
-// Up to kFoldMaxSegs independent fixed-order folds (same order as
-// fold_launch) in one launch per pass.  Segment sg folds `splits` partial
-// vectors of n floats spaced `stride` apart (folded in place in its part
-// buffer when splits > 64) into dst[sg][i / piece][i % piece].
+// Up to kFoldMaxSegs independent fixed-order folds in one launch (fold_launch
+// is the one-segment case).  Segment sg folds `splits` partial vectors of n
+// floats spaced `stride` apart into dst[sg][i / piece][i % piece]; the
+// partials are left unchanged.
 constexpr int kFoldMaxSegs = 4;
 struct FoldSegs {
   const float* part[kFoldMaxSegs];
   float* dst[kFoldMaxSegs][4];
   int64_t n[kFoldMaxSegs], stride[kFoldMaxSegs], piece[kFoldMaxSegs];
   int splits[kFoldMaxSegs], gbase[kFoldMaxSegs];
+  int ranges[kFoldMaxSegs];  // set by fold_multi
   int nseg;
 };
 int fold_multi(FoldSegs f, hipStream_t stream, const char* fn);
