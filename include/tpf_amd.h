@@ -53,6 +53,8 @@ int tpf_abi_version(void);
 enum {
   TPF_QKV_SEQ_MAJOR = 1,   /* q, k, v (and dq, dk, dv) in sequence-major storage */
   TPF_BIAS_TRANSPOSED = 2, /* bias given as the transpose of a contiguous tensor */
+  TPF_DBIAS_BF16 = 4,      /* backward: dbias is bf16 (the f32 fold rounded once), stored
+                              in the bias's own order (transposed with TPF_BIAS_TRANSPOSED) */
 };
 
 /* Bytes of device workspace tpf_attn_forward_bf16 needs (the bias in f32,
@@ -113,14 +115,16 @@ int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64
 
 /* Single-reconstruction backward: dq, dk, dv (bf16, same storage order as
  * q) and dbias (f32 [bias_batches, H, N, N], summed over every (b, o) that
- * shares the bias), all reduced in fixed orders (bitwise reproducible).
+ * shares the bias; with TPF_DBIAS_BF16 the same sums rounded to bf16 and
+ * stored in the bias's order), all reduced in fixed orders (bitwise
+ * reproducible).
  * Replaces turbopairformer_triangle_sr_backward_out
  * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dq_dbias.cu:2526-2648)
  * together with its planner (turbopairformer_triangle_dq_dbias.py:466-566)
  * and the broadcast dBias reduction (:1788-1825, .py:326-376). */
 int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
                            const float* lse, const float* delta, const float* mask,
-                           const void* bias, void* dq, void* dk, void* dv, float* dbias,
+                           const void* bias, void* dq, void* dk, void* dv, void* dbias,
                            void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
                            int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
                            double scale, void* stream);
@@ -136,7 +140,7 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                                 int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
                                 int64_t N, int64_t D, int layout, int64_t bias_batches,
                                 double scale, void* stream);
-int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
+int tpf_attn_backward_finish_bf16(void* dq, void* dbias, const void* workspace, int64_t B,
                                   int64_t O, int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream);
 

@@ -32,6 +32,7 @@ _PAD_QUANTUM = 64  # kernels tile the sequence in 64-key blocks
 # Layout bits of the C ABI (include/tpf_amd.h TPF_QKV_SEQ_MAJOR, TPF_BIAS_TRANSPOSED).
 _QKV_SEQ_MAJOR = 1
 _BIAS_TRANSPOSED = 2
+_DBIAS_BF16 = 4  # backward: bf16 dbias in the bias's own storage order
 _MAX_HEAD_DIM = 64
 _MAX_GRID_YZ = 65_535
 _SUPPORT_CACHE: dict = {}
@@ -261,7 +262,13 @@ class _TriangleAttentionFn(torch.autograd.Function):
                 dq, dk, dv = (torch.empty_like(q, memory_format=torch.contiguous_format)
                               for _ in range(3))
             Bb = int(bias_k.shape[0])
-            dbias = torch.empty((Bb, H, N, N), device=q.device, dtype=torch.float32)
+            # A bf16 bias gets its gradient from the fold directly: the f32
+            # sums rounded once (as the reference's .to(bf16)), stored in the
+            # bias's own order (a transposed bias gets a transposed gradient).
+            direct = ctx.bias_reduce is None and ctx.bias_dtype == torch.bfloat16
+            layout = ctx.layout | (_DBIAS_BF16 if direct else 0)
+            dbias = torch.empty((Bb, H, N, N), device=q.device,
+                                dtype=torch.bfloat16 if direct else torch.float32)
             ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
             workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
             _native.call(
@@ -269,8 +276,12 @@ class _TriangleAttentionFn(torch.autograd.Function):
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), lse.data_ptr(),
                 delta.data_ptr(), mask.data_ptr(), bias_k.data_ptr(), dq.data_ptr(),
                 dk.data_ptr(), dv.data_ptr(), dbias.data_ptr(), workspace.data_ptr(), ws_bytes,
-                B, O, H, N, D, ctx.layout, Bb, ctx.scale, stream,
+                B, O, H, N, D, layout, Bb, ctx.scale, stream,
             )
+        if direct:
+            if ctx.layout & _BIAS_TRANSPOSED:
+                dbias = dbias.transpose(-1, -2)
+            return dq, dk, dv, None, None, dbias.reshape(ctx.bias_shape), None, None, None, None
         d_bias = dbias
         if ctx.bias_reduce is not None:
             d_bias = ctx.bias_reduce(d_bias)

@@ -554,39 +554,10 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const float inv_scale = 1.f / g.scale;
   __bf16* Ss = dSs[w];
 
-  // Zero the Q / dO buffers once: chunks past D are never loaded.
-  for (int i = tid; i < 2 * 4 * 2 * QDE / 8; i += NT)
-    reinterpret_cast<bf16x8*>(&QDb[0][0][0])[i] = zero8();
   if (!plane_ok && kh == 0) {  // statistics of an idle outer row: P = 0 everywhere
     RSb[0][pw][lane] = lane < 32 ? -INFINITY : 0.f;
     RSb[1][pw][lane] = lane < 32 ? -INFINITY : 0.f;
   }
-
-  // Per-wave constant operands for this key block.
-  bf16x8 kB[2][DP / 16], vB[2][DP / 16];  // B operands of S and dP (lane = key)
-  bf16x8 kA[DP / 32][4];                  // A operand of dQ^T = K^T dS^T
-  float mk2[2];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int key = key_base + cb * 32 + kl;
-#pragma unroll
-    for (int s = 0; s < DP / 16; ++s) {
-      const int d0 = 16 * s + 8 * hl;
-      const int64_t off = plane_off + (int64_t)key * g.s_row + d0;
-      kB[cb][s] = (active && d0 < D) ? ld8(k + off) : zero8();
-      vB[cb][s] = (active && d0 < D) ? ld8(v + off) : zero8();
-      *reinterpret_cast<bf16x8*>(&Ss[(cb * 32 + kl) * KT + d0]) = kB[cb][s];
-    }
-    mk2[cb] = active ? mask[(int64_t)plane * N + key] * inv_scale : (keys_ok ? 0.f : -INFINITY);
-  }
-  const bool wmask = __any(mk2[0] != 0.f || mk2[1] != 0.f);
-  __syncthreads();
-#pragma unroll
-  for (int db = 0; db < DP / 32; ++db)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      kA[db][t] = cat8(tr_col4(Ss, KT, 16 * t, 16 * t + 8, 32 * db),
-                       tr_col4(Ss, KT, 16 * t + 4, 16 * t + 12, 32 * db));
 
   const int64_t bb = (g.bias_bstride == 0) ? 0 : b;
   const int nb32 = N / 32;
@@ -658,6 +629,49 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
       g2lds16(src, &RS[pw][0]);
     }
   };
+
+  // The first step's loads go out before the key block's setup loads, so
+  // the two latencies overlap (Q / dO chunks past D and idle rows read
+  // zeros through the buffer range check).
+  issue(0, Bfb[0], QDb[0], RSb[0]);
+
+  // Per-wave constant operands for this key block.
+  bf16x8 kB[2][DP / 16], vB[2][DP / 16];  // B operands of S and dP (lane = key)
+  bf16x8 kA[DP / 32][4];                  // A operand of dQ^T = K^T dS^T
+  float mk2[2];
+  {
+    // All loads first (branch-free, zeros outside the tensor), one wait.
+    const __amdgpu_buffer_rsrc_t rk = raw_rsrc(k + plane_off), rv = raw_rsrc(v + plane_off);
+    const __amdgpu_buffer_rsrc_t rm = raw_rsrc(mask + (int64_t)plane * N);
+    float mraw[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int key = key_base + cb * 32 + kl;
+#pragma unroll
+      for (int s = 0; s < DP / 16; ++s) {
+        const int d0 = 16 * s + 8 * hl;
+        const uint32_t off = (active && d0 < D) ? (uint32_t)(((int64_t)key * g.s_row + d0) * 2) : kBufOOB;
+        kB[cb][s] = buf_ld8(rk, off);
+        vB[cb][s] = buf_ld8(rv, off);
+      }
+      mraw[cb] = buf_ldf(rm, active ? (uint32_t)(key * 4) : kBufOOB);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int s = 0; s < DP / 16; ++s)
+        *reinterpret_cast<bf16x8*>(&Ss[(cb * 32 + kl) * KT + 16 * s + 8 * hl]) = kB[cb][s];
+      mk2[cb] = active ? mraw[cb] * inv_scale : (keys_ok ? 0.f : -INFINITY);
+    }
+  }
+  const bool wmask = __any(mk2[0] != 0.f || mk2[1] != 0.f);
+  __syncthreads();
+#pragma unroll
+  for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      kA[db][t] = cat8(tr_col4(Ss, KT, 16 * t, 16 * t + 8, 32 * db),
+                       tr_col4(Ss, KT, 16 * t + 4, 16 * t + 12, 32 * db));
 
   f32x16 dKacc[DP / 32][2], dVacc[DP / 32][2];
 #pragma unroll
@@ -835,7 +849,6 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
       }
     }
   };
-  issue(0, Bfb[0], QDb[0], RSb[0]);
 #pragma unroll 1
   for (int q0 = 0; q0 < N; q0 += 32) {
     const int cur = (q0 >> 5) & 1;
@@ -911,28 +924,50 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
     dq_fold_block(part, dq, g, nkb, blockIdx.x, ph);
 }
 
-// dBias[bb,h,q,k] (f32) = fold over the f32 (b, outer group) partials that
-// share bias batch bb (Bb == 1 folds every batch; Bb == B folds per batch).
-// Workgroup = 64 chunks of 8 consecutive outputs x 4 ranges of partials:
-// thread (range s, chunk c) sums its range in ascending order (4 partials,
-// 8 loads in flight; each load instruction of a wave reads 1 KB contiguous), and the
-// four range sums are added in the fixed order ((s0 + s1) + s2) + s3.
+// dBias[bb,h,q,k] = fold over the f32 (b, outer group) partials that share
+// bias batch bb (Bb == 1 folds every batch; Bb == B folds per batch).
+// Workgroup = 512 outputs x 4 ranges of partials: thread (range s, chunk c)
+// sums its range for 8 consecutive keys in ascending order (4 partials, 8
+// loads in flight; each load instruction of a wave reads 1 KB, or 8 x 128 B
+// for a tile), and the four range sums are added in the fixed order
+// ((s0 + s1) + s2) + s3.  Output: f32 in [Bb, H, N, N] order, or (out_bf16)
+// rounded to bf16, either in that order or (transposed) in the order of a
+// transposed bias, dbias[bb, h, k, q]: then the workgroup covers an 8-query
+// x 64-key tile and writes it transposed through LDS, 16 bytes per key.
 __device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
-                                                 float* __restrict__ dbias, int B, int Bb,
-                                                 int groups, int H, int N, int64_t blk) {
+                                                 void* __restrict__ dbias, int B, int Bb,
+                                                 int groups, int H, int N, int64_t blk,
+                                                 bool out_bf16, bool transposed) {
   __shared__ float red[4][64][9];
   const int c = threadIdx.x & 63, sl = threadIdx.x >> 6;
-  const int64_t hnn8 = (int64_t)H * N * N / 8;
-  const int64_t idx = blk * 64 + c;
-  const bool act = idx < (int64_t)Bb * hnn8;
-  const int bb = act ? (int)(idx / hnn8) : 0;
-  const int64_t e = act ? (idx % hnn8) * 8 : 0;
+  const int64_t hnn = (int64_t)H * N * N;
+  bool act;
+  int bb;
+  int64_t e;  // offset of the thread's first output in the [H, N, N] block
+  int th = 0, tq0 = 0, tk0 = 0;  // transposed tile: head, first query, first key
+  if (!transposed) {
+    const int64_t idx = blk * 64 + c;
+    act = idx < (int64_t)Bb * (hnn / 8);
+    bb = act ? (int)(idx / (hnn / 8)) : 0;
+    e = act ? (idx % (hnn / 8)) * 8 : 0;
+  } else {
+    // Tiles of 8 queries x 64 keys (N % 64 == 0): thread c -> query c / 8,
+    // keys 8 (c % 8) .. +7.
+    const int kt_n = N / 64, tiles = (N / 8) * kt_n;
+    const int64_t bh = blk / tiles;
+    const int r = (int)(blk % tiles), qt = r / kt_n, kt = r % kt_n;
+    act = bh < (int64_t)Bb * H;
+    bb = act ? (int)(bh / H) : 0;
+    th = (int)(bh % H);
+    tq0 = qt * 8;
+    tk0 = kt * 64;
+    e = act ? (int64_t)th * N * N + (int64_t)(tq0 + c / 8) * N + tk0 + (c % 8) * 8 : 0;
+  }
   const int b_lo = (Bb == 1) ? 0 : bb, b_hi = (Bb == 1) ? B : bb + 1;
   const int n = (b_hi - b_lo) * groups;
   const int per = (n + 3) / 4;
   const int s0 = sl * per, s1 = min(n, s0 + per);
-  const int64_t stride = (int64_t)H * N * N;
-  const float* src = part + (int64_t)b_lo * groups * stride + e;
+  const float* src = part + (int64_t)b_lo * groups * hnn + e;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -942,7 +977,7 @@ __device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if (s + u < s1) {
-          const float* p = src + (int64_t)(s + u) * stride;
+          const float* p = src + (int64_t)(s + u) * hnn;
           x[u][0] = ld4f_nt(p);
           x[u][1] = ld4f_nt(p + 4);
         }
@@ -960,29 +995,50 @@ __device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
 #pragma unroll
   for (int i = 0; i < 8; ++i) red[sl][c][i] = acc[i];
   __syncthreads();
-  if (sl != 0 || !act) return;
-  f32x4 lo, hi;
+  float v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float v = red[0][c][i];
+    v[i] = red[0][c][i];
     for (int r = 1; r < 4; ++r)
-      if (r * per < n) v += red[r][c][i];
-    if (i < 4) lo[i] = v; else hi[i - 4] = v;
+      if (r * per < n) v[i] += red[r][c][i];
   }
-  float* d = dbias + (int64_t)bb * H * N * N + e;
-  *reinterpret_cast<f32x4*>(d) = lo;
-  *reinterpret_cast<f32x4*>(d + 4) = hi;
+  if (!transposed) {
+    if (sl != 0 || !act) return;
+    if (out_bf16) {
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = f2bf(v[i]);
+      st8((__bf16*)dbias + (int64_t)bb * hnn + e, o);
+    } else {
+      float* d = (float*)dbias + (int64_t)bb * hnn + e;
+      *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    }
+    return;
+  }
+  // Transposed bf16 tile: T[query][key] in LDS, then thread c writes key c's
+  // 8 queries as one 16-byte chunk of dbias[bb, h, key, qt*8 .. +7].
+  __shared__ __bf16 T[8][64 + 8];
+  __syncthreads();  // every range's red reads done (sl > 0 threads read too)
+  if (sl == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) T[c / 8][(c % 8) * 8 + i] = f2bf(v[i]);
+  }
+  __syncthreads();
+  if (sl != 0 || !act) return;
+  bf16x8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = T[i][c];
+  st8((__bf16*)dbias + (int64_t)bb * hnn + (int64_t)th * N * N + (int64_t)(tk0 + c) * N + tq0, o);
 }
 
-// Both folds of the backward in one launch: blocks [0, n_db) fold dBias
-// (the longer blocks first), the rest fold dQ ((plane, head) major).
 __global__ __launch_bounds__(256) void attn_fold_kernel(
     const __bf16* __restrict__ dq_part, __bf16* __restrict__ dq, AttnGeom g, int nkb, int dq_bx,
-    const float* __restrict__ db_part, float* __restrict__ dbias, int Bb, int groups,
-    int64_t n_db) {
+    const float* __restrict__ db_part, void* __restrict__ dbias, int Bb, int groups,
+    int64_t n_db, int db_mode) {
   const int64_t b = blockIdx.x;
   if (b < n_db) {
-    dbias_fold_block(db_part, dbias, g.B, Bb, groups, g.H, g.N, b);
+    dbias_fold_block(db_part, dbias, g.B, Bb, groups, g.H, g.N, b, db_mode != 0, db_mode == 2);
   } else {
     const int64_t r = b - n_db;
     dq_fold_block(dq_part, dq, g, nkb, (int)(r % dq_bx), r / dq_bx);
@@ -1155,7 +1211,7 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
                      int layout, int64_t bias_batches, double scale, const char* fn) {
   if (B > INT32_MAX || O > INT32_MAX || N > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: dimension exceeds int32", fn);
-  if (layout & ~(TPF_QKV_SEQ_MAJOR | TPF_BIAS_TRANSPOSED))
+  if (layout & ~(TPF_QKV_SEQ_MAJOR | TPF_BIAS_TRANSPOSED | TPF_DBIAS_BF16))
     return set_error(TPF_ERR_ARG, "%s: unknown layout flags 0x%x", fn, layout);
   const bool seq_major = layout & TPF_QKV_SEQ_MAJOR;
   g->B = (int)B; g->O = (int)O; g->H = (int)H; g->N = (int)N; g->D = (int)D;
@@ -1290,9 +1346,10 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
   return check_launch(fn);
 }
 
-static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
+// db_mode: 0 = f32 dBias, 1 = bf16, 2 = bf16 in transposed-bias order.
+static int attn_backward_finish_impl(const AttnGeom& g, void* dq, void* dbias,
                                      int64_t bias_batches, const void* workspace, hipStream_t s,
-                                     const char* fn) {
+                                     const char* fn, int db_mode = 0) {
   const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
   BwdParts pt;
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
@@ -1304,7 +1361,7 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, float* dbias,
     return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
   hipLaunchKernelGGL(attn_fold_kernel, dim3((unsigned)(n_db + dq_bx * nph)), dim3(256), 0, s,
                      pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
-                     (int)bias_batches, (int)groups, n_db);
+                     (int)bias_batches, (int)groups, n_db, db_mode);
   return check_launch(fn);
 }
 
@@ -1484,7 +1541,7 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
 }
 
 // Stage 2 of the backward: fixed-order folds of the dQ and dBias partials.
-int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace, int64_t B,
+int tpf_attn_backward_finish_bf16(void* dq, void* dbias, const void* workspace, int64_t B,
                                   int64_t O, int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream) {
   const char* fn = "tpf_attn_backward_finish_bf16";
@@ -1492,13 +1549,14 @@ int tpf_attn_backward_finish_bf16(void* dq, float* dbias, const void* workspace,
   int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
   return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, (hipStream_t)stream,
-                                   fn);
+                                   fn, db_mode);
 }
 
 int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
                            const float* lse, const float* delta, const float* mask,
-                           const void* bias, void* dq, void* dk, void* dv, float* dbias,
+                           const void* bias, void* dq, void* dk, void* dv, void* dbias,
                            void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
                            int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
                            double scale, void* stream) {

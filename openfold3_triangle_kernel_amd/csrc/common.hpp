@@ -201,6 +201,20 @@ __device__ __forceinline__ void buf2lds16_so(i32x4 rsrc, uint32_t voff, uint32_t
                :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
 
+// Raw buffer resource over [base, base + 2^31 - 1) for the load/store
+// builtins; a byte offset of kBufOOB reads zeros and drops stores.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+// Branch-free 16-byte / 4-byte loads through a buffer resource (zeros at
+// kBufOOB): a run of them issues back to back and is waited on once.
+__device__ __forceinline__ bf16x8 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+
 // Division by a run-time invariant d (Granlund-Montgomery): for n < 2^31,
 // n / d = (umulhi(n, m) + n) >> s with s = ceil(log2 d),
 // m = floor(2^32 (2^s - d) / d) + 1.  Replaces 32/64-bit integer division

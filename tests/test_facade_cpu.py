@@ -93,7 +93,13 @@ class FakeBackend:
                     _arr(ptr, (B, O, N, H, D), np.uint16)[...] = _f2bf(np.swapaxes(g, 2, 3))
                 else:
                     _arr(ptr, (B, O, H, N, D), np.uint16)[...] = _f2bf(g)
-            _arr(dbias, (Bb, H, N, N), np.float32)[...] = gb[:, 0]
+            if sm & 4:  # TPF_DBIAS_BF16: bf16 in the bias's storage order
+                g = gb[:, 0].astype(np.float32)
+                if sm & 2:
+                    g = np.swapaxes(g, -1, -2)
+                _arr(dbias, (Bb, H, N, N), np.uint16)[...] = _f2bf(g)
+            else:
+                _arr(dbias, (Bb, H, N, N), np.float32)[...] = gb[:, 0]
         else:
             raise AssertionError(name)
         return 0
