@@ -144,6 +144,21 @@ int tpf_attn_backward_finish_bf16(void* dq, void* dbias, const void* workspace, 
                                   int64_t O, int64_t H, int64_t N, int64_t D, int layout,
                                   int64_t bias_batches, double scale, void* stream);
 
+/* The whole backward from the forward's outputs in three launches: delta
+ * (rowsum(f32(dout) * (f32(out) + f32(residual))), residual nullable),
+ * the row statistics and the prescaled bias in one kernel, then the
+ * reconstruction kernel and the folds.  Same results as
+ * tpf_attn_delta[_shadow]_bf16 followed by tpf_attn_backward_bf16 (the
+ * delta values never leave the workspace).  No single counterpart in the
+ * reference, whose facade launches delta_out / delta_shadow_out and
+ * sr_backward_out back to back (turbopairformer_triangle_attention.py:287-304). */
+int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, const void* dout,
+                                 const void* out, const void* residual, const float* lse,
+                                 const float* mask, const void* bias, void* dq, void* dk,
+                                 void* dv, void* dbias, void* workspace, int64_t workspace_bytes,
+                                 int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                 int layout, int64_t bias_batches, double scale, void* stream);
+
 /* FP32 forward (inference): q, k, v, bias f32 in the layouts above (layout:
  * TPF_QKV_SEQ_MAJOR only; the bias is contiguous), out f32
  * [B, O, N, H, D], lse (nullable) f32 [B, O, H, N].  Requirements: N % 64 == 0,

@@ -49,6 +49,10 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P] * 13 + [_I64] * 6 + [_I32, _I64, _F64, _P],
     ),
+    "tpf_attn_backward_fused_bf16": (
+        _I32,
+        [_P] * 14 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
     "tpf_attn_backward_main_bf16": (
         _I32,
         [_P] * 11 + [_I64] * 6 + [_I32, _I64, _F64, _P],

@@ -242,17 +242,6 @@ class _TriangleAttentionFn(torch.autograd.Function):
             d_out = d_out.to(torch.bfloat16)
         with _device_ctx(q.device):
             stream = _native.stream_of(q)
-            delta = torch.empty_like(lse)
-            if residual is None:
-                _native.call(
-                    "tpf_attn_delta_bf16", d_out.data_ptr(), out.data_ptr(), delta.data_ptr(),
-                    B, O, H, N, D, stream,
-                )
-            else:
-                _native.call(
-                    "tpf_attn_delta_shadow_bf16", d_out.data_ptr(), out.data_ptr(),
-                    residual.data_ptr(), delta.data_ptr(), B, O, H, N, D, stream,
-                )
             if ctx.seq_major:
                 dq, dk, dv = (
                     torch.empty((B, O, N, H, D), device=q.device, dtype=q.dtype).transpose(2, 3)
@@ -271,11 +260,14 @@ class _TriangleAttentionFn(torch.autograd.Function):
                                 dtype=torch.bfloat16 if direct else torch.float32)
             ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
             workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+            # delta (with the shadow residual when saved), row statistics and
+            # bias preparation in one launch, then reconstruction and folds.
             _native.call(
-                "tpf_attn_backward_bf16",
-                q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), lse.data_ptr(),
-                delta.data_ptr(), mask.data_ptr(), bias_k.data_ptr(), dq.data_ptr(),
-                dk.data_ptr(), dv.data_ptr(), dbias.data_ptr(), workspace.data_ptr(), ws_bytes,
+                "tpf_attn_backward_fused_bf16",
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), out.data_ptr(),
+                0 if residual is None else residual.data_ptr(), lse.data_ptr(),
+                mask.data_ptr(), bias_k.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                dbias.data_ptr(), workspace.data_ptr(), ws_bytes,
                 B, O, H, N, D, layout, Bb, ctx.scale, stream,
             )
         if direct:

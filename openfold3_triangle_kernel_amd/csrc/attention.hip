@@ -362,11 +362,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
 // (workgroup w takes items [w * per, (w + 1) * per), per a multiple of D/8)
 // and are added in chunk order.
 // ---------------------------------------------------------------------------
+// Row sums of one workgroup's items: returns the delta index [plane][h][q]
+// of the row the calling thread finalises, with its sum in *sum (-1 for
+// every other thread).
 template <bool SHADOW>
-__global__ __launch_bounds__(256) void attn_delta_kernel(
-    const __bf16* __restrict__ dout, const __bf16* __restrict__ out,
-    const __bf16* __restrict__ res, float* __restrict__ delta, int64_t items, int per, int H,
-    int N, int D) {
+__device__ __forceinline__ int64_t delta_row(const __bf16* __restrict__ dout,
+                                             const __bf16* __restrict__ out,
+                                             const __bf16* __restrict__ res, int64_t items,
+                                             int per, int H, int N, int D, float* sum) {
   __shared__ float part[256];
   const int tid = threadIdx.x;
   const int64_t t = (int64_t)blockIdx.x * per + tid;
@@ -387,16 +390,27 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
   part[tid] = s;
   __syncthreads();
   const int d8 = D / 8;
-  if (!act || (t % d8) != 0) return;
+  if (!act || (t % d8) != 0) return -1;
   float acc = 0.f;
   for (int u = 0; u < d8; ++u) acc += part[tid + u];
+  *sum = acc;
   // r enumerates [plane][q][h]; delta is [plane][h][q].
   const int64_t r = t / d8;
   const int hh = (int)(r % H);
   const int64_t pq = r / H;
   const int qq = (int)(pq % N);
   const int64_t plane = pq / N;
-  delta[(plane * H + hh) * N + qq] = acc;
+  return (plane * H + hh) * N + qq;
+}
+
+template <bool SHADOW>
+__global__ __launch_bounds__(256) void attn_delta_kernel(
+    const __bf16* __restrict__ dout, const __bf16* __restrict__ out,
+    const __bf16* __restrict__ res, float* __restrict__ delta, int64_t items, int per, int H,
+    int N, int D) {
+  float sum;
+  const int64_t idx = delta_row<SHADOW>(dout, out, res, items, per, H, N, D, &sum);
+  if (idx >= 0) delta[idx] = sum;
 }
 
 // ---------------------------------------------------------------------------
@@ -411,24 +425,11 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 // ---------------------------------------------------------------------------
 // One launch for both: workgroups [0, row_blocks) take rowprep items, the
 // rest take bias items (256 items per workgroup each).
-__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ lse,
-                                                            const float* __restrict__ delta,
-                                                            float* __restrict__ nl2,
-                                                            float* __restrict__ nd, int64_t rows,
-                                                            int64_t row_blocks,
-                                                            const __bf16* __restrict__ bias,
-                                                            float* __restrict__ out, int64_t items,
-                                                            int N, float inv_scale, BiasView bv) {
-  if ((int64_t)blockIdx.x < row_blocks) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows) return;
-    const float l = lse[i];
-    nl2[i] = (l == -INFINITY) ? -INFINITY : -l * kLog2e;
-    nd[i] = -delta[i];
-    return;
-  }
-  const int64_t i = ((int64_t)blockIdx.x - row_blocks) * 256 + threadIdx.x;  // (block, j, lane)
-  if (i >= items) return;
+// One bias item: 4 values of the fragment-major prescaled bias (item i =
+// (fragment block, j, lane)).
+__device__ __forceinline__ void bwd_bias_item(const __bf16* __restrict__ bias,
+                                              float* __restrict__ out, int64_t i, int N,
+                                              float inv_scale, const BiasView& bv) {
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
   const int64_t blk = i >> 8;
   const int nb = N / 32;
@@ -442,6 +443,55 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restr
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = bf2f(src[(int64_t)e * bv.s_q]) * inv_scale;
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
+}
+
+__device__ __forceinline__ float neg_lse_log2(float l) {
+  return (l == -INFINITY) ? -INFINITY : -l * kLog2e;
+}
+
+// One launch for both: workgroups [0, row_blocks) take rowprep items, the
+// rest take bias items (256 items per workgroup each).
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ lse,
+                                                            const float* __restrict__ delta,
+                                                            float* __restrict__ nl2,
+                                                            float* __restrict__ nd, int64_t rows,
+                                                            int64_t row_blocks,
+                                                            const __bf16* __restrict__ bias,
+                                                            float* __restrict__ out, int64_t items,
+                                                            int N, float inv_scale, BiasView bv) {
+  if ((int64_t)blockIdx.x < row_blocks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows) return;
+    nl2[i] = neg_lse_log2(lse[i]);
+    nd[i] = -delta[i];
+    return;
+  }
+  const int64_t i = ((int64_t)blockIdx.x - row_blocks) * 256 + threadIdx.x;
+  if (i < items) bwd_bias_item(bias, out, i, N, inv_scale, bv);
+}
+
+// Delta and the backward preparation in one launch (the fused backward
+// entry point): workgroups [0, delta_blocks) compute delta rows as
+// attn_delta_kernel does and write nd = -delta and nl2 = -lse * log2(e) for
+// them; the rest take bias items.
+template <bool SHADOW>
+__global__ __launch_bounds__(256) void attn_bwd_rows_kernel(
+    const __bf16* __restrict__ dout, const __bf16* __restrict__ out,
+    const __bf16* __restrict__ res, const float* __restrict__ lse, float* __restrict__ nl2,
+    float* __restrict__ nd, int64_t items, int per, int H, int N, int D, int64_t delta_blocks,
+    const __bf16* __restrict__ bias, float* __restrict__ bias_out, int64_t bias_items,
+    float inv_scale, BiasView bv) {
+  if ((int64_t)blockIdx.x >= delta_blocks) {
+    const int64_t i = ((int64_t)blockIdx.x - delta_blocks) * 256 + threadIdx.x;
+    if (i < bias_items) bwd_bias_item(bias, bias_out, i, N, inv_scale, bv);
+    return;
+  }
+  float sum;
+  const int64_t idx = delta_row<SHADOW>(dout, out, res, items, per, H, N, D, &sum);
+  if (idx >= 0) {
+    nd[idx] = -sum;
+    nl2[idx] = neg_lse_log2(lse[idx]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1312,11 +1362,40 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   return off;
 }
 
+// Delta, row statistics and the prescaled bias in one launch (fused
+// backward); attn_backward_main_impl then runs with rows_ready.
+static int attn_backward_rows_impl(const AttnGeom& g, const void* dout, const void* out,
+                                   const void* res, const float* lse, const void* bias,
+                                   const BiasView& bv, int64_t bias_batches, void* workspace,
+                                   hipStream_t s, const char* fn) {
+  const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
+  const int64_t items = B * O * N * H * (D / 8);
+  const int per = 256 - 256 % (int)(D / 8);
+  const int64_t delta_blocks = (items + per - 1) / per;
+  const int64_t bias_items = bias_batches * H * N * N / 4;
+  const int64_t blocks = delta_blocks + (bias_items + 255) / 256;
+  if (blocks > INT32_MAX) return set_error(TPF_ERR_SHAPE, "%s: row grid too large", fn);
+  if (res)
+    hipLaunchKernelGGL(attn_bwd_rows_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const __bf16*)dout, (const __bf16*)out, (const __bf16*)res, lse, pt.nl2,
+                       pt.nd, items, per, (int)H, (int)N, (int)D, delta_blocks,
+                       (const __bf16*)bias, pt.bias_f, bias_items, 1.f / g.scale, bv);
+  else
+    hipLaunchKernelGGL(attn_bwd_rows_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const __bf16*)dout, (const __bf16*)out, (const __bf16*)nullptr, lse,
+                       pt.nl2, pt.nd, items, per, (int)H, (int)N, (int)D, delta_blocks,
+                       (const __bf16*)bias, pt.bias_f, bias_items, 1.f / g.scale, bv);
+  return check_launch(fn);
+}
+
 static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void* k,
                                    const void* v, const void* dout, const float* lse,
                                    const float* delta, const float* mask, const void* bias,
                                    const BiasView& bv, int64_t bias_batches, void* dk, void* dv,
-                                   void* workspace, hipStream_t s, const char* fn) {
+                                   void* workspace, hipStream_t s, const char* fn,
+                                   bool rows_ready = false) {
   const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
   if ((H * bwd_key_blocks(N, D) * B * groups + 7) / 8 * 8 > INT32_MAX)
@@ -1328,11 +1407,13 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
   const int64_t row_blocks = (rows + 255) / 256;
   if (row_blocks + (items + 255) / 256 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: backward preparation grid too large", fn);
-  hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)(row_blocks + (items + 255) / 256)),
-                     dim3(256), 0, s, lse, delta, pt.nl2, pt.nd, rows, row_blocks,
-                     (const __bf16*)bias, pt.bias_f, items, (int)N, 1.f / g.scale, bv);
-  int rc = check_launch(fn);
-  if (rc) return rc;
+  if (!rows_ready) {
+    hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)(row_blocks + (items + 255) / 256)),
+                       dim3(256), 0, s, lse, delta, pt.nl2, pt.nd, rows, row_blocks,
+                       (const __bf16*)bias, pt.bias_f, items, (int)N, 1.f / g.scale, bv);
+    int rc = check_launch(fn);
+    if (rc) return rc;
+  }
   const int64_t total = H * bwd_key_blocks(N, D) * B * groups;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
@@ -1567,6 +1648,34 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
   if (rc) return rc;
   return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, layout,
                                        bias_batches, scale, stream);
+}
+
+// Whole backward from the forward's outputs: delta (with the shadow residual
+// when given), row statistics and bias preparation in one launch, then the
+// reconstruction kernel and the folds.
+int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, const void* dout,
+                                 const void* out, const void* residual, const float* lse,
+                                 const float* mask, const void* bias, void* dq, void* dk,
+                                 void* dv, void* dbias, void* workspace, int64_t workspace_bytes,
+                                 int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                 int layout, int64_t bias_batches, double scale, void* stream) {
+  const char* fn = "tpf_attn_backward_fused_bf16";
+  AttnGeom g;
+  // delta is computed in the workspace: the prepare check's delta slot gets lse.
+  int rc = attn_bwd_prepare(&g, fn, q, k, v, dout, lse, lse, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale);
+  if (rc) return rc;
+  if (!out || !dq || !dk || !dv || !dbias) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  const BiasView bv = dense_bias(H, N, bias_batches, layout);
+  hipStream_t s = (hipStream_t)stream;
+  rc = attn_backward_rows_impl(g, dout, out, residual, lse, bias, bv, bias_batches, workspace, s,
+                               fn);
+  if (rc) return rc;
+  rc = attn_backward_main_impl(g, q, k, v, dout, lse, nullptr, mask, bias, bv, bias_batches, dk,
+                               dv, workspace, s, fn, true);
+  if (rc) return rc;
+  const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
+  return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, s, fn, db_mode);
 }
 
 // ---------------------------------------------------------------------------

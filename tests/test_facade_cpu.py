@@ -39,6 +39,7 @@ class FakeBackend:
     def __init__(self):
         self.calls = []
         self.layouts = []
+        self.shadow = []
 
     def _bias(self, ptr, Bb, H, N, layout):
         b = _bf2f(_arr(ptr, (Bb, H, N, N), np.uint16))
@@ -79,9 +80,14 @@ class FakeBackend:
             if res is not None:
                 Ov = Ov + _bf2f(_arr(res, (B, O, N, H, D), np.uint16))
             _arr(delta, (B, O, H, N), np.float32)[...] = np.swapaxes((dO * Ov).sum(-1), 2, 3)
-        elif name == "tpf_attn_backward_bf16":
-            (q, k, v, do, lse, delta, mask, bias, dq, dk, dv, dbias, ws, wsb, B, O, H, N, D, sm,
-             Bb, scale, _) = a
+        elif name in ("tpf_attn_backward_bf16", "tpf_attn_backward_fused_bf16"):
+            if name == "tpf_attn_backward_bf16":
+                (q, k, v, do, lse, delta, mask, bias, dq, dk, dv, dbias, ws, wsb, B, O, H, N, D,
+                 sm, Bb, scale, _) = a
+            else:
+                (q, k, v, do, out, res, lse, mask, bias, dq, dk, dv, dbias, ws, wsb, B, O, H, N,
+                 D, sm, Bb, scale, _) = a
+                self.shadow.append(bool(res))
             Q, K, V = (self._qkv(p, B, O, H, N, D, sm & 1) for p in (q, k, v))
             M = _arr(mask, (B, O, N), np.float32).reshape(B, O, 1, 1, N)
             Bi = self._bias(bias, Bb, H, N, sm)
@@ -141,7 +147,7 @@ def test_facade_padding_and_layouts(fake, shape, seq_major):
     for g, r in zip(got, ref):
         assert g.shape == r.shape
         assert max_rel(g, r) < 1e-2
-    assert fake.calls.count("tpf_attn_backward_bf16") == 1
+    assert fake.calls.count("tpf_attn_backward_fused_bf16") == 1
 
 
 def test_facade_batch_prefix_and_broadcast_bias(fake):
@@ -246,11 +252,12 @@ def test_shadow_residual_policy_routes_entry_points(fake, monkeypatch, canonical
             monkeypatch.setenv(name, value)
     case = attention_case(1, 2, 2, 64, 16, mask_frac=0.1, seed=9)
     got = _grads(*case)
-    shadow_calls = {"tpf_attn_forward_shadow_bf16", "tpf_attn_delta_shadow_bf16"}
-    plain_calls = {"tpf_attn_forward_bf16", "tpf_attn_delta_bf16"}
     used = set(fake.calls)
-    assert (shadow_calls <= used) == expect_shadow
-    assert (plain_calls <= used) == (not expect_shadow)
+    # The forward saves the residual and the fused backward's delta pairs it
+    # with out (a non-null residual argument).
+    assert ("tpf_attn_forward_shadow_bf16" in used) == expect_shadow
+    assert ("tpf_attn_forward_bf16" in used) == (not expect_shadow)
+    assert fake.shadow == [expect_shadow]
     q, k, v, mask, bias, dout = (t.numpy() for t in case)
     ref = attention_backward(q, k, v, mask, bias, dout)
     for g, r in zip(got[1:], ref):
