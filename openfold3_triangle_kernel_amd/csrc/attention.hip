@@ -552,7 +552,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g) {
+    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g, int run) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
@@ -567,8 +567,10 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   __shared__ __attribute__((aligned(16))) float Bfb[2][2 * KH][1024];  // bias fragments [32-key block]
   __shared__ __attribute__((aligned(16))) __bf16 QDb[2][4][2 * QDE];   // [outer row] Q | dO rows
   __shared__ __attribute__((aligned(16))) float RSb[2][4][64];         // [outer row] nl2 | nd
-  constexpr int SSE = 64 * (KT > SP ? KT : SP);  // dS^T tile, or the K tile at setup
-  __shared__ __attribute__((aligned(16))) __bf16 dSs[NW][SSE];
+  // The waves' dS^T tiles [64 keys][SP]; at setup their K tiles [64 keys][KT].
+  constexpr int SSE = 64 * (KT > SP ? KT : SP);
+  __shared__ __attribute__((aligned(16))) __bf16 dSs[NW * SSE];
+  __bf16* const dSbase = dSs;
   // Key half 1's dQ^T tiles for key half 0 [outer row][d block][16 regs][lane].
   __shared__ __attribute__((aligned(16))) float Xq[KH == 2 ? 4 : 1][DP / 32][16][64];
 
@@ -578,31 +580,44 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const int N = g.N, D = g.D, H = g.H;
   const int nkb = (N + 64 * KH - 1) / (64 * KH);
   const int groups = (g.O + kBwdGroup - 1) / kBwdGroup;
-  const int64_t total = (int64_t)H * nkb * g.B * groups;
+  const int runs = (groups + run - 1) / run;
+  const int64_t total = (int64_t)H * nkb * g.B * runs;
   int64_t T;
   {
     const int64_t L = blockIdx.x, per = (total + 7) / 8;
     T = (L % 8) * per + L / 8;
     if (T >= total) return;
   }
-  // Tile order (head, outer group, key block): the nkb workgroups that share
-  // one group's Q / dO rows run back to back on one XCD (L2 reuse).
+  // Tile order (head, batch and run of outer groups, key block): the nkb
+  // workgroups that share one group's Q / dO rows run side by side on one
+  // XCD (L2 reuse).  A workgroup walks the `run` consecutive outer groups of
+  // its run and accumulates their dBias into one partial (slot brun).
   const int kblk = (int)(T % nkb);
   const int64_t hb = T / nkb;
-  const int bog = (int)(hb % ((int64_t)g.B * groups));
-  const int h = (int)(hb / ((int64_t)g.B * groups));
-  const int b = bog / groups, og = bog % groups;
+  const int brun = (int)(hb % ((int64_t)g.B * runs));
+  const int h = (int)(hb / ((int64_t)g.B * runs));
+  const int b = brun / runs;
+  const int og_lo = (brun % runs) * run, og_hi = min(groups, og_lo + run);
+  const int key_base = kblk * 64 * KH + 64 * kh;
+  // A key half past N (N % 128 == 64) runs with every key masked: P = dS = 0.
+  const bool keys_ok = key_base < N;
+  const float c2 = g.scale * kLog2e;
+  const float inv_scale = 1.f / g.scale;
+  __bf16* const Ss = dSbase + w * SSE;  // this wave's dS^T tile, and its K tile at setup
+  __bf16* const Kt = Ss;
+  float* const dbp = dbias_part + ((int64_t)brun * H + h) * N * N;
+
+#pragma unroll 1
+  for (int og = og_lo; og < og_hi; ++og) {
+  const bool first = og == og_lo;
+  // Every wave's LDS reads of the previous group are done before this
+  // group's setup writes the K tiles, statistics and first loads.
+  if (!first) __syncthreads();
   const int o = og * kBwdGroup + pw;
   const bool plane_ok = o < g.O;
   const int plane = b * g.O + (plane_ok ? o : 0);
   const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
-  const int key_base = kblk * 64 * KH + 64 * kh;
-  // A key half past N (N % 128 == 64) runs with every key masked: P = dS = 0.
-  const bool keys_ok = key_base < N;
   const bool active = plane_ok && keys_ok;
-  const float c2 = g.scale * kLog2e;
-  const float inv_scale = 1.f / g.scale;
-  __bf16* Ss = dSs[w];
 
   if (!plane_ok && kh == 0) {  // statistics of an idle outer row: P = 0 everywhere
     RSb[0][pw][lane] = lane < 32 ? -INFINITY : 0.f;
@@ -619,11 +634,19 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const int key_blk0 = kblk * 64 * KH;  // first key of the workgroup
   // Partial stores through buffer resources: per-lane offsets fixed for the
   // walk, the step's offset in a scalar.  dQ: this wave's outer row and
-  // head; dBias: the (outer group, head) N x N block.
+  // head; dBias: the (run, head) N x N block, which the first group of the
+  // run writes and the later ones read back (range 0: reads give zeros) and
+  // rewrite with their rows added.
   const __amdgpu_buffer_rsrc_t rs_dq = __builtin_amdgcn_make_buffer_rsrc(dqp, 0, 0x7FFFFFFF, 0x00020000);
   const uint32_t vdq = (uint32_t)((kl * D + 4 * hl) * 2);
-  const __amdgpu_buffer_rsrc_t rs_db = __builtin_amdgcn_make_buffer_rsrc(
-      dbias_part + ((int64_t)bog * H + h) * N * N, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_db = __builtin_amdgcn_make_buffer_rsrc(dbp, 0, 0x7FFFFFFF, 0x00020000);
+  const int dbkey = tid % (64 * KH), dbqb = tid / (64 * KH);
+  const uint32_t vdb = key_blk0 + dbkey < N ? (uint32_t)((8 * dbqb * N + key_blk0 + dbkey) * 4) : kBufOOB;
+  // The run's partial so far: read back by the thread that writes it
+  // (range 0 for the run's first group: zeros), at device scope (sc1), so
+  // the load misses the CU's L1, which may hold an older copy of the line.
+  const __amdgpu_buffer_rsrc_t rs_dbr =
+      __builtin_amdgcn_make_buffer_rsrc(dbp, 0, first ? 0 : 0x7FFFFFFF, 0x00020000);
 
   // Issue the direct-to-LDS loads of step q0 into buffer `buf`.
   typedef float BfT[2 * KH][1024];
@@ -710,7 +733,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     for (int cb = 0; cb < 2; ++cb) {
 #pragma unroll
       for (int s = 0; s < DP / 16; ++s)
-        *reinterpret_cast<bf16x8*>(&Ss[(cb * 32 + kl) * KT + 16 * s + 8 * hl]) = kB[cb][s];
+        *reinterpret_cast<bf16x8*>(&Kt[(cb * 32 + kl) * KT + 16 * s + 8 * hl]) = kB[cb][s];
       mk2[cb] = active ? mraw[cb] * inv_scale : (keys_ok ? 0.f : -INFINITY);
     }
   }
@@ -720,8 +743,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      kA[db][t] = cat8(tr_col4(Ss, KT, 16 * t, 16 * t + 8, 32 * db),
-                       tr_col4(Ss, KT, 16 * t + 4, 16 * t + 12, 32 * db));
+      kA[db][t] = cat8(tr_col4(Kt, KT, 16 * t, 16 * t + 8, 32 * db),
+                       tr_col4(Kt, KT, 16 * t + 4, 16 * t + 12, 32 * db));
 
   f32x16 dKacc[DP / 32][2], dVacc[DP / 32][2];
 #pragma unroll
@@ -734,6 +757,13 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   // step's loads, compute.  Barriers are bare s_barrier with an explicit LDS
   // counter wait, so the prefetch stays in flight across them.
   auto step = [&](int q0, BfT& Bc, QDT& QDc, RST& RSc, BfT& Bn, QDT& QDn, RST& RSn) {
+    float dbprev[8];
+    auto load_dbprev = [&] {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        dbprev[e] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(rs_dbr, vdb, (q0 + e) * N * 4, 16));
+    };
     // This step's loads were issued one step ago; wait for them, read the
     // shared bias fragments and the row statistics, then start the next
     // step's loads so they overlap this step's compute.
@@ -827,6 +857,9 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         for (int i = 0; i < 4; ++i) s4[i] = h[4 * (j & 1) + i];
         *reinterpret_cast<bf16x4*>(&Ss[(cb * 32 + kl) * SP + 8 * j + 4 * hl]) = s4;
       }
+    // The run's partial so far for this step's dBias outputs, loaded here
+    // so the dQ phase and its barrier cover the latency.
+    load_dbprev();
     // dQ^T (d x 32 queries) = K^T dS^T over this wave's 64 keys; key half 1
     // hands its tile to key half 0 through LDS (read after the barrier).
     f32x16 dqacc[DP / 32];
@@ -873,7 +906,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     // reads of each wave's row, and each store instruction of a wave writes
     // 64 consecutive keys of one query row (128 bytes).
     {
-      const int key = tid % (64 * KH), qb = tid / (64 * KH);
+      const int key = dbkey, qb = dbqb;
       const int kw = 4 * (key >> 6);  // first wave of this key's half
       // Each add is one v_dot2 with a one-hot selector: x * 1 + y * 0 + acc
       // is the f32 sum acc + x (unpack and add in one instruction).
@@ -882,7 +915,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const __bf16* src = &dSs[kw + ww][(key & 63) * SP + 8 * qb];
+        const __bf16* src = dSbase + (kw + ww) * SSE + (key & 63) * SP + 8 * qb;
         const bf16x4 lo = *reinterpret_cast<const bf16x4*>(src);
         const bf16x4 hi = *reinterpret_cast<const bf16x4*>(src + 4);
         const bf16x2 pr[4] = {{lo[0], lo[1]}, {lo[2], lo[3]}, {hi[0], hi[1]}, {hi[2], hi[3]}};
@@ -890,13 +923,11 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         for (int e = 0; e < 8; ++e)
           acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
       }
-      if (key_blk0 + key < N) {
-        const uint32_t voff = (uint32_t)((8 * qb * N + key_blk0 + key) * 4);
+      // The run's partial: earlier groups first, then this group's rows.
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[e]), rs_db, voff,
-                                                (q0 + e) * N * 4, 0);
-      }
+      for (int e = 0; e < 8; ++e)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dbprev[e] + acc[e]), rs_db, vdb,
+                                              (q0 + e) * N * 4, 0);
     }
   };
 #pragma unroll 1
@@ -904,8 +935,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const int cur = (q0 >> 5) & 1;
     step(q0, Bfb[cur], QDb[cur], RSb[cur], Bfb[cur ^ 1], QDb[cur ^ 1], RSb[cur ^ 1]);
   }
-  if (!active) return;
   // dK (scaled) and dV, in Q/K/V storage order.
+  if (active) {
 #pragma unroll
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
@@ -927,6 +958,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         }
       }
     }
+  }
+  }  // outer groups of the run
 }
 
 // dQ = bf16(scale * sum_kb partial[kb]) in ascending key-block order; bf16
@@ -1331,6 +1364,26 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   return check_launch(fn);
 }
 
+// Outer groups per backward workgroup (the run whose dBias it accumulates
+// into one partial): the largest run length that keeps the whole backward in
+// the fewest rounds of one workgroup per CU, i.e. minimises
+// ceil(workgroups / CUs) * run.  run = 1 gives one partial per group.
+static int bwd_run_len(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D) {
+  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  const int64_t per_run = H * bwd_key_blocks(N, D) * B;
+  const int64_t cus = device_cus();
+  int64_t best = 1, best_cost = INT64_MAX;
+  for (int64_t r = 1; r <= groups; ++r) {
+    const int64_t wgs = per_run * ((groups + r - 1) / r);
+    const int64_t cost = (wgs + cus - 1) / cus * r;
+    if (cost <= best_cost) { best = r; best_cost = cost; }
+  }
+  return (int)best;
+}
+static int64_t bwd_runs(int64_t O, int run) {
+  return ((O + kBwdGroup - 1) / kBwdGroup + run - 1) / run;
+}
+
 // Backward workspace: bf16 dQ partials [key blocks][B,O,H,N,D] | f32 dBias
 // partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
 // f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
@@ -1414,16 +1467,17 @@ static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void*
     int rc = check_launch(fn);
     if (rc) return rc;
   }
-  const int64_t total = H * bwd_key_blocks(N, D) * B * groups;
+  const int run = bwd_run_len(B, O, H, N, D);
+  const int64_t total = H * bwd_key_blocks(N, D) * B * bwd_runs(O, run);
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
     hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256 * bwd_kh(32)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, run);
   else
     hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256 * bwd_kh(64)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g);
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, run);
   return check_launch(fn);
 }
 
@@ -1434,7 +1488,9 @@ static int attn_backward_finish_impl(const AttnGeom& g, void* dq, void* dbias,
   const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
   BwdParts pt;
   bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+  // dBias partials per batch: one per run of outer groups (same run length
+  // as the main stage, which ran on this device).
+  const int64_t groups = bwd_runs(O, bwd_run_len(B, O, H, N, D));
   const int64_t nph = B * O * H;
   const int64_t dq_bx = (N * (D / 8) + 255) / 256;
   const int64_t n_db = (bias_batches * H * N * N / 8 + 63) / 64;
@@ -1790,7 +1846,7 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
                      dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
                      dim3(256), 0, s, pt.dq, dp, g, (int)bwd_key_blocks(N, D));
   if ((rc = check_launch(fn))) return rc;
-  const int64_t groups = (N + kBwdGroup - 1) / kBwdGroup;
+  const int64_t groups = bwd_runs(N, bwd_run_len(B, N, H, N, D));
   const dim3 db_grid((unsigned)(B * N * N / 512));
   hipLaunchKernelGGL(attn_dbias_pair_kernel, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
                      (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
