@@ -935,7 +935,11 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const int cur = (q0 >> 5) & 1;
     step(q0, Bfb[cur], QDb[cur], RSb[cur], Bfb[cur ^ 1], QDb[cur ^ 1], RSb[cur ^ 1]);
   }
-  // dK (scaled) and dV, in Q/K/V storage order.
+  // dK (scaled) and dV, in Q/K/V storage order.  A lane holds channels
+  // 8j + 4hl .. +3 (j = 0..3) of its key; one exchange with lane l ^ 32 per
+  // register pair (j, j + 1) gives it 8 consecutive channels, 16j + 8hl ..
+  // +7, so each store instruction writes 32 contiguous bytes per key (two
+  // 16-byte stores per key and tensor instead of four 8-byte ones).
   if (active) {
 #pragma unroll
   for (int db = 0; db < DP / 32; ++db)
@@ -943,18 +947,36 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     for (int cb = 0; cb < 2; ++cb) {
       const int key = key_base + cb * 32 + kl;
       const int64_t row = plane_off + (int64_t)key * g.s_row;
+      uint32_t pk[4][2], pv[4][2];  // [j][pair] packed bf16
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * hl;
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const bf16x2 a = {f2bf(dKacc[db][cb][4 * j + 2 * e] * g.scale),
+                            f2bf(dKacc[db][cb][4 * j + 2 * e + 1] * g.scale)};
+          const bf16x2 v2 = {f2bf(dVacc[db][cb][4 * j + 2 * e]), f2bf(dVacc[db][cb][4 * j + 2 * e + 1])};
+          pk[j][e] = __builtin_bit_cast(uint32_t, a);
+          pv[j][e] = __builtin_bit_cast(uint32_t, v2);
+        }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        // Lanes < 32 keep chunk 2p and receive chunk 2p of lane l + 32;
+        // lanes >= 32 receive chunk 2p + 1 of lane l - 32 and keep theirs.
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          auto rk = __builtin_amdgcn_permlane32_swap(pk[2 * p][e], pk[2 * p + 1][e], false, false);
+          pk[2 * p][e] = rk[0];
+          pk[2 * p + 1][e] = rk[1];
+          auto rv = __builtin_amdgcn_permlane32_swap(pv[2 * p][e], pv[2 * p + 1][e], false, false);
+          pv[2 * p][e] = rv[0];
+          pv[2 * p + 1][e] = rv[1];
+        }
+        const int d0 = db * 32 + 16 * p + 8 * hl;
         if (d0 < D) {
-          bf16x4 a4, b4;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            a4[i] = f2bf(dKacc[db][cb][4 * j + i] * g.scale);
-            b4[i] = f2bf(dVacc[db][cb][4 * j + i]);
-          }
-          *reinterpret_cast<bf16x4*>(dk + row + d0) = a4;
-          *reinterpret_cast<bf16x4*>(dv + row + d0) = b4;
+          const u32x4 ok = {pk[2 * p][0], pk[2 * p][1], pk[2 * p + 1][0], pk[2 * p + 1][1]};
+          const u32x4 ov = {pv[2 * p][0], pv[2 * p][1], pv[2 * p + 1][0], pv[2 * p + 1][1]};
+          *reinterpret_cast<u32x4*>(dk + row + d0) = ok;
+          *reinterpret_cast<u32x4*>(dv + row + d0) = ov;
         }
       }
     }
