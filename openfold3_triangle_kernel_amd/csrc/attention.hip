@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   // run writes and the later ones read back (range 0: reads give zeros) and
   // rewrite with their rows added.
   const __amdgpu_buffer_rsrc_t rs_dq = __builtin_amdgcn_make_buffer_rsrc(dqp, 0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t vdq = (uint32_t)((kl * D + 4 * hl) * 2);
+  const uint32_t vdq = (uint32_t)(kl * D * 2);  // query row kl of the step
   const __amdgpu_buffer_rsrc_t rs_db = __builtin_amdgcn_make_buffer_rsrc(dbp, 0, 0x7FFFFFFF, 0x00020000);
   const int dbkey = tid % (64 * KH), dbqb = tid / (64 * KH);
   const uint32_t vdb = key_blk0 + dbkey < N ? (uint32_t)((8 * dbqb * N + key_blk0 + dbkey) * 4) : kBufOOB;
@@ -888,16 +888,27 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[r] += Xq[pw][db][r][lane];
         }
+        // Lane-pair exchange as for dK / dV below: 16-byte stores of
+        // channels 16p + 8hl .. +7 (chunks past D dropped by the range check).
+        uint32_t pq[4][2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d0 = db * 32 + 8 * j + 4 * hl;
-          if (d0 < D) {
-            bf16x4 o4;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o4[i] = f2bf(acc[4 * j + i]);
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o4), rs_dq,
-                                                  vdq + (db * 32 + 8 * j) * 2, q0 * D * 2, 0);
+          for (int e = 0; e < 2; ++e)
+            pq[j][e] = __builtin_bit_cast(
+                uint32_t, bf16x2{f2bf(acc[4 * j + 2 * e]), f2bf(acc[4 * j + 2 * e + 1])});
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            auto r = __builtin_amdgcn_permlane32_swap(pq[2 * pp][e], pq[2 * pp + 1][e], false, false);
+            pq[2 * pp][e] = r[0];
+            pq[2 * pp + 1][e] = r[1];
           }
+          const int d0 = db * 32 + 16 * pp + 8 * hl;
+          const u32x4 o = {pq[2 * pp][0], pq[2 * pp][1], pq[2 * pp + 1][0], pq[2 * pp + 1][1]};
+          __builtin_amdgcn_raw_buffer_store_b128(o, rs_dq, d0 < D ? vdq + (uint32_t)d0 * 2 : kBufOOB,
+                                                 q0 * D * 2, 0);
         }
       }
     }
