@@ -132,6 +132,33 @@ def test_per_batch_bf16_bias_backward(gpu):
 
 
 @pytest.mark.gpu
+def test_runs_of_outer_groups_idle_rows_per_batch_bias(gpu):
+    """B=2, O=130, H=4, N=128 on a 256-CU device gives 264 one-group
+    workgroups, so the backward walks runs of 2 outer groups per workgroup:
+    the last run of each batch holds the ragged group (2 of 4 rows idle) alone,
+    and each batch's dBias is folded from its own runs.  Checked against the
+    oracle and for bitwise replay."""
+    print("[attn parity] runs of outer groups, O=130 ragged, per-batch bias B=2", flush=True)
+    _bias_variant(gpu, 2, 130, 4, 128, 32, (2, 1, 4, 128, 128), torch.bfloat16, seed=13)
+    from openfold3_triangle_kernel_amd import turbopairformer_triangle_attention
+
+    q, k, v, mask, _, dout = attention_case(2, 130, 4, 128, 32, mask_frac=0.15, seed=13)
+    bias = torch.randn((2, 1, 4, 128, 128), generator=torch.Generator().manual_seed(113))
+
+    def grads():
+        tq, tk, tv = (t.to(gpu, torch.bfloat16).requires_grad_(True) for t in (q, k, v))
+        tb = bias.to(gpu, torch.bfloat16).requires_grad_(True)
+        out = turbopairformer_triangle_attention(tq, tk, tv, mask.to(gpu), tb)
+        out.backward(dout.to(gpu, torch.bfloat16))
+        torch.cuda.synchronize()
+        return [t.detach().cpu() for t in (tq.grad, tk.grad, tv.grad, tb.grad)]
+
+    a, b = grads(), grads()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.gpu
 def test_partially_broadcast_bias_backward(gpu):
     """Prefix [2, 3] with a bias prefix [1, 3]: per-batch gradients summed over
     the broadcast dimension (reference dq_dbias.py:326-376)."""
