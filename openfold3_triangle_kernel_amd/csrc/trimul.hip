@@ -31,6 +31,8 @@
 //             GEMMs -> fixed-order folds.
 // 32-deep k stages: every TriMul GEMM has K = C or 5H (small).
 #define TPF_GEMM_GK 32
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "tpf_gemm.hpp"
@@ -1149,14 +1151,20 @@ __global__ __launch_bounds__(256, 2) void tm_ln_out_bwd_kernel(
 // ---------------------------------------------------------------------------
 // LN_in backward, weight-stationary: G = dproj5 W5 (K = 5H) and the LayerNorm
 // backward of LN_in, per 32-row block of natural rows, persistent workgroups
-// of C / 16 waves.  Wave w holds the W5^T rows of channels 16 w .. 16 w + 15
-// (B operands of v_mfma_f32_16x16x32_bf16) for the whole kernel; the loading
-// waves stream each block's dproj5 rows (chunks rotated by row, so A-fragment
-// reads are conflict-free), z rows and the row statistics into a 3-deep LDS
-// ring.  Accumulator register r of lane l holds G[row 4 (l / 16) + r][channel
-// 16 w + l % 16] (+ 16 per row tile); z is read back transposed to match.
-// Row sums of g = G gamma and g xhat are reduced across a wave's 16 channels
-// with a transposing butterfly and across the waves in LDS (fixed order);
+// of C / 16 waves.  Wave w = (channel group cg = w / 2 of 32 channels, k half
+// kh = w % 2) holds the W5^T rows of its 32 channels over its half of K (B
+// operands of v_mfma_f32_32x32x16_bf16) for the whole kernel, so each dproj5
+// fragment read from LDS feeds a 32 x 32 product: every block's dproj5 tile is
+// read from LDS C / 32 times instead of C / 16.  The loading waves stream each
+// block's dproj5 rows (chunks rotated by row, so fragment reads are
+// conflict-free) into a 3-deep LDS ring and its z rows and row statistics
+// into a 2-deep one.  The two k halves of a channel group meet through LDS:
+// each wave keeps the accumulator registers of 8 of its lane's 16 rows and
+// hands the other 8 to its partner, so a lane ends with G[row][channel
+// 32 cg + lane % 32] for rows 16 kh + 8 g + 4 (lane / 32) + e (g < 2, e < 4),
+// the sum (k half 0) + (k half 1).  z is read back transposed to match.  Row
+// sums of g = G gamma and g xhat are reduced across a group's 32 channels
+// with a transposing butterfly and across the groups in LDS (fixed order);
 // dz = rstd (g - mean(g) - xhat mean(g xhat)) is staged in LDS and stored as
 // full rows by the storing waves.  The d gamma / d beta column sums of each
 // lane stay in registers over all of a workgroup's blocks and are written
@@ -1170,27 +1178,37 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
     const float* __restrict__ gamma, __bf16* __restrict__ dz, float* __restrict__ lnp, TmGeom g,
     int64_t nblocks) {
   constexpr int NW = C / 16;         // waves
+  constexpr int NG = C / 32;         // channel groups
   constexpr int K = 5 * C;           // contraction depth
   constexpr int KC = K / 8;          // 16-byte chunks per dproj5 row
+  constexpr int KH = KC / 2;         // chunks per k half
+  constexpr int KT = K / 32;         // 16-deep MFMA steps per k half
   constexpr int CPR = C / 8;         // 16-byte chunks per z row
-  constexpr int KS = K / 32;         // 32-deep k steps
   constexpr int SP = C + 8;          // dz staging pitch (bf16)
   constexpr int PI = 32 * KC / 64 / (NW / 2);  // dproj5 load instructions per loading wave
+  constexpr int XB = NG * 2 * 8 * 64 * 4;      // k-half exchange [cg][kh][register][lane] f32
+  constexpr int OB = 32 * SP * 2;              // dz staging tile
   __shared__ __attribute__((aligned(1024))) __bf16 Ps[kLnInDepth][32 * K];
-  __shared__ __attribute__((aligned(1024))) __bf16 Zs[kLnInDepth][32 * C];
-  __shared__ __attribute__((aligned(256))) float Ss[kLnInDepth][2][64];  // mean | rstd
-  __shared__ __attribute__((aligned(16))) float Rs[2][NW][32];           // row sums [q][wave][row]
-  __shared__ __attribute__((aligned(16))) __bf16 So[32 * SP];
+  __shared__ __attribute__((aligned(1024))) __bf16 Zs[2][32 * C];
+  __shared__ __attribute__((aligned(256))) float Ss[2][2][64];           // mean | rstd
+  __shared__ __attribute__((aligned(16))) float Rs[2][NG][32];           // row sums [q][group][row]
+  // The exchange is read before the block's row-sum barrier and the staging
+  // tile written after it, so the two share memory.
+  __shared__ __attribute__((aligned(16))) char XO[XB > OB ? XB : OB];
+  float* const X = reinterpret_cast<float*>(XO);
+  __bf16* const So = reinterpret_cast<__bf16*>(XO);
   static_assert(PI * 64 * (NW / 2) == 32 * KC, "dproj5 loads split evenly");
+  static_assert(KC % 2 == 0 && KH % 2 == 0, "k halves of whole MFMA steps");
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int ch = 16 * w + l16;
+  const int l16 = lane & 15, l32 = lane & 31, hl = lane >> 5, q = lane >> 4;
+  const int cg = w >> 1, kh = w & 1;
+  const int ch = 32 * cg + l32;
   const bool loader = w < NW / 2;
 
-  bf16x8 wf[KS];
+  bf16x8 wf[KT];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) wf[ks] = ld8(w5t + (int64_t)ch * K + 8 * (4 * ks + lg));
+  for (int t = 0; t < KT; ++t) wf[t] = ld8(w5t + (int64_t)ch * K + 8 * (kh * KH + 2 * t + hl));
   const float gam = gamma[ch];
 
   const i32x4 rs_p = buffer_rsrc(dproj5);
@@ -1201,110 +1219,146 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
   const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
   const int64_t bbeg = blockIdx.x * per;
   const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
-  // Loads per block: PI dproj5 + 2 z instructions per loading wave, and the
-  // two statistics rows by wave 0.
-  auto issue = [&](int64_t blk) {
-    const int stage = (int)(blk % kLnInDepth);
-#pragma unroll
-    for (int j = 0; j < PI; ++j) {
-      const int ci = (PI * w + j) * 64 + lane;
-      const int r = ci / KC, slot = ci % KC;
-      const int gc = (slot - r % KC + KC) % KC;
-      const uint32_t m = (uint32_t)blk * 32 + r;
-      const bool ok = blk < bend && m < (uint32_t)g.R;
-      buf2lds16(rs_p, ok ? (m * K + 8 * gc) * 2 : kBufOOB, &Ps[stage][(PI * w + j) * 512]);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+  // Loads per block and loading wave: 2 z instructions and, by wave 0, the
+  // two statistics rows (load j < 2, block blk, into the 2-deep ring), then PI
+  // dproj5 instructions (load j >= 2, into the 3-deep ring).
+  auto load = [&](int j, int64_t blk) {
+    if (j < 2) {
+      const int stage = (int)(blk & 1);
       const int ci = (2 * w + j) * 64 + lane;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
       const uint32_t m = (uint32_t)blk * 32 + r;
       const bool ok = blk < bend && m < (uint32_t)g.R;
       buf2lds16(rs_z, ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Zs[stage][(2 * w + j) * 512]);
-    }
-    if (w == 0) {
-      const uint32_t m = (uint32_t)blk * 32 + lane;
-      const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
-      buf2lds4(rs_mu, ok ? m * 4 : kBufOOB, &Ss[stage][0][0]);
-      buf2lds4(rs_rs, ok ? m * 4 : kBufOOB, &Ss[stage][1][0]);
+      if (j == 1 && w == 0) {
+        const uint32_t mr = (uint32_t)blk * 32 + lane;
+        const bool okr = lane < 32 && blk < bend && mr < (uint32_t)g.R;
+        buf2lds4(rs_mu, okr ? mr * 4 : kBufOOB, &Ss[stage][0][0]);
+        buf2lds4(rs_rs, okr ? mr * 4 : kBufOOB, &Ss[stage][1][0]);
+      }
+    } else {
+      const int stage = (int)(blk % kLnInDepth);
+      const int ci = (PI * w + j - 2) * 64 + lane;
+      const int r = ci / KC, slot = ci % KC;
+      const int gc = (slot - r % KC + KC) % KC;
+      const uint32_t m = (uint32_t)blk * 32 + r;
+      const bool ok = blk < bend && m < (uint32_t)g.R;
+      buf2lds16(rs_p, ok ? (m * K + 8 * gc) * 2 : kBufOOB, &Ps[stage][(PI * w + j - 2) * 512]);
     }
   };
-  float cg = 0.f, cgx = 0.f;  // this lane's channel: sum G, sum G xhat over its rows
+  constexpr int NL = PI + 2;
+  float cgs = 0.f, cgx = 0.f;  // this lane's channel: sum G, sum G xhat over its rows
   if (loader) {
-    issue(bbeg);
-    issue(bbeg + 1);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) load(j, bbeg);
+#pragma unroll
+    for (int j = 2; j < NL; ++j) load(j, bbeg + 1);
   }
 #pragma unroll 1
   for (int64_t blk = bbeg; blk < bend; ++blk) {
-    const int stage = (int)(blk % kLnInDepth);
-    if (loader) {  // block blk landed (block blk + 1 may be in flight)
-      if (w == 0) wait_vmcnt<PI + 4>(); else wait_vmcnt<PI + 2>();
-    }
+    const int sp = (int)(blk % kLnInDepth), sz = (int)(blk & 1);
+    // Issued since block blk's loads: at most block blk + 1's dproj5 (the
+    // last PI loads of the previous iteration).
+    if (loader) wait_vmcnt<PI>();
     __syncthreads();
-    if (loader) issue(blk + 2);
-    // G for rows 16 rt + 4 lg + r, channel ch.
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    const __bf16* P = Ps[stage];
+    // This k half's partial G: rows 8 (r / 4) + 4 hl + r % 4, channel ch.
+    // The loading waves spread the next blocks' loads (z of blk + 1, then
+    // dproj5 of blk + 2) over the MFMA chain, whose stalls hide their issue.
+    f32x16 acc = zero16();
+    const __bf16* P = Ps[sp];
+    auto chain = [&](auto with_loads) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+      for (int t = 0; t < KT; ++t) {
+        const int gc = kh * KH + 2 * t + hl;
+        const bf16x8 pf = *reinterpret_cast<const bf16x8*>(&P[l32 * K + 8 * ((gc + l32) % KC)]);
+        acc = mfma32(pf, wf[t], acc);
+        if constexpr (decltype(with_loads)::value) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const int row = 16 * rt + l16;
-        const bf16x8 pf =
-            *reinterpret_cast<const bf16x8*>(&P[row * K + 8 * ((4 * ks + lg + row) % KC)]);
-        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, wf[ks], acc[rt], 0, 0, 0);
+          for (int j = 0; j < NL; ++j)
+            if (j * KT / NL == t) load(j, j < 2 ? blk + 1 : blk + 2);
+        }
       }
-    // x for the same (row, channel) pairs: lane L of a 16-lane group reads
-    // row 16 rt + 4 lg + L / 4, channels 16 w + 4 (L % 4) .. + 3 (rotated chunk).
-    float xh[2][4], gv[2][4], a[8], b[8];
+    };
+    if (loader) chain(std::true_type{});
+    else chain(std::false_type{});
+    // Registers 8 kh .. 8 kh + 7 stay (rows 16 kh + 8 g + 4 hl + e), the
+    // other eight go to the partner wave.
+    float G[8];
+    {
+      float* xs = X + (cg * 2 + kh) * 8 * 64 + lane;
+      if (kh == 0) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int rr = 16 * rt + 4 * lg + (l16 >> 2);
-      const int cc = 16 * w + 4 * (l16 & 3);
-      const __bf16* src = &Zs[stage][rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)];
+        for (int j = 0; j < 8; ++j) xs[j * 64] = acc[8 + j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[j * 64] = acc[j];
+      }
+      __syncthreads();
+      const float* xr = X + (cg * 2 + (kh ^ 1)) * 8 * 64 + lane;
+      if (kh == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G[j] = acc[j] + xr[j * 64];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G[j] = xr[j * 64] + acc[8 + j];
+      }
+    }
+    // x for the same (row, channel) pairs: lane L of a 16-lane group reads
+    // row r0 + L / 4, channels 32 cg + 16 (q % 2) + 4 (L % 4) .. + 3 (rotated chunk).
+    float xh[8], gv[8], a[8], b[8];
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int r0 = 16 * kh + 8 * gg + 4 * hl;
+      const int rr = r0 + (l16 >> 2);
+      const int cc = 32 * cg + 16 * (q & 1) + 4 * (l16 & 3);
+      const __bf16* src = &Zs[sz][rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)];
       const bf16x4 xv = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)src);
-      const f32x4 mu = *reinterpret_cast<const f32x4*>(&Ss[stage][0][16 * rt + 4 * lg]);
-      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][16 * rt + 4 * lg]);
+      const f32x4 mu = *reinterpret_cast<const f32x4*>(&Ss[sz][0][r0]);
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[sz][1][r0]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        xh[rt][e] = (bf2f(xv[e]) - mu[e]) * rsd[e];
-        const float G = acc[rt][e];
-        gv[rt][e] = G * gam;
-        a[4 * rt + e] = gv[rt][e];
-        b[4 * rt + e] = gv[rt][e] * xh[rt][e];
-        cg += G;
-        cgx = fmaf(G, xh[rt][e], cgx);
+        const int i = 4 * gg + e;
+        xh[i] = (bf2f(xv[e]) - mu[e]) * rsd[e];
+        gv[i] = G[i] * gam;
+        a[i] = gv[i];
+        b[i] = gv[i] * xh[i];
+        cgs += G[i];
+        cgx = fmaf(G[i], xh[i], cgx);
       }
     }
-    // Row sums over the 16 channels of this wave: lane ends with row
-    // t = l16 & 7 of its lane group, summed over the 16 lanes.
+    // Row sums over the 32 channels of this group: lanes with l16 = t < 8
+    // end with value t (row 16 kh + 8 (t / 4) + 4 hl + t % 4), summed over
+    // the 16 lanes of their group and the 16 of the neighbouring group.
     tm_butterfly<4>(a, b, lane);
     tm_butterfly<2>(a, b, lane);
     tm_butterfly<1>(a, b, lane);
     a[0] += __shfl_xor(a[0], 8);
     b[0] += __shfl_xor(b[0], 8);
-    if (l16 < 8) {
-      const int t = l16, row = 16 * (t >> 2) + 4 * lg + (t & 3);
-      Rs[0][w][row] = a[0];
-      Rs[1][w][row] = b[0];
+    a[0] += __shfl_xor(a[0], 16);
+    b[0] += __shfl_xor(b[0], 16);
+    if ((lane & 24) == 0) {
+      const int t = l16, row = 16 * kh + 8 * (t >> 2) + 4 * hl + (t & 3);
+      Rs[0][cg][row] = a[0];
+      Rs[1][cg][row] = b[0];
     }
     __syncthreads();
     const float invC = 1.f / C;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int r0 = 16 * rt + 4 * lg;
-      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][r0]);
+    for (int gg = 0; gg < 2; ++gg) {
+      const int r0 = 16 * kh + 8 * gg + 4 * hl;
+      const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[sz][1][r0]);
       f32x4 sg = *reinterpret_cast<const f32x4*>(&Rs[0][0][r0]);
       f32x4 sx = *reinterpret_cast<const f32x4*>(&Rs[1][0][r0]);
 #pragma unroll
-      for (int v = 1; v < NW; ++v) {
+      for (int v = 1; v < NG; ++v) {
         sg += *reinterpret_cast<const f32x4*>(&Rs[0][v][r0]);
         sx += *reinterpret_cast<const f32x4*>(&Rs[1][v][r0]);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float o = rsd[e] * (gv[rt][e] - sg[e] * invC - xh[rt][e] * (sx[e] * invC));
+        const int i = 4 * gg + e;
+        const float o = rsd[e] * (gv[i] - sg[e] * invC - xh[i] * (sx[e] * invC));
         So[(r0 + e) * SP + ch] = f2bf(o);
       }
     }
@@ -1315,12 +1369,12 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
       bf16x8 v[2];
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
-        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        const int qq = st + 2 * C * it, row = qq / CPR, k = qq % CPR;
         v[it] = *reinterpret_cast<const bf16x8*>(&So[row * SP + 8 * k]);
       }
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
-        const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
+        const int qq = st + 2 * C * it, row = qq / CPR, k = qq % CPR;
         const uint32_t m = (uint32_t)blk * 32 + row;
         const uint32_t off = m < (uint32_t)g.R ? (m * C + 8 * k) * 2 : kBufOOB;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o, off, 0, 0);
@@ -1330,14 +1384,19 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
   // The ring loads issued past the last block still write LDS: let them land
   // before the workgroup releases its LDS.
   if (loader) wait_vmcnt<0>();
-  // Column sums: the 4 lane groups of each channel, then one lane writes.
-  cg += __shfl_xor(cg, 16);
-  cgx += __shfl_xor(cgx, 16);
-  cg += __shfl_xor(cg, 32);
+  // Column sums: the two row halves of a lane's channel (lanes l, l ^ 32),
+  // then the two k-half waves of the group through LDS, k half 0 first.
+  cgs += __shfl_xor(cgs, 32);
   cgx += __shfl_xor(cgx, 32);
-  if (lg == 0) {
-    lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx;
-    lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cg;
+  __syncthreads();
+  if (kh == 1 && hl == 0) {
+    Rs[0][cg][l32] = cgx;
+    Rs[1][cg][l32] = cgs;
+  }
+  __syncthreads();
+  if (kh == 0 && hl == 0) {
+    lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx + Rs[0][cg][l32];
+    lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cgs + Rs[1][cg][l32];
   }
 }
 
