@@ -69,6 +69,64 @@ __device__ __forceinline__ float xor32_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Exchange with lane l ^ 16 through v_permlane16_swap (rows of 16 lanes
+// swapped pairwise), summed in the order (even row) + (odd row) on both rows.
+__device__ __forceinline__ float xor16_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Cross-lane moves on the VALU (DPP), no LDS round trip.  Controls used:
+// quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane ^ 7 within 8-lane blocks), row_ror:8 (lane ^ 8
+// within rows of 16).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppXor8 = 0x128;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of L lanes (L a power of two <= 64); every lane
+// of a group ends with the same bits (each level adds a lane pair's values,
+// a + b on one lane and b + a on the other).
+template <int L>
+__device__ __forceinline__ float lanes_sum(float x) {
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "lane group");
+  if constexpr (L >= 2) x += dpp_f<kDppXor1>(x);
+  if constexpr (L >= 4) x += dpp_f<kDppXor2>(x);
+  if constexpr (L >= 8) x += dpp_f<kDppHalfMirror>(x);
+  if constexpr (L >= 16) x += dpp_f<kDppXor8>(x);
+  if constexpr (L >= 32) x = xor16_sum(x);
+  if constexpr (L >= 64) x = xor32_sum(x);
+  return x;
+}
+__device__ __forceinline__ float row16_sum(float x) { return lanes_sum<16>(x); }
+
+// Partner value for one level of a transposing butterfly over lanes: a lane
+// whose level bit H differs and whose bits above H agree (exact xor for
+// H = 1, 2, 8, 16, 32; for H = 4 the mirror lane ^ 7 of its 8-lane block).
+template <int H>
+__device__ __forceinline__ float butterfly_partner(float x, int lane) {
+  if constexpr (H == 1) {
+    return dpp_f<kDppXor1>(x);
+  } else if constexpr (H == 2) {
+    return dpp_f<kDppXor2>(x);
+  } else if constexpr (H == 4) {
+    return dpp_f<kDppHalfMirror>(x);
+  } else if constexpr (H == 8) {
+    return dpp_f<kDppXor8>(x);
+  } else if constexpr (H == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(H == 32, "butterfly level");
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((lane & 32) ? r[0] : r[1]);
+  }
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Logistic function with the hardware reciprocal (v_rcp_f32, 1 ulp): the

@@ -93,8 +93,7 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
   for (int k = 0; k < K; ++k)
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += v[k][e];
-#pragma unroll
-  for (int m = 1; m < L; m <<= 1) s += __shfl_xor(s, m);
+  s = lanes_sum<L>(s);
   const float inv_c = 1.f / (float)C;
   const float mean = s * inv_c;
   float q = 0.f;
@@ -107,8 +106,7 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
       q = fmaf(d, d, q);
     }
   }
-#pragma unroll
-  for (int m = 1; m < L; m <<= 1) q += __shfl_xor(q, m);
+  q = lanes_sum<L>(q);
   const float rstd = rsqrtf(q * inv_c + eps);
   if (!row_ok) return;
 #pragma unroll
@@ -210,11 +208,8 @@ __global__ __launch_bounds__(256) void ln_bwd_bf16_kernel(
           dbet[k][e] += d;
         }
       }
-#pragma unroll
-      for (int m = 1; m < L; m <<= 1) {
-        s1 += __shfl_xor(s1, m);
-        s2 += __shfl_xor(s2, m);
-      }
+      s1 = lanes_sum<L>(s1);
+      s2 = lanes_sum<L>(s2);
       const float m1 = s1 * inv_c, m2 = s2 * inv_c;
       __bf16* dxr = dx + ln_row_offset(gdx, (uint32_t)rows[u]);
 #pragma unroll

@@ -202,8 +202,7 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += x[k][e];
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
+    s = row16_sum(s);
     const float mean = s * (1.f / C);
     float v2 = 0.f;
 #pragma unroll
@@ -211,8 +210,7 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
       const float d = act ? x[k][e] - mean : 0.f;
       v2 = fmaf(d, d, v2);
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
+    v2 = row16_sum(v2);
     const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
     if (act) {
       bf16x8 o;
@@ -277,8 +275,7 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
   auto channel_sum = [&](float (&q)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      q[e] += __shfl_xor(q[e], 16);
-      q[e] += __shfl_xor(q[e], 32);
+      q[e] = xor32_sum(xor16_sum(q[e]));
     }
     if ((tid & 48) == 0) {
 #pragma unroll
@@ -1021,8 +1018,8 @@ __device__ __forceinline__ void tm_butterfly(float* a, float* b, int lane) {
   for (int k = 0; k < HALF; ++k) {
     const float sa = up ? a[k] : a[k + HALF];
     const float sb = up ? b[k] : b[k + HALF];
-    const float ra = __shfl_xor(sa, HALF);
-    const float rb = __shfl_xor(sb, HALF);
+    const float ra = butterfly_partner<HALF>(sa, lane);
+    const float rb = butterfly_partner<HALF>(sb, lane);
     a[k] = (up ? a[k + HALF] : a[k]) + ra;
     b[k] = (up ? b[k + HALF] : b[k]) + rb;
   }
@@ -1333,10 +1330,8 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
     tm_butterfly<4>(a, b, lane);
     tm_butterfly<2>(a, b, lane);
     tm_butterfly<1>(a, b, lane);
-    a[0] += __shfl_xor(a[0], 8);
-    b[0] += __shfl_xor(b[0], 8);
-    a[0] += __shfl_xor(a[0], 16);
-    b[0] += __shfl_xor(b[0], 16);
+    a[0] = xor16_sum(a[0] + dpp_f<kDppXor8>(a[0]));
+    b[0] = xor16_sum(b[0] + dpp_f<kDppXor8>(b[0]));
     if ((lane & 24) == 0) {
       const int t = l16, row = 16 * kh + 8 * (t >> 2) + 4 * hl + (t & 3);
       Rs[0][cg][row] = a[0];
@@ -1386,8 +1381,8 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
   if (loader) wait_vmcnt<0>();
   // Column sums: the two row halves of a lane's channel (lanes l, l ^ 32),
   // then the two k-half waves of the group through LDS, k half 0 first.
-  cgs += __shfl_xor(cgs, 32);
-  cgx += __shfl_xor(cgx, 32);
+  cgs = xor32_sum(cgs);
+  cgx = xor32_sum(cgx);
   __syncthreads();
   if (kh == 1 && hl == 0) {
     Rs[0][cg][l32] = cgx;
@@ -1573,8 +1568,8 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     tm_butterfly<4>(a, b, lane);
     tm_butterfly<2>(a, b, lane);
     tm_butterfly<1>(a, b, lane);
-    a[0] += __shfl_xor(a[0], 8);
-    b[0] += __shfl_xor(b[0], 8);
+    a[0] += dpp_f<kDppXor8>(a[0]);
+    b[0] += dpp_f<kDppXor8>(b[0]);
     if (l16 < 8) {
       const int t = l16, row = 16 * (t >> 2) + 4 * lg + (t & 3);
       Rs[0][w][row] = a[0];
@@ -1631,10 +1626,8 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
   // The ring loads issued past the last block still write LDS: let them land
   // before the workgroup releases its LDS.
   if (loader) wait_vmcnt<0>();
-  cg += __shfl_xor(cg, 16);
-  cgx += __shfl_xor(cgx, 16);
-  cg += __shfl_xor(cg, 32);
-  cgx += __shfl_xor(cgx, 32);
+  cg = xor32_sum(xor16_sum(cg));
+  cgx = xor32_sum(xor16_sum(cgx));
   if (lg == 0) {
     lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx;
     lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cg;
