@@ -99,16 +99,14 @@ __global__ __launch_bounds__(256) void tm32_ln_rows_kernel(const float* __restri
   const float* xr = x + row * ld_in;
   float s = 0.f;
   for (int c = lane; c < C; c += 64) s += xr[c];
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s += __shfl_xor(s, m);
+  s = lanes_sum<64>(s);
   const float mean = s / C;
   float v2 = 0.f;
   for (int c = lane; c < C; c += 64) {
     const float d = xr[c] - mean;
     v2 = fmaf(d, d, v2);
   }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v2 += __shfl_xor(v2, m);
+  v2 = lanes_sum<64>(v2);
   const float rstd = 1.f / sqrtf(v2 / C + eps);
   float* yr = y + row * ld_out;
   for (int c = lane; c < ld_out; c += 64) {
@@ -150,16 +148,14 @@ __global__ __launch_bounds__(256) void tm32_ln_planes_kernel(const float* __rest
     const int pp = tid >> 3, part = tid & 7;
     float s = 0.f;
     for (int c = part; c < g.H; c += 8) s += Xs[c * XP + pp];
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) s += __shfl_xor(s, m);
+    s = lanes_sum<8>(s);
     const float mean = s / g.H;
     float v2 = 0.f;
     for (int c = part; c < g.H; c += 8) {
       const float d = Xs[c * XP + pp] - mean;
       v2 = fmaf(d, d, v2);
     }
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) v2 += __shfl_xor(v2, m);
+    v2 = lanes_sum<8>(v2);
     if (part == 0) {
       mu_s[pp] = mean;
       rs_s[pp] = 1.f / sqrtf(v2 / g.H + eps);
@@ -204,8 +200,7 @@ __global__ __launch_bounds__(256) void tm32_ln_rows_vec_kernel(const float* __re
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
+  s = lanes_sum<16>(s);
   const float mean = s / C;
   float v2 = 0.f;
 #pragma unroll
@@ -217,8 +212,7 @@ __global__ __launch_bounds__(256) void tm32_ln_rows_vec_kernel(const float* __re
       v2 = fmaf(d, d, v2);
     }
   }
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) v2 += __shfl_xor(v2, m);
+  v2 = lanes_sum<16>(v2);
   const float rstd = 1.f / sqrtf(v2 / C + eps);
   if (!ok) return;
 #pragma unroll
@@ -265,16 +259,14 @@ __global__ __launch_bounds__(256) void tm32_ln_planes_vec_kernel(const float* __
     const int pp = tid >> 2, part = tid & 3;
     float s = 0.f;
     for (int c = part; c < g.H; c += 4) s += Xs[c * XP + pp];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s = lanes_sum<4>(s);
     const float mean = s / g.H;
     float v2 = 0.f;
     for (int c = part; c < g.H; c += 4) {
       const float d = Xs[c * XP + pp] - mean;
       v2 = fmaf(d, d, v2);
     }
-    v2 += __shfl_xor(v2, 1);
-    v2 += __shfl_xor(v2, 2);
+    v2 = lanes_sum<4>(v2);
     if (part == 0) {
       mu_s[pp] = mean;
       rs_s[pp] = 1.f / sqrtf(v2 / g.H + eps);
@@ -352,8 +344,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
           a = fmaf(d, d, a);
         }
       }
-      a += __shfl_xor(a, 16);
-      a += __shfl_xor(a, 32);
+      a = xor32_sum(xor16_sum(a));
       q[e] = a;
     }
     if ((tid & 48) == 0) {
