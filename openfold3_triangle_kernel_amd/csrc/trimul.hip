@@ -1025,6 +1025,29 @@ __device__ __forceinline__ void tm_butterfly(float* a, float* b, int lane) {
   }
 }
 
+// Row totals of per-wave partial sums P [2][NWV][32] (quantity, wave, row)
+// in LDS, for the four rows r0 .. r0 + 3 that all 16 lanes of a lane group
+// share: lane 8 q + v of the group reads wave v's partials of quantity q
+// (zeros for v >= NWV), the 8 lanes of a quantity are summed on DPP and the
+// two quantities swapped across the group's halves.  s0 / s1 are the totals
+// of quantity 0 / 1 (the same bits on every lane).
+template <int NWV>
+__device__ __forceinline__ void wave_row_sums(const float* P, int r0, int lane, f32x4& s0,
+                                              f32x4& s1) {
+  static_assert(NWV >= 1 && NWV <= 8, "waves per lane group");
+  const int v = lane & 7, q = (lane >> 3) & 1;
+  f32x4 r = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (v < NWV) r = *reinterpret_cast<const f32x4*>(&P[(q * NWV + v) * 32 + r0]);
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = lanes_sum<8>(r[e]);
+    o[e] = dpp_f<kDppXor8>(r[e]);
+  }
+  s0 = q ? o : r;
+  s1 = q ? r : o;
+}
+
 __global__ __launch_bounds__(256, 2) void tm_ln_out_bwd_kernel(
     const __bf16* __restrict__ a_op, int64_t a_ld, const __bf16* __restrict__ w_op, int K,
     const __bf16* __restrict__ xsrc, const float* __restrict__ mean, const float* __restrict__ rstd,
@@ -1343,13 +1366,8 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
     for (int gg = 0; gg < 2; ++gg) {
       const int r0 = 16 * kh + 8 * gg + 4 * hl;
       const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[sz][1][r0]);
-      f32x4 sg = *reinterpret_cast<const f32x4*>(&Rs[0][0][r0]);
-      f32x4 sx = *reinterpret_cast<const f32x4*>(&Rs[1][0][r0]);
-#pragma unroll
-      for (int v = 1; v < NG; ++v) {
-        sg += *reinterpret_cast<const f32x4*>(&Rs[0][v][r0]);
-        sx += *reinterpret_cast<const f32x4*>(&Rs[1][v][r0]);
-      }
+      f32x4 sg, sx;
+      wave_row_sums<NG>(&Rs[0][0][0], r0, lane, sg, sx);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 4 * gg + e;
@@ -1581,13 +1599,8 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     for (int rt = 0; rt < 2; ++rt) {
       const int r0 = 16 * rt + 4 * lg;
       const f32x4 rsd = *reinterpret_cast<const f32x4*>(&Ss[stage][1][r0]);
-      f32x4 sg = *reinterpret_cast<const f32x4*>(&Rs[0][0][r0]);
-      f32x4 sx = *reinterpret_cast<const f32x4*>(&Rs[1][0][r0]);
-#pragma unroll
-      for (int v = 1; v < NW; ++v) {
-        sg += *reinterpret_cast<const f32x4*>(&Rs[0][v][r0]);
-        sx += *reinterpret_cast<const f32x4*>(&Rs[1][v][r0]);
-      }
+      f32x4 sg, sx;
+      wave_row_sums<NW>(&Rs[0][0][0], r0, lane, sg, sx);
       bf16x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
