@@ -1419,12 +1419,14 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
 //   y = xln Wz^T (recomputed), s = s(gl):  dy = dout s,  d gl = dout y s (1 - s);
 //   G = dy Wz, then the LN_out backward of x (planes) into dx (planes).
 // Wave w owns channels 16 w .. 16 w + 15 of both products: its rows of Wz
-// (B operand of the first) and of Wz^T (B operand of the second) stay in
-// registers.  Accumulator register r of lane l holds row 4 (l / 16) + r
-// (+ 16 per row tile), channel 16 w + l % 16.  The loading waves stream each
-// block's xln, gl and dout rows (chunk-rotated) and x plane segments
-// ([channel][32 positions]) and the LN_out statistics into a 3-deep LDS ring;
-// gl and dout are read back transposed to match the accumulators.  dy (the
+// (A operand of the first, which forms y^T) and of Wz^T (B operand of the
+// second) stay in registers.  In the first product register r of lane l
+// holds row l % 16, channel 16 w + 4 (l / 16) + r, so gl and dout are read
+// and dy / d gl written as 4-channel runs; in the second, row 4 (l / 16) + r,
+// channel 16 w + l % 16 (+ 16 rows per row tile).  The loading waves stream
+// each block's xln, gl and dout rows (chunk-rotated) and x plane segments
+// ([channel][32 positions]) and the LN_out statistics into a 3-deep LDS
+// ring.  dy (the
 // second product's A operand), d gl and dx are staged in LDS and stored by
 // the storing waves: dy rows, d gl into the last block of dproj5, dx plane
 // segments.  Row sums of the LayerNorm backward are reduced across each
@@ -1507,15 +1509,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
       buf2lds4(rs_rs, ok ? m * 4 : kBufOOB, &Ss[stage][1][0]);
     }
   };
-  // Rows 16 rt + 4 lg + e, channel ch of a chunk-rotated [32][C] tile: lane
-  // L of a 16-lane group reads row 16 rt + 4 lg + L / 4, channels
-  // 16 w + 4 (L % 4) .. + 3 (transposing read).
-  auto col4 = [&](const __bf16* T, int rt) {
-    const int rr = 16 * rt + 4 * lg + (l16 >> 2);
-    const int cc = 16 * w + 4 * (l16 & 3);
-    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (lds_bf16x4*)&T[rr * C + 8 * (((cc >> 3) + rr) % CPR) + (cc & 7)]);
-  };
+
   float cg = 0.f, cgx = 0.f;
   if (loader) {
     issue(bbeg);
@@ -1529,7 +1523,9 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     }
     __syncthreads();
     if (loader) issue(blk + 2);
-    // y = xln Wz^T for rows 16 rt + 4 lg + r, channel ch.
+    // y^T = Wz xln^T (the weight rows as the A operand): register e of lane
+    // l holds y[row 16 rt + l16][channel 16 w + 4 lg + e], so gl and dout are
+    // plain 8-byte reads of the row tiles and dy / d gl 8-byte writes.
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
     const __bf16* Xl = Rg[stage][0];
 #pragma unroll
@@ -1539,20 +1535,24 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
         const int row = 16 * rt + l16;
         const bf16x8 af =
             *reinterpret_cast<const bf16x8*>(&Xl[row * C + 8 * ((4 * ks + lg + row) % CPR)]);
-        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf[ks], acc[rt], 0, 0, 0);
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ks], af, acc[rt], 0, 0, 0);
       }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const bf16x4 gv4 = col4(Rg[stage][1], rt);
-      const bf16x4 go4 = col4(Rg[stage][2], rt);
+      const int row = 16 * rt + l16, cc = 16 * w + 4 * lg;
+      const int off = row * C + 8 * (((cc >> 3) + row) % CPR) + (cc & 7);
+      const bf16x4 gv4 = *reinterpret_cast<const bf16x4*>(&Rg[stage][1][off]);
+      const bf16x4 go4 = *reinterpret_cast<const bf16x4*>(&Rg[stage][2][off]);
+      bf16x4 vy, vg;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int row = 16 * rt + 4 * lg + e;
         const float sg = sigmoidf(bf2f(gv4[e]));
         const float go = bf2f(go4[e]);
-        Dy[row * RP + ch] = f2bf(go * sg);
-        Dg[row * RP + ch] = f2bf(go * acc[rt][e] * sg * (1.f - sg));
+        vy[e] = f2bf(go * sg);
+        vg[e] = f2bf(go * acc[rt][e] * sg * (1.f - sg));
       }
+      *reinterpret_cast<bf16x4*>(&Dy[row * RP + cc]) = vy;
+      *reinterpret_cast<bf16x4*>(&Dg[row * RP + cc]) = vg;
     }
     __syncthreads();
     // G = dy Wz, then the LayerNorm backward (channel ch of LN_out).
