@@ -48,6 +48,19 @@ struct BiasView {
   int H;
 };
 
+// Output item of thread item i of a fragment-major bias pass (items per
+// (batch, head) block: per_bh).  With the heads adjacent in memory (the
+// projection rows' bias columns, s_h = 1) the heads are the fastest thread
+// index, so the lanes of one pair row read its one sector together instead
+// of H workgroups fetching it apart; a wave then still writes 256-byte runs
+// of each head's block.
+__device__ __forceinline__ int64_t bias_item_order(int64_t i, int64_t per_bh, const BiasView& bv) {
+  if (bv.s_h != 1 || bv.H == 1) return i;
+  const int64_t h = i % bv.H, r = i / bv.H;
+  const int64_t bb = r / per_bh;
+  return (bb * bv.H + h) * per_bh + (r - bb * per_bh);
+}
+
 __device__ __forceinline__ const __bf16* bias_at(const __bf16* bias, const BiasView& bv,
                                                  int64_t bh, int64_t q, int64_t k) {
   const int64_t bb = bh / bv.H, h = bh - bb * bv.H;
@@ -87,8 +100,9 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
                                                                  float* __restrict__ out,
                                                                  int64_t items, int N,
                                                                  float inv_scale, BiasView bv) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (block, j, lane)
-  if (i >= items) return;
+  const int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (it >= items) return;
+  const int64_t i = bias_item_order(it, (int64_t)(N / 32) * (N / 32) * 256, bv);  // (block, j, lane)
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
   const int64_t blk = i >> 8;
   const int nkb = N / 32;
@@ -428,8 +442,9 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(
 // One bias item: 4 values of the fragment-major prescaled bias (item i =
 // (fragment block, j, lane)).
 __device__ __forceinline__ void bwd_bias_item(const __bf16* __restrict__ bias,
-                                              float* __restrict__ out, int64_t i, int N,
+                                              float* __restrict__ out, int64_t it, int N,
                                               float inv_scale, const BiasView& bv) {
+  const int64_t i = bias_item_order(it, (int64_t)(N / 32) * (N / 32) * 256, bv);
   const int lane = (int)(i & 63), j = (int)((i >> 6) & 3);
   const int64_t blk = i >> 8;
   const int nb = N / 32;
