@@ -1193,11 +1193,12 @@ __global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __rest
                                                             const __bf16* __restrict__ gate,
                                                             int64_t pitch,
                                                             __bf16* __restrict__ og,
-                                                            int64_t items, int hc8) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, chunk)
-  if (t >= items) return;
-  const int64_t row = t / hc8;
-  const int c = (int)(t - row * hc8);
+                                                            int64_t items, FastDiv hc8) {
+  // items < 2^31 (checked on the host): 32-bit index math.
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;  // (row, chunk)
+  if (t >= (uint32_t)items) return;
+  const uint32_t row = fdiv(t, hc8);
+  const int c = (int)(t - row * hc8.d);
   const bf16x8 ov = ld8(o + t * 8), gv = ld8(gate + row * pitch + c * 8);
   bf16x8 r;
 #pragma unroll
@@ -1212,17 +1213,18 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     const __bf16* __restrict__ d_og, const __bf16* __restrict__ o,
     const __bf16* __restrict__ res, const __bf16* __restrict__ gate, int64_t pitch,
     __bf16* __restrict__ d_o,
-    float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, int N, int H,
-    int D) {
+    float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, FastDiv fN,
+    int H, int D, FastDiv fhc8) {
+  // items < 2^31 (checked on the host): 32-bit index math.
   __shared__ float part[256];
   const int tid = threadIdx.x;
-  const int64_t t = (int64_t)blockIdx.x * per + tid;  // (row, chunk)
-  const int hc8 = H * D / 8, d8 = D / 8;
-  const bool act = tid < per && t < items;
+  const uint32_t t = blockIdx.x * (uint32_t)per + tid;  // (row, chunk)
+  const int d8 = D / 8;
+  const bool act = tid < per && t < (uint32_t)items;
+  const uint32_t row = fdiv(t, fhc8);
+  const int c = (int)(t - row * fhc8.d);
   float sdot = 0.f;
   if (act) {
-    const int64_t row = t / hc8;
-    const int c = (int)(t - row * hc8);
     const bf16x8 dv = ld8(d_og + t * 8), ov = ld8(o + t * 8),
                  gv = ld8(gate + row * pitch + c * 8);
     bf16x8 rv;
@@ -1244,16 +1246,14 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
   part[tid] = sdot;
   __syncthreads();
   if (!act) return;
-  const int64_t row = t / hc8;
-  const int c = (int)(t - row * hc8);
   if (c % d8 != 0) return;
   float s = 0.f;
   for (int u = 0; u < d8; ++u) s += part[tid + u];
   // row = (b, i, j): plane (b, i), query j; delta is [plane][h][j].
   const int h = c / d8;
-  const int64_t plane = row / N;
-  const int j = (int)(row - plane * N);
-  delta[(plane * H + h) * N + j] = s;
+  const uint32_t plane = fdiv(row, fN);
+  const int j = (int)(row - plane * fN.d);
+  delta[((int64_t)plane * H + h) * fN.d + j] = s;
 }
 
 // Pair-bias gradient into the projection gradient rows.  Workgroup = 512
@@ -1836,8 +1836,11 @@ int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mas
                               residual, workspace, s, fn)))
     return rc;
   const int64_t items = B * N * N * (hc / 8);
+  if (items >= (int64_t)kBufOOB - 256)
+    return set_error(TPF_ERR_SHAPE, "%s: %lld gate chunks exceed 2^31", fn, (long long)items);
   hipLaunchKernelGGL(attn_gate_fwd_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
-                     (const __bf16*)o, p + 3 * hc, pitch, (__bf16*)og, items, (int)(hc / 8));
+                     (const __bf16*)o, p + 3 * hc, pitch, (__bf16*)og, items,
+                     make_fastdiv((uint32_t)(hc / 8)));
   return check_launch(fn);
 }
 
@@ -1873,16 +1876,19 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   __bf16* dp = (__bf16*)dproj;
   hipStream_t s = (hipStream_t)stream;
   const int64_t items = B * N * N * (hc / 8);
+  if (items >= (int64_t)kBufOOB - 256)
+    return set_error(TPF_ERR_SHAPE, "%s: %lld gate chunks exceed 2^31", fn, (long long)items);
   const int per = 256 - 256 % (int)(D / 8);
   const dim3 ggrid((unsigned)((items + per - 1) / per));
+  const FastDiv fN = make_fastdiv((uint32_t)N), fhc8 = make_fastdiv((uint32_t)(hc / 8));
   if (residual)
     hipLaunchKernelGGL(attn_gate_bwd_kernel<true>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)residual, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
+                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8);
   else
     hipLaunchKernelGGL(attn_gate_bwd_kernel<false>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)nullptr, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, (int)N, (int)H, (int)D);
+                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8);
   if ((rc = check_launch(fn))) return rc;
   if ((rc = attn_backward_main_impl(g, p, p + hc, p + 2 * hc, d_o, lse, delta, mask, p + 4 * hc,
                                     bv, B, dp + hc, dp + 2 * hc, workspace, s, fn)))
