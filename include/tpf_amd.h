@@ -109,15 +109,37 @@ int tpf_attn_delta_shadow_bf16(const void* dout, const void* out, const void* re
                                float* delta, int64_t B, int64_t O, int64_t H, int64_t N,
                                int64_t D, void* stream);
 
-/* Bytes of device workspace tpf_attn_backward_bf16 needs (dQ and dBias partials). */
+/* Bytes of device workspace of the one-slab backward plan (dQ partials of
+ * every outer row, one f32 dBias partial per run of outer groups, the
+ * prescaled bias and the row statistics).  tpf_attn_backward_main_bf16 /
+ * _finish_bf16 need this much. */
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
                                           int64_t D);
+
+/* Workspace bytes of the backward plan under a budget: the full plan when it
+ * fits, otherwise slabs of consecutive runs of outer rows whose dQ partials
+ * fit (each slab's dQ folded before the next reuses the space; dBias partials
+ * stay resident, so every summation order, and every result bit, is that of
+ * the full plan).  Below the one-run minimum the minimum is returned (it
+ * exceeds the budget), as the reference's planner returns its irreducible
+ * tile.  tpf_attn_backward_bf16 and tpf_attn_backward_fused_bf16 accept any
+ * workspace of at least the minimum and plan their slabs from its size.
+ * Replaces workspace_plan / sr_workspace_plan
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dq_dbias.py:149-300,569-669),
+ * whose 256 MiB budget bounds its dBias leaves. */
+int64_t tpf_attn_backward_workspace_bytes_budget(int64_t B, int64_t O, int64_t H, int64_t N,
+                                                 int64_t D, int64_t budget_bytes);
+/* Slabs the backward runs in for a workspace of workspace_bytes (0 when it
+ * is below the minimum; -1 for non-positive sizes). */
+int tpf_attn_backward_slab_count(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                 int64_t workspace_bytes);
 
 /* Single-reconstruction backward: dq, dk, dv (bf16, same storage order as
  * q) and dbias (f32 [bias_batches, H, N, N], summed over every (b, o) that
  * shares the bias; with TPF_DBIAS_BF16 the same sums rounded to bf16 and
- * stored in the bias's order), all reduced in fixed orders (bitwise
- * reproducible).
+ * stored in the bias's order), all reduced in fixed orders that depend on
+ * the problem shape only (not on the device's CU count or the workspace
+ * size): bitwise reproducible on any gfx950 device and for any budget.
  * Replaces turbopairformer_triangle_sr_backward_out
  * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dq_dbias.cu:2526-2648)
  * together with its planner (turbopairformer_triangle_dq_dbias.py:466-566)

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
     "tpf_attn_delta_bf16": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "tpf_attn_delta_shadow_bf16": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "tpf_attn_backward_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "tpf_attn_backward_workspace_bytes_budget": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "tpf_attn_backward_slab_count": (_I32, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "tpf_attn_backward_bf16": (
         _I32,
         [_P] * 13 + [_I64] * 6 + [_I32, _I64, _F64, _P],

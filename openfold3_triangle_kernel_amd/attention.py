@@ -189,6 +189,41 @@ def _storage_order(t: torch.Tensor) -> str | None:
     return None
 
 
+# Workspace budget of the backward (bytes).  The reference plans its SR
+# backward under a budget too (turbopairformer_triangle_dq_dbias.py:35,
+# 150-300); here the budget bounds the dQ partials, the only part of the
+# workspace that grows with O * N^2 * H * D / 64: when the full plan exceeds
+# it, the reconstruction kernel runs over slabs of outer rows, each slab's dQ
+# partials folded before the next slab reuses the space.  Results are
+# bitwise equal for every budget.  The default keeps config-5 sized problems
+# (N = 768, H = 8, D = 64: a 7.9 GB full plan) within 4 GiB.
+DEFAULT_SR_WORKSPACE_BUDGET_BYTES = 4 << 30
+_SR_WORKSPACE_BUDGET = DEFAULT_SR_WORKSPACE_BUDGET_BYTES
+
+
+def set_sr_workspace_budget(budget_bytes: int | None) -> None:
+    """Set the backward workspace budget in bytes (None restores the default)."""
+    global _SR_WORKSPACE_BUDGET
+    if budget_bytes is None:
+        _SR_WORKSPACE_BUDGET = DEFAULT_SR_WORKSPACE_BUDGET_BYTES
+        return
+    budget_bytes = int(budget_bytes)
+    if budget_bytes <= 0:
+        raise ValueError("workspace_budget_bytes must be positive")
+    _SR_WORKSPACE_BUDGET = budget_bytes
+
+
+def sr_workspace_plan(B: int, O: int, H: int, N: int, D: int,
+                      budget_bytes: int | None = None) -> tuple[int, int]:
+    """(workspace bytes, slabs) of the backward plan for a kernel-shaped problem
+    (N a multiple of 64, D a multiple of 8).  Below the one-run minimum the
+    minimum is returned, as the reference's planner does for its irreducible tile."""
+    budget = _SR_WORKSPACE_BUDGET if budget_bytes is None else int(budget_bytes)
+    ws = int(_native.query("tpf_attn_backward_workspace_bytes_budget", B, O, H, N, D, budget))
+    slabs = int(_native.query("tpf_attn_backward_slab_count", B, O, H, N, D, ws))
+    return ws, slabs
+
+
 class _TriangleAttentionFn(torch.autograd.Function):
     """Owns the kernels' saved state (reference ``:223-320``).
 
@@ -258,7 +293,7 @@ class _TriangleAttentionFn(torch.autograd.Function):
             layout = ctx.layout | (_DBIAS_BF16 if direct else 0)
             dbias = torch.empty((Bb, H, N, N), device=q.device,
                                 dtype=torch.bfloat16 if direct else torch.float32)
-            ws_bytes = int(_native.query("tpf_attn_backward_workspace_bytes", B, O, H, N, D))
+            ws_bytes = sr_workspace_plan(B, O, H, N, D)[0]
             workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
             # delta (with the shadow residual when saved), row statistics and
             # bias preparation in one launch, then reconstruction and folds.

@@ -24,6 +24,7 @@
 //   mask   [B, O, N] f32 additive.    bias [Bb, H, N, N] bf16, Bb in {1, B}.
 //   out    [B, O, N, H, D] bf16.      lse / delta [B, O, H, N] f32.
 // N must be a multiple of 64 (the host pads) and D a multiple of 8, D <= 64.
+#include <algorithm>
 #include <mutex>
 
 #include "common.hpp"
@@ -532,6 +533,13 @@ __global__ __launch_bounds__(256) void attn_bwd_rows_kernel(
 // ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
+// A slab of the backward: the flattened runs [brun0, brun0 + nbrun) of
+// outer groups (run index b * runs + r) and the planes they cover, whose dQ
+// partials [key block][planes][H][N][D] sit in the workspace at once.
+struct BwdSlab {
+  int brun0, nbrun;
+  int64_t plane0, planes;
+};
 // Key halves per backward workgroup (keys per workgroup = 64 * KH).
 __host__ __device__ constexpr int bwd_kh(int dp) { return dp == 32 ? 2 : 1; }
 // Backward key blocks (= dQ partials) for head dimension D.
@@ -567,7 +575,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const float* __restrict__ nl2_g, const float* __restrict__ nd_g,
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
-    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g, int run) {
+    __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g, int run,
+    BwdSlab sl) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
@@ -596,7 +605,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const int nkb = (N + 64 * KH - 1) / (64 * KH);
   const int groups = (g.O + kBwdGroup - 1) / kBwdGroup;
   const int runs = (groups + run - 1) / run;
-  const int64_t total = (int64_t)H * nkb * g.B * runs;
+  const int64_t total = (int64_t)H * nkb * sl.nbrun;
   int64_t T;
   {
     const int64_t L = blockIdx.x, per = (total + 7) / 8;
@@ -609,8 +618,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   // its run and accumulates their dBias into one partial (slot brun).
   const int kblk = (int)(T % nkb);
   const int64_t hb = T / nkb;
-  const int brun = (int)(hb % ((int64_t)g.B * runs));
-  const int h = (int)(hb / ((int64_t)g.B * runs));
+  const int brun = sl.brun0 + (int)(hb % sl.nbrun);
+  const int h = (int)(hb / sl.nbrun);
   const int b = brun / runs;
   const int og_lo = (brun % runs) * run, og_hi = min(groups, og_lo + run);
   const int key_base = kblk * 64 * KH + 64 * kh;
@@ -645,7 +654,9 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   const float* bfrag = bias_f + ((bb * H + h) * nb32 + kblk * 2 * KH) * (int64_t)nb32 * 1024;
   const int64_t do_plane = (int64_t)plane * N * H * D + (int64_t)h * D;  // dO is [B,O,N,H,D]
   const int64_t st_plane = ((int64_t)plane * H + h) * N;                // row statistics
-  __bf16* dqp = dq_part + ((int64_t)kblk * g.B * g.O + plane) * H * N * D + (int64_t)h * N * D;
+  // dQ partials of the slab's planes [key block][plane - plane0][h][q][D].
+  __bf16* dqp = dq_part + ((int64_t)kblk * sl.planes + (plane_ok ? plane - sl.plane0 : 0)) * H * N * D +
+                (int64_t)h * N * D;
   const int key_blk0 = kblk * 64 * KH;  // first key of the workgroup
   // Partial stores through buffer resources: per-lane offsets fixed for the
   // walk, the step's offset in a scalar.  dQ: this wave's outer row and
@@ -1016,15 +1027,15 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
 // ph.  Up to 8 partial loads are in flight; they are added in key-block order.
 __device__ __forceinline__ void dq_fold_block(const __bf16* __restrict__ part,
                                               __bf16* __restrict__ dq, const AttnGeom& g, int nkb,
-                                              int bx, int64_t ph) {
+                                              int bx, int64_t ph, int64_t plane0, int64_t planes) {
   const int D8 = g.D / 8;
   const int t = bx * 256 + threadIdx.x;
   if (t >= g.N * D8) return;
   const int qq = t / D8, d0 = (t - qq * D8) * 8;
-  const int64_t nph = (int64_t)g.B * g.O * g.H;
-  const int64_t stride = nph * g.N * g.D;
-  const int64_t plane = ph / g.H;
-  const int hh = (int)(ph - plane * g.H);
+  const int64_t stride = planes * g.H * g.N * g.D;
+  const int64_t lp = ph / g.H;  // plane within the slab
+  const int hh = (int)(ph - lp * g.H);
+  const int64_t plane = plane0 + lp;
   const __bf16* src = part + (ph * g.N + qq) * g.D + d0;
   float acc[8];
 #pragma unroll
@@ -1052,7 +1063,7 @@ __global__ __launch_bounds__(256) void attn_dq_reduce_kernel(
     const __bf16* __restrict__ part, __bf16* __restrict__ dq, AttnGeom g, int nkb) {
   const int64_t nph = (int64_t)g.B * g.O * g.H;
   for (int64_t ph = blockIdx.y; ph < nph; ph += gridDim.y)
-    dq_fold_block(part, dq, g, nkb, blockIdx.x, ph);
+    dq_fold_block(part, dq, g, nkb, blockIdx.x, ph, 0, (int64_t)g.B * g.O);
 }
 
 // dBias[bb,h,q,k] = fold over the f32 (b, outer group) partials that share
@@ -1166,13 +1177,13 @@ __device__ __forceinline__ void dbias_fold_block(const float* __restrict__ part,
 __global__ __launch_bounds__(256) void attn_fold_kernel(
     const __bf16* __restrict__ dq_part, __bf16* __restrict__ dq, AttnGeom g, int nkb, int dq_bx,
     const float* __restrict__ db_part, void* __restrict__ dbias, int Bb, int groups,
-    int64_t n_db, int db_mode) {
+    int64_t n_db, int db_mode, int64_t plane0, int64_t planes) {
   const int64_t b = blockIdx.x;
   if (b < n_db) {
     dbias_fold_block(db_part, dbias, g.B, Bb, groups, g.H, g.N, b, db_mode != 0, db_mode == 2);
   } else {
     const int64_t r = b - n_db;
-    dq_fold_block(dq_part, dq, g, nkb, (int)(r % dq_bx), r / dq_bx);
+    dq_fold_block(dq_part, dq, g, nkb, (int)(r % dq_bx), r / dq_bx, plane0, planes);
   }
 }
 
@@ -1194,16 +1205,17 @@ __global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __rest
                                                             int64_t pitch,
                                                             __bf16* __restrict__ og,
                                                             int64_t items, FastDiv hc8) {
-  // items < 2^31 (checked on the host): 32-bit index math.
+  // items < 2^31 (checked on the host): 32-bit item index; element offsets
+  // (8 per item) are formed in 64 bits.
   const uint32_t t = blockIdx.x * 256u + threadIdx.x;  // (row, chunk)
   if (t >= (uint32_t)items) return;
   const uint32_t row = fdiv(t, hc8);
   const int c = (int)(t - row * hc8.d);
-  const bf16x8 ov = ld8(o + t * 8), gv = ld8(gate + row * pitch + c * 8);
+  const bf16x8 ov = ld8(o + (size_t)t * 8), gv = ld8(gate + (size_t)row * pitch + c * 8);
   bf16x8 r;
 #pragma unroll
   for (int e = 0; e < 8; ++e) r[e] = f2bf(bf2f(ov[e]) * gate_sigmoid(bf2f(gv[e])));
-  st8(og + t * 8, r);
+  st8(og + (size_t)t * 8, r);
 }
 
 // Workgroup w takes items [w * per, (w + 1) * per) with per a multiple of
@@ -1215,7 +1227,8 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     __bf16* __restrict__ d_o,
     float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, FastDiv fN,
     int H, int D, FastDiv fhc8) {
-  // items < 2^31 (checked on the host): 32-bit index math.
+  // items < 2^31 (checked on the host): 32-bit item index; element offsets
+  // (8 per item) are formed in 64 bits.
   __shared__ float part[256];
   const int tid = threadIdx.x;
   const uint32_t t = blockIdx.x * (uint32_t)per + tid;  // (row, chunk)
@@ -1225,10 +1238,10 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
   const int c = (int)(t - row * fhc8.d);
   float sdot = 0.f;
   if (act) {
-    const bf16x8 dv = ld8(d_og + t * 8), ov = ld8(o + t * 8),
-                 gv = ld8(gate + row * pitch + c * 8);
+    const bf16x8 dv = ld8(d_og + (size_t)t * 8), ov = ld8(o + (size_t)t * 8),
+                 gv = ld8(gate + (size_t)row * pitch + c * 8);
     bf16x8 rv;
-    if (SHADOW) rv = ld8(res + t * 8);
+    if (SHADOW) rv = ld8(res + (size_t)t * 8);
     bf16x8 r_do, r_dg;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1240,8 +1253,8 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
       // SHADOW, with O + its rounding residual, summed in f32).
       sdot = fmaf(bf2f(r_do[e]), SHADOW ? oo + bf2f(rv[e]) : oo, sdot);
     }
-    st8(d_o + t * 8, r_do);
-    st8(dgate + row * pitch + c * 8, r_dg);
+    st8(d_o + (size_t)t * 8, r_do);
+    st8(dgate + (size_t)row * pitch + c * 8, r_dg);
   }
   part[tid] = sdot;
   __syncthreads();
@@ -1415,15 +1428,18 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
 // Outer groups per backward workgroup (the run whose dBias it accumulates
 // into one partial): the largest run length that keeps the whole backward in
 // the fewest rounds of one workgroup per CU, i.e. minimises
-// ceil(workgroups / CUs) * run.  run = 1 gives one partial per group.
+// ceil(workgroups / CUs) * run.  run = 1 gives one partial per group.  The
+// run length fixes the dBias summation order, so it is chosen for a fixed
+// 256-CU device (MI355X) from the problem shape alone: the same inputs give
+// the same bits on every device.
+constexpr int64_t kBwdPlanCus = 256;
 static int bwd_run_len(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D) {
   const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
   const int64_t per_run = H * bwd_key_blocks(N, D) * B;
-  const int64_t cus = device_cus();
   int64_t best = 1, best_cost = INT64_MAX;
   for (int64_t r = 1; r <= groups; ++r) {
     const int64_t wgs = per_run * ((groups + r - 1) / r);
-    const int64_t cost = (wgs + cus - 1) / cus * r;
+    const int64_t cost = (wgs + kBwdPlanCus - 1) / kBwdPlanCus * r;
     if (cost <= best_cost) { best = r; best_cost = cost; }
   }
   return (int)best;
@@ -1432,9 +1448,10 @@ static int64_t bwd_runs(int64_t O, int run) {
   return ((O + kBwdGroup - 1) / kBwdGroup + run - 1) / run;
 }
 
-// Backward workspace: bf16 dQ partials [key blocks][B,O,H,N,D] | f32 dBias
-// partials [B*ceil(O/4)][H,N,N] | f32 fragment-major bias [<=B][H,N,N] |
-// f32 row statistics nl2, nd [B,O,H,N]; each region 256-byte aligned.
+// Backward workspace: bf16 dQ partials [key blocks][slab planes][H,N,D] |
+// f32 dBias partials [B * runs][H,N,N] (one per run of outer groups) | f32
+// fragment-major bias [<=B][H,N,N] | f32 row statistics nl2, nd [B,O,H,N];
+// each region 256-byte aligned.  Only the dQ partials depend on the slab.
 struct BwdParts {
   __bf16* dq;
   float* db;
@@ -1445,14 +1462,14 @@ struct BwdParts {
 
 static int64_t a256(int64_t v) { return (v + 255) / 256 * 256; }
 
-static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D, char* base,
-                          BwdParts* parts) {
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
+static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                          int64_t slab_planes, char* base, BwdParts* parts) {
+  const int64_t runs = bwd_runs(O, bwd_run_len(B, O, H, N, D));
   const int64_t rows = B * O * H * N;
   int64_t off = 0;
   auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
-  char* dq = take(bwd_key_blocks(N, D) * rows * D * 2);
-  char* db = take(B * groups * H * N * N * 4);
+  char* dq = take(bwd_key_blocks(N, D) * slab_planes * H * N * D * 2);
+  char* db = take(B * runs * H * N * N * 4);
   char* bf = take(B * H * N * N * 4);
   char* nl = take(rows * 4);
   char* nd = take(rows * 4);
@@ -1462,16 +1479,73 @@ static int64_t bwd_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
   }
   return off;
 }
+static int64_t bwd_full_bytes(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D) {
+  return bwd_layout(B, O, H, N, D, B * O, nullptr, nullptr);
+}
+
+// Slab plan for a workspace of `bytes`: every slab holds `per` consecutive
+// flattened runs (the last one fewer), sized evenly so the slabs' grids
+// are alike.  One slab when the full plan fits; per = 0 when not even one
+// run's dQ partials fit.  Slabs change where the dQ partials live, not any
+// summation order: results are bitwise equal to the one-slab plan.
+struct BwdPlan {
+  int run;       // outer groups per run
+  int runs;      // runs per batch
+  int per;       // flattened runs per slab
+  int slabs;
+};
+static int64_t bwd_slab_planes(int64_t B, int64_t O, int per_runs, int run) {
+  // Upper bound of the planes of any `per_runs` consecutive runs.
+  return std::min<int64_t>(B * O, (int64_t)per_runs * run * kBwdGroup);
+}
+static BwdPlan bwd_plan(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D, int64_t bytes) {
+  BwdPlan p;
+  p.run = bwd_run_len(B, O, H, N, D);
+  p.runs = (int)bwd_runs(O, p.run);
+  const int fr = (int)(B * p.runs);
+  if (bytes >= bwd_full_bytes(B, O, H, N, D)) {
+    p.per = fr;
+    p.slabs = 1;
+    return p;
+  }
+  int lo = 0, hi = fr;  // largest per whose layout fits
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (bwd_layout(B, O, H, N, D, bwd_slab_planes(B, O, mid, p.run), nullptr, nullptr) <= bytes)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  if (lo == 0) { p.per = 0; p.slabs = 0; return p; }
+  p.slabs = (fr + lo - 1) / lo;
+  p.per = (fr + p.slabs - 1) / p.slabs;
+  return p;
+}
+// Slab s of a plan: its flattened runs and the contiguous planes they cover.
+static BwdSlab bwd_slab(const BwdPlan& p, int64_t B, int64_t O, int s) {
+  BwdSlab sl;
+  const int fr = (int)(B * p.runs);
+  sl.brun0 = s * p.per;
+  sl.nbrun = std::min(fr, sl.brun0 + p.per) - sl.brun0;
+  auto plane_of = [&](int frun) {  // first plane of flattened run frun (frun <= fr)
+    if (frun >= fr) return B * O;
+    const int64_t b = frun / p.runs, r = frun % p.runs;
+    return b * O + std::min<int64_t>(O, r * p.run * kBwdGroup);
+  };
+  sl.plane0 = plane_of(sl.brun0);
+  sl.planes = plane_of(sl.brun0 + sl.nbrun) - sl.plane0;
+  return sl;
+}
 
 // Delta, row statistics and the prescaled bias in one launch (fused
 // backward); attn_backward_main_impl then runs with rows_ready.
 static int attn_backward_rows_impl(const AttnGeom& g, const void* dout, const void* out,
                                    const void* res, const float* lse, const void* bias,
                                    const BiasView& bv, int64_t bias_batches, void* workspace,
-                                   hipStream_t s, const char* fn) {
+                                   int64_t slab_planes, hipStream_t s, const char* fn) {
   const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
   BwdParts pt;
-  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
+  bwd_layout(B, O, H, N, D, slab_planes, (char*)workspace, &pt);
   const int64_t items = B * O * N * H * (D / 8);
   const int per = 256 - 256 % (int)(D / 8);
   const int64_t delta_blocks = (items + per - 1) / per;
@@ -1491,62 +1565,61 @@ static int attn_backward_rows_impl(const AttnGeom& g, const void* dout, const vo
   return check_launch(fn);
 }
 
-static int attn_backward_main_impl(const AttnGeom& g, const void* q, const void* k,
-                                   const void* v, const void* dout, const float* lse,
-                                   const float* delta, const float* mask, const void* bias,
-                                   const BiasView& bv, int64_t bias_batches, void* dk, void* dv,
-                                   void* workspace, hipStream_t s, const char* fn,
-                                   bool rows_ready = false) {
-  const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
-  const int64_t groups = (O + kBwdGroup - 1) / kBwdGroup;
-  if ((H * bwd_key_blocks(N, D) * B * groups + 7) / 8 * 8 > INT32_MAX)
-    return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
-  BwdParts pt;
-  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
-  const int64_t rows = B * O * H * N;
-  const int64_t items = bias_batches * H * N * N / 4;
+// Row statistics and the prescaled bias from lse and delta (when the rows
+// kernel has not run).
+static int attn_backward_prep_impl(const AttnGeom& g, const float* lse, const float* delta,
+                                   const void* bias, const BiasView& bv, int64_t bias_batches,
+                                   const BwdParts& pt, hipStream_t s, const char* fn) {
+  const int64_t rows = (int64_t)g.B * g.O * g.H * g.N;
+  const int64_t items = bias_batches * g.H * (int64_t)g.N * g.N / 4;
   const int64_t row_blocks = (rows + 255) / 256;
   if (row_blocks + (items + 255) / 256 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: backward preparation grid too large", fn);
-  if (!rows_ready) {
-    hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)(row_blocks + (items + 255) / 256)),
-                       dim3(256), 0, s, lse, delta, pt.nl2, pt.nd, rows, row_blocks,
-                       (const __bf16*)bias, pt.bias_f, items, (int)N, 1.f / g.scale, bv);
-    int rc = check_launch(fn);
-    if (rc) return rc;
-  }
-  const int run = bwd_run_len(B, O, H, N, D);
-  const int64_t total = H * bwd_key_blocks(N, D) * B * bwd_runs(O, run);
+  hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)(row_blocks + (items + 255) / 256)),
+                     dim3(256), 0, s, lse, delta, pt.nl2, pt.nd, rows, row_blocks,
+                     (const __bf16*)bias, pt.bias_f, items, (int)g.N, 1.f / g.scale, bv);
+  return check_launch(fn);
+}
+
+// The reconstruction kernel over one slab (dK, dV of its planes and their
+// dQ / dBias partials).
+static int attn_backward_slab_impl(const AttnGeom& g, const void* q, const void* k,
+                                   const void* v, const void* dout, const float* mask,
+                                   void* dk, void* dv, const BwdParts& pt, const BwdPlan& plan,
+                                   const BwdSlab& sl, hipStream_t s, const char* fn) {
+  const int64_t H = g.H, N = g.N, D = g.D;
+  const int64_t total = H * bwd_key_blocks(N, D) * sl.nbrun;
+  if ((total + 7) / 8 * 8 > INT32_MAX)
+    return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
   dim3 grid((unsigned)((total + 7) / 8 * 8));
   if (D <= 32)
     hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256 * bwd_kh(32)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, run);
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, plan.run, sl);
   else
     hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256 * bwd_kh(64)), 0, s, (const __bf16*)q,
                        (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, run);
+                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, plan.run, sl);
   return check_launch(fn);
 }
 
-// db_mode: 0 = f32 dBias, 1 = bf16, 2 = bf16 in transposed-bias order.
-static int attn_backward_finish_impl(const AttnGeom& g, void* dq, void* dbias,
-                                     int64_t bias_batches, const void* workspace, hipStream_t s,
-                                     const char* fn, int db_mode = 0) {
-  const int64_t B = g.B, O = g.O, H = g.H, N = g.N, D = g.D;
-  BwdParts pt;
-  bwd_layout(B, O, H, N, D, (char*)workspace, &pt);
-  // dBias partials per batch: one per run of outer groups (same run length
-  // as the main stage, which ran on this device).
-  const int64_t groups = bwd_runs(O, bwd_run_len(B, O, H, N, D));
-  const int64_t nph = B * O * H;
+// Folds of one slab: its planes' dQ, and (with_dbias, after the last slab)
+// every dBias partial.  db_mode: 0 = f32 dBias, 1 = bf16, 2 = bf16 in
+// transposed-bias order.
+static int attn_backward_fold_impl(const AttnGeom& g, void* dq, void* dbias,
+                                   int64_t bias_batches, const BwdParts& pt, const BwdPlan& plan,
+                                   const BwdSlab& sl, bool with_dbias, hipStream_t s,
+                                   const char* fn, int db_mode) {
+  const int64_t H = g.H, N = g.N, D = g.D;
+  const int64_t nph = sl.planes * H;
   const int64_t dq_bx = (N * (D / 8) + 255) / 256;
-  const int64_t n_db = (bias_batches * H * N * N / 8 + 63) / 64;
+  const int64_t n_db = with_dbias ? (bias_batches * H * N * N / 8 + 63) / 64 : 0;
   if (n_db + dq_bx * nph > 0x7fffffff)
     return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
+  if (n_db + dq_bx * nph == 0) return TPF_OK;
   hipLaunchKernelGGL(attn_fold_kernel, dim3((unsigned)(n_db + dq_bx * nph)), dim3(256), 0, s,
                      pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
-                     (int)bias_batches, (int)groups, n_db, db_mode);
+                     (int)bias_batches, plan.runs, n_db, db_mode, sl.plane0, sl.planes);
   return check_launch(fn);
 }
 
@@ -1687,22 +1760,46 @@ int tpf_attn_delta_shadow_bf16(const void* dout, const void* out, const void* re
 
 int64_t tpf_attn_backward_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N,
                                           int64_t D) {
-  return bwd_layout(B, O, H, N, D, nullptr, nullptr);
+  return bwd_full_bytes(B, O, H, N, D);
 }
 
-static int attn_bwd_prepare(AttnGeom* g, const char* fn, const void* q, const void* k,
-                            const void* v, const void* dout, const float* lse, const float* delta,
-                            const float* mask, const void* bias, const void* workspace,
-                            int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
-                            int64_t D, int layout, int64_t bias_batches, double scale) {
+int64_t tpf_attn_backward_workspace_bytes_budget(int64_t B, int64_t O, int64_t H, int64_t N,
+                                                 int64_t D, int64_t budget_bytes) {
+  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 1) return -1;
+  const int64_t full = bwd_full_bytes(B, O, H, N, D);
+  if (budget_bytes >= full) return full;
+  BwdPlan p = bwd_plan(B, O, H, N, D, budget_bytes);
+  // Below the one-run minimum the minimum is returned (it exceeds the budget).
+  const int per = p.per > 0 ? p.per : 1;
+  const int slabs = (int)((B * p.runs + per - 1) / per);
+  const int even = (int)((B * p.runs + slabs - 1) / slabs);
+  return bwd_layout(B, O, H, N, D, bwd_slab_planes(B, O, even, p.run), nullptr, nullptr);
+}
+
+int tpf_attn_backward_slab_count(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                 int64_t workspace_bytes) {
+  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 1) return -1;
+  return bwd_plan(B, O, H, N, D, workspace_bytes).slabs;
+}
+
+// full_only: the split main / finish stages need the one-slab plan.
+static int attn_bwd_prepare(AttnGeom* g, BwdPlan* plan, const char* fn, const void* q,
+                            const void* k, const void* v, const void* dout, const float* lse,
+                            const float* delta, const float* mask, const void* bias,
+                            const void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
+                            int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
+                            double scale, bool full_only) {
   int rc = make_geom(g, B, O, H, N, D, layout, bias_batches, scale, fn);
   if (rc) return rc;
   if (!q || !k || !v || !dout || !lse || !delta || !mask || !bias || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  const int64_t need = tpf_attn_backward_workspace_bytes(B, O, H, N, D);
+  const int64_t need = full_only ? bwd_full_bytes(B, O, H, N, D)
+                                 : tpf_attn_backward_workspace_bytes_budget(B, O, H, N, D, 0);
   if (workspace_bytes < need)
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
+  *plan = bwd_plan(B, O, H, N, D, workspace_bytes);
+  if (plan->slabs < 1) return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
   return TPF_OK;
 }
 
@@ -1716,13 +1813,19 @@ int tpf_attn_backward_main_bf16(const void* q, const void* k, const void* v, con
                                 double scale, void* stream) {
   const char* fn = "tpf_attn_backward_main_bf16";
   AttnGeom g;
-  int rc = attn_bwd_prepare(&g, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
-                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale);
+  BwdPlan plan;
+  int rc = attn_bwd_prepare(&g, &plan, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale, true);
   if (rc) return rc;
   if (!dk || !dv) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  return attn_backward_main_impl(g, q, k, v, dout, lse, delta, mask, bias,
-                                 dense_bias(H, N, bias_batches, layout), bias_batches, dk, dv, workspace,
-                                 (hipStream_t)stream, fn);
+  hipStream_t s = (hipStream_t)stream;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, B * O, (char*)workspace, &pt);
+  if ((rc = attn_backward_prep_impl(g, lse, delta, bias, dense_bias(H, N, bias_batches, layout),
+                                    bias_batches, pt, s, fn)))
+    return rc;
+  return attn_backward_slab_impl(g, q, k, v, dout, mask, dk, dv, pt, plan, bwd_slab(plan, B, O, 0),
+                                 s, fn);
 }
 
 // Stage 2 of the backward: fixed-order folds of the dQ and dBias partials.
@@ -1735,8 +1838,28 @@ int tpf_attn_backward_finish_bf16(void* dq, void* dbias, const void* workspace, 
   if (rc) return rc;
   if (!dq || !dbias || !workspace) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
-  return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, (hipStream_t)stream,
-                                   fn, db_mode);
+  const BwdPlan plan = bwd_plan(B, O, H, N, D, INT64_MAX);
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, B * O, (char*)workspace, &pt);
+  return attn_backward_fold_impl(g, dq, dbias, bias_batches, pt, plan, bwd_slab(plan, B, O, 0),
+                                 true, (hipStream_t)stream, fn, db_mode);
+}
+
+// Every slab of a plan: reconstruction, then that slab's dQ fold; the dBias
+// fold joins the last slab's fold launch.
+static int attn_backward_slabs(const AttnGeom& g, const BwdPlan& plan, const void* q,
+                               const void* k, const void* v, const void* dout, const float* mask,
+                               void* dq, void* dk, void* dv, void* dbias, int64_t bias_batches,
+                               const BwdParts& pt, hipStream_t s, const char* fn, int db_mode) {
+  for (int i = 0; i < plan.slabs; ++i) {
+    const BwdSlab sl = bwd_slab(plan, g.B, g.O, i);
+    int rc = attn_backward_slab_impl(g, q, k, v, dout, mask, dk, dv, pt, plan, sl, s, fn);
+    if (rc) return rc;
+    rc = attn_backward_fold_impl(g, dq, dbias, bias_batches, pt, plan, sl, i + 1 == plan.slabs, s,
+                                 fn, db_mode);
+    if (rc) return rc;
+  }
+  return TPF_OK;
 }
 
 int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const void* dout,
@@ -1745,18 +1868,27 @@ int tpf_attn_backward_bf16(const void* q, const void* k, const void* v, const vo
                            void* workspace, int64_t workspace_bytes, int64_t B, int64_t O,
                            int64_t H, int64_t N, int64_t D, int layout, int64_t bias_batches,
                            double scale, void* stream) {
-  if (!dq || !dbias) return set_error(TPF_ERR_ARG, "tpf_attn_backward_bf16: null pointer");
-  int rc = tpf_attn_backward_main_bf16(q, k, v, dout, lse, delta, mask, bias, dk, dv, workspace,
-                                       workspace_bytes, B, O, H, N, D, layout, bias_batches,
-                                       scale, stream);
+  const char* fn = "tpf_attn_backward_bf16";
+  AttnGeom g;
+  BwdPlan plan;
+  int rc = attn_bwd_prepare(&g, &plan, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale, false);
   if (rc) return rc;
-  return tpf_attn_backward_finish_bf16(dq, dbias, workspace, B, O, H, N, D, layout,
-                                       bias_batches, scale, stream);
+  if (!dq || !dk || !dv || !dbias) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  hipStream_t s = (hipStream_t)stream;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, bwd_slab_planes(B, O, plan.per, plan.run), (char*)workspace, &pt);
+  if ((rc = attn_backward_prep_impl(g, lse, delta, bias, dense_bias(H, N, bias_batches, layout),
+                                    bias_batches, pt, s, fn)))
+    return rc;
+  const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
+  return attn_backward_slabs(g, plan, q, k, v, dout, mask, dq, dk, dv, dbias, bias_batches, pt, s,
+                             fn, db_mode);
 }
 
 // Whole backward from the forward's outputs: delta (with the shadow residual
 // when given), row statistics and bias preparation in one launch, then the
-// reconstruction kernel and the folds.
+// reconstruction kernel and the folds, slab by slab.
 int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, const void* dout,
                                  const void* out, const void* residual, const float* lse,
                                  const float* mask, const void* bias, void* dq, void* dk,
@@ -1765,21 +1897,23 @@ int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, co
                                  int layout, int64_t bias_batches, double scale, void* stream) {
   const char* fn = "tpf_attn_backward_fused_bf16";
   AttnGeom g;
+  BwdPlan plan;
   // delta is computed in the workspace: the prepare check's delta slot gets lse.
-  int rc = attn_bwd_prepare(&g, fn, q, k, v, dout, lse, lse, mask, bias, workspace,
-                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale);
+  int rc = attn_bwd_prepare(&g, &plan, fn, q, k, v, dout, lse, lse, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale, false);
   if (rc) return rc;
   if (!out || !dq || !dk || !dv || !dbias) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const BiasView bv = dense_bias(H, N, bias_batches, layout);
   hipStream_t s = (hipStream_t)stream;
-  rc = attn_backward_rows_impl(g, dout, out, residual, lse, bias, bv, bias_batches, workspace, s,
-                               fn);
+  const int64_t slab_planes = bwd_slab_planes(B, O, plan.per, plan.run);
+  rc = attn_backward_rows_impl(g, dout, out, residual, lse, bias, bv, bias_batches, workspace,
+                               slab_planes, s, fn);
   if (rc) return rc;
-  rc = attn_backward_main_impl(g, q, k, v, dout, lse, nullptr, mask, bias, bv, bias_batches, dk,
-                               dv, workspace, s, fn, true);
-  if (rc) return rc;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, slab_planes, (char*)workspace, &pt);
   const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
-  return attn_backward_finish_impl(g, dq, dbias, bias_batches, workspace, s, fn, db_mode);
+  return attn_backward_slabs(g, plan, q, k, v, dout, mask, dq, dk, dv, dbias, bias_batches, pt, s,
+                             fn, db_mode);
 }
 
 // ---------------------------------------------------------------------------
@@ -1847,7 +1981,7 @@ int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mas
 // Workspace: the attention backward's, then d_o [B, N, N, H*D] bf16 and
 // delta [B, N, H, N] f32.
 int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D) {
-  return bwd_layout(B, N, H, N, D, nullptr, nullptr) + a256(B * N * N * H * D * 2) +
+  return bwd_full_bytes(B, N, H, N, D) + a256(B * N * N * H * D * 2) +
          a256(B * N * H * N * 4);
 }
 
@@ -1869,7 +2003,7 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   if (workspace_bytes < tpf_attn_pair_backward_workspace_bytes(B, N, H, D))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
   const int64_t hc = H * D;
-  const int64_t main_bytes = bwd_layout(B, N, H, N, D, nullptr, nullptr);
+  const int64_t main_bytes = bwd_full_bytes(B, N, H, N, D);
   __bf16* d_o = (__bf16*)((char*)workspace + main_bytes);
   float* delta = (float*)((char*)workspace + main_bytes + a256(B * N * N * hc * 2));
   const __bf16* p = (const __bf16*)proj;
@@ -1890,17 +2024,19 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
                        (const __bf16*)o, (const __bf16*)nullptr, p + 3 * hc, pitch, d_o, delta,
                        dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8);
   if ((rc = check_launch(fn))) return rc;
-  if ((rc = attn_backward_main_impl(g, p, p + hc, p + 2 * hc, d_o, lse, delta, mask, p + 4 * hc,
-                                    bv, B, dp + hc, dp + 2 * hc, workspace, s, fn)))
-    return rc;
   BwdParts pt;
-  bwd_layout(B, N, H, N, D, (char*)workspace, &pt);
+  bwd_layout(B, N, H, N, D, B * N, (char*)workspace, &pt);
+  const BwdPlan plan = bwd_plan(B, N, H, N, D, INT64_MAX);
+  if ((rc = attn_backward_prep_impl(g, lse, delta, p + 4 * hc, bv, B, pt, s, fn))) return rc;
+  if ((rc = attn_backward_slab_impl(g, p, p + hc, p + 2 * hc, d_o, mask, dp + hc, dp + 2 * hc, pt,
+                                    plan, bwd_slab(plan, B, N, 0), s, fn)))
+    return rc;
   const int64_t nph = B * N * H;
   hipLaunchKernelGGL(attn_dq_reduce_kernel,
                      dim3((unsigned)((N * (D / 8) + 255) / 256), (unsigned)(nph < 65535 ? nph : 65535)),
                      dim3(256), 0, s, pt.dq, dp, g, (int)bwd_key_blocks(N, D));
   if ((rc = check_launch(fn))) return rc;
-  const int64_t groups = bwd_runs(N, bwd_run_len(B, N, H, N, D));
+  const int64_t groups = plan.runs;
   const dim3 db_grid((unsigned)(B * N * N / 512));
   hipLaunchKernelGGL(attn_dbias_pair_kernel, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
                      (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);

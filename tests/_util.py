@@ -52,3 +52,24 @@ def attention_case(B, O, H, N, D, *, mask_tail=0, mask_frac=0.0, full_planes=0,
     if full_planes:
         dout[:, :full_planes] = 0
     return q, k, v, mask, bias, dout
+
+
+def record(name: str, key: str, values: dict) -> None:
+    """Merge ``{key: values}`` into ``$TPF_NUMERICS_OUT/<name>.json`` when that
+    environment variable names a directory (GPU runs set it so the measured
+    error figures are kept as a record); otherwise do nothing."""
+    import json
+    import os
+
+    out = os.environ.get("TPF_NUMERICS_OUT")
+    if not out:
+        return
+    os.makedirs(out, exist_ok=True)
+    path = os.path.join(out, f"{name}.json")
+    data = {}
+    if os.path.exists(path):
+        with open(path) as f:
+            data = json.load(f)
+    data[key] = values
+    with open(path, "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)

@@ -83,7 +83,9 @@ def test_workspace_sizes(lib):
 
     ws = _native.query("tpf_attn_backward_workspace_bytes", 1, 384, 4, 384, 32)
     dq = 3 * 384 * 4 * 384 * 32 * 2  # bf16 dQ partial per 128-key block (D <= 32)
-    assert ws >= dq + 96 * 4 * 384 * 384 * 2  # bf16 dBias partial per 4 outer rows
+    db = 20 * 4 * 384 * 384 * 4  # f32 dBias partial per run of 5 outer groups (20 runs)
+    rest = 4 * 384 * 384 * 4 + 2 * 384 * 4 * 384 * 4  # prescaled bias, two row statistics
+    assert ws == dq + db + rest
     assert _native.query("tpf_trimul_plane_pitch", 113) == 120
     assert _native.query("tpf_trimul_plane_pitch", 384) == 384
     assert _native.query("tpf_trimul_backward_workspace_bytes", 1, 384, 128) > 0
@@ -91,3 +93,30 @@ def test_workspace_sizes(lib):
     assert _native.query("tpf_layer_norm_backward_workspace_bytes", 384 * 384, 128) == 2048 * 2 * 128 * 4
     assert _native.query("tpf_layer_norm_backward_workspace_bytes", 16, 128) == 1 * 2 * 128 * 4
     assert _native.query("tpf_layer_norm_backward_workspace_bytes", 16, 12) == -1
+
+
+def test_backward_workspace_budget_plan(lib):
+    """The budgeted plan: the full plan when it fits, otherwise slabs whose
+    workspace stays within the budget, down to a one-run minimum that is
+    returned (and exceeds the budget) for budgets below it."""
+    from openfold3_triangle_kernel_amd import _native
+
+    for shape in ((1, 384, 4, 384, 32), (1, 768, 8, 768, 64), (2, 130, 4, 128, 32)):
+        full = _native.query("tpf_attn_backward_workspace_bytes", *shape)
+        assert _native.query("tpf_attn_backward_workspace_bytes_budget", *shape, full) == full
+        assert _native.query("tpf_attn_backward_slab_count", *shape, full) == 1
+        minimum = _native.query("tpf_attn_backward_workspace_bytes_budget", *shape, 1)
+        assert 0 < minimum < full
+        assert _native.query("tpf_attn_backward_slab_count", *shape, minimum - 1) == 0
+        last = 1
+        for frac in (0.9, 0.6, 0.4, 0.2):
+            budget = max(minimum, int(full * frac))
+            ws = _native.query("tpf_attn_backward_workspace_bytes_budget", *shape, budget)
+            assert minimum <= ws <= budget
+            slabs = _native.query("tpf_attn_backward_slab_count", *shape, ws)
+            assert slabs >= last  # fewer bytes never means fewer slabs
+            last = slabs
+    # Config 5's H=8, D=64 attention needs 7.46 GB in one slab; 4 GiB gives two.
+    ws = _native.query("tpf_attn_backward_workspace_bytes_budget", 1, 768, 8, 768, 64, 4 << 30)
+    assert ws <= 4 << 30
+    assert _native.query("tpf_attn_backward_slab_count", 1, 768, 8, 768, 64, ws) == 2

@@ -16,9 +16,10 @@ cropped as the tool does and whose gradients are zero either way.
 
 Besides the gate, each case checks what the tool checks: finite values,
 bitwise self-replay and exact zeros on fully masked planes.  The production
-flags of the tool keep the shadow residual on (``PROD_FLAGS``, :31), and the
-rule gates that policy; the same cases also run with it off (the reference's
-ablation setting), held to 1.3 * stock.
+flags of the tool keep the shadow residual on (``PROD_FLAGS``, :31); the same
+cases also run with it off (the reference's "classic" setting, :130-139),
+and the rule is the same 1.1 * stock for both, as the tool applies it to its
+classic cases too (:174-180).
 
 Published H100 values (release_artifacts/turbopairformer-h100-20260918/
 single_h100_numerics.json:130-412) are printed beside ours for reference.
@@ -31,6 +32,7 @@ import pytest
 import torch
 
 from oracle.attention import attention_backward, attention_forward
+from tests._util import record
 
 LABELS = ("out", "dq", "dk", "dv", "dbias")
 
@@ -133,10 +135,8 @@ def test_release_numeric_gate(gpu, monkeypatch, case, shadow):
         rows.append((label, e, es, 1.1 * es + 1e-6))
     print("  " + "  ".join(f"{l}: {e:.2e}/{es:.2e} (H100 {H100[name][i]:.2e})"
                            for i, (l, e, es, _) in enumerate(rows)), flush=True)
-    # The rule applies to the production policy (shadow on).  Shadow off is
-    # the reference's accuracy-ablation setting: reported, and held to a
-    # looser 1.3 * stock (its delta pairs dO with the bf16-rounded output).
-    factor = 1.1 if shadow == "1" else 1.3
-    for label, e, es, _ in rows:
-        limit = factor * es + 1e-6
-        assert e <= limit, f"{name} {label}: rel-L2 {e:.3e} exceeds {factor}*stock+1e-6 = {limit:.3e}"
+    record("attention_release_gate_rel_l2", f"{name} shadow={shadow}",
+           {l: {"ours": e, "stock": es, "limit": lim, "h100": H100[name][i]}
+            for i, (l, e, es, lim) in enumerate(rows)})
+    for label, e, es, limit in rows:
+        assert e <= limit, f"{name} {label}: rel-L2 {e:.3e} exceeds 1.1*stock+1e-6 = {limit:.3e}"

@@ -61,6 +61,15 @@ def test_noalloc_forward_rejects_oversized_bias(gpu):
     from openfold3_triangle_kernel_amd import _native
 
     # H * N * N = 8 * 768 * 768 = 4,718,592 > 4,194,304 f32 values of scratch.
+    # Every operand is a real device tensor of the declared shape, so even a
+    # host check that failed to fire could not launch on a bogus address.
+    B, O, H, N, D = 1, 1, 8, 768, 32
+    q, k, v = (torch.zeros(B, O, H, N, D, device=gpu, dtype=torch.bfloat16) for _ in range(3))
+    mask = torch.zeros(B, O, N, device=gpu)
+    bias = torch.zeros(1, H, N, N, device=gpu, dtype=torch.bfloat16)
+    out = torch.empty(B, O, N, H, D, device=gpu, dtype=torch.bfloat16)
+    lse = torch.empty(B, O, H, N, device=gpu)
     with pytest.raises(RuntimeError, match="static scratch"):
-        _native.call("tpf_attn_forward_noalloc_bf16", 16, 16, 16, 16, 16, 16, 16, 1, 1, 8, 768,
-                     32, 0, 1, 0.17, None)
+        _native.call("tpf_attn_forward_noalloc_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                     mask.data_ptr(), bias.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                     B, O, H, N, D, 0, 1, 1.0 / D ** 0.5, None)
