@@ -125,43 +125,79 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
 }
 
-// Longest mask row the forward stages in LDS (128 KiB of dynamic LDS).
-constexpr int kFwdMaskLdsMaxN = 32768;
+// Longest mask row the forward stages in LDS (64 KiB of dynamic LDS).
+constexpr int kFwdMaskLdsMaxN = 16384;
 
 // ---------------------------------------------------------------------------
 // Forward.  One workgroup = NW waves = 32*NW queries of one plane (NW = 4:
-// 2, 3 and 6 measured slower at N = 384); each wave owns
-// 32 queries and walks all keys in 64-key tiles staged in LDS (double
-// buffered, fetched into registers one tile ahead).  Scores are produced
-// transposed (S^T = K Q^T) so each lane owns one query column: row max / sum
-// need only the lane^32 exchange, and the C-layout P^T block is fed directly
-// as the B operand of O^T += V^T P^T.
-// Softmax works on 32-key blocks.  The S^T accumulator is seeded with the
-// prescaled bias (loaded one block ahead), scores stay in raw units
+// 2, 3 and 6 measured slower at N = 384); each wave owns 32 queries and
+// walks all keys in 64-key tiles that the workgroup stages in LDS.
+// Scores are produced transposed (S^T = K Q^T) so each lane owns one query
+// column: row max / sum need only the lane^32 exchange, and the C-layout P^T
+// block is fed directly as the B operand of O^T += V^T P^T.
+//
+// Memory pipeline.  K and V tiles are staged row-major in LDS (16-byte
+// chunks XOR-swizzled per row) and double-buffered; each wave fetches its
+// share of tile t+2 into registers during tile t (buffer loads, two
+// register sets) and writes tile t+1 to LDS at the end of tile t, so a
+// tile's loads have a full tile of compute to arrive.  V^T operands come
+// from the row-major V tile through transposing LDS reads.  The prescaled
+// bias of a 32-key block (fragment-major, one 4 KiB read per wave) is loaded
+// two blocks ahead into two register sets (even / odd blocks) and seeds the
+// S^T accumulator.  Every load is issued unconditionally (past the last
+// tile or block it reloads the last one, whose copy is never consumed; lane
+// chunks past D read zeros through the buffer range check) and is visible
+// to the compiler's wait counting, and loads are issued in the
+// order they are consumed, so waiting for block b's bias never waits for a
+// K / V tile issued after it.
+//
+// Softmax works on 32-key blocks.  Scores stay in raw units
 // r = <Q,K> + bias_s (+ mask / scale), and p = exp2(r * c2 - m * c2) with
 // c2 = scale * log2(e): one FMA + one exp per score.  Row sums use packed
 // bf16 dot products of the rounded P (the values that also enter P V).  The
 // running max is raised only when a block exceeds it by more than 8 in log2
 // units (p <= 256 otherwise), so the O rescale is rare.
 // ---------------------------------------------------------------------------
+// Swizzle of the 16-byte chunks of K / V tile rows: a 16-byte row read by 8
+// consecutive rows (8 lanes = 128 bytes) and an 8-byte transposing read of 4
+// consecutive rows x 2 chunks (16 lanes = 128 bytes) each cover all 32
+// banks once.  DP = 32 (64-byte rows): rows 0..7 -> 0, 0, 2, 2, 1, 1, 3, 3;
+// DP = 64 (128-byte rows): 0, 2, 4, 6, 1, 3, 5, 7.
+template <int DP>
+__device__ __forceinline__ int kv_swz(int r) {
+  return (DP == 32) ? ((((r >> 1) & 1) << 1) | ((r >> 2) & 1)) : (((r & 3) << 1) | ((r >> 2) & 1));
+}
+template <int DP>
+__device__ __forceinline__ int kv_off(int r, int col) {  // element offset of (row, col)
+  return r * DP + (((col >> 3) ^ kv_swz<DP>(r)) << 3) + (col & 7);
+}
+
+// tr_col4 (common.hpp) on a swizzled K / V tile: lane l receives
+// { M[r0 + e][c0 + l % 32] : e = 0..3 }, r0 = rbase_lo (l < 32) or rbase_hi.
+template <int DP>
+__device__ __forceinline__ bf16x4 kv_tr_col4(const __bf16* M, int rbase_lo, int rbase_hi, int c0) {
+  const int l = threadIdx.x & 63, gq = l >> 4, ip = l & 15;
+  const int r = ((gq >> 1) ? rbase_hi : rbase_lo) + (ip >> 2);
+  const __bf16* p = M + kv_off<DP>(r, c0 + 16 * (gq & 1) + 4 * (ip & 3));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 4 : 2, 8))) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
     const float* __restrict__ bias_s, __bf16* __restrict__ out,
     float* __restrict__ lse, __bf16* __restrict__ res, AttnGeom g) {
-  constexpr int KP = DP + 8;     // K tile pitch (bf16): conflict-free 16-byte reads
-  constexpr int VP = 64 + 4;     // V^T tile pitch (bf16): conflict-free 8-byte reads
-  constexpr int NT = 64 * NW;           // threads
-  constexpr int QT = 32 * NW;           // queries per workgroup
-  constexpr int KITEMS = 64 * DP / 8;   // 16-byte K chunks per tile
-  constexpr int VITEMS = 16 * DP / 8;   // (4-key group, 8-channel chunk) V items
-  __shared__ __attribute__((aligned(16))) __bf16 Ks[2][64 * KP];
-  __shared__ __attribute__((aligned(16))) __bf16 Vt[2][DP * VP];
+  constexpr int TE = 64 * DP;                 // elements of one K (or V) tile
+  constexpr int KV_CH = 2 * TE / 8;           // 16-byte chunks of a K + V tile pair
+  constexpr int CPT = KV_CH / (64 * NW);      // chunks per thread per tile
+  static_assert(KV_CH % (64 * NW) == 0, "K / V chunks split over the threads");
+  constexpr int QT = 32 * NW;                 // queries per workgroup
+  __shared__ __attribute__((aligned(16))) __bf16 KVs[2][2][TE];  // [buffer][K, V]
   // This plane's mask row divided by the scale (dynamic LDS of N floats).
   extern __shared__ __attribute__((aligned(16))) float Ms[];
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int ql = lane & 31, hl = lane >> 5;
   const int N = g.N, D = g.D;
   TileId tile;
@@ -174,67 +210,80 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
   const int qi = q0 + ql;
 
   const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
-  const __bf16* qb = q + plane_off;
-  const __bf16* kb = k + plane_off;
-  const __bf16* vb = v + plane_off;
   const float* mrow = mask + (int64_t)plane * N;
-  // Fragment-major bias blocks of this wave's 32 queries: 1024 floats per
-  // 32-key block, lane-interleaved.
-  const float* brow = bias_s + (int64_t)b * g.bias_bstride +
-                      ((int64_t)h * (N / 32) + (active ? q0 / 32 : 0)) * (int64_t)(N / 32) * 1024 + lane * 4;
   const float c2 = g.scale * kLog2e;
   const float inv_scale = 1.f / g.scale;
   const float thr = 8.f / c2;  // lazy-rescale threshold in raw units
+  const int ntiles = N / 64, nblk = N / 32;
 
+  // Q rows of this wave (B operand of S^T = K Q^T), zeros past D.
   bf16x8 qreg[DP / 16];
+  {
+    const __amdgpu_buffer_rsrc_t rq = raw_rsrc(q + plane_off);
 #pragma unroll
-  for (int s = 0; s < DP / 16; ++s) {
-    const int d0 = 16 * s + 8 * hl;
-    qreg[s] = (active && d0 < D) ? ld8(qb + (int64_t)qi * g.s_row + d0) : zero8();
+    for (int s2 = 0; s2 < DP / 16; ++s2) {
+      const int d0 = 16 * s2 + 8 * hl;
+      qreg[s2] = buf_ld8(rq, (active && d0 < D) ? (uint32_t)(((int64_t)qi * g.s_row + d0) * 2) : kBufOOB);
+    }
   }
 
-  // K: thread -> (key, 8-channel chunk) items; V: thread -> (4-key group,
-  // chunk), transposed into Vt[d][key] with 8-byte stores.
-  constexpr int KPT = (KITEMS + NT - 1) / NT;  // K items per thread
-  static_assert(VITEMS <= NT, "V items");
-  const int vgrp = tid % 16, vc = tid / 16;
-  const bool vthread = tid < VITEMS;
-  const bool vload = vthread && vc * 8 < D;
-  bf16x8 kr[KPT], vr[4];
-  auto load_kv = [&](int kt) {
+  // K / V chunks of a thread: chunk n = tid + 64 NW i of the tile pair
+  // (first TE / 8 chunks K, then V); LDS chunk position -> (row, physical
+  // chunk), reading the logical chunk the swizzle stores there.  Per-lane
+  // byte offsets are fixed; a tile adds 64 rows.
+  const __amdgpu_buffer_rsrc_t rk = raw_rsrc(k + plane_off), rv = raw_rsrc(v + plane_off);
+  uint32_t vkv[CPT];
 #pragma unroll
-    for (int it = 0; it < KPT; ++it) {
-      const int idx = it * NT + tid;
-      const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
-      kr[it] = (idx < KITEMS && kc * 8 < D) ? ld8(kb + (int64_t)(kt + kkey) * g.s_row + kc * 8) : zero8();
-    }
+  for (int i = 0; i < CPT; ++i) {
+    const int n = tid + 64 * NW * i;
+    const int e = (n % (TE / 8)) * 8;  // element offset within the K (or V) tile
+    const int r = e / DP, c = ((e % DP) / 8) ^ kv_swz<DP>(r);
+    vkv[i] = c * 8 < D ? (uint32_t)(((int64_t)r * g.s_row + c * 8) * 2) : kBufOOB;
+  }
+  static_assert((TE / 8) % (64 * NW) == 0, "a thread's K and V chunks split evenly");
+  const uint32_t tile_bytes = (uint32_t)(64 * g.s_row * 2);
+  auto load_kv = [&](int t, bf16x8* dst) {
+    // Tiles past the last one reload the last one (never consumed), so the
+    // count of loads in flight is the same at every step; the tile offset is
+    // a scalar, the lane offsets fixed.
+    const uint32_t so = (uint32_t)min(t, ntiles - 1) * tile_bytes;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      vr[r] = vload ? ld8(vb + (int64_t)(kt + vgrp * 4 + r) * g.s_row + vc * 8) : zero8();
+    for (int i = 0; i < CPT; ++i)  // chunks [0, TE/8) are K
+      dst[i] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(i < CPT / 2 ? rk : rv, vkv[i], so, 0));
   };
-  auto store_kv = [&](int buf) {
+  auto store_kv = [&](int buf, const bf16x8* src) {
 #pragma unroll
-    for (int it = 0; it < KPT; ++it) {
-      const int idx = it * NT + tid;
-      const int kkey = idx / (DP / 8), kc = idx % (DP / 8);
-      if (idx < KITEMS) *reinterpret_cast<bf16x8*>(&Ks[buf][kkey * KP + kc * 8]) = kr[it];
+    for (int i = 0; i < CPT; ++i) {
+      const int n = tid + 64 * NW * i;
+      *reinterpret_cast<bf16x8*>(&KVs[buf][0][0] + n * 8) = src[i];
     }
-    if (vthread) {
+  };
+
+  // Fragment-major bias blocks of this wave's 32 queries: 1024 floats per
+  // 32-key block, lane-interleaved (see attn_bias_prescale_kernel).
+  const __amdgpu_buffer_rsrc_t rs_b = raw_rsrc(
+      bias_s + (int64_t)b * g.bias_bstride +
+      ((int64_t)h * (N / 32) + (active ? q0 / 32 : 0)) * (int64_t)(N / 32) * 1024);
+  const uint32_t vb_lane = (uint32_t)lane * 16;
+  auto load_bias = [&](int blk) {
+    // Blocks past the last one reload the last one (never consumed).
+    const uint32_t so = (uint32_t)min(blk, nblk - 1) * 4096;
+    f32x16 r;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bf16x4 col;
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 x = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_b, vb_lane + j * 1024, so, 0));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) col[r] = vr[r][e];
-        *reinterpret_cast<bf16x4*>(&Vt[buf][(vc * 8 + e) * VP + vgrp * 4]) = col;
-      }
+      for (int i = 0; i < 4; ++i) r[4 * j + i] = x[i];
     }
+    return r;
   };
 
   // Tiles whose 64 mask entries are all zero skip the mask add (the mask
   // is per plane, so the flag is uniform); computed up front so no wait on
   // the mask sits inside the pipelined loop.
-  const int ntiles = N / 64;
-  for (int i = tid; i < N; i += NT) Ms[i] = mrow[i] * inv_scale;
+  for (int i = tid; i < N; i += 64 * NW) Ms[i] = mrow[i] * inv_scale;
   uint64_t mbits = ~0ull;
   if (ntiles <= 64) {
     mbits = 0ull;
@@ -242,101 +291,108 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
       if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
   }
 
+  // Pipeline fill: K / V of tile 0 (to LDS) and 1 (registers), bias of
+  // blocks 0 and 1.  The two K / V register sets swap roles every tile (the
+  // tile loop is unrolled by two, so no register copies: a copy would wait
+  // for the loads in flight).
+  bf16x8 kvr0[CPT], kvr1[CPT];
+  load_kv(0, kvr1);
+  f32x16 bias_e = load_bias(0);
+  load_kv(1, kvr0);
+  f32x16 bias_o = load_bias(1);
+  store_kv(0, kvr1);
+
   f32x16 acc[DP / 32];
 #pragma unroll
   for (int i = 0; i < DP / 32; ++i) acc[i] = zero16();
   float m = -INFINITY, l = 0.f, nm = 0.f;
   const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 
-  // The bias block for the next 32 keys is fetched while the current block
-  // is processed; K/V for the next tile are fetched at the start of a tile
-  // and stored to the other LDS buffer at its end.
-  auto load_bias = [&](int blk) {
-    f32x16 r;
+  // One 32-key block: S^T (seeded with the bias in `bset`, which is then
+  // reloaded with block blk + 2), mask, online softmax, O^T += V^T P^T.
+  auto block = [&](const __bf16* Kt, const __bf16* Vt, int sb, int blk, bool masked, int kt,
+                   f32x16& bset) {
+    f32x16 s = bset;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f32x4 x = *reinterpret_cast<const f32x4*>(brow + (int64_t)blk * 1024 + j * 256);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[4 * j + i] = x[i];
+    for (int ks = 0; ks < DP / 16; ++ks) {
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Kt[kv_off<DP>(sb * 32 + ql, 16 * ks + 8 * hl)]);
+      s = mfma32(ka, qreg[ks], s);
     }
-    return r;
+    if (masked) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 mv = *reinterpret_cast<const f32x4*>(&Ms[kt + sb * 32 + 8 * j + 4 * hl]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * j + i] += mv[i];
+      }
+    }
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = xor32_max(mx);
+    if (__any(mx > m + thr)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2((m - m_new) * c2);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+      m = m_new;
+      nm = (m == -INFINITY) ? 0.f : -m * c2;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // P in packed bf16 pairs (one v_cvt_pk each), summed by v_dot2 and
+      // reassembled into the B operand without permutes.
+      uint32_t pw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f32x2 f;
+        f[0] = fast_exp2(fmaf(s[8 * t + 2 * e], c2, nm));
+        f[1] = fast_exp2(fmaf(s[8 * t + 2 * e + 1], c2, nm));
+        const bf16x2 pr = __builtin_convertvector(f, bf16x2);
+        l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);
+        pw[e] = __builtin_bit_cast(uint32_t, pr);
+      }
+      u32x4 pwv = {pw[0], pw[1], pw[2], pw[3]};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pwv);
+      // The scores are consumed: block blk + 2's bias goes into the same
+      // registers (one register assignment in every iteration, so no copies
+      // that would wait for it).
+      if (t == 1) bset = load_bias(blk + 2);
+      // V^T operand: keys {16t + 4hl .. +3, 16t + 8 + 4hl .. +3} of the
+      // block (the key order of the P^T registers), channel 32 db + ql.
+      const int k0 = sb * 32 + 16 * t;
+#pragma unroll
+      for (int db = 0; db < DP / 32; ++db) {
+        const bf16x8 va = cat8(kv_tr_col4<DP>(Vt, k0, k0 + 4, 32 * db),
+                               kv_tr_col4<DP>(Vt, k0 + 8, k0 + 12, 32 * db));
+        acc[db] = mfma32(va, pb, acc[db]);
+      }
+    }
   };
-  f32x16 bnext = load_bias(0);
-  load_kv(0);
-  store_kv(0);
-  __syncthreads();
-  const int nblk = N / 32;
-  for (int kt = 0, buf = 0; kt < N; kt += 64, buf ^= 1) {
-    const bool more = kt + 64 < N;
-    if (more) load_kv(kt + 64);
-    const bool masked = (mbits >> ((kt >> 6) & 63)) & 1ull;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int blk = (kt >> 5) + sb;
-      if (!active) continue;
-      // The MFMAs read the prefetched bias as their C operand before the
-      // next block's bias is loaded into the same registers (no copies).
-      f32x16 s = bnext;
-#pragma unroll
-      for (int ks = 0; ks < DP / 16; ++ks) {
-        bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[buf][(sb * 32 + ql) * KP + 16 * ks + 8 * hl]);
-        s = mfma32(ka, qreg[ks], s);
-      }
-      if (blk + 1 < nblk) bnext = load_bias(blk + 1);
-      if (masked) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 mv = *reinterpret_cast<const f32x4*>(&Ms[kt + sb * 32 + 8 * j + 4 * hl]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s[4 * j + i] += mv[i];
-        }
-      }
-      float mx = s[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-      mx = xor32_max(mx);
-      if (__any(mx > m + thr)) {
-        const float m_new = fmaxf(m, mx);
-        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2((m - m_new) * c2);
-        l *= alpha;
-#pragma unroll
-        for (int db = 0; db < DP / 32; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-        m = m_new;
-        nm = (m == -INFINITY) ? 0.f : -m * c2;
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        // P in packed bf16 pairs (one v_cvt_pk each), summed by v_dot2 and
-        // reassembled into the B operand without permutes.
-        uint32_t pw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f32x2 f;
-          f[0] = fast_exp2(fmaf(s[8 * t + 2 * e], c2, nm));
-          f[1] = fast_exp2(fmaf(s[8 * t + 2 * e + 1], c2, nm));
-          const bf16x2 pr = __builtin_convertvector(f, bf16x2);
-          l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);
-          pw[e] = __builtin_bit_cast(uint32_t, pr);
-        }
-        u32x4 pwv = {pw[0], pw[1], pw[2], pw[3]};
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, pwv);
-        const int key0 = sb * 32 + 16 * t + 4 * hl;
-#pragma unroll
-        for (int db = 0; db < DP / 32; ++db) {
-          const __bf16* vr2 = &Vt[buf][(db * 32 + ql) * VP + key0];
-          bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr2);
-          bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr2 + 8);
-          bf16x8 va;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { va[e] = lo[e]; va[4 + e] = hi[e]; }
-          acc[db] = mfma32(va, pb, acc[db]);
-        }
-      }
-    }
-    if (more) store_kv(buf ^ 1);
+
+  // Tile t: in LDS buffer t % 2 (written before the barrier); tile t+1 in
+  // `nxt`; tile t+2 loaded into `far` during this tile.
+  auto tile_step = [&](int t, bf16x8* nxt, bf16x8* far) {
     __syncthreads();
+    const __bf16* Kt = &KVs[t & 1][0][0];
+    const __bf16* Vt = &KVs[t & 1][1][0];
+    const bool masked = (mbits >> (t & 63)) & 1ull;
+    // Waves past N (the last query tile when N % (32 NW) != 0) compute on
+    // zero Q rows and store nothing: no branch splits the loads' register
+    // state.
+    block(Kt, Vt, 0, 2 * t, masked, t * 64, bias_e);
+    load_kv(t + 2, far);
+    block(Kt, Vt, 1, 2 * t + 1, masked, t * 64, bias_o);
+    // Buffer (t+1) % 2 was last read in tile t-1, before the barrier above.
+    store_kv((t + 1) & 1, nxt);
+  };
+#pragma unroll 1
+  for (int t = 0; t < ntiles; t += 2) {
+    tile_step(t, kvr0, kvr1);
+    if (t + 1 < ntiles) tile_step(t + 1, kvr1, kvr0);
   }
   if (!active) return;
 
