@@ -125,8 +125,8 @@ __global__ __launch_bounds__(256) void attn_bias_prescale_kernel(const __bf16* _
   *reinterpret_cast<f32x4*>(out + i * 4) = o;
 }
 
-// Longest mask row the forward stages in LDS (64 KiB of dynamic LDS).
-constexpr int kFwdMaskLdsMaxN = 16384;
+// Longest mask row the forward stages in LDS (up to 2 rows, 64 KiB of dynamic LDS).
+constexpr int kFwdMaskLdsMaxN = 8192;
 
 // ---------------------------------------------------------------------------
 // Forward.  One workgroup = NW waves = 32*NW queries of one plane (NW = 4:
@@ -182,86 +182,101 @@ __device__ __forceinline__ bf16x4 kv_tr_col4(const __bf16* M, int rbase_lo, int 
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
 }
 
-template <int DP, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 32 ? 4 : 2, 8))) void attn_fwd_kernel(
+template <int DP, int NW, int PL>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8))) void attn_fwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
     const float* __restrict__ bias_s, __bf16* __restrict__ out,
     float* __restrict__ lse, __bf16* __restrict__ res, AttnGeom g) {
-  constexpr int TE = 64 * DP;                 // elements of one K (or V) tile
-  constexpr int KV_CH = 2 * TE / 8;           // 16-byte chunks of a K + V tile pair
-  constexpr int CPT = KV_CH / (64 * NW);      // chunks per thread per tile
-  static_assert(KV_CH % (64 * NW) == 0, "K / V chunks split over the threads");
-  constexpr int QT = 32 * NW;                 // queries per workgroup
-  __shared__ __attribute__((aligned(16))) __bf16 KVs[2][2][TE];  // [buffer][K, V]
-  // This plane's mask row divided by the scale (dynamic LDS of N floats).
+  constexpr int TE = 64 * DP;                  // elements of one K (or V) tile
+  constexpr int REG = TE / 8;                  // 16-byte chunks of one K (or V) tile
+  constexpr int CPT = 2 * PL * REG / (64 * NW);  // chunks per thread per tile
+  static_assert(REG % (64 * NW) == 0, "a thread's chunks split evenly over K / V tiles");
+  constexpr int QT = 32 * NW;                  // queries per workgroup
+  // [buffer][plane][K, V] tiles.
+  __shared__ __attribute__((aligned(16))) __bf16 KVs[2][PL][2][TE];
+  // The planes' mask rows divided by the scale (dynamic LDS of PL * N floats).
   extern __shared__ __attribute__((aligned(16))) float Ms[];
 
   const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int ql = lane & 31, hl = lane >> 5;
   const int N = g.N, D = g.D;
+  // Groups of PL consecutive outer rows of one batch (the last group of a
+  // batch may hold fewer: its missing planes recompute the first one and
+  // store nothing).
+  const int groups = (g.O + PL - 1) / PL;
   TileId tile;
   const int qtiles = (N + QT - 1) / QT;
-  if (!xcd_tile((int64_t)qtiles * g.H * g.B * g.O, qtiles, g.B * g.O, &tile)) return;
-  const int h = tile.h, plane = tile.plane;
-  const int b = plane / g.O;
+  if (!xcd_tile((int64_t)qtiles * g.H * g.B * groups, qtiles, g.B * groups, &tile)) return;
+  const int h = tile.h;
+  const int b = tile.plane / groups;
+  const int o0 = (tile.plane - b * groups) * PL;
   const int q0 = tile.qt * QT + w * 32;
   const bool active = q0 < N;
   const int qi = q0 + ql;
+  int plane[PL];
+  bool pvalid[PL];
+#pragma unroll
+  for (int p = 0; p < PL; ++p) {
+    pvalid[p] = o0 + p < g.O;
+    plane[p] = b * g.O + (pvalid[p] ? o0 + p : o0);
+  }
 
-  const int64_t plane_off = (int64_t)plane * g.s_plane + (int64_t)h * g.s_head;
-  const float* mrow = mask + (int64_t)plane * N;
   const float c2 = g.scale * kLog2e;
   const float inv_scale = 1.f / g.scale;
   const float thr = 8.f / c2;  // lazy-rescale threshold in raw units
   const int ntiles = N / 64, nblk = N / 32;
 
-  // Q rows of this wave (B operand of S^T = K Q^T), zeros past D.
-  bf16x8 qreg[DP / 16];
-  {
-    const __amdgpu_buffer_rsrc_t rq = raw_rsrc(q + plane_off);
+  // Q rows of this wave for every plane (B operand of S^T = K Q^T), zeros
+  // past D.
+  bf16x8 qreg[PL][DP / 16];
+#pragma unroll
+  for (int p = 0; p < PL; ++p) {
+    const __amdgpu_buffer_rsrc_t rq = raw_rsrc(q + (int64_t)plane[p] * g.s_plane + (int64_t)h * g.s_head);
 #pragma unroll
     for (int s2 = 0; s2 < DP / 16; ++s2) {
       const int d0 = 16 * s2 + 8 * hl;
-      qreg[s2] = buf_ld8(rq, (active && d0 < D) ? (uint32_t)(((int64_t)qi * g.s_row + d0) * 2) : kBufOOB);
+      qreg[p][s2] = buf_ld8(rq, (active && d0 < D) ? (uint32_t)(((int64_t)qi * g.s_row + d0) * 2) : kBufOOB);
     }
   }
 
-  // K / V chunks of a thread: chunk n = tid + 64 NW i of the tile pair
-  // (first TE / 8 chunks K, then V); LDS chunk position -> (row, physical
+  // K / V chunks of a thread: chunk n = tid + 64 NW i of the tile group,
+  // region n / REG = (plane, K or V); LDS chunk position -> (row, physical
   // chunk), reading the logical chunk the swizzle stores there.  Per-lane
   // byte offsets are fixed; a tile adds 64 rows.
-  const __amdgpu_buffer_rsrc_t rk = raw_rsrc(k + plane_off), rv = raw_rsrc(v + plane_off);
+  __amdgpu_buffer_rsrc_t rkv[2 * PL];
+#pragma unroll
+  for (int p = 0; p < PL; ++p) {
+    const int64_t off = (int64_t)plane[p] * g.s_plane + (int64_t)h * g.s_head;
+    rkv[2 * p] = raw_rsrc(k + off);
+    rkv[2 * p + 1] = raw_rsrc(v + off);
+  }
   uint32_t vkv[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int n = tid + 64 * NW * i;
-    const int e = (n % (TE / 8)) * 8;  // element offset within the K (or V) tile
+    const int e = ((tid + 64 * NW * i) % REG) * 8;  // element offset within its tile
     const int r = e / DP, c = ((e % DP) / 8) ^ kv_swz<DP>(r);
     vkv[i] = c * 8 < D ? (uint32_t)(((int64_t)r * g.s_row + c * 8) * 2) : kBufOOB;
   }
-  static_assert((TE / 8) % (64 * NW) == 0, "a thread's K and V chunks split evenly");
   const uint32_t tile_bytes = (uint32_t)(64 * g.s_row * 2);
   auto load_kv = [&](int t, bf16x8* dst) {
-    // Tiles past the last one reload the last one (never consumed), so the
-    // count of loads in flight is the same at every step; the tile offset is
-    // a scalar, the lane offsets fixed.
+    // Tiles past the last one reload the last one (never consumed); the
+    // tile offset is a scalar, the lane offsets fixed.
     const uint32_t so = (uint32_t)min(t, ntiles - 1) * tile_bytes;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i)  // chunks [0, TE/8) are K
+    for (int i = 0; i < CPT; ++i)
       dst[i] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(i < CPT / 2 ? rk : rv, vkv[i], so, 0));
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rkv[64 * NW * i / REG], vkv[i], so, 0));
   };
   auto store_kv = [&](int buf, const bf16x8* src) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int n = tid + 64 * NW * i;
-      *reinterpret_cast<bf16x8*>(&KVs[buf][0][0] + n * 8) = src[i];
-    }
+    for (int i = 0; i < CPT; ++i)
+      *reinterpret_cast<bf16x8*>(&KVs[buf][0][0][0] + (tid + 64 * NW * i) * 8) = src[i];
   };
 
   // Fragment-major bias blocks of this wave's 32 queries: 1024 floats per
-  // 32-key block, lane-interleaved (see attn_bias_prescale_kernel).
+  // 32-key block, lane-interleaved (see attn_bias_prescale_kernel); shared by
+  // the PL planes.
   const __amdgpu_buffer_rsrc_t rs_b = raw_rsrc(
       bias_s + (int64_t)b * g.bias_bstride +
       ((int64_t)h * (N / 32) + (active ? q0 / 32 : 0)) * (int64_t)(N / 32) * 1024);
@@ -280,147 +295,172 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DP == 3
     return r;
   };
 
-  // Tiles whose 64 mask entries are all zero skip the mask add (the mask
-  // is per plane, so the flag is uniform); computed up front so no wait on
-  // the mask sits inside the pipelined loop.
-  for (int i = tid; i < N; i += 64 * NW) Ms[i] = mrow[i] * inv_scale;
+  // Tiles whose 64 mask entries are all zero in every plane skip the mask
+  // add (uniform flags); computed up front so no wait on the mask sits
+  // inside the pipelined loop.
   uint64_t mbits = ~0ull;
-  if (ntiles <= 64) {
-    mbits = 0ull;
-    for (int t = 0; t < ntiles; ++t)
-      if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
+  if (ntiles <= 64) mbits = 0ull;
+#pragma unroll
+  for (int p = 0; p < PL; ++p) {
+    const float* mrow = mask + (int64_t)plane[p] * N;
+    for (int i = tid; i < N; i += 64 * NW) Ms[p * N + i] = mrow[i] * inv_scale;
+    if (ntiles <= 64)
+      for (int t = 0; t < ntiles; ++t)
+        if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
   }
 
-  // Pipeline fill: K / V of tile 0 (to LDS) and 1 (registers), bias of
-  // blocks 0 and 1.  The two K / V register sets swap roles every tile (the
-  // tile loop is unrolled by two, so no register copies: a copy would wait
-  // for the loads in flight).
-  bf16x8 kvr0[CPT], kvr1[CPT];
-  load_kv(0, kvr1);
-  f32x16 bias_e = load_bias(0);
-  load_kv(1, kvr0);
-  f32x16 bias_o = load_bias(1);
-  store_kv(0, kvr1);
+  // Pipeline fill: K / V of tile 0 (to LDS), bias of block 0.
+  bf16x8 kvr[CPT];
+  load_kv(0, kvr);
+  f32x16 bset = load_bias(0);
+  store_kv(0, kvr);
 
-  f32x16 acc[DP / 32];
+  f32x16 acc[PL][DP / 32];
+  float m[PL], l[PL], nm[PL];
 #pragma unroll
-  for (int i = 0; i < DP / 32; ++i) acc[i] = zero16();
-  float m = -INFINITY, l = 0.f, nm = 0.f;
+  for (int p = 0; p < PL; ++p) {
+#pragma unroll
+    for (int i = 0; i < DP / 32; ++i) acc[p][i] = zero16();
+    m[p] = -INFINITY;
+    l[p] = 0.f;
+    nm[p] = 0.f;
+  }
   const bf16x2 ones = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
 
-  // One 32-key block: S^T (seeded with the bias in `bset`, which is then
-  // reloaded with block blk + 2), mask, online softmax, O^T += V^T P^T.
-  auto block = [&](const __bf16* Kt, const __bf16* Vt, int sb, int blk, bool masked, int kt,
-                   f32x16& bset) {
-    f32x16 s = bset;
+  // One 32-key block for every plane: S^T seeded with the shared bias (whose
+  // registers then take block blk + 1's bias), mask, online softmax (one
+  // rescale branch for all planes), O^T += V^T P^T.  The planes' chains are
+  // independent, so their MFMA and VALU work interleave.
+  auto block = [&](int buf, int sb, int blk, bool masked, int kt) {
+    // Every K fragment of the block is read before the first MFMA, so the
+    // LDS latency is paid once.
+    bf16x8 ka[PL][DP / 16];
 #pragma unroll
-    for (int ks = 0; ks < DP / 16; ++ks) {
-      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Kt[kv_off<DP>(sb * 32 + ql, 16 * ks + 8 * hl)]);
-      s = mfma32(ka, qreg[ks], s);
+    for (int p = 0; p < PL; ++p)
+#pragma unroll
+      for (int ks = 0; ks < DP / 16; ++ks)
+        ka[p][ks] = *reinterpret_cast<const bf16x8*>(
+            &KVs[buf][p][0][kv_off<DP>(sb * 32 + ql, 16 * ks + 8 * hl)]);
+    f32x16 s[PL];
+#pragma unroll
+    for (int p = 0; p < PL; ++p) {
+      s[p] = mfma32(ka[p][0], qreg[p][0], bset);
+#pragma unroll
+      for (int ks = 1; ks < DP / 16; ++ks) s[p] = mfma32(ka[p][ks], qreg[p][ks], s[p]);
     }
+    bset = load_bias(blk + 1);
     if (masked) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 mv = *reinterpret_cast<const f32x4*>(&Ms[kt + sb * 32 + 8 * j + 4 * hl]);
+      for (int p = 0; p < PL; ++p)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[4 * j + i] += mv[i];
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 mv = *reinterpret_cast<const f32x4*>(&Ms[p * N + kt + sb * 32 + 8 * j + 4 * hl]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[p][4 * j + i] += mv[i];
+        }
+    }
+    float mx[PL];
+    bool up = false;
+#pragma unroll
+    for (int p = 0; p < PL; ++p) {
+      float x = fmaxf(s[p][0], s[p][1]);
+#pragma unroll
+      for (int r = 2; r < 16; ++r) x = fmaxf(x, s[p][r]);
+      mx[p] = xor32_max(x);
+      up = up || (mx[p] > m[p] + thr);
+    }
+    if (__any(up)) {
+#pragma unroll
+      for (int p = 0; p < PL; ++p) {
+        const float m_new = fmaxf(m[p], mx[p]);
+        const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2((m[p] - m_new) * c2);
+        l[p] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[p][db][r] *= alpha;
+        m[p] = m_new;
+        nm[p] = (m_new == -INFINITY) ? 0.f : -m_new * c2;
       }
     }
-    float mx = fmaxf(s[0], s[1]);
 #pragma unroll
-    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s[r]);
-    mx = xor32_max(mx);
-    if (__any(mx > m + thr)) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2((m - m_new) * c2);
-      l *= alpha;
+    for (int p = 0; p < PL; ++p) {
+      const __bf16* Vt = &KVs[buf][p][1][0];
 #pragma unroll
-      for (int db = 0; db < DP / 32; ++db)
+      for (int t = 0; t < 2; ++t) {
+        // P in packed bf16 pairs (one v_cvt_pk each), summed by v_dot2 and
+        // reassembled into the B operand without permutes.
+        uint32_t pw[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-      m = m_new;
-      nm = (m == -INFINITY) ? 0.f : -m * c2;
-    }
+        for (int e = 0; e < 4; ++e) {
+          f32x2 f;
+          f[0] = fast_exp2(fmaf(s[p][8 * t + 2 * e], c2, nm[p]));
+          f[1] = fast_exp2(fmaf(s[p][8 * t + 2 * e + 1], c2, nm[p]));
+          const bf16x2 pr = __builtin_convertvector(f, bf16x2);
+          l[p] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l[p], false);
+          pw[e] = __builtin_bit_cast(uint32_t, pr);
+        }
+        u32x4 pwv = {pw[0], pw[1], pw[2], pw[3]};
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pwv);
+        // V^T operand: keys {16t + 4hl .. +3, 16t + 8 + 4hl .. +3} of the
+        // block (the key order of the P^T registers), channel 32 db + ql.
+        const int k0 = sb * 32 + 16 * t;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      // P in packed bf16 pairs (one v_cvt_pk each), summed by v_dot2 and
-      // reassembled into the B operand without permutes.
-      uint32_t pw[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        f32x2 f;
-        f[0] = fast_exp2(fmaf(s[8 * t + 2 * e], c2, nm));
-        f[1] = fast_exp2(fmaf(s[8 * t + 2 * e + 1], c2, nm));
-        const bf16x2 pr = __builtin_convertvector(f, bf16x2);
-        l = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, l, false);
-        pw[e] = __builtin_bit_cast(uint32_t, pr);
-      }
-      u32x4 pwv = {pw[0], pw[1], pw[2], pw[3]};
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, pwv);
-      // The scores are consumed: block blk + 2's bias goes into the same
-      // registers (one register assignment in every iteration, so no copies
-      // that would wait for it).
-      if (t == 1) bset = load_bias(blk + 2);
-      // V^T operand: keys {16t + 4hl .. +3, 16t + 8 + 4hl .. +3} of the
-      // block (the key order of the P^T registers), channel 32 db + ql.
-      const int k0 = sb * 32 + 16 * t;
-#pragma unroll
-      for (int db = 0; db < DP / 32; ++db) {
-        const bf16x8 va = cat8(kv_tr_col4<DP>(Vt, k0, k0 + 4, 32 * db),
-                               kv_tr_col4<DP>(Vt, k0 + 8, k0 + 12, 32 * db));
-        acc[db] = mfma32(va, pb, acc[db]);
+        for (int db = 0; db < DP / 32; ++db) {
+          const bf16x8 va = cat8(kv_tr_col4<DP>(Vt, k0, k0 + 4, 32 * db),
+                                 kv_tr_col4<DP>(Vt, k0 + 8, k0 + 12, 32 * db));
+          acc[p][db] = mfma32(va, pb, acc[p][db]);
+        }
       }
     }
   };
 
-  // Tile t: in LDS buffer t % 2 (written before the barrier); tile t+1 in
-  // `nxt`; tile t+2 loaded into `far` during this tile.
-  auto tile_step = [&](int t, bf16x8* nxt, bf16x8* far) {
-    __syncthreads();
-    const __bf16* Kt = &KVs[t & 1][0][0];
-    const __bf16* Vt = &KVs[t & 1][1][0];
-    const bool masked = (mbits >> (t & 63)) & 1ull;
-    // Waves past N (the last query tile when N % (32 NW) != 0) compute on
-    // zero Q rows and store nothing: no branch splits the loads' register
-    // state.
-    block(Kt, Vt, 0, 2 * t, masked, t * 64, bias_e);
-    load_kv(t + 2, far);
-    block(Kt, Vt, 1, 2 * t + 1, masked, t * 64, bias_o);
-    // Buffer (t+1) % 2 was last read in tile t-1, before the barrier above.
-    store_kv((t + 1) & 1, nxt);
-  };
+  // Tile t: in LDS buffer t % 2 (written before the barrier); tile t+1 is
+  // loaded into registers during the tile's first block and written to the
+  // other buffer at its end.  Waves past N (the last query tile when
+  // N % (32 NW) != 0) compute on zero Q rows and store nothing: no branch
+  // splits the loads' register state.
 #pragma unroll 1
-  for (int t = 0; t < ntiles; t += 2) {
-    tile_step(t, kvr0, kvr1);
-    if (t + 1 < ntiles) tile_step(t + 1, kvr1, kvr0);
+  for (int t = 0; t < ntiles; ++t) {
+    __syncthreads();
+    const bool masked = (mbits >> (t & 63)) & 1ull;
+    block(t & 1, 0, 2 * t, masked, t * 64);
+    load_kv(t + 1, kvr);
+    block(t & 1, 1, 2 * t + 1, masked, t * 64);
+    // Buffer (t+1) % 2 was last read in tile t-1, before the barrier above.
+    store_kv((t + 1) & 1, kvr);
   }
   if (!active) return;
 
-  const float l_tot = xor32_sum(l);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  const int64_t orow_off = (((int64_t)plane * N + qi) * g.H + h) * D;
-  __bf16* orow = out + orow_off;
 #pragma unroll
-  for (int db = 0; db < DP / 32; ++db)
+  for (int p = 0; p < PL; ++p) {
+    if (!pvalid[p]) continue;
+    const float l_tot = xor32_sum(l[p]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const int64_t orow_off = (((int64_t)plane[p] * N + qi) * g.H + h) * D;
+    __bf16* orow = out + orow_off;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = db * 32 + 8 * j + 4 * hl;
-      if (d0 < D) {
-        bf16x4 o4, r4;
+    for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float of = acc[db][4 * j + i] * inv;
-          o4[i] = f2bf(of);
-          // Shadow residual: the part of the f32 output the bf16 store drops.
-          r4[i] = f2bf(of - bf2f(o4[i]));
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = db * 32 + 8 * j + 4 * hl;
+        if (d0 < D) {
+          bf16x4 o4, r4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float of = acc[p][db][4 * j + i] * inv;
+            o4[i] = f2bf(of);
+            // Shadow residual: the part of the f32 output the bf16 store drops.
+            r4[i] = f2bf(of - bf2f(o4[i]));
+          }
+          *reinterpret_cast<bf16x4*>(orow + d0) = o4;
+          if (res) *reinterpret_cast<bf16x4*>(res + orow_off + d0) = r4;
         }
-        *reinterpret_cast<bf16x4*>(orow + d0) = o4;
-        if (res) *reinterpret_cast<bf16x4*>(res + orow_off + d0) = r4;
       }
+    if (hl == 0) {
+      lse[((int64_t)plane[p] * g.H + h) * N + qi] =
+          l_tot > 0.f ? (m[p] * c2 + log2f(l_tot)) * kLn2 : -INFINITY;
     }
-  if (hl == 0) {
-    lse[((int64_t)plane * g.H + h) * N + qi] =
-        l_tot > 0.f ? (m * c2 + log2f(l_tot)) * kLn2 : -INFINITY;
   }
 }
 
@@ -1453,10 +1493,12 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
                              const float* mask, const void* bias, const BiasView& bv,
                              int64_t bias_batches, void* out, float* lse, void* res,
                              void* workspace, hipStream_t s, const char* fn) {
-  // Waves (32 queries each) per workgroup.
-  constexpr int kFwdWaves32 = 4, kFwdWaves64 = 4;
-  const int nw = g.D <= 32 ? kFwdWaves32 : kFwdWaves64;
-  const int64_t total = ((g.N + 32 * nw - 1) / (32 * nw)) * (int64_t)g.H * g.B * g.O;
+  // Waves (32 queries each) per workgroup, and outer rows per wave (planes
+  // sharing one bias load).
+  constexpr int kFwdWaves = 4, kFwdPlanes32 = 2, kFwdPlanes64 = 1;
+  const int pl = g.D <= 32 ? kFwdPlanes32 : kFwdPlanes64;
+  const int64_t total = ((g.N + 32 * kFwdWaves - 1) / (32 * kFwdWaves)) * (int64_t)g.H * g.B *
+                        ((g.O + pl - 1) / pl);
   if ((total + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many query tiles", fn);
   if (g.N > kFwdMaskLdsMaxN)
@@ -1467,17 +1509,15 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   if (rc) return rc;
   g.bias_bstride = (bias_batches == 1) ? 0 : (int64_t)g.H * g.N * g.N;
   dim3 grid((unsigned)((total + 7) / 8 * 8));
-  const unsigned mask_lds = (unsigned)g.N * 4u;
+  const unsigned mask_lds = (unsigned)(pl * g.N) * 4u;
   if (g.D <= 32)
-    hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves32>), grid, dim3(64 * kFwdWaves32), mask_lds, s,
-                       (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
-                       (__bf16*)res, g);
+    hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves, kFwdPlanes32>), grid, dim3(64 * kFwdWaves),
+                       mask_lds, s, (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, mask,
+                       bias_s, (__bf16*)out, lse, (__bf16*)res, g);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves64>), grid, dim3(64 * kFwdWaves64), mask_lds, s,
-                       (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, mask, bias_s, (__bf16*)out, lse,
-                       (__bf16*)res, g);
+    hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves, kFwdPlanes64>), grid, dim3(64 * kFwdWaves),
+                       mask_lds, s, (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, mask,
+                       bias_s, (__bf16*)out, lse, (__bf16*)res, g);
   return check_launch(fn);
 }
 
