@@ -664,6 +664,52 @@ __device__ __forceinline__ bf16x4 qd_tr_col4(const __bf16* M, int rbase_lo, int 
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
 }
 
+// Batched LDS reads for the register-starved backward loop: the reads of a
+// group go out back to back and are waited for once (the compiler, at full
+// register pressure, reuses one destination pair and waits after each read).
+// Outputs are early-clobber so no read overwrites a later read's address.
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+// 16 dwords at a + 256 r (r = 0..15): one lane's column of a [16][64] f32 tile.
+__device__ __forceinline__ u32x16 lds_read_col16(unsigned a) {
+  u32x2 v0, v1, v2, v3, v4, v5, v6, v7;
+  asm volatile(
+      "ds_read2st64_b32 %0, %8 offset1:1\n\t"
+      "ds_read2st64_b32 %1, %8 offset0:2 offset1:3\n\t"
+      "ds_read2st64_b32 %2, %8 offset0:4 offset1:5\n\t"
+      "ds_read2st64_b32 %3, %8 offset0:6 offset1:7\n\t"
+      "ds_read2st64_b32 %4, %8 offset0:8 offset1:9\n\t"
+      "ds_read2st64_b32 %5, %8 offset0:10 offset1:11\n\t"
+      "ds_read2st64_b32 %6, %8 offset0:12 offset1:13\n\t"
+      "ds_read2st64_b32 %7, %8 offset0:14 offset1:15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
+      : "v"(a)
+      : "memory");
+  const u32x2 vs[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+  u32x16 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { r[2 * i] = vs[i][0]; r[2 * i + 1] = vs[i][1]; }
+  return r;
+}
+// 16 bytes (as two 8-byte halves) at each of four 8-byte aligned addresses.
+typedef uint32_t u32x4v __attribute__((__vector_size__(16)));
+__device__ __forceinline__ void lds_read_rows4(u32x4* out, unsigned a0, unsigned a1, unsigned a2,
+                                               unsigned a3) {
+  u32x4v r0, r1, r2, r3;
+  asm volatile(
+      "ds_read2_b64 %0, %4 offset1:1\n\t"
+      "ds_read2_b64 %1, %5 offset1:1\n\t"
+      "ds_read2_b64 %2, %6 offset1:1\n\t"
+      "ds_read2_b64 %3, %7 offset1:1\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+  const u32x4v rs[4] = {r0, r1, r2, r3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = u32x4{rs[i][0], rs[i][1], rs[i][2], rs[i][3]};
+}
+
 template <int DP>
 __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
@@ -889,7 +935,16 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     // This step's loads were issued one step ago; wait for them, read the
     // shared bias fragments and the row statistics, then start the next
     // step's loads so they overlap this step's compute.
-    wait_vmcnt<0>();
+    // Younger than those loads: this wave's previous-step partial loads
+    // (8 read-backs) and stores (8 dBias, plus dQ on key half 0), all issued
+    // by every wave; they may stay in flight (different rows from this
+    // step's).  The first step of a group waits for everything: its setup
+    // loads are younger, and the last group's partial stores must land
+    // before this group reads the same addresses back.
+    if (q0 == 0)
+      wait_vmcnt<0>();
+    else
+      wait_vmcnt<16>();
     lds_barrier();
     f32x16 sinit[2];
 #pragma unroll
@@ -1007,8 +1062,11 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
       for (int db = 0; db < DP / 32; ++db) {
         f32x16 acc = dqacc[db];
         if (KH == 2) {
+          // All 16 values in one batch of LDS reads and one wait (at full
+          // register pressure the compiler issues them one pair at a time).
+          const u32x16 x = lds_read_col16(lds_offset(&Xq[pw][db][0][lane]));
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[r] += Xq[pw][db][r][lane];
+          for (int r = 0; r < 16; ++r) acc[r] += __uint_as_float(x[r]);
         }
         // Lane-pair exchange as for dK / dV below: 16-byte stores of
         // channels 16p + 8hl .. +7 (chunks past D dropped by the range check).
@@ -1046,15 +1104,19 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
       const bf16x2 sel[2] = {__builtin_bit_cast(bf16x2, sel_lo_bits),
                              {static_cast<__bf16>(0.f), static_cast<__bf16>(1.f)}};
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      // The 4 rows' chunks in one batch of LDS reads and one wait.
+      const __bf16* src = dSbase + kw * SSE + (key & 63) * SP + 8 * qb;
+      u32x4 rows[4];
+      lds_read_rows4(rows, lds_offset(src), lds_offset(src + SSE), lds_offset(src + 2 * SSE),
+                     lds_offset(src + 3 * SSE));
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const __bf16* src = dSbase + (kw + ww) * SSE + (key & 63) * SP + 8 * qb;
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(src);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(src + 4);
-        const bf16x2 pr[4] = {{lo[0], lo[1]}, {lo[2], lo[3]}, {hi[0], hi[1]}, {hi[2], hi[3]}};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          acc[e] = __builtin_amdgcn_fdot2_f32_bf16(pr[e >> 1], sel[e & 1], acc[e], false);
+          // (A vector element is copied to a scalar before the bit cast:
+          // hipcc 7.2 folds a bit cast of an element expression to element 0.)
+          acc[e] = __builtin_amdgcn_fdot2_f32_bf16(
+              __builtin_bit_cast(bf16x2, (uint32_t)rows[ww][e >> 1]), sel[e & 1], acc[e], false);
       }
       // The run's partial: earlier groups first, then this group's rows.
 #pragma unroll
