@@ -195,9 +195,11 @@ def _storage_order(t: torch.Tensor) -> str | None:
 # workspace that grows with O * N^2 * H * D / 64: when the full plan exceeds
 # it, the reconstruction kernel runs over slabs of outer rows, each slab's dQ
 # partials folded before the next slab reuses the space.  Results are
-# bitwise equal for every budget.  The default keeps config-5 sized problems
-# (N = 768, H = 8, D = 64: a 7.9 GB full plan) within 4 GiB.
-DEFAULT_SR_WORKSPACE_BUDGET_BYTES = 4 << 30
+# bitwise equal for every budget.  The default (8 GiB of the MI355X's 288 GB)
+# holds config-5 sized problems (N = 768, H = 8, D = 64: a 7.46 GB plan) in
+# one slab; larger problems run in slabs (each slab adds a partly filled
+# round of workgroups: two slabs at that size cost about 13 %).
+DEFAULT_SR_WORKSPACE_BUDGET_BYTES = 8 << 30
 _SR_WORKSPACE_BUDGET = DEFAULT_SR_WORKSPACE_BUDGET_BYTES
 
 

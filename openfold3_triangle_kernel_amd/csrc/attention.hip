@@ -187,7 +187,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const float* __restrict__ mask,
     const float* __restrict__ bias_s, __bf16* __restrict__ out,
-    float* __restrict__ lse, __bf16* __restrict__ res, AttnGeom g) {
+    float* __restrict__ lse, __bf16* __restrict__ res, const __bf16* __restrict__ gate,
+    __bf16* __restrict__ og, AttnGeom g) {
   constexpr int TE = 64 * DP;                  // elements of one K (or V) tile
   constexpr int REG = TE / 8;                  // 16-byte chunks of one K (or V) tile
   constexpr int CPT = 2 * PL * REG / (64 * NW);  // chunks per thread per tile
@@ -455,6 +456,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
           }
           *reinterpret_cast<bf16x4*>(orow + d0) = o4;
           if (res) *reinterpret_cast<bf16x4*>(res + orow_off + d0) = r4;
+          if (gate) {
+            // Output gate of the pair-row module: og = o * sigmoid(g), with g
+            // in Q's storage order (the gate columns of the projection rows).
+            const bf16x4 g4 = ld4(gate + (int64_t)plane[p] * g.s_plane + (int64_t)h * g.s_head +
+                                  (int64_t)qi * g.s_row + d0);
+            bf16x4 og4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) og4[i] = f2bf(bf2f(o4[i]) * sigmoidf(bf2f(g4[i])));
+            *reinterpret_cast<bf16x4*>(og + orow_off + d0) = og4;
+          }
         }
       }
     if (hl == 0) {
@@ -937,11 +948,12 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     // step's loads so they overlap this step's compute.
     // Younger than those loads: this wave's previous-step partial loads
     // (8 read-backs) and stores (8 dBias, plus dQ on key half 0), all issued
-    // by every wave; they may stay in flight (different rows from this
-    // step's).  The first step of a group waits for everything: its setup
-    // loads are younger, and the last group's partial stores must land
-    // before this group reads the same addresses back.
-    if (q0 == 0)
+    // by every wave; with two key halves they may stay in flight (different
+    // rows from this step's; measured faster), with one (D = 64) waiting for
+    // them measured faster.  The first step of a group waits for
+    // everything: its setup loads are younger, and the last group's partial
+    // stores must land before this group reads the same addresses back.
+    if (q0 == 0 || KH == 1)
       wait_vmcnt<0>();
     else
       wait_vmcnt<16>();
@@ -1346,10 +1358,11 @@ __global__ __launch_bounds__(256) void attn_fold_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Output gate of the pair-row module core.  One thread per (pair row,
-// 8-channel chunk), so consecutive lanes touch consecutive 16 bytes:
-//   forward   og = o * sigmoid(g)
-//   backward  d_o = d_og * sigmoid(g),  dg = d_og * o * s * (1 - s), and
+// Output gate of the pair-row module core (the forward applies it in the
+// attention forward's epilogue, og = o * sigmoid(g)).  Backward: one thread
+// per (pair row, 8-channel chunk), so consecutive lanes touch consecutive 16
+// bytes:
+//   d_o = d_og * sigmoid(g),  dg = d_og * o * s * (1 - s), and
 //             delta[b,i,h,j] = sum_d d_o * o (the softmax backward's row term;
 //             the D/8 chunk partials of a head meet in LDS), with o + res when
 //             the forward saved the shadow residual res of o.
@@ -1357,24 +1370,6 @@ __global__ __launch_bounds__(256) void attn_fold_kernel(
 // columns (offset 3*H*D) of the projection rows (row pitch `pitch`).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float gate_sigmoid(float x) { return sigmoidf(x); }
-
-__global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const __bf16* __restrict__ o,
-                                                            const __bf16* __restrict__ gate,
-                                                            int64_t pitch,
-                                                            __bf16* __restrict__ og,
-                                                            int64_t items, FastDiv hc8) {
-  // items < 2^31 (checked on the host): 32-bit item index; element offsets
-  // (8 per item) are formed in 64 bits.
-  const uint32_t t = blockIdx.x * 256u + threadIdx.x;  // (row, chunk)
-  if (t >= (uint32_t)items) return;
-  const uint32_t row = fdiv(t, hc8);
-  const int c = (int)(t - row * hc8.d);
-  const bf16x8 ov = ld8(o + (size_t)t * 8), gv = ld8(gate + (size_t)row * pitch + c * 8);
-  bf16x8 r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = f2bf(bf2f(ov[e]) * gate_sigmoid(bf2f(gv[e])));
-  st8(og + (size_t)t * 8, r);
-}
 
 // Workgroup w takes items [w * per, (w + 1) * per) with per a multiple of
 // D/8, so a head's chunks never straddle two workgroups.
@@ -1554,7 +1549,8 @@ static int attn_prescale_bias(const AttnGeom& g, const void* bias, const BiasVie
 static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const void* v,
                              const float* mask, const void* bias, const BiasView& bv,
                              int64_t bias_batches, void* out, float* lse, void* res,
-                             void* workspace, hipStream_t s, const char* fn) {
+                             void* workspace, hipStream_t s, const char* fn,
+                             const void* gate = nullptr, void* og = nullptr) {
   // Waves (32 queries each) per workgroup, and outer rows per wave (planes
   // sharing one bias load).
   constexpr int kFwdWaves = 4, kFwdPlanes32 = 2, kFwdPlanes64 = 1;
@@ -1575,11 +1571,13 @@ static int attn_forward_impl(AttnGeom g, const void* q, const void* k, const voi
   if (g.D <= 32)
     hipLaunchKernelGGL((attn_fwd_kernel<32, kFwdWaves, kFwdPlanes32>), grid, dim3(64 * kFwdWaves),
                        mask_lds, s, (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, mask,
-                       bias_s, (__bf16*)out, lse, (__bf16*)res, g);
+                       bias_s, (__bf16*)out, lse, (__bf16*)res, (const __bf16*)gate, (__bf16*)og,
+                       g);
   else
     hipLaunchKernelGGL((attn_fwd_kernel<64, kFwdWaves, kFwdPlanes64>), grid, dim3(64 * kFwdWaves),
                        mask_lds, s, (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, mask,
-                       bias_s, (__bf16*)out, lse, (__bf16*)res, g);
+                       bias_s, (__bf16*)out, lse, (__bf16*)res, (const __bf16*)gate, (__bf16*)og,
+                       g);
   return check_launch(fn);
 }
 
@@ -1675,8 +1673,17 @@ static BwdPlan bwd_plan(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D, i
       hi = mid - 1;
   }
   if (lo == 0) { p.per = 0; p.slabs = 0; return p; }
-  p.slabs = (fr + lo - 1) / lo;
-  p.per = (fr + p.slabs - 1) / p.slabs;
+  // Among the slab sizes that fit, the one with the fewest rounds of
+  // workgroups over a 256-CU device (a slab's last round may be partly
+  // empty), then the largest.
+  const int64_t wpr = H * bwd_key_blocks(N, D);  // workgroups per run
+  int64_t best_rounds = INT64_MAX;
+  for (int per = lo; per >= 1; --per) {
+    const int slabs = (fr + per - 1) / per, last = fr - (slabs - 1) * per;
+    const int64_t rounds = (int64_t)(slabs - 1) * ((per * wpr + kBwdPlanCus - 1) / kBwdPlanCus) +
+                           (last * wpr + kBwdPlanCus - 1) / kBwdPlanCus;
+    if (rounds < best_rounds) { best_rounds = rounds; p.per = per; p.slabs = slabs; }
+  }
   return p;
 }
 // Slab s of a plan: its flattened runs and the contiguous planes they cover.
@@ -2124,16 +2131,9 @@ int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mas
   hipStream_t s = (hipStream_t)stream;
   if (residual && (uintptr_t)residual % 16)
     return set_error(TPF_ERR_ARG, "%s: residual must be 16-byte aligned", fn);
-  if ((rc = attn_forward_impl(g, p, p + hc, p + 2 * hc, mask, p + 4 * hc, bv, B, o, lse,
-                              residual, workspace, s, fn)))
-    return rc;
-  const int64_t items = B * N * N * (hc / 8);
-  if (items >= (int64_t)kBufOOB - 256)
-    return set_error(TPF_ERR_SHAPE, "%s: %lld gate chunks exceed 2^31", fn, (long long)items);
-  hipLaunchKernelGGL(attn_gate_fwd_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
-                     (const __bf16*)o, p + 3 * hc, pitch, (__bf16*)og, items,
-                     make_fastdiv((uint32_t)(hc / 8)));
-  return check_launch(fn);
+  // The forward's epilogue applies the output gate (og = o * sigmoid(g)).
+  return attn_forward_impl(g, p, p + hc, p + 2 * hc, mask, p + 4 * hc, bv, B, o, lse, residual,
+                           workspace, s, fn, p + 3 * hc, og);
 }
 
 // Workspace: the attention backward's, then d_o [B, N, N, H*D] bf16 and

@@ -106,6 +106,26 @@ def _wgrad(dy2: torch.Tensor, x2: torch.Tensor, dtype: torch.dtype) -> torch.Ten
     return dw32.to(dtype)
 
 
+def _mm(a: torch.Tensor, b: torch.Tensor, b_kc: bool) -> torch.Tensor:
+    """Row GEMM of the pair-row modules on the bf16 MFMA GEMM
+    (``tpf_gemm_bf16``): ``a [R, K] @ b.t()`` for ``b [N, K]`` (b_kc) or
+    ``a @ b`` for ``b [K, N]``, f32 accumulation, bf16 out.  Operands are
+    made contiguous; a feature size that is not a multiple of 8 (16-byte
+    rows) takes torch's matmul."""
+    a = a.contiguous()
+    b = b.contiguous()
+    R, K = a.shape
+    N = b.shape[0] if b_kc else b.shape[1]
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or K % 8 or N % 8:
+        return a @ (b.t() if b_kc else b)
+    out = torch.empty((R, N), device=a.device, dtype=torch.bfloat16)
+    with _device_ctx(a.device):
+        _native.call("tpf_gemm_bf16", a.data_ptr(), 1, K, 0, b.data_ptr(), int(b_kc),
+                     b.stride(0), 0, out.data_ptr(), 0, N, 0, R, N, K, 1, 1.0,
+                     _native.stream_of(a))
+    return out
+
+
 class _PairAttentionCore(torch.autograd.Function):
     """Projection -> triangle attention -> gate -> output projection of the
     triangle-attention module over BF16 pair rows, with explicit buffers.
@@ -127,7 +147,7 @@ class _PairAttentionCore(torch.autograd.Function):
         x2 = x.reshape(R, C)
         wa = w_all.to(torch.bfloat16)
         wo = w_o.to(torch.bfloat16)
-        proj = x2 @ wa.t()
+        proj = _mm(x2, wa, True)
         o = torch.empty((R, hc), device=dev, dtype=torch.bfloat16)
         og = torch.empty_like(o)
         lse = torch.empty((B, N, H, N), device=dev, dtype=torch.float32)
@@ -142,7 +162,7 @@ class _PairAttentionCore(torch.autograd.Function):
                          int(transpose_bias), o.data_ptr(), lse.data_ptr(), og.data_ptr(),
                          _native.ptr(res), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
                          _native.stream_of(proj))
-        out = og @ wo.t()
+        out = _mm(og, wo, True)
         ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add, res)
         ctx.dims = (B, N, H, D, C, P, bool(transpose_bias), scale)
         ctx.w_dtypes = (w_all.dtype, w_o.dtype)
@@ -158,7 +178,7 @@ class _PairAttentionCore(torch.autograd.Function):
         R = B * N * N
         dev = x2.device
         dout2 = dout.reshape(R, C).to(torch.bfloat16).contiguous()
-        d_og = dout2 @ wo
+        d_og = _mm(dout2, wo, False)
         dw_o = _wgrad(dout2, og, ctx.w_dtypes[1]) if ctx.needs_input_grad[2] else None
         dproj = torch.empty((R, P), device=dev, dtype=torch.bfloat16)
         ws_bytes = int(_native.query("tpf_attn_pair_backward_workspace_bytes", B, N, H, D))
@@ -169,7 +189,7 @@ class _PairAttentionCore(torch.autograd.Function):
                          d_og.data_ptr(), dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D,
                          scale,
                          _native.stream_of(dproj))
-        dx = (dproj @ wa).view(B, N, N, C) if ctx.needs_input_grad[0] else None
+        dx = _mm(dproj, wa, False).view(B, N, N, C) if ctx.needs_input_grad[0] else None
         dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None
         return dx, dw_all, dw_o, None, None, None, None
 
@@ -183,14 +203,15 @@ class _ProjLinear(torch.autograd.Function):
         wb = w.to(x.dtype)
         ctx.save_for_backward(x, wb)
         ctx.w_dtype = w.dtype
-        return x @ wb.t()
+        return _mm(x.reshape(-1, x.shape[-1]), wb, True).view(*x.shape[:-1], wb.shape[0])
 
     @staticmethod
     def backward(ctx, dy):
         x, wb = ctx.saved_tensors
         dx = dw = None
         if ctx.needs_input_grad[0]:
-            dx = dy @ wb
+            dx = _mm(dy.reshape(-1, dy.shape[-1]).to(torch.bfloat16), wb, False).view(
+                *dy.shape[:-1], wb.shape[1])
         if ctx.needs_input_grad[1]:
             M, K = wb.shape
             dy2 = dy.reshape(-1, M).to(torch.bfloat16).contiguous()
