@@ -56,7 +56,7 @@ def parse():
                          "pair-stack block through the modules); for profiling runs whose kernel "
                          "trace should hold only the config-3 / config-4 launches")
     ap.add_argument("--kernel-reps", type=int, default=20)
-    ap.add_argument("--probe", choices=("attention", "trimul"),
+    ap.add_argument("--probe", choices=("attention", "trimul", "pair-block"),
                     help="launch a 256 MiB calibration copy, then two fwd+bwd passes of one path "
                          "(attention: config 3 starting node; trimul: config 4 outgoing + incoming) "
                          "six times and exit: the program that the per-kernel rocprofv3 counter passes "
@@ -109,6 +109,45 @@ def trimul_inputs(torch, dev, seed=1):
     return z, wts, mask, dout
 
 
+def pair_block_setup(torch, dev):
+    """Config 5's pair block through the drop-in modules (TriMul out, TriMul
+    in, triangle attention starting and ending node, residual adds) at
+    N = 768, C = 128, H = 4, D = 32; returns its fwd+bwd step and the state
+    that keeps its tensors alive."""
+    from openfold3_triangle_kernel_amd import (
+        TriangleAttention,
+        TriangleMultiplicationIncoming,
+        TriangleMultiplicationOutgoing,
+    )
+
+    torch.manual_seed(5)
+    Np, Cz = 768, 128
+    mods = [TriangleMultiplicationOutgoing(Cz, Cz), TriangleMultiplicationIncoming(Cz, Cz),
+            TriangleAttention(Cz, 32, 4, starting=True), TriangleAttention(Cz, 32, 4, starting=False)]
+    for mo in mods:
+        for prm in mo.parameters():
+            if prm.dim() == 2:
+                torch.nn.init.normal_(prm, std=1.0 / math.sqrt(prm.shape[1]))
+    mods = [mo.to(dev, torch.bfloat16) for mo in mods]
+    zp = torch.randn(1, Np, Np, Cz, device=dev).to(torch.bfloat16).requires_grad_(True)
+    mp = torch.ones(1, Np, Np, device=dev, dtype=torch.bfloat16)
+    params = [zp] + [prm for mo in mods for prm in mo.parameters()]
+
+    # A fixed upstream gradient (seeded N(0,1) bf16) drives the backward, as
+    # the measurement rules allow (autograd.grad with a fixed grad_out): the
+    # block is timed without an FP32 loss's elementwise passes.
+    g = torch.Generator(device=dev).manual_seed(6)
+    dh = torch.randn(1, Np, Np, Cz, device=dev, generator=g).to(torch.bfloat16)
+
+    def block_step():
+        h = zp
+        for mo in mods:
+            h = h + mo(h, mp)
+        torch.autograd.grad(h, params, dh)
+
+    return block_step, (zp, mods, params, dh)
+
+
 def probe(torch, dev, target):
     """Calibration copy (256 MiB read + 256 MiB written), then six fwd+bwd
     passes of one path, for per-kernel counter passes (the last pass runs
@@ -120,7 +159,11 @@ def probe(torch, dev, target):
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    if target == "attention":
+    if target == "pair-block":
+        block_step, _state = pair_block_setup(torch, dev)
+        for _ in range(PROBE_PASSES):
+            block_step()
+    elif target == "attention":
         q, k, v, bias, mask, dout = attention_inputs(torch, dev)
         xs = [t.detach().requires_grad_(True) for t in (q, k, v, bias)]
         for _ in range(PROBE_PASSES):
@@ -392,41 +435,17 @@ def main():
     # ------------- config 5: pair-stack block at N=768 (modules) -----------
     pair_block = None
     if not args.no_config5:
-        from openfold3_triangle_kernel_amd import (
-            TriangleAttention,
-            TriangleMultiplicationIncoming,
-            TriangleMultiplicationOutgoing,
-        )
-
-        torch.manual_seed(5)
-        Np, Cz = 768, 128
-        mods = [TriangleMultiplicationOutgoing(Cz, Cz), TriangleMultiplicationIncoming(Cz, Cz),
-                TriangleAttention(Cz, 32, 4, starting=True), TriangleAttention(Cz, 32, 4, starting=False)]
-        for mo in mods:
-            for prm in mo.parameters():
-                if prm.dim() == 2:
-                    torch.nn.init.normal_(prm, std=1.0 / math.sqrt(prm.shape[1]))
-        mods = [mo.to(dev, torch.bfloat16) for mo in mods]
-        zp = torch.randn(1, Np, Np, Cz, device=dev).to(torch.bfloat16).requires_grad_(True)
-        mp = torch.ones(1, Np, Np, device=dev, dtype=torch.bfloat16)
-        params = [zp] + [prm for mo in mods for prm in mo.parameters()]
-
-        def block_step():
-            h = zp
-            for mo in mods:
-                h = h + mo(h, mp)
-            torch.autograd.grad(h.float().square().mean(), params)
-
+        block_step, pb_state = pair_block_setup(torch, dev)
         blk_ms = gpu_time(torch, block_step, max(10, args.steps // 4), 3)["median"]
         pair_block = {
             "ms_fwd_bwd": round(blk_ms, 3),
-            "config": {"N": Np, "C": Cz, "blocks": ["trimul_out", "trimul_in", "tri_att_start",
+            "config": {"N": 768, "C": 128, "blocks": ["trimul_out", "trimul_in", "tri_att_start",
                                                       "tri_att_end"], "H": 4, "D": 32},
             "note": "config 5: residual pair block through the drop-in modules (bf16 params; "
-                    "LayerNorm, fused q/k/v/g/bias projection, attention core and TriMul in the "
-                    "HIP kernels, linear_o and the residual adds in torch)",
+                    "LayerNorm, projections, attention core, gate and TriMul in the HIP kernels, "
+                    "the residual adds in torch); backward driven by a fixed bf16 grad_out",
         }
-        del zp, mods, params
+        del pb_state
 
     # -------------------------- CPU baseline -----------------------------
     cpu = None

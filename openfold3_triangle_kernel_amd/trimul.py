@@ -350,8 +350,8 @@ def run_stable_trimul(module, z, mask):
         module.linear_a_p.weight, module.linear_a_g.weight,
         module.linear_b_p.weight, module.linear_b_g.weight,
         module.linear_g.weight, module.linear_z.weight,
-        module.layer_norm_in.weight.float(), module.layer_norm_in.bias.float(),
-        module.layer_norm_out.weight.float(), module.layer_norm_out.bias.float(),
+        module.layer_norm_in.weight, module.layer_norm_in.bias,
+        module.layer_norm_out.weight, module.layer_norm_out.bias,
         bool(module._outgoing),
     )
 
