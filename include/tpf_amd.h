@@ -277,6 +277,24 @@ int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap,
                            double ln_out_eps, int outgoing, int64_t B, int64_t N, int64_t C,
                            int64_t H, float* out, void* workspace, int64_t workspace_bytes,
                            void* stream);
+/* tpf_trimul_forward_f32 with the contraction, LN_out and output projection
+ * run over chunks of row_chunk output rows i (per batch item), so the product
+ * scratch is [H, row_chunk, N] instead of [B, H, N, N]; the outputs are
+ * bitwise those of the unchunked call.  Replaces the output_row_chunk_size
+ * path of run_trimul_fp32
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_trimul_fp32.py:203-221,344-345). */
+int64_t tpf_trimul_forward_f32_workspace_bytes_chunked(int64_t B, int64_t N, int64_t C, int64_t H,
+                                                       int64_t row_chunk);
+int tpf_trimul_forward_f32_chunked(const float* z, const float* mask, const float* w_ap,
+                                   const float* w_ag, const float* w_bp, const float* w_bg,
+                                   const float* w_g, const float* w_z, const float* b_ap,
+                                   const float* b_ag, const float* b_bp, const float* b_bg,
+                                   const float* b_g, const float* b_z, const float* ln_in_w,
+                                   const float* ln_in_b, double ln_in_eps, const float* ln_out_w,
+                                   const float* ln_out_b, double ln_out_eps, int outgoing,
+                                   int64_t B, int64_t N, int64_t C, int64_t H, int64_t row_chunk,
+                                   float* out, void* workspace, int64_t workspace_bytes,
+                                   void* stream);
 
 /* Batched bf16 MFMA GEMM C[z] = alpha * A[z] B[z]^T with each operand
  * K-contiguous (x_kc = 1: X[r*ld + k]) or MN-contiguous (0: X[k*ld + r]);

@@ -93,6 +93,11 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P] * 16 + [_F64, _P, _P, _F64, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _P],
     ),
+    "tpf_trimul_forward_f32_workspace_bytes_chunked": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "tpf_trimul_forward_f32_chunked": (
+        _I32,
+        [_P] * 16 + [_F64, _P, _P, _F64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P],
+    ),
     "tpf_wgrad_bf16_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "tpf_wgrad_bf16": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "tpf_trimul_wgrad_fixed_fold": (_I32, [_P, _I64, _I64, _P, _I32, _P]),

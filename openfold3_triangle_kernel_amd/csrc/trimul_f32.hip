@@ -552,7 +552,10 @@ struct Tm32Work {
   float *wp, *bp, *wz, *bz, *zln, *gate, *a, *b, *x, *xln;
 };
 
-static int64_t tm32_layout(const Tm32Geom& g, char* base, Tm32Work* w) {
+// Workspace: packed weights, zln and gate logits [R, C4], the a and b
+// planes [B, H, N, Np], and the product and its LayerNorm for one chunk of
+// output rows: x [H, rows, Np], xln [rows * N, H4] (rows = row_chunk).
+static int64_t tm32_layout(const Tm32Geom& g, int64_t row_chunk, char* base, Tm32Work* w) {
   const int64_t wp_rows = (int64_t)(2 * g.ntg + g.ntgo) * 128;
   const int64_t planes = (int64_t)g.B * g.H * g.PS;
   int64_t off = 0;
@@ -566,44 +569,52 @@ static int64_t tm32_layout(const Tm32Geom& g, char* base, Tm32Work* w) {
   t.gate = take(g.R * g.C4 * 4);
   t.a = take(planes * 4);
   t.b = take(planes * 4);
-  t.x = take(planes * 4);
-  t.xln = take(g.R * g.H4 * 4);
+  t.x = take((int64_t)g.H * row_chunk * g.Np * 4);
+  t.xln = take(row_chunk * g.N * g.H4 * 4);
   if (w) *w = t;
   return off;
 }
 
 extern "C" {
 
-int64_t tpf_trimul_forward_f32_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t H) {
+int64_t tpf_trimul_forward_f32_workspace_bytes_chunked(int64_t B, int64_t N, int64_t C, int64_t H,
+                                                       int64_t row_chunk) {
   Tm32Geom g;
   if (tm32_geom(&g, B, N, C, H, 1, "tpf_trimul_forward_f32_workspace_bytes")) return -1;
-  return tm32_layout(g, nullptr, nullptr);
+  if (row_chunk < 1) return -1;
+  return tm32_layout(g, row_chunk < N ? row_chunk : N, nullptr, nullptr);
 }
 
-int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap, const float* w_ag,
+int64_t tpf_trimul_forward_f32_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t H) {
+  return tpf_trimul_forward_f32_workspace_bytes_chunked(B, N, C, H, N);
+}
+
+int tpf_trimul_forward_f32_chunked(const float* z, const float* mask, const float* w_ap, const float* w_ag,
                            const float* w_bp, const float* w_bg, const float* w_g,
                            const float* w_z, const float* b_ap, const float* b_ag,
                            const float* b_bp, const float* b_bg, const float* b_g,
                            const float* b_z, const float* ln_in_w, const float* ln_in_b,
                            double ln_in_eps, const float* ln_out_w, const float* ln_out_b,
                            double ln_out_eps, int outgoing, int64_t B, int64_t N, int64_t C,
-                           int64_t H, float* out, void* workspace, int64_t workspace_bytes,
-                           void* stream) {
+                           int64_t H, int64_t row_chunk, float* out, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
   const char* fn = "tpf_trimul_forward_f32";
   Tm32Geom g;
   int rc = tm32_geom(&g, B, N, C, H, outgoing, fn);
   if (rc) return rc;
+  if (row_chunk < 1) return set_error(TPF_ERR_ARG, "%s: row_chunk must be positive", fn);
+  if (row_chunk > N) row_chunk = N;
   if (!z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !out || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   if (!(ln_in_eps > 0) || !(ln_out_eps > 0))
     return set_error(TPF_ERR_ARG, "%s: LayerNorm eps must be positive", fn);
-  const int64_t need = tm32_layout(g, nullptr, nullptr);
+  const int64_t need = tm32_layout(g, row_chunk, nullptr, nullptr);
   if (workspace_bytes < need)
     return set_error(TPF_ERR_ARG, "%s: workspace %lld < required %lld", fn,
                      (long long)workspace_bytes, (long long)need);
   hipStream_t s = (hipStream_t)stream;
   Tm32Work wk;
-  tm32_layout(g, (char*)workspace, &wk);
+  tm32_layout(g, row_chunk, (char*)workspace, &wk);
   Tm32Weights w{{w_ap, w_ag, w_bp, w_bg, w_g, w_z}, {b_ap, b_ag, b_bp, b_bg, b_g, b_z}};
   hipLaunchKernelGGL(tm32_pack_kernel, dim3(1024), dim3(256), 0, s, w, wk.wp, wk.bp, wk.wz, wk.bz, g);
   if ((rc = check_launch(fn))) return rc;
@@ -635,30 +646,57 @@ int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap,
   hipLaunchKernelGGL(tm32_in_proj_kernel, dim3((unsigned)((ptiles + 7) / 8 * 8)), dim3(256), 0, s,
                      wk.zln, wk.wp, wk.bp, mask, wk.a, wk.b, wk.gate, g);
   if ((rc = check_launch(fn))) return rc;
-  GemmArgsF32 ga{};
-  ga.A = wk.a; ga.a_ld = g.Np; ga.a_bs = g.PS;
-  ga.B = wk.b; ga.b_ld = g.Np; ga.b_bs = g.PS;
-  ga.C = wk.x; ga.c_ld = g.Np; ga.c_bs = g.PS;
-  ga.M = g.N; ga.N = g.N; ga.K = g.Np; ga.alpha = 1.f; ga.bias = nullptr;
-  if ((rc = gemm_f32_launch(ga, 1, 1, (int)(B * H), s, "tpf_trimul_forward_f32(contract)")))
-    return rc;
-  if (N % 4 == 0 && g.Np % 4 == 0 && H <= 128)
-    hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<8>, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
-                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
-  else if (N % 4 == 0 && g.Np % 4 == 0 && H <= 256)
-    hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<16>, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
-                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
-  else if (N % 4 == 0 && g.Np % 4 == 0)
-    hipLaunchKernelGGL(tm32_ln_planes_vec_kernel, dim3((unsigned)((g.NN + 63) / 64), (unsigned)B),
-                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
-  else
-    hipLaunchKernelGGL(tm32_ln_planes_kernel, dim3((unsigned)((g.NN + 31) / 32), (unsigned)B),
-                       dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, g);
-  if ((rc = check_launch(fn))) return rc;
-  const int64_t otiles = tiles * ((C + 127) / 128);
-  hipLaunchKernelGGL(tm32_out_proj_kernel, dim3((unsigned)((otiles + 7) / 8 * 8)), dim3(256), 0, s,
-                     wk.xln, wk.wz, wk.bz, wk.gate, out, g);
-  return check_launch(fn);
+  // Contraction, LN_out and the output projection over chunks of output
+  // rows i (every element keeps its full K = N reduction and its own
+  // LayerNorm and projection: the results do not depend on the chunking).
+  for (int64_t bb = 0; bb < B; ++bb) {
+    for (int64_t i0 = 0; i0 < N; i0 += row_chunk) {
+      const int64_t rows = N - i0 < row_chunk ? N - i0 : row_chunk;
+      GemmArgsF32 ga{};
+      ga.A = wk.a + bb * g.H * g.PS + i0 * g.Np; ga.a_ld = g.Np; ga.a_bs = g.PS;
+      ga.B = wk.b + bb * g.H * g.PS; ga.b_ld = g.Np; ga.b_bs = g.PS;
+      ga.C = wk.x; ga.c_ld = g.Np; ga.c_bs = rows * g.Np;
+      ga.M = (int)rows; ga.N = g.N; ga.K = g.Np; ga.alpha = 1.f; ga.bias = nullptr;
+      if ((rc = gemm_f32_launch(ga, 1, 1, (int)H, s, "tpf_trimul_forward_f32(contract)"))) return rc;
+      // The chunk as a one-batch problem of rows * N positions.
+      Tm32Geom gc = g;
+      gc.B = 1; gc.NN = rows * N; gc.PS = rows * g.Np; gc.R = rows * N;
+      const int64_t r0 = bb * g.NN + i0 * N;  // first pair row of the chunk
+      if (N % 4 == 0 && g.Np % 4 == 0 && H <= 128)
+        hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<8>, dim3((unsigned)((gc.NN + 63) / 64), 1u),
+                           dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, gc);
+      else if (N % 4 == 0 && g.Np % 4 == 0 && H <= 256)
+        hipLaunchKernelGGL(tm32_ln_planes_reg_kernel<16>, dim3((unsigned)((gc.NN + 63) / 64), 1u),
+                           dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, gc);
+      else if (N % 4 == 0 && g.Np % 4 == 0)
+        hipLaunchKernelGGL(tm32_ln_planes_vec_kernel, dim3((unsigned)((gc.NN + 63) / 64), 1u),
+                           dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, gc);
+      else
+        hipLaunchKernelGGL(tm32_ln_planes_kernel, dim3((unsigned)((gc.NN + 31) / 32), 1u),
+                           dim3(256), 0, s, wk.x, ln_out_w, ln_out_b, (float)ln_out_eps, wk.xln, gc);
+      if ((rc = check_launch(fn))) return rc;
+      const int64_t otiles = (gc.R + 127) / 128 * ((C + 127) / 128);
+      hipLaunchKernelGGL(tm32_out_proj_kernel, dim3((unsigned)((otiles + 7) / 8 * 8)), dim3(256), 0,
+                         s, wk.xln, wk.wz, wk.bz, wk.gate + r0 * g.C4, out + r0 * C, gc);
+      if ((rc = check_launch(fn))) return rc;
+    }
+  }
+  return TPF_OK;
+}
+
+int tpf_trimul_forward_f32(const float* z, const float* mask, const float* w_ap, const float* w_ag,
+                           const float* w_bp, const float* w_bg, const float* w_g,
+                           const float* w_z, const float* b_ap, const float* b_ag,
+                           const float* b_bp, const float* b_bg, const float* b_g,
+                           const float* b_z, const float* ln_in_w, const float* ln_in_b,
+                           double ln_in_eps, const float* ln_out_w, const float* ln_out_b,
+                           double ln_out_eps, int outgoing, int64_t B, int64_t N, int64_t C,
+                           int64_t H, float* out, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  return tpf_trimul_forward_f32_chunked(z, mask, w_ap, w_ag, w_bp, w_bg, w_g, w_z, b_ap, b_ag,
+                                        b_bp, b_bg, b_g, b_z, ln_in_w, ln_in_b, ln_in_eps, ln_out_w,
+                                        ln_out_b, ln_out_eps, outgoing, B, N, C, H, N, out,
+                                        workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

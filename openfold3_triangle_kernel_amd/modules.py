@@ -219,12 +219,34 @@ class _ProjLinear(torch.autograd.Function):
         return dx, dw
 
 
+def _mm_f32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a [R, K] @ b.t()`` for FP32 ``b [N, K]`` on the FP32 MFMA GEMM
+    (``tpf_gemm_f32``, strict FP32: no TF32-style rounding)."""
+    a = a.contiguous()
+    b = b.contiguous()
+    R, K = a.shape
+    N = b.shape[0]
+    out = torch.empty((R, N), device=a.device, dtype=torch.float32)
+    with _device_ctx(a.device):
+        _native.call("tpf_gemm_f32", a.data_ptr(), 1, K, 0, b.data_ptr(), 1, K, 0, out.data_ptr(),
+                     N, 0, R, N, K, 1, 1.0, None, _native.stream_of(a))
+    return out
+
+
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """Projection over the pair rows: the split-K weight gradient for BF16
-    activations whose feature sizes are multiples of 8, torch otherwise."""
-    if (x.dtype == torch.bfloat16 and x.is_cuda and w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0
-            and torch.is_grad_enabled()):
-        return _ProjLinear.apply(x, w)
+    """Projection over the pair rows on the MFMA GEMMs: BF16 activations
+    (feature sizes multiples of 8) with the split-K weight gradient under
+    autograd, FP32 inference on the FP32 GEMM; anything else (CPU, other
+    dtypes or sizes) takes torch.  Each output row depends only on its input
+    row, so row chunks give the same bits."""
+    if x.is_cuda and x.numel() > 0 and w.shape[0] % 8 == 0 and w.shape[1] % 8 == 0:
+        if x.dtype == torch.bfloat16:
+            if torch.is_grad_enabled():
+                return _ProjLinear.apply(x, w)
+            y = _mm(x.reshape(-1, x.shape[-1]), w.to(torch.bfloat16), True)
+            return y.view(*x.shape[:-1], w.shape[0])
+        if x.dtype == torch.float32 and not torch.is_grad_enabled() and w.dtype == torch.float32:
+            return _mm_f32(x.reshape(-1, x.shape[-1]), w).view(*x.shape[:-1], w.shape[0])
     return nn.functional.linear(x, w.to(x.dtype))
 
 
@@ -268,8 +290,11 @@ class TriangleAttention(nn.Module):
                 use_protenix_triangle_attention: bool = False) -> torch.Tensor:
         """x: [*, I, J, C_in]; mask: [*, I, J] (1 keep, 0 drop).
 
-        ``chunk_size`` and ``inplace_safe`` only bound memory in the reference;
-        one MI355X holds the whole problem, so both are accepted and unused.
+        ``chunk_size`` (inference only on the stable route, as the reference's
+        ``triangular_attention.py:114-158, 322-327``) runs the projections,
+        attention, gate and output projection over chunks of outer rows with
+        the full pair bias; the output is bitwise the unchunked one.
+        ``inplace_safe`` only saves memory in the reference and is accepted.
         """
         _reject_backends(use_deepspeed_evo_attention=use_deepspeed_evo_attention,
                          use_cueq_triangle_kernels=use_cueq_triangle_kernels,
@@ -282,7 +307,15 @@ class TriangleAttention(nn.Module):
             x = x.transpose(-2, -3)
             mask = mask.transpose(-1, -2)
         if self._stable_route(x, use_stable_triangle_attention):
-            out = self._stable_forward(x, mask, transpose_bias)
+            if chunk_size is not None:
+                if chunk_size < 1:
+                    raise ValueError("chunk_size must be positive")
+                if torch.is_grad_enabled() and (x.requires_grad or any(
+                        p.requires_grad for p in self.parameters())):
+                    raise ValueError(
+                        "stable Triangle Attention chunking is inference-only; "
+                        "use eval() with gradients disabled outside checkpointing")
+            out = self._stable_forward(x, mask, transpose_bias, chunk_size)
         else:
             out = self._stock_forward(x, mask, transpose_bias)
         if not self.starting:
@@ -335,11 +368,13 @@ class TriangleAttention(nn.Module):
         g = torch.sigmoid(_stock_linear(m.linear_g, x)).reshape(o.shape)
         return _stock_linear(m.linear_o, (o * g).flatten(-2))
 
-    def _stable_forward(self, x, mask, transpose_bias):
+    def _stable_forward(self, x, mask, transpose_bias, chunk_size=None):
         x = _layer_norm(self.layer_norm, x)
         mask_bias = (self.inf * (mask.float() - 1))[..., :, None, None, :]
         m = self.mha
         H, c = m.no_heads, m.c_hidden
+        if chunk_size is not None and chunk_size < x.shape[-3]:
+            return self._chunked_forward(x, mask_bias, transpose_bias, chunk_size)
         # One projection GEMM for q, k, v, the gate and the pair bias.  Rows are
         # padded to a multiple of 64 outputs (128-byte aligned projection rows
         # for the pair-row core) or of 8 (per-projection route); the pad
@@ -372,18 +407,68 @@ class TriangleAttention(nn.Module):
             return t.reshape(t.shape[:-1] + (H, c)).transpose(-2, -3)
 
         q, k, v = heads(qp), heads(kp), heads(vp)
-        if _fp32_inference(x):
-            o = turbopairformer_attention_fp32(q, k, v, mask_bias, tri_bias.float())
-        else:
-            args = (q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
-                    tri_bias.to(torch.bfloat16))
-            ok, reason = is_turbopairformer_supported(*args)
-            if not ok:
-                routing.report_fallback(type(self).__qualname__, tuple(q.shape), reason)
-                return self._stock_forward_from_ln(x, mask_bias, tri_bias, q, k, v, gp)
-            o = turbopairformer_triangle_attention(*args).to(x.dtype)
+        o = self._attend(q, k, v, mask_bias, tri_bias, x.dtype, _fp32_inference(x))
+        if o is None:
+            return self._stock_forward_from_ln(x, mask_bias, tri_bias, q, k, v, gp)
         g = torch.sigmoid(gp).reshape(o.shape)
         return _linear((o * g).flatten(-2), m.linear_o.weight)
+
+    def _attend(self, q, k, v, mask_bias, tri_bias, x_dtype, fp32_inference):
+        """Attention core on sequence-major q / k / v views (or None when the
+        bf16 kernel's verdict rejects the case)."""
+        if fp32_inference:
+            return turbopairformer_attention_fp32(q, k, v, mask_bias, tri_bias.float())
+        args = (q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), mask_bias,
+                tri_bias.to(torch.bfloat16))
+        ok, reason = is_turbopairformer_supported(*args)
+        if not ok:
+            routing.report_fallback(type(self).__qualname__, tuple(q.shape), reason)
+            return None
+        return turbopairformer_triangle_attention(*args).to(x_dtype)
+
+    def _chunked_forward(self, x, mask_bias, transpose_bias, chunk_size):
+        """Inference over chunks of outer rows (reference ``_chunk_stable``,
+        ``triangular_attention.py:114-158``): the pair bias of every pair is
+        projected once; each chunk projects its rows' q / k / v / gate, runs
+        attention over its planes with the full bias, gates and projects its
+        output rows.  Per-row GEMMs and per-plane attention make the output
+        bitwise that of the unchunked call."""
+        m = self.mha
+        H, c = m.no_heads, m.c_hidden
+        hc = H * c
+        outer = x.shape[-3]
+        zb = _linear(x, self.linear_z.weight) if H % 8 == 0 else None
+        if zb is None:  # pad the bias projection to 8 outputs (16-byte rows)
+            wz = torch.cat([self.linear_z.weight,
+                            self.linear_z.weight.new_zeros((-H) % 8, self.c_in)])
+            zb = _linear(x, wz)[..., :H]
+        perm = (-1, -2, -3) if transpose_bias else (-1, -3, -2)
+        tri_bias = zb.permute(*range(zb.dim() - 3), *(zb.dim() + p for p in perm)).unsqueeze(-4)
+        w_qkvg = torch.cat([m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
+                            m.linear_g.weight])
+        fp32_inf = _fp32_inference(x)
+
+        def heads(t):  # [*, I, J, H*c] -> [*, I, H, J, c]
+            return t.reshape(t.shape[:-1] + (H, c)).transpose(-2, -3)
+
+        out = None
+        for start in range(0, outer, chunk_size):
+            rows = slice(start, min(start + chunk_size, outer))
+            xs = x[..., rows, :, :]
+            proj = _linear(xs, w_qkvg)
+            qp, kp, vp, gp = torch.split(proj, [hc, hc, hc, hc], -1)
+            q, k, v = heads(qp), heads(kp), heads(vp)
+            mb = mask_bias[..., rows, :, :, :]
+            o = self._attend(q, k, v, mb, tri_bias, x.dtype, fp32_inf)
+            if o is None:
+                o_rows = self._stock_forward_from_ln(xs, mb, tri_bias, q, k, v, gp)
+            else:
+                g = torch.sigmoid(gp).reshape(o.shape)
+                o_rows = _linear((o * g).flatten(-2), m.linear_o.weight)
+            if out is None:
+                out = o_rows.new_empty(x.shape[:-1] + (o_rows.shape[-1],))
+            out[..., rows, :, :] = o_rows
+        return out
 
     def _stock_forward_from_ln(self, x, mask_bias, tri_bias, q, k, v, gp):
         """Stock attention on projections already formed (the reference's

@@ -6,9 +6,13 @@ pure FP32 storage and arithmetic for an official OpenFold3 TriMul module
 (separate ``linear_{a,b}_{p,g}`` or fused ``linear_ab_{p,g}`` projections,
 optional linear biases, optional LayerNorm affine parameters with their eps,
 outgoing / incoming from ``module._outgoing``), under ``torch.no_grad()``.
-All compute runs in ``csrc/trimul_f32.hip`` (FP32 MFMA).  The reference's
-chunking arguments are validated and accepted; one MI355X holds the whole
-problem (HBM is 288 GB), so no chunking is applied.
+All compute runs in ``csrc/trimul_f32.hip`` (FP32 MFMA).  As in the
+reference, the contraction runs over chunks of output rows: by default as
+many rows as fit ``contraction_workspace_bytes`` of FP32 product scratch
+([H, rows, N]), or ``output_row_chunk_size`` rows; the LayerNorm and output
+projection of a chunk follow it, and the result does not depend on the
+chunking (bitwise).  ``projection_workspace_bytes`` is validated as in the
+reference; the input projections run over all rows at once.
 """
 
 from __future__ import annotations
@@ -166,8 +170,15 @@ def run_trimul_fp32(module, z, mask=None, *, output_row_chunk_size=None,
     biases = [ptr(b) for _, b in parts]
     lnw = [ptr(t) for t in (norm_in[0], norm_in[1], norm_out[0], norm_out[1])]
     out = torch.empty((batch, sequence, sequence, channels), device=dev, dtype=torch.float32)
-    ws_bytes = int(_native.query("tpf_trimul_forward_f32_workspace_bytes", batch, sequence,
-                                 channels, hidden))
+    if output_row_chunk_size is None:
+        # Rows of FP32 product scratch [H, rows, N] that fit the budget
+        # (reference turbopairformer_trimul_fp32.py:203-221), at least one.
+        row_bytes = hidden * ((sequence + 3) // 4 * 4) * 4
+        row_chunk = max(1, min(sequence, contraction_workspace_bytes // row_bytes))
+    else:
+        row_chunk = min(sequence, output_row_chunk_size)
+    ws_bytes = int(_native.query("tpf_trimul_forward_f32_workspace_bytes_chunked", batch,
+                                 sequence, channels, hidden, row_chunk))
     if ws_bytes < 0:
         raise ValueError("FP32 TriMul: problem too large for one call")
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
@@ -177,10 +188,10 @@ def run_trimul_fp32(module, z, mask=None, *, output_row_chunk_size=None,
 
     with torch.autocast("cuda", enabled=False), _device_ctx(dev):
         _native.call(
-            "tpf_trimul_forward_f32", zf.data_ptr(), mf.data_ptr(),
+            "tpf_trimul_forward_f32_chunked", zf.data_ptr(), mf.data_ptr(),
             *[addr(w) for w in weights], *[addr(b) for b in biases],
             addr(lnw[0]), addr(lnw[1]), norm_in[2], addr(lnw[2]), addr(lnw[3]), norm_out[2],
-            int(module._outgoing), batch, sequence, channels, hidden, out.data_ptr(),
+            int(module._outgoing), batch, sequence, channels, hidden, row_chunk, out.data_ptr(),
             ws.data_ptr(), ws_bytes, _native.stream_of(zf),
         )
     _INVOCATIONS += 1
