@@ -351,25 +351,32 @@ int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64_t B, int64
  * [B, N, N, pitch] bf16 holds, per pair row (i, j), the module's projections
  * q | k | v | gate (H*D columns each, head-major inside) | pair bias (H) |
  * pad (pitch a multiple of 8); plane i attends over j.  mask f32 [B, N, N]
- * additive; transpose_bias selects bias[h, q, k] = proj[b, k, q, 4HD + h]
- * instead of proj[b, q, k, 4HD + h].  Forward writes o [B, N, N, H*D], lse
- * [B, N, H, N] f32 and the gated og = o * sigmoid(gate).  Backward takes
- * d_og and writes the whole projection gradient row into dproj (same
- * layout as proj, pad columns zeroed).  residual (nullable, bf16 like o):
+ * additive.  flags: TPF_PAIR_BIAS_TRANSPOSED selects bias[h, q, k] =
+ * proj[b, k, q, 4HD + h] instead of proj[b, q, k, 4HD + h];
+ * TPF_PAIR_OG_TRANSPOSED stores og (forward) and reads d_og (backward) of
+ * pair row (i, j) at row (j, i), so the ending node's module output leaves
+ * its output projection in the caller's pair order.  Forward writes o
+ * [B, N, N, H*D], lse [B, N, H, N] f32 and the gated og = o * sigmoid(gate).
+ * Backward takes d_og and writes the whole projection gradient row into
+ * dproj (same layout as proj, pad columns zeroed).  residual (nullable, bf16 like o):
  * when given, the forward writes o's shadow residual there and the backward
  * forms delta from o + residual, as the standalone shadow entry points do.
  * Replaces the module glue around the
  * kernel (openfold3/core/model/layers/triangular_attention.py:160-243 with
  * openfold3/core/model/primitives/attention.py:640-692: q/k/v/gate/bias
  * projections split into views, gating, and the gradient concatenation). */
+enum {
+  TPF_PAIR_BIAS_TRANSPOSED = 1, /* pair bias read as bias[h, q, k] = proj[b, k, q, 4HD + h] */
+  TPF_PAIR_OG_TRANSPOSED = 2    /* og / d_og rows in transposed pair order */
+};
 int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H);
 int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int transpose_bias, void* o, float* lse, void* og, void* residual,
+                               int flags, void* o, float* lse, void* og, void* residual,
                                void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
                                int64_t H, int64_t D, double scale, void* stream);
 int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D);
 int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
-                                int transpose_bias, const void* o, const float* lse,
+                                int flags, const void* o, const float* lse,
                                 const void* residual, const void* d_og, void* dproj,
                                 void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,

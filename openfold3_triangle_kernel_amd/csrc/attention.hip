@@ -38,6 +38,7 @@ struct AttnGeom {
   int64_t s_plane;         // elements between (b, o) planes of Q/K/V/dQ/dK/dV
   int64_t bias_bstride;    // elements between bias batches (0 = broadcast)
   float scale;             // softmax scale (1/sqrt(D_true))
+  int og_t;                // pair-row core: og rows in transposed pair order (O == N)
 };
 
 // Element strides of a pair bias bias[bb, h, q, k]: the standalone op's
@@ -464,7 +465,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
             bf16x4 og4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) og4[i] = f2bf(bf2f(o4[i]) * sigmoidf(bf2f(g4[i])));
-            *reinterpret_cast<bf16x4*>(og + orow_off + d0) = og4;
+            // og_t: the row of pair (o, qi) is stored at (b, qi, o) (O == N).
+            int64_t og_off = orow_off;
+            if (g.og_t) {
+              const int64_t ob = plane[p] % g.O;
+              og_off = ((((int64_t)plane[p] - ob) * N + (int64_t)qi * N + ob) * g.H + h) * D;
+            }
+            *reinterpret_cast<bf16x4*>(og + og_off + d0) = og4;
           }
         }
       }
@@ -1379,7 +1386,7 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     const __bf16* __restrict__ res, const __bf16* __restrict__ gate, int64_t pitch,
     __bf16* __restrict__ d_o,
     float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, FastDiv fN,
-    int H, int D, FastDiv fhc8) {
+    int H, int D, FastDiv fhc8, int og_t) {
   // items < 2^31 (checked on the host): 32-bit item index; element offsets
   // (8 per item) are formed in 64 bits.
   __shared__ float part[256];
@@ -1391,7 +1398,14 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
   const int c = (int)(t - row * fhc8.d);
   float sdot = 0.f;
   if (act) {
-    const bf16x8 dv = ld8(d_og + (size_t)t * 8), ov = ld8(o + (size_t)t * 8),
+    // og_t: d_og of pair row (b, i, j) is stored at row (b, j, i).
+    size_t dog = (size_t)t * 8;
+    if (og_t) {
+      const uint32_t pl = fdiv(row, fN), j = row - pl * fN.d;
+      const uint32_t bb = fdiv(pl, fN), i = pl - bb * fN.d;
+      dog = (((size_t)bb * fN.d + j) * fN.d + i) * (8 * (size_t)fhc8.d) + (size_t)c * 8;
+    }
+    const bf16x8 dv = ld8(d_og + dog), ov = ld8(o + (size_t)t * 8),
                  gv = ld8(gate + (size_t)row * pitch + c * 8);
     bf16x8 rv;
     if (SHADOW) rv = ld8(res + (size_t)t * 8);
@@ -1520,6 +1534,7 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
                      (long long)bias_batches, (long long)B);
   g->bias_bstride = (bias_batches == 1) ? 0 : H * N * N;
   g->scale = (float)scale;
+  g->og_t = 0;
   return check_geom(*g, fn);
 }
 
@@ -2087,10 +2102,14 @@ int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, co
 // columns are q | k | v | gate (H*D each) | pair bias (H) | pad.
 // ---------------------------------------------------------------------------
 
-static int pair_geom(AttnGeom* g, BiasView* bv, int64_t pitch, int transpose_bias, int64_t B,
+static int pair_geom(AttnGeom* g, BiasView* bv, int64_t pitch, int flags, int64_t B,
                      int64_t N, int64_t H, int64_t D, double scale, const char* fn) {
+  if (flags & ~(TPF_PAIR_BIAS_TRANSPOSED | TPF_PAIR_OG_TRANSPOSED))
+    return set_error(TPF_ERR_ARG, "%s: unknown flags 0x%x", fn, flags);
   int rc = make_geom(g, B, N, H, N, D, 1, B, scale, fn);
   if (rc) return rc;
+  const int transpose_bias = (flags & TPF_PAIR_BIAS_TRANSPOSED) != 0;
+  g->og_t = (flags & TPF_PAIR_OG_TRANSPOSED) != 0;
   const int64_t hc = H * D;
   if (pitch < 4 * hc + H || pitch % 8 != 0)
     return set_error(TPF_ERR_SHAPE, "%s: pitch %lld must be a multiple of 8 >= 4*H*D + H", fn,
@@ -2112,13 +2131,13 @@ int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H) {
 }
 
 int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int transpose_bias, void* o, float* lse, void* og, void* residual,
+                               int flags, void* o, float* lse, void* og, void* residual,
                                void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
                                int64_t H, int64_t D, double scale, void* stream) {
   const char* fn = "tpf_attn_pair_forward_bf16";
   AttnGeom g;
   BiasView bv;
-  int rc = pair_geom(&g, &bv, pitch, transpose_bias, B, N, H, D, scale, fn);
+  int rc = pair_geom(&g, &bv, pitch, flags, B, N, H, D, scale, fn);
   if (rc) return rc;
   if (!proj || !mask || !o || !lse || !og || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
@@ -2144,7 +2163,7 @@ int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, 
 }
 
 int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
-                                int transpose_bias, const void* o, const float* lse,
+                                int flags, const void* o, const float* lse,
                                 const void* residual, const void* d_og, void* dproj,
                                 void* workspace,
                                 int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
@@ -2152,7 +2171,7 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   const char* fn = "tpf_attn_pair_backward_bf16";
   AttnGeom g;
   BiasView bv;
-  int rc = pair_geom(&g, &bv, pitch, transpose_bias, B, N, H, D, scale, fn);
+  int rc = pair_geom(&g, &bv, pitch, flags, B, N, H, D, scale, fn);
   if (rc) return rc;
   if (!proj || !mask || !o || !lse || !d_og || !dproj || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
@@ -2176,11 +2195,11 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   if (residual)
     hipLaunchKernelGGL(attn_gate_bwd_kernel<true>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)residual, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8);
+                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
   else
     hipLaunchKernelGGL(attn_gate_bwd_kernel<false>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)nullptr, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8);
+                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
   if ((rc = check_launch(fn))) return rc;
   BwdParts pt;
   bwd_layout(B, N, H, N, D, B * N, (char*)workspace, &pt);
@@ -2197,7 +2216,8 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   const int64_t groups = plan.runs;
   const dim3 db_grid((unsigned)(B * N * N / 512));
   hipLaunchKernelGGL(attn_dbias_pair_kernel, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
-                     (int)groups, (int)H, (int)N, dp, pitch, 4 * hc, transpose_bias);
+                     (int)groups, (int)H, (int)N, dp, pitch, 4 * hc,
+                     (flags & TPF_PAIR_BIAS_TRANSPOSED) != 0);
   return check_launch(fn);
 }
 

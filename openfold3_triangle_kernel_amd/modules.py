@@ -126,6 +126,12 @@ def _mm(a: torch.Tensor, b: torch.Tensor, b_kc: bool) -> torch.Tensor:
     return out
 
 
+def _pair_flags(transpose_bias: bool, og_t: bool) -> int:
+    """Flags of the pair-row entry points (TPF_PAIR_BIAS_TRANSPOSED = 1,
+    TPF_PAIR_OG_TRANSPOSED = 2)."""
+    return (1 if transpose_bias else 0) | (2 if og_t else 0)
+
+
 class _PairAttentionCore(torch.autograd.Function):
     """Projection -> triangle attention -> gate -> output projection of the
     triangle-attention module over BF16 pair rows, with explicit buffers.
@@ -136,10 +142,15 @@ class _PairAttentionCore(torch.autograd.Function):
     The backward's ``tpf_attn_pair_backward_bf16`` writes every column of the
     projection gradient row (gate, q, k, v, bias, zeroed pad) into one
     buffer, so dx = dproj W_all and dW_all = dproj^T x are single GEMMs.
+
+    ``og_t`` (the ending node, whose x rows are the transposed pair order):
+    og is stored in the caller's pair order, so ``out`` leaves the output
+    projection in that order and the module returns it without a transposed
+    copy; the backward reads d_og in the same order.
     """
 
     @staticmethod
-    def forward(ctx, x, w_all, w_o, mask_add, H, D, transpose_bias):
+    def forward(ctx, x, w_all, w_o, mask_add, H, D, transpose_bias, og_t=False):
         B, N, _, C = x.shape
         P = w_all.shape[0]
         R, hc = B * N * N, H * D
@@ -159,12 +170,13 @@ class _PairAttentionCore(torch.autograd.Function):
         res = torch.empty_like(o) if shadow_enabled() else None
         with _device_ctx(dev):
             _native.call("tpf_attn_pair_forward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
-                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), og.data_ptr(),
+                         _pair_flags(transpose_bias, og_t), o.data_ptr(), lse.data_ptr(),
+                         og.data_ptr(),
                          _native.ptr(res), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
                          _native.stream_of(proj))
         out = _mm(og, wo, True)
         ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add, res)
-        ctx.dims = (B, N, H, D, C, P, bool(transpose_bias), scale)
+        ctx.dims = (B, N, H, D, C, P, _pair_flags(transpose_bias, og_t), scale)
         ctx.w_dtypes = (w_all.dtype, w_o.dtype)
         ctx.set_materialize_grads(False)
         return out.view(B, N, N, C)
@@ -172,9 +184,9 @@ class _PairAttentionCore(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         if dout is None:
-            return (None,) * 7
+            return (None,) * 8
         x2, wa, wo, proj, o, og, lse, mask_add, res = ctx.saved_tensors
-        B, N, H, D, C, P, transpose_bias, scale = ctx.dims
+        B, N, H, D, C, P, flags, scale = ctx.dims
         R = B * N * N
         dev = x2.device
         dout2 = dout.reshape(R, C).to(torch.bfloat16).contiguous()
@@ -185,13 +197,13 @@ class _PairAttentionCore(torch.autograd.Function):
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         with _device_ctx(dev):
             _native.call("tpf_attn_pair_backward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
-                         int(transpose_bias), o.data_ptr(), lse.data_ptr(), _native.ptr(res),
+                         flags, o.data_ptr(), lse.data_ptr(), _native.ptr(res),
                          d_og.data_ptr(), dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D,
                          scale,
                          _native.stream_of(dproj))
         dx = _mm(dproj, wa, False).view(B, N, N, C) if ctx.needs_input_grad[0] else None
         dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None
-        return dx, dw_all, dw_o, None, None, None, None
+        return dx, dw_all, dw_o, None, None, None, None, None
 
 
 class _ProjLinear(torch.autograd.Function):
@@ -392,10 +404,16 @@ class TriangleAttention(nn.Module):
         if pair_core:
             B = math.prod(prefix)
             mask_add = mask_bias.reshape(B, N, N).contiguous()
+            # The ending node's x is the transposed view of the caller's
+            # pair rows: the core returns its output in the caller's order,
+            # handed back as the transposed view the caller transposes again
+            # (no copy, and a contiguous result).
+            og_t = not self.starting
             out = _PairAttentionCore.apply(x.reshape(B, N, N, self.c_in), w_all,
                                            m.linear_o.weight, mask_add, H, c,
-                                           bool(transpose_bias))
-            return out.reshape(x.shape)
+                                           bool(transpose_bias), og_t)
+            out = out.reshape(x.shape)
+            return out.transpose(-2, -3) if og_t else out
         proj = _linear(x, w_all)
         # split (not slicing): its backward is one concatenation of the part
         # gradients instead of a zero-filled full-size buffer per part.
