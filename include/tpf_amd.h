@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (4). */
+/* ABI revision of this header (5). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -180,6 +180,42 @@ int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, co
                                  void* dv, void* dbias, void* workspace, int64_t workspace_bytes,
                                  int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
                                  int layout, int64_t bias_batches, double scale, void* stream);
+
+/* Split backward route for direct callers (not on the facade path), from
+ * caller-supplied lse and delta, in the layouts and flags of
+ * tpf_attn_backward_bf16 (TPF_DBIAS_BF16 excluded).
+ *
+ * dK / dV only: dk, dv bf16 in Q/K/V storage order.  With delta_true
+ * (nullable, f32 [B, O, H, N]) the call also forms delta_true = sum_k P dP
+ * of each query row: per-64-key-block f32 partials in delta_true_partials
+ * ([B, O, H, ceil(N/64), N], tpf_attn_dkdv_delta_true_partial_elements
+ * floats, 16-byte aligned) folded in ascending block order.  dS uses the
+ * supplied delta either way.  dk and dv are bitwise those of
+ * tpf_attn_backward_bf16 on the same inputs.  Replaces
+ * turbopairformer_triangle_dkdv_out / _dkdv_delta_true_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dkdv.py:101-174). */
+int64_t tpf_attn_dkdv_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                      int64_t bias_batches);
+int64_t tpf_attn_dkdv_delta_true_partial_elements(int64_t B, int64_t O, int64_t H, int64_t N);
+int tpf_attn_dkdv_bf16(const void* q, const void* k, const void* v, const void* dout,
+                       const float* lse, const float* delta, const float* mask, const void* bias,
+                       void* dk, void* dv, float* delta_true_partials, float* delta_true,
+                       void* workspace, int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
+                       int64_t N, int64_t D, int layout, int64_t bias_batches, double scale,
+                       void* stream);
+/* dQ / dBias only: dq bf16 in Q's storage order and dbias f32 per batch item
+ * [B, H, N, N] (a bias shared by the batch still gets one gradient per
+ * item; the caller reduces a broadcast).  Workspace and slabs as
+ * tpf_attn_backward_bf16 (its size queries apply); dq and each batch's
+ * dbias are bitwise that route's.  Replaces turbopairformer_triangle_dq_dbias_out
+ * (openfold3/core/kernels/turbopairformer/turbopairformer_triangle_dq_dbias.py:379-463). */
+int64_t tpf_attn_dq_dbias_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D);
+int tpf_attn_dq_dbias_bf16(const void* q, const void* k, const void* v, const void* dout,
+                           const float* lse, const float* delta, const float* mask,
+                           const void* bias, void* dq, float* dbias, void* workspace,
+                           int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                           int64_t D, int layout, int64_t bias_batches, double scale,
+                           void* stream);
 
 /* FP32 forward (inference): q, k, v, bias f32 in the layouts above (layout:
  * TPF_QKV_SEQ_MAJOR only; the bias is contiguous), out f32

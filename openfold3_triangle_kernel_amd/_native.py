@@ -63,6 +63,17 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P, _P, _P] + [_I64] * 5 + [_I32, _I64, _F64, _P],
     ),
+    "tpf_attn_dkdv_workspace_bytes": (_I64, [_I64] * 6),
+    "tpf_attn_dkdv_delta_true_partial_elements": (_I64, [_I64] * 4),
+    "tpf_attn_dkdv_bf16": (
+        _I32,
+        [_P] * 13 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
+    "tpf_attn_dq_dbias_workspace_bytes": (_I64, [_I64] * 5),
+    "tpf_attn_dq_dbias_bf16": (
+        _I32,
+        [_P] * 11 + [_I64] * 6 + [_I32, _I64, _F64, _P],
+    ),
     "tpf_gemm_bf16": (
         _I32,
         [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I64, _I64,

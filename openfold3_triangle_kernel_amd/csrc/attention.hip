@@ -647,6 +647,11 @@ __global__ __launch_bounds__(256) void attn_bwd_rows_kernel(
 // ordered XCD-aware by (head, outer group, key block).
 // ---------------------------------------------------------------------------
 constexpr int kBwdGroup = 4;
+// What one backward launch produces: every gradient (the single-
+// reconstruction route), or one half of the split route of direct callers:
+// dK / dV (optionally with the per-64-key-block partials of
+// delta_true = sum_k P dP), or the dQ / dBias partials.
+constexpr int kBwdSR = 0, kBwdDKDV = 1, kBwdDQDB = 2;
 // A slab of the backward: the flattened runs [brun0, brun0 + nbrun) of
 // outer groups (run index b * runs + r) and the planes they cover, whose dQ
 // partials [key block][planes][H][N][D] sit in the workspace at once.
@@ -728,7 +733,7 @@ __device__ __forceinline__ void lds_read_rows4(u32x4* out, unsigned a0, unsigned
   for (int i = 0; i < 4; ++i) out[i] = u32x4{rs[i][0], rs[i][1], rs[i][2], rs[i][3]};
 }
 
-template <int DP>
+template <int DP, int MODE>
 __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k,
     const __bf16* __restrict__ v, const __bf16* __restrict__ dout,
@@ -736,7 +741,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     const float* __restrict__ mask, const float* __restrict__ bias_f,
     __bf16* __restrict__ dk, __bf16* __restrict__ dv,
     __bf16* __restrict__ dq_part, float* __restrict__ dbias_part, AttnGeom g, int run,
-    BwdSlab sl) {
+    BwdSlab sl, float* __restrict__ dtrue_part) {
   constexpr int KT = DP + 16;  // K tile pitch at setup (bf16)
   constexpr int SP = 32 + 4;   // dS^T tile [64 keys][32 queries] pitch (bf16): the
                                // 8-byte row writes of 32 lanes cover all banks once
@@ -960,7 +965,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     // them measured faster.  The first step of a group waits for
     // everything: its setup loads are younger, and the last group's partial
     // stores must land before this group reads the same addresses back.
-    if (q0 == 0 || KH == 1)
+    if (q0 == 0 || KH == 1 || MODE == kBwdDKDV)
       wait_vmcnt<0>();
     else
       wait_vmcnt<16>();
@@ -997,6 +1002,9 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
     // The other buffers were last read before the barrier above.
     if (q0 + 32 < N) issue(q0 + 32, Bn, QDn, RSn);
     f32x16 P[2], dS[2];
+    float tsum[16];  // delta_true: this lane's sum over its keys of P dP per query row
+#pragma unroll
+    for (int r = 0; r < 16; ++r) tsum[r] = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       f32x16 sacc = sinit[cb];
@@ -1015,6 +1023,25 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         const float p = fast_exp2(fmaf(sacc[r], c2, nl2v[r]));
         P[cb][r] = p;
         dS[cb][r] = p * dp[r];
+        // dP itself is the accumulator minus its -delta seed.
+        if constexpr (MODE == kBwdDKDV) tsum[r] = fmaf(p, dp[r] - ndv[r], tsum[r]);
+      }
+    }
+    if constexpr (MODE == kBwdDKDV) {
+      // delta_true partial of this wave's 64 keys: the 32 key lanes of each
+      // half summed on DPP / permlane (fixed order), written by lanes 0 / 32
+      // as the 16 query rows 8j + 4hl + i.
+      if (dtrue_part && active) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tsum[r] = lanes_sum<32>(tsum[r]);
+        if (kl == 0) {
+          const int nkb64 = (N + 63) / 64;
+          float* dst = dtrue_part + (((int64_t)plane * H + h) * nkb64 + kblk * KH + kh) * N + q0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(dst + 8 * j + 4 * hl) =
+                f32x4{tsum[4 * j], tsum[4 * j + 1], tsum[4 * j + 2], tsum[4 * j + 3]};
+        }
       }
     }
     // P and dS in bf16, packed once: B operands of dV^T += dO^T P and
@@ -1027,6 +1054,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         pP[cb][t] = pack8(P[cb], 8 * t);
         pS[cb][t] = pack8(dS[cb], 8 * t);
       }
+    if constexpr (MODE != kBwdDQDB) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -1042,6 +1070,8 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         }
       }
     }
+    }  // dK / dV
+    if constexpr (MODE != kBwdDKDV) {
     // dS -> LDS as bf16 [key][query]: the dQ operand and the dBias sum.
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
@@ -1143,6 +1173,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dbprev[e] + acc[e]), rs_db, vdb,
                                               (q0 + e) * N * 4, 0);
     }
+    }  // dQ / dBias
   };
 #pragma unroll 1
   for (int q0 = 0; q0 < N; q0 += 32) {
@@ -1154,7 +1185,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
   // register pair (j, j + 1) gives it 8 consecutive channels, 16j + 8hl ..
   // +7, so each store instruction writes 32 contiguous bytes per key (two
   // 16-byte stores per key and tensor instead of four 8-byte ones).
-  if (active) {
+  if (MODE != kBwdDQDB && active) {
 #pragma unroll
   for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
@@ -1763,23 +1794,38 @@ static int attn_backward_prep_impl(const AttnGeom& g, const float* lse, const fl
 
 // The reconstruction kernel over one slab (dK, dV of its planes and their
 // dQ / dBias partials).
+template <int DP, int MODE>
+static void bwd_kernel_launch(dim3 grid, const AttnGeom& g, const void* q, const void* k,
+                              const void* v, const void* dout, const float* mask, void* dk,
+                              void* dv, const BwdParts& pt, const BwdPlan& plan,
+                              const BwdSlab& sl, float* dtrue, hipStream_t s) {
+  hipLaunchKernelGGL((attn_bwd_kernel<DP, MODE>), grid, dim3(256 * bwd_kh(DP)), 0, s,
+                     (const __bf16*)q, (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout,
+                     pt.nl2, pt.nd, mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g,
+                     plan.run, sl, dtrue);
+}
 static int attn_backward_slab_impl(const AttnGeom& g, const void* q, const void* k,
                                    const void* v, const void* dout, const float* mask,
                                    void* dk, void* dv, const BwdParts& pt, const BwdPlan& plan,
-                                   const BwdSlab& sl, hipStream_t s, const char* fn) {
+                                   const BwdSlab& sl, hipStream_t s, const char* fn,
+                                   int mode = kBwdSR, float* dtrue = nullptr) {
   const int64_t H = g.H, N = g.N, D = g.D;
   const int64_t total = H * bwd_key_blocks(N, D) * sl.nbrun;
   if ((total + 7) / 8 * 8 > INT32_MAX)
     return set_error(TPF_ERR_SHAPE, "%s: too many backward tiles", fn);
   dim3 grid((unsigned)((total + 7) / 8 * 8));
-  if (D <= 32)
-    hipLaunchKernelGGL(attn_bwd_kernel<32>, grid, dim3(256 * bwd_kh(32)), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, plan.run, sl);
-  else
-    hipLaunchKernelGGL(attn_bwd_kernel<64>, grid, dim3(256 * bwd_kh(64)), 0, s, (const __bf16*)q,
-                       (const __bf16*)k, (const __bf16*)v, (const __bf16*)dout, pt.nl2, pt.nd,
-                       mask, pt.bias_f, (__bf16*)dk, (__bf16*)dv, pt.dq, pt.db, g, plan.run, sl);
+#define TPF_BWD_LAUNCH(DP, MODE) \
+  bwd_kernel_launch<DP, MODE>(grid, g, q, k, v, dout, mask, dk, dv, pt, plan, sl, dtrue, s)
+  if (D <= 32) {
+    if (mode == kBwdDKDV) TPF_BWD_LAUNCH(32, kBwdDKDV);
+    else if (mode == kBwdDQDB) TPF_BWD_LAUNCH(32, kBwdDQDB);
+    else TPF_BWD_LAUNCH(32, kBwdSR);
+  } else {
+    if (mode == kBwdDKDV) TPF_BWD_LAUNCH(64, kBwdDKDV);
+    else if (mode == kBwdDQDB) TPF_BWD_LAUNCH(64, kBwdDQDB);
+    else TPF_BWD_LAUNCH(64, kBwdSR);
+  }
+#undef TPF_BWD_LAUNCH
   return check_launch(fn);
 }
 
@@ -1801,6 +1847,21 @@ static int attn_backward_fold_impl(const AttnGeom& g, void* dq, void* dbias,
                      pt.dq, (__bf16*)dq, g, (int)bwd_key_blocks(N, D), (int)dq_bx, pt.db, dbias,
                      (int)bias_batches, plan.runs, n_db, db_mode, sl.plane0, sl.planes);
   return check_launch(fn);
+}
+
+// delta_true[row] = sum over the 64-key blocks kb (ascending) of
+// part[row][kb], row = (plane, head), query; part is [B, O, H, kb, N].
+__global__ __launch_bounds__(256) void attn_delta_true_fold_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ out,
+                                                                   int64_t rows, int N, int nkb) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t ph = r / N;
+  const int qq = (int)(r - ph * N);
+  const float* src = part + ph * nkb * N + qq;
+  float acc = src[0];
+  for (int kb = 1; kb < nkb; ++kb) acc += src[(int64_t)kb * N];
+  out[r] = acc;
 }
 
 extern "C" {
@@ -2030,10 +2091,11 @@ int tpf_attn_backward_finish_bf16(void* dq, void* dbias, const void* workspace, 
 static int attn_backward_slabs(const AttnGeom& g, const BwdPlan& plan, const void* q,
                                const void* k, const void* v, const void* dout, const float* mask,
                                void* dq, void* dk, void* dv, void* dbias, int64_t bias_batches,
-                               const BwdParts& pt, hipStream_t s, const char* fn, int db_mode) {
+                               const BwdParts& pt, hipStream_t s, const char* fn, int db_mode,
+                               int mode = kBwdSR) {
   for (int i = 0; i < plan.slabs; ++i) {
     const BwdSlab sl = bwd_slab(plan, g.B, g.O, i);
-    int rc = attn_backward_slab_impl(g, q, k, v, dout, mask, dk, dv, pt, plan, sl, s, fn);
+    int rc = attn_backward_slab_impl(g, q, k, v, dout, mask, dk, dv, pt, plan, sl, s, fn, mode);
     if (rc) return rc;
     rc = attn_backward_fold_impl(g, dq, dbias, bias_batches, pt, plan, sl, i + 1 == plan.slabs, s,
                                  fn, db_mode);
@@ -2094,6 +2156,112 @@ int tpf_attn_backward_fused_bf16(const void* q, const void* k, const void* v, co
   const int db_mode = !(layout & TPF_DBIAS_BF16) ? 0 : (layout & TPF_BIAS_TRANSPOSED) ? 2 : 1;
   return attn_backward_slabs(g, plan, q, k, v, dout, mask, dq, dk, dv, dbias, bias_batches, pt, s,
                              fn, db_mode);
+}
+
+// ---------------------------------------------------------------------------
+// Split backward route of direct callers: the reconstruction kernel in a
+// mode that produces one half of the gradients from caller-supplied lse and
+// delta.  dK / dV (with optional delta_true = sum_k P dP per query row, from
+// per-64-key-block f32 partials folded in ascending block order); dQ and the
+// per-batch f32 dBias through the same partials and folds as the single-
+// reconstruction route, so each half is bitwise that route's output.
+// ---------------------------------------------------------------------------
+static int64_t dkdv_layout(int64_t B, int64_t O, int64_t H, int64_t N, int64_t bias_batches,
+                           char* base, BwdParts* parts) {
+  const int64_t rows = B * O * H * N;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) { char* p = base ? base + off : nullptr; off += a256(bytes); return p; };
+  char* bf = take(bias_batches * H * N * N * 4);
+  char* nl = take(rows * 4);
+  char* nd = take(rows * 4);
+  if (parts) {
+    parts->dq = nullptr; parts->db = nullptr; parts->bias_f = (float*)bf;
+    parts->nl2 = (float*)nl; parts->nd = (float*)nd;
+  }
+  return off;
+}
+
+int64_t tpf_attn_dkdv_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D,
+                                      int64_t bias_batches) {
+  (void)D;
+  if (B < 1 || O < 1 || H < 1 || N < 1 || bias_batches < 1) return -1;
+  return dkdv_layout(B, O, H, N, bias_batches, nullptr, nullptr);
+}
+
+int64_t tpf_attn_dkdv_delta_true_partial_elements(int64_t B, int64_t O, int64_t H, int64_t N) {
+  if (B < 1 || O < 1 || H < 1 || N < 1) return -1;
+  return B * O * H * N * ((N + 63) / 64);
+}
+
+int tpf_attn_dkdv_bf16(const void* q, const void* k, const void* v, const void* dout,
+                       const float* lse, const float* delta, const float* mask, const void* bias,
+                       void* dk, void* dv, float* delta_true_partials, float* delta_true,
+                       void* workspace, int64_t workspace_bytes, int64_t B, int64_t O, int64_t H,
+                       int64_t N, int64_t D, int layout, int64_t bias_batches, double scale,
+                       void* stream) {
+  const char* fn = "tpf_attn_dkdv_bf16";
+  AttnGeom g;
+  int rc = make_geom(&g, B, O, H, N, D, layout, bias_batches, scale, fn);
+  if (rc) return rc;
+  if (layout & TPF_DBIAS_BF16) return set_error(TPF_ERR_ARG, "%s: TPF_DBIAS_BF16 has no meaning here", fn);
+  if (!q || !k || !v || !dout || !lse || !delta || !mask || !bias || !dk || !dv || !workspace)
+    return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if ((delta_true_partials == nullptr) != (delta_true == nullptr))
+    return set_error(TPF_ERR_ARG, "%s: delta_true and its partials are given together", fn);
+  if (delta_true_partials && ((uintptr_t)delta_true_partials % 16))
+    return set_error(TPF_ERR_ARG, "%s: delta_true partials must be 16-byte aligned", fn);
+  if (workspace_bytes < tpf_attn_dkdv_workspace_bytes(B, O, H, N, D, bias_batches))
+    return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
+  hipStream_t s = (hipStream_t)stream;
+  BwdParts pt;
+  dkdv_layout(B, O, H, N, bias_batches, (char*)workspace, &pt);
+  if ((rc = attn_backward_prep_impl(g, lse, delta, bias, dense_bias(H, N, bias_batches, layout),
+                                    bias_batches, pt, s, fn)))
+    return rc;
+  const BwdPlan plan = bwd_plan(B, O, H, N, D, INT64_MAX);
+  for (int i = 0; i < plan.slabs; ++i)
+    if ((rc = attn_backward_slab_impl(g, q, k, v, dout, mask, dk, dv, pt, plan,
+                                      bwd_slab(plan, B, O, i), s, fn, kBwdDKDV,
+                                      delta_true_partials)))
+      return rc;
+  if (delta_true) {
+    const int64_t rows = B * O * H * N;
+    hipLaunchKernelGGL(attn_delta_true_fold_kernel, dim3((unsigned)((rows + 255) / 256)),
+                       dim3(256), 0, s, delta_true_partials, delta_true, rows, (int)N,
+                       (int)((N + 63) / 64));
+    return check_launch(fn);
+  }
+  return TPF_OK;
+}
+
+int64_t tpf_attn_dq_dbias_workspace_bytes(int64_t B, int64_t O, int64_t H, int64_t N, int64_t D) {
+  if (B < 1 || O < 1 || H < 1 || N < 1 || D < 1) return -1;
+  return bwd_full_bytes(B, O, H, N, D);
+}
+
+int tpf_attn_dq_dbias_bf16(const void* q, const void* k, const void* v, const void* dout,
+                           const float* lse, const float* delta, const float* mask,
+                           const void* bias, void* dq, float* dbias, void* workspace,
+                           int64_t workspace_bytes, int64_t B, int64_t O, int64_t H, int64_t N,
+                           int64_t D, int layout, int64_t bias_batches, double scale,
+                           void* stream) {
+  const char* fn = "tpf_attn_dq_dbias_bf16";
+  AttnGeom g;
+  BwdPlan plan;
+  int rc = attn_bwd_prepare(&g, &plan, fn, q, k, v, dout, lse, delta, mask, bias, workspace,
+                            workspace_bytes, B, O, H, N, D, layout, bias_batches, scale, false);
+  if (rc) return rc;
+  if (layout & TPF_DBIAS_BF16) return set_error(TPF_ERR_ARG, "%s: dbias is f32 here", fn);
+  if (!dq || !dbias) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  hipStream_t s = (hipStream_t)stream;
+  BwdParts pt;
+  bwd_layout(B, O, H, N, D, bwd_slab_planes(B, O, plan.per, plan.run), (char*)workspace, &pt);
+  if ((rc = attn_backward_prep_impl(g, lse, delta, bias, dense_bias(H, N, bias_batches, layout),
+                                    bias_batches, pt, s, fn)))
+    return rc;
+  // dBias per batch item (B output batches), whatever the bias's batch count.
+  return attn_backward_slabs(g, plan, q, k, v, dout, mask, dq, nullptr, nullptr, dbias, B, pt, s,
+                             fn, 0, kBwdDQDB);
 }
 
 // ---------------------------------------------------------------------------
