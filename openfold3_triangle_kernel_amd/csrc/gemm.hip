@@ -165,6 +165,15 @@ extern "C" int tpf_gemm_bf16(const void* A, int a_kc, int64_t a_ld, int64_t a_bs
   if (!A || !B || !C) return tpf::set_error(TPF_ERR_ARG, "tpf_gemm_bf16: null pointer");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return tpf::set_error(TPF_ERR_SHAPE, "tpf_gemm_bf16: dimension exceeds int32");
+  // Tall row-major products with a small weight (the pair-row projections)
+  // run on the weight-stationary row kernel; the choice depends on the
+  // operand shapes only, so rows give the same bits in any row chunking.
+  if (batch == 1 && !out_f32 && a_kc == 1 && alpha == 1.0) {
+    int rc = TPF_OK;
+    if (tpf::rowgemm_try((const __bf16*)A, a_ld, (const __bf16*)B, b_kc, b_ld, (__bf16*)C, c_ld, M,
+                         N, K, (hipStream_t)stream, &rc, "tpf_gemm_bf16"))
+      return rc;
+  }
   tpf::GemmArgs g{};
   g.A = (const __bf16*)A; g.a_ld = a_ld; g.a_bs = a_bs;
   g.B = (const __bf16*)B; g.b_ld = b_ld; g.b_bs = b_bs;

@@ -1,0 +1,188 @@
+// Weight-stationary row GEMM on gfx950: y[R, N] = x[R, K] W^T for a tall x
+// (R = the pair rows of a module, up to millions) and a small weight W
+// (N x K bf16, N and K at most a few hundred), bf16 in and out, f32
+// accumulation.  These are the projections of the triangle-attention module
+// (x_ln W_all^T, og W_o^T, dout W_o; K = 128): the 128 x 128 tile GEMM
+// spends most of a short-K tile in its prologue and epilogue and re-reads
+// each x tile once per output tile column, while here every workgroup keeps
+// its slice of W in registers for the whole launch and streams x once.
+//
+// Launch: one persistent workgroup of 8 waves per CU walks contiguous
+// 32-row blocks.  Wave w owns the output tiles t = w, w + 8, ... (16
+// channels each, t < N / 16) and holds their weight rows as the A operands
+// of v_mfma_f32_16x16x32_bf16 (MT x KS registers of 8 bf16, K = 32 KS).
+// Waves 0-3 stream x blocks into a DEPTH-deep LDS ring with direct
+// buffer->LDS loads (rows chunk-rotated, so the 16 rows of a fragment read
+// hit distinct banks); waves 4-7 store: each block's outputs are staged in
+// LDS as [row][N] bf16 (two buffers) and leave as 16-byte row chunks.  The
+// loading waves issue only loads and the storing waves only stores, so each
+// side's vmcnt waits count its own operations.
+//
+// Each output element is sum_k x[r, k] W[n, k] in one fixed MFMA order
+// (k-steps ascending), whatever the row's block or position in it, so a row
+// gives the same bits in any launch (row chunks equal the whole).
+
+#include "common.hpp"
+#include "tpf_gemm.hpp"
+#include "tpf_status.hpp"
+
+namespace tpf {
+
+constexpr int kRowNW = 8;  // waves per workgroup
+
+template <int KS>
+constexpr int row_depth() { return KS <= 4 ? 4 : 3; }
+// (K = 576, the dx = dproj W_all product, measured slower here than on the
+// tile GEMM, 216 against 197 us at 589,824 rows, and is left to it.)
+
+template <int KS, int MT>
+__global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
+    const __bf16* __restrict__ x, int64_t ldx, const __bf16* __restrict__ w, int w_kc,
+    int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int R, int N, int64_t nblocks) {
+  constexpr int K = 32 * KS;
+  constexpr int CPR = K / 8;               // 16-byte chunks per x row
+  constexpr int DEPTH = row_depth<KS>();
+  constexpr int XCH = 32 * CPR;            // chunks of one x block
+  constexpr int LPT = XCH / 256;           // loads per loading thread per block
+  static_assert(XCH % 256 == 0, "x block splits evenly over the loading waves");
+  constexpr int NMAX = 16 * kRowNW * MT;  // widest output the instance serves
+  __shared__ __attribute__((aligned(1024))) __bf16 Xs[DEPTH][32 * K];
+  __shared__ __attribute__((aligned(16))) __bf16 Ys[2 * 32 * (NMAX + 8)];  // [2][32][N + 8]
+  const int YP = N + 8;
+
+  const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const bool loader = wv < kRowNW / 2;
+  const int tiles = N / 16;
+
+  // Stationary A operands: channel 16 t + l16, k chunk 4 ks + lg.
+  bf16x8 wf[MT][KS];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int t = wv + kRowNW * m;
+    const int ch = 16 * (t < tiles ? t : 0) + l16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k0 = 8 * (4 * ks + lg);
+      if (w_kc) {
+        wf[m][ks] = ld8(w + (int64_t)ch * ldw + k0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wf[m][ks][e] = w[(int64_t)(k0 + e) * ldw + ch];
+      }
+    }
+  }
+
+  const i32x4 rs_x = buffer_rsrc(x);
+  const __amdgpu_buffer_rsrc_t rs_y = __builtin_amdgcn_make_buffer_rsrc(y, 0, 0x7FFFFFFF, 0x00020000);
+  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
+  const int64_t bbeg = blockIdx.x * per;
+  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Loading thread i of 256 takes chunks ci = 256 j + i of the block: row
+  // r = ci / CPR, stored at slot (c + r) % CPR of its row.
+  auto issue = [&](int64_t blk) {
+    const int stage = (int)(blk % DEPTH);
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int ci = 256 * j + tid;
+      const int r = ci / CPR, slot = ci % CPR;
+      const int gc = (slot - r % CPR + CPR) % CPR;
+      const uint32_t m = (uint32_t)blk * 32 + r;
+      const bool ok = blk < bend && m < (uint32_t)R;
+      buf2lds16(rs_x, ok ? (uint32_t)(((int64_t)m * ldx + 8 * gc) * 2) : kBufOOB,
+                &Xs[stage][(256 * j + 64 * wv) * 8]);
+    }
+  };
+  if (loader) {
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) issue(bbeg + d);
+    wait_vmcnt<LPT * (DEPTH - 2)>();  // block bbeg landed
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int64_t blk = bbeg; blk < bend; ++blk) {
+    const int stage = (int)(blk % DEPTH);
+    __bf16* Yb = Ys + (int)(blk & 1) * 32 * YP;
+    if (loader) issue(blk + DEPTH - 1);
+    const __bf16* Xb = Xs[stage];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int t = wv + kRowNW * m;
+      if (t >= tiles) break;  // wave-uniform
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const int row = 16 * rt + l16;
+          const bf16x8 af =
+              *reinterpret_cast<const bf16x8*>(&Xb[row * K + 8 * ((4 * ks + lg + row) % CPR)]);
+          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[m][ks], af, acc[rt], 0, 0, 0);
+        }
+      // The weight rows are the A operand, so the tile comes out transposed:
+      // register e of lane l holds row 16 rt + l16, channel 16 t + 4 lg + e,
+      // and each lane writes 4 consecutive channels of one row at once.
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = f2bf(acc[rt][e]);
+        *reinterpret_cast<bf16x4*>(&Yb[(16 * rt + l16) * YP + 16 * t + 4 * lg]) = o;
+      }
+    }
+    if (loader) wait_vmcnt<LPT * (DEPTH - 2)>();  // block blk + 1 landed
+    __syncthreads();
+    if (!loader) {
+      // 32 rows x N / 8 chunks over the 256 storing threads: every LDS read
+      // first, then the stores back to back.
+      constexpr int SIT = (32 * NMAX / 8 + 255) / 256;
+      const int st = tid - 256, cpr = N / 8;
+      const int nch = 32 * cpr;
+      bf16x8 v[SIT];
+      uint32_t off[SIT];
+#pragma unroll
+      for (int i = 0; i < SIT; ++i) {
+        const int q = st + 256 * i;
+        const int row = q / cpr, k = q - row * cpr;
+        const uint32_t m = (uint32_t)blk * 32 + row;
+        const bool ok = q < nch && m < (uint32_t)R;
+        v[i] = *reinterpret_cast<const bf16x8*>(&Yb[(q < nch ? row * YP + 8 * k : 0)]);
+        off[i] = ok ? (uint32_t)(((int64_t)m * ldy + 8 * k) * 2) : kBufOOB;
+      }
+#pragma unroll
+      for (int i = 0; i < SIT; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rs_y, off[i], 0, 0);
+    }
+  }
+  // The ring loads issued past the last block still write LDS: let them land
+  // before the workgroup releases its LDS.
+  if (loader) wait_vmcnt<0>();
+}
+
+// Runs y = x W^T on the row kernel when the shape has an instance (K = 128,
+// N a multiple of 16 with N / 16 <= 8 MT, 16-byte aligned rows,
+// every byte offset below 2^31); returns false (nothing launched) otherwise.
+bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_t ldw, __bf16* y,
+                 int64_t ldy, int64_t R, int64_t N, int64_t K, hipStream_t stream, int* rc,
+                 const char* fn) {
+  if (R < 1 || N < 16 || N % 16 || N > 640 || ldx % 8 || ldy % 8 || ldx < K || ldy < N ||
+      (uintptr_t)x % 16 || (uintptr_t)y % 16 || (w_kc && (ldw % 8 || (uintptr_t)w % 16)))
+    return false;
+  if (R * ldx * 2 >= (int64_t)kBufOOB || R * ldy * 2 >= (int64_t)kBufOOB) return false;
+  const int tiles = (int)(N / 16);
+  const int64_t nblocks = (R + 31) / 32;
+  const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
+#define TPF_ROW_CASE(KS, MT)                                                                   \
+  if (K == 32 * KS && tiles <= kRowNW * MT) {                                                  \
+    hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT>), dim3(grid), dim3(64 * kRowNW), 0, stream,   \
+                       x, ldx, w, w_kc, ldw, y, ldy, (int)R, (int)N, nblocks);                 \
+    *rc = check_launch(fn);                                                                    \
+    return true;                                                                               \
+  }
+  TPF_ROW_CASE(4, 1)   // K = 128, N <= 128: linear_o, d_og
+  TPF_ROW_CASE(4, 5)   // K = 128, N <= 640: the q | k | v | gate | bias projection
+#undef TPF_ROW_CASE
+  return false;
+}
+
+}  // namespace tpf

@@ -65,5 +65,11 @@ struct FoldSegs {
   int nseg;
 };
 int fold_multi(FoldSegs f, hipStream_t stream, const char* fn);
+// y[R, N] = x[R, K] W^T on the weight-stationary row kernel (rowgemm.hip)
+// when the shape has an instance; false (nothing launched) otherwise.  W is
+// [N, K] (w_kc = 1) or [K, N] (w_kc = 0) with leading dimension ldw.
+bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_t ldw, __bf16* y,
+                 int64_t ldy, int64_t R, int64_t N, int64_t K, hipStream_t stream, int* rc,
+                 const char* fn);
 
 }  // namespace tpf

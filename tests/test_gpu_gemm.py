@@ -83,3 +83,50 @@ def test_wgrad_split_k(gpu, R, M, N):
                  ws.data_ptr(), ws_bytes, stream)
     torch.cuda.synchronize()
     assert torch.equal(dw, dw2)  # fixed-order fold: bitwise replay
+
+
+# Tall products with a small weight (the pair-row projections) dispatch to the
+# weight-stationary row kernel: batch 1, K-contiguous x, bf16 out, alpha 1,
+# K = 128, N a multiple of 16 up to 640 (W K- or MN-contiguous); the K = 576
+# cases (dx = dproj W_all) take the tile GEMM through the same entry point.
+ROW_CASES = [
+    # R, N, K
+    (1, 16, 128),
+    (31, 128, 128),
+    (1000, 576, 128),
+    (4133, 48, 128),
+    (70000, 576, 128),
+    (9999, 128, 576),
+    (33, 112, 576),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ROW_CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("w_kc", [1, 0], ids=["W_NK", "W_KN"])
+def test_row_gemm(gpu, case, w_kc):
+    """Against the FP64 product (bf16 output: <= 8e-3 max-rel) and row-chunk
+    invariance: rows computed in a separate call give the same bits."""
+    from openfold3_triangle_kernel_amd import _native
+
+    R, N, K = case
+    print(f"row gemm R={R} N={N} K={K} w_kc={w_kc}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(R + N + K)
+    x = torch.randn(R, K, generator=g).to(torch.bfloat16).to(gpu)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(gpu)
+    tw, ldw = _operand(w, w_kc)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(xs):
+        y = torch.full((xs.shape[0], N), float("nan"), device=gpu, dtype=torch.bfloat16)
+        _native.call("tpf_gemm_bf16", xs.data_ptr(), 1, K, 0, tw.data_ptr(), w_kc, ldw, 0,
+                     y.data_ptr(), 0, N, 0, xs.shape[0], N, K, 1, 1.0, stream)
+        return y
+
+    y = run(x)
+    lo, hi = R // 3, R // 3 + max(1, R // 2)
+    part = run(x[lo:hi].contiguous())
+    torch.cuda.synchronize()
+    ref = x.double().cpu() @ w.double().cpu().t()
+    assert max_rel(y.float().cpu().numpy(), ref.numpy()) <= 8e-3
+    assert torch.equal(part.view(torch.int16), y[lo:hi].view(torch.int16)), "row chunk differs"
