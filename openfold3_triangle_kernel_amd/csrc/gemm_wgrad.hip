@@ -38,9 +38,15 @@ int gemm_launch_pair_wgrad(const GemmArgs& p0, const GemmArgs& p1, hipStream_t s
 // (dy [R][M] and x [R][N] row-major bf16, both read MN-contiguous), split over
 // R with f32 partials and the fixed-order fold (deterministic).  The shape
 // of every projection weight gradient of the pair stack (K = B*N^2 rows).
+// The split count fills one round of 512 workgroups (two per CU on 256 CUs)
+// without spilling into a second: a launch of 515 for 5 output tiles ran
+// its last 3 workgroups as a round of their own, doubling the time.  At
+// most 256 splits: a one-tile product gains nothing from 512 (its fold of
+// twice the partials cost more, 9 -> 25 us at 128 x 128).  The count depends
+// on the shape only (fixed fold order on every device).
 static int wgrad_splits(int64_t R, int64_t M, int64_t N) {
   const int64_t tiles = ((M + tpf::kGM - 1) / tpf::kGM) * ((N + tpf::kGN - 1) / tpf::kGN);
-  int64_t s = (512 + tiles - 1) / tiles;
+  int64_t s = 512 / tiles;
   if (s > R / 256) s = R / 256;
   if (s > 256) s = 256;
   if (s < 1) s = 1;

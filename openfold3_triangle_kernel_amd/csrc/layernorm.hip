@@ -36,6 +36,10 @@ __device__ __forceinline__ int64_t ln_row_offset(const LnRows& g, uint32_t r) {
   return (int64_t)b * g.sb + (int64_t)i * g.si + (int64_t)j * g.sj;
 }
 
+// A workgroup normalises two groups of RPB rows (rows 2 * blockIdx.x * RPB
+// + u * RPB + slot, u = 0, 1): both rows' loads are issued before either
+// row's sums, so each thread keeps twice the bytes in flight (one row per
+// thread measured 4.6 TB/s at 589,824 rows of 128 channels).
 template <int L, int K>
 __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restrict__ x,
                                                           const float* __restrict__ w,
@@ -46,11 +50,17 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
                                                           LnRows g, int C, float eps) {
   constexpr int RPB = 256 / L;
   const int lane = threadIdx.x % L;
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / L;
-  const bool row_ok = row < g.R;
   const int n8 = C / 8;
-  const __bf16* xr = x + (row_ok ? ln_row_offset(g, (uint32_t)row) : 0);
-  // The affine parameters are loaded as vectors next to the row, so every
+  int64_t row[2];
+  bool row_ok[2];
+  const __bf16* xr[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    row[u] = ((int64_t)blockIdx.x * 2 + u) * RPB + threadIdx.x / L;
+    row_ok[u] = row[u] < g.R;
+    xr[u] = x + (row_ok[u] ? ln_row_offset(g, (uint32_t)row[u]) : 0);
+  }
+  // The affine parameters are loaded as vectors next to the rows, so every
   // load of the thread is in flight at once.
   float wv[K][8], bv[K][8];
 #pragma unroll
@@ -75,52 +85,58 @@ __global__ __launch_bounds__(256) void ln_fwd_bf16_kernel(const __bf16* __restri
       bv[k][e + 4] = b1[e];
     }
   }
-  float v[K][8];
+  float v[2][K][8];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int ch = k * L + lane;
-    if (row_ok && ch < n8) {
-      const bf16x8 t = ld8(xr + ch * 8);
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[k][e] = bf2f(t[e]);
-    } else {
+    for (int k = 0; k < K; ++k) {
+      const int ch = k * L + lane;
+      if (row_ok[u] && ch < n8) {
+        const bf16x8 t = ld8(xr[u] + ch * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[k][e] = 0.f;
+        for (int e = 0; e < 8; ++e) v[u][k][e] = bf2f(t[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[u][k][e] = 0.f;
+      }
     }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < K; ++k)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += v[k][e];
-  s = lanes_sum<L>(s);
   const float inv_c = 1.f / (float)C;
-  const float mean = s * inv_c;
-  float q = 0.f;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const bool ok = k * L + lane < n8;
+  for (int u = 0; u < 2; ++u) {
+    float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float d = ok ? v[k][e] - mean : 0.f;
-      q = fmaf(d, d, q);
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[u][k][e];
+    s = lanes_sum<L>(s);
+    const float mean = s * inv_c;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const bool ok = k * L + lane < n8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = ok ? v[u][k][e] - mean : 0.f;
+        q = fmaf(d, d, q);
+      }
     }
-  }
-  q = lanes_sum<L>(q);
-  const float rstd = rsqrtf(q * inv_c + eps);
-  if (!row_ok) return;
+    q = lanes_sum<L>(q);
+    const float rstd = rsqrtf(q * inv_c + eps);
+    if (!row_ok[u]) continue;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int ch = k * L + lane;
-    if (ch >= n8) continue;
-    bf16x8 o;
+    for (int k = 0; k < K; ++k) {
+      const int ch = k * L + lane;
+      if (ch >= n8) continue;
+      bf16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = f2bf(fmaf((v[k][e] - mean) * rstd, wv[k][e], bv[k][e]));
-    st8(y + row * C + ch * 8, o);
-  }
-  if (lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
+      for (int e = 0; e < 8; ++e)
+        o[e] = f2bf(fmaf((v[u][k][e] - mean) * rstd, wv[k][e], bv[k][e]));
+      st8(y + row[u] * C + ch * 8, o);
+    }
+    if (lane == 0) {
+      mean_out[row[u]] = mean;
+      rstd_out[row[u]] = rstd;
+    }
   }
 }
 
@@ -324,7 +340,7 @@ extern "C" int tpf_layer_norm_forward_bf16(const void* x, int64_t B, int64_t I, 
   if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) % 16 != 0)
     return set_error(TPF_ERR_ARG, "%s: x, y, w and b must be 16-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
-#define TPF_LN_FGRID(L) dim3((unsigned)((g.R + 256 / (L) - 1) / (256 / (L))))
+#define TPF_LN_FGRID(L) dim3((unsigned)((g.R + 512 / (L) - 1) / (512 / (L))))
 #define TPF_LN_NOSMEM(L) 0
   TPF_LN_DISPATCH(ln_fwd_bf16_kernel, TPF_LN_FGRID, TPF_LN_NOSMEM, (const __bf16*)x, w, b,
                   (__bf16*)y, mean, rstd, g, (int)C, (float)eps);
