@@ -24,9 +24,9 @@ using namespace gk32;
 // Several fixed-order folds in one launch.  Segment sg owns workgroups
 // [gbase[sg], gbase[sg + 1]); a workgroup covers 256 / RC consecutive
 // elements x RC ranges of splits (RC = ranges[sg], a power of two chosen so
-// that a range holds at most about 16 splits): thread (range r, element i)
+// that a range holds at most 16 splits): thread (range r, element i)
 // sums splits [r * per, min((r + 1) * per, splits)) in ascending order with
-// 8 loads in flight, and the ranges meet in LDS in the fixed order
+// all of its loads in flight, and the ranges meet in LDS in the fixed order
 // ((r0 + r1) + r2) + ...; element i of the segment lands in
 // dst[i / piece][i % piece].  The order depends only on the shapes.
 __global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
@@ -44,16 +44,18 @@ __global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
   const int64_t stride = f.stride[sg];
   float acc = 0.f;
   if (act && s0 < s1) {
-    acc = part[(int64_t)s0 * stride + i];
-    int s = s0 + 1;
-    for (; s + 8 <= s1; s += 8) {
-      float v[8];
+    // Up to 16 loads go out together (a range holds at most 16 splits
+    // unless the range count is capped), then they are added in ascending
+    // order.
+    for (int s = s0; s < s1; s += 16) {
+      float v[16];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = part[(int64_t)(s + e) * stride + i];
+      for (int e = 0; e < 16; ++e)
+        if (s + e < s1) v[e] = part[(int64_t)(s + e) * stride + i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += v[e];
+      for (int e = 0; e < 16; ++e)
+        if (s + e < s1) acc = (s + e == s0) ? v[e] : acc + v[e];
     }
-    for (; s < s1; ++s) acc += part[(int64_t)s * stride + i];
   }
   red[threadIdx.x] = acc;
   __syncthreads();

@@ -123,9 +123,11 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
   const int64_t t5 = total + (int64_t)C * 5 * cpr;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < t5 + (int64_t)C * cpr;
        idx += (int64_t)gridDim.x * 256) {
+    // The transposed parts take consecutive source columns on consecutive
+    // lanes (coalesced loads; the 16-byte stores are the scattered side).
     if (idx >= t5) {
       const int64_t j = idx - t5;
-      const int h = (int)(j / cpr), c0 = 8 * (int)(j % cpr);
+      const int h = (int)(j % C), c0 = 8 * (int)(j / C);
       bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = f2bf(w.z[(int64_t)(c0 + e) * C + h]);
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
     }
     if (idx >= total) {
       const int64_t j = idx - total;
-      const int c = (int)(j / (5 * cpr)), k0 = 8 * (int)(j % (5 * cpr));
+      const int c = (int)(j % C), k0 = 8 * (int)(j / C);
       bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
