@@ -1442,13 +1442,14 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     const __bf16* __restrict__ xln, const __bf16* __restrict__ wz, const __bf16* __restrict__ wzt,
     const __bf16* __restrict__ gl, const __bf16* __restrict__ dout, const __bf16* __restrict__ x,
     const float* __restrict__ mean, const float* __restrict__ rstd, const float* __restrict__ gamma,
-    __bf16* __restrict__ dy, __bf16* __restrict__ dproj5, __bf16* __restrict__ dx,
-    float* __restrict__ lnp, TmGeom g, int64_t nblocks) {
+    __bf16* __restrict__ dproj5, __bf16* __restrict__ dx, float* __restrict__ lnp,
+    float* __restrict__ wzp, TmGeom g, int64_t nblocks) {
   constexpr int NW = C / 16;         // waves
   constexpr int CPR = C / 8;         // 16-byte chunks per row
   constexpr int KS = C / 32;         // 32-deep k steps
   constexpr int RP = C + 8;          // row staging pitch (bf16)
   constexpr int PP = 40;             // plane staging pitch (bf16)
+  constexpr int HT = C / 16;         // 16-channel tiles of the xln side of dWz
   constexpr int TILE = 32 * C;       // elements of one [32][C] (or [C][32]) tile
   __shared__ __attribute__((aligned(1024))) __bf16 Rg[kOutBwdDepth][4][TILE];  // xln | gl | dout | x
   __shared__ __attribute__((aligned(256))) float Ss[kOutBwdDepth][2][64];      // mean | rstd
@@ -1474,7 +1475,6 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
   const i32x4 rs_x = buffer_rsrc(x);
   const i32x4 rs_mu = buffer_rsrc(mean);
   const i32x4 rs_rs = buffer_rsrc(rstd);
-  const __amdgpu_buffer_rsrc_t rs_dy = __builtin_amdgcn_make_buffer_rsrc(dy, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_dp = __builtin_amdgcn_make_buffer_rsrc(dproj5, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_dx = __builtin_amdgcn_make_buffer_rsrc(dx, 0, 0x7FFFFFFF, 0x00020000);
   const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
@@ -1513,6 +1513,22 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
   };
 
   float cg = 0.f, cgx = 0.f;
+  // dWz partial of this workgroup's rows: dWz[o][h] = sum_r dy[r][o] xln[r][h]
+  // with dy^T (wave w's 16 output channels) as the A operand and xln as the
+  // B operand, both column fragments of the row-major LDS tiles (32 rows =
+  // the MFMA's k); register e of lane l: o = 16 w + 4 lg + e, h = 16 j + l16.
+  f32x4 dwz[HT];
+#pragma unroll
+  for (int j = 0; j < HT; ++j) dwz[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Column fragment of 4 rows r0 .. r0 + 3 x 16 columns c0 .. c0 + 15 of a
+  // row-major tile (element (r, c) at off(r, c)): lane j of each 16-lane
+  // group receives { M[r0 + e][c0 + j] : e = 0..3 } (ds_read_b64_tr_b16).
+  auto col4 = [&](const __bf16* M, auto off, int r0, int c0) {
+    const int r = r0 + (l16 >> 2), c = c0 + 4 * (l16 & 3);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)&M[off(r, c)]);
+  };
+  auto dy_off = [](int r, int c) { return r * RP + c; };
+  auto xl_off = [](int r, int c) { return r * C + 8 * (((c >> 3) + r) % CPR) + (c & 7); };
   if (loader) {
     issue(bbeg);
     issue(bbeg + 1);
@@ -1567,6 +1583,15 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
         const bf16x8 af = *reinterpret_cast<const bf16x8*>(&Dy[(16 * rt + l16) * RP + 8 * (4 * ks + lg)]);
         acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wtf[ks], acc[rt], 0, 0, 0);
       }
+    {
+      const bf16x8 dyt = cat8(col4(Dy, dy_off, 8 * lg, 16 * w), col4(Dy, dy_off, 8 * lg + 4, 16 * w));
+      const __bf16* Xl2 = Rg[stage][0];
+#pragma unroll
+      for (int j = 0; j < HT; ++j) {
+        const bf16x8 xb = cat8(col4(Xl2, xl_off, 8 * lg, 16 * j), col4(Xl2, xl_off, 8 * lg + 4, 16 * j));
+        dwz[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dyt, xb, dwz[j], 0, 0, 0);
+      }
+    }
     float xh[2][4], gv[2][4], a[8], b[8];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
@@ -1611,14 +1636,13 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     }
     __syncthreads();
     if (!loader) {
-      // dy rows, d gl rows (into dproj5's last block), dx plane segments:
-      // 4 C chunks each over the 2 C storing threads.
+      // d gl rows (into dproj5's last block), dx plane segments: 4 C chunks
+      // each over the 2 C storing threads.
       const int st = tid - 2 * C;
       bf16x8 v[6];
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
-        v[it] = *reinterpret_cast<const bf16x8*>(&Dy[row * RP + 8 * k]);
         v[2 + it] = *reinterpret_cast<const bf16x8*>(&Dg[row * RP + 8 * k]);
         v[4 + it] = *reinterpret_cast<const bf16x8*>(&Dx[(q >> 2) * PP + 8 * (q & 3)]);
       }
@@ -1627,8 +1651,6 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
         const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
         const uint32_t m = (uint32_t)blk * 32 + row;
         const bool ok = m < (uint32_t)g.R;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_dy,
-                                               ok ? (m * C + 8 * k) * 2 : kBufOOB, 0, 0);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[2 + it]), rs_dp,
                                                ok ? (m * 5 * C + 4 * C + 8 * k) * 2 : kBufOOB, 0, 0);
         const uint32_t mb = (uint32_t)blk * 32 + 8 * (q & 3);
@@ -1647,6 +1669,11 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     lnp[(int64_t)blockIdx.x * 2 * C + ch] = cgx;
     lnp[(int64_t)blockIdx.x * 2 * C + C + ch] = cg;
   }
+  float* wp = wzp + (int64_t)blockIdx.x * C * C;
+#pragma unroll
+  for (int j = 0; j < HT; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wp[(16 * w + 4 * lg + e) * C + 16 * j + l16] = dwz[j][e];
 }
 
 // ---------------------------------------------------------------------------
@@ -1949,6 +1976,15 @@ static int tm_split(int64_t R, int64_t per, int cap) {
 // 576-row dWz ranges cost 18 us more per out + in step, in the larger fold).
 static int tm_w5_splits(int64_t R) { return tm_split(R, 2304, 64); }
 static int tm_wz_splits(int64_t R) { return tm_split(R, 2304, 64); }
+// Workgroups of the persistent backward kernels that leave per-workgroup
+// partials (LN parameter and dWz sums): a fixed plan of 256 CUs, so the
+// partition of the rows, and every summation order, depends on the shape
+// only (the same bits on any device).
+constexpr int64_t kTmPlanCus = 256;
+static int64_t tm_bwd_grid(int64_t R, int64_t C) {
+  const int64_t nblk = (R + 31) / 32, cap = kTmPlanCus * (128 / C);
+  return nblk < cap ? nblk : cap;
+}
 
 int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   const int64_t Np = (N + 7) / 8 * 8, R = B * N * N;
@@ -1960,7 +1996,8 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   t += align256((R + 31) / 32 * 2 * C * 4);        // LN_out parameter partials (tiles or workgroups)
   t += align256((R + 31) / 32 * 2 * C * 4);        // LN_in parameter partials (per workgroup)
   t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
-  t += align256((int64_t)tm_wz_splits(R) * C * C * 4);
+  const int64_t wz_parts = tm_wz_splits(R) > tm_bwd_grid(R, C) ? tm_wz_splits(R) : tm_bwd_grid(R, C);
+  t += align256(wz_parts * C * C * 4);  // dWz partials (split-K GEMM or per workgroup)
   return t;
 }
 
@@ -2005,7 +2042,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   float* lnp = (float*)take((R + 31) / 32 * 2 * C * 4);
   float* lnin = (float*)take((R + 31) / 32 * 2 * C * 4);
   float* w5p = (float*)take((int64_t)s5 * 5 * C * C * 4);
-  float* wzp = (float*)take((int64_t)sz * C * C * 4);
+  float* wzp = (float*)take((int64_t)(sz > tm_bwd_grid(R, C) ? sz : tm_bwd_grid(R, C)) * C * C * 4);
   if ((rc = tm_pack(w, k, (int)C, g.ntg, s, fn))) return rc;
   // Pad columns of dx are read by the dA GEMM (K = Np) and must be zero.
   if (g.Np != g.N && (rc = zero_fill(dx, plane_bytes, s, fn))) return rc;
@@ -2014,15 +2051,14 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   if (g.Np == g.N) {
     // Output projection backward + LN_out backward in one pass.
     const int64_t nblk = (R + 31) / 32;
-    const int64_t cap = (int64_t)device_cus() * (128 / C);
-    lnp_splits = (int)(nblk < cap ? nblk : cap);
+    lnp_splits = (int)tm_bwd_grid(R, C);
     switch (C) {
 #define TM_OUT_BWD(CC)                                                                          \
   case CC:                                                                                      \
     hipLaunchKernelGGL(tm_out_bwd_ws_kernel<CC>, dim3(lnp_splits), dim3(4 * CC), 0, s,          \
                        (const __bf16*)xln, k.wz, k.wzt, (const __bf16*)gate,                    \
                        (const __bf16*)grad_out, (const __bf16*)x, mean_out, rstd_out, ln_out_w, \
-                       dy, dproj5, dx, lnp, g, nblk);                                           \
+                       dproj5, dx, lnp, wzp, g, nblk);                                          \
     break;
       TM_OUT_BWD(32) TM_OUT_BWD(64) TM_OUT_BWD(96) TM_OUT_BWD(128)
 #undef TM_OUT_BWD
@@ -2077,8 +2113,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   }
   if ((rc = check_launch("tpf_trimul_backward_bf16(in_proj)"))) return rc;
   const int64_t ln_blk = (R + 31) / 32;
-  const int64_t ln_cap = (int64_t)device_cus() * (128 / C);
-  const int ln_grid = (int)(ln_blk < ln_cap ? ln_blk : ln_cap);
+  const int ln_grid = (int)tm_bwd_grid(R, C);
   switch (C) {
 #define TM_LN_IN(CC)                                                                            \
   case CC:                                                                                      \
@@ -2104,12 +2139,17 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   gz.C = wzp; gz.c_ld = H; gz.c_bs = 0; gz.c_split = C * H;
   gz.M = (int)C; gz.N = (int)H; gz.K = (int)R; gz.ksplit = sz;
   gz.k_chunk = (int)((R + sz - 1) / sz); gz.alpha = 1.f;
-  // dW5 and dWz are independent split-K GEMMs of ~300 tiles each: one
-  // launch keeps both in flight together.
   gw.batch = 1;
   gz.batch = 1;
-  if ((rc = gemm_launch_pair_wgrad(gw, gz, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
-    return rc;
+  const bool wz_fused = g.Np == g.N;  // tm_out_bwd_ws_kernel left per-workgroup dWz partials
+  if (wz_fused) {
+    if ((rc = gemm_launch_wgrad(gw, s, "tpf_trimul_backward_bf16(dW5)"))) return rc;
+  } else {
+    // dW5 and dWz are independent split-K GEMMs of ~300 tiles each: one
+    // launch keeps both in flight together.
+    if ((rc = gemm_launch_pair_wgrad(gw, gz, s, "tpf_trimul_backward_bf16(dW5, dWz)")))
+      return rc;
+  }
   // The four weight-gradient folds in one launch per pass; the LayerNorm
   // partials ([tiles][ln_out_w | ln_out_b] and [workgroups][ln_in_w |
   // ln_in_b]) land directly in the four parameter gradients.
@@ -2117,7 +2157,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   f.nseg = 4;
   f.part[0] = w5p; f.n[0] = 5 * C * C; f.stride[0] = 5 * C * C; f.splits[0] = s5;
   f.piece[0] = 5 * C * C; f.dst[0][0] = d_w5;
-  f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = sz;
+  f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = wz_fused ? lnp_splits : sz;
   f.piece[1] = C * H; f.dst[1][0] = d_w_z;
   f.part[2] = lnp; f.n[2] = 2 * C; f.stride[2] = 2 * C; f.splits[2] = lnp_splits;
   f.piece[2] = C;
