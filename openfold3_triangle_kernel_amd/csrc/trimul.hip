@@ -1972,9 +1972,15 @@ static int tm_split(int64_t R, int64_t per, int cap) {
   if (s > cap) s = cap;
   return (int)s;
 }
-// Both weight gradients take K ranges of 2304 rows (measured at N = 384:
-// 576-row dWz ranges cost 18 us more per out + in step, in the larger fold).
-static int tm_w5_splits(int64_t R) { return tm_split(R, 2304, 64); }
+// dWz on the split-K GEMM (N % 8 != 0) takes K ranges of 2304 rows
+// (measured at N = 384: 576-row ranges cost 18 us more per out + in step, in
+// the larger fold).  dW5 takes as many K ranges as fill one round of 512
+// workgroups with its ceil(5C / 128) x ceil(C / 128) output tiles (at least
+// 256 rows each): shape-only, so its fold order is the same on any device.
+static int tm_w5_splits(int64_t R, int64_t C) {
+  const int64_t tiles = ((5 * C + 127) / 128) * ((C + 127) / 128);
+  return tm_split(R, 256, (int)(512 / tiles));
+}
 static int tm_wz_splits(int64_t R) { return tm_split(R, 2304, 64); }
 // Workgroups of the persistent backward kernels that leave per-workgroup
 // partials (LN parameter and dWz sums): a fixed plan of 256 CUs, so the
@@ -1995,7 +2001,7 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   t += 3 * align256(B * C * N * Np * 2);           // dx, da, db
   t += align256((R + 31) / 32 * 2 * C * 4);        // LN_out parameter partials (tiles or workgroups)
   t += align256((R + 31) / 32 * 2 * C * 4);        // LN_in parameter partials (per workgroup)
-  t += align256((int64_t)tm_w5_splits(R) * 5 * C * C * 4);
+  t += align256((int64_t)tm_w5_splits(R, C) * 5 * C * C * 4);
   const int64_t wz_parts = tm_wz_splits(R) > tm_bwd_grid(R, C) ? tm_wz_splits(R) : tm_bwd_grid(R, C);
   t += align256(wz_parts * C * C * 4);  // dWz partials (split-K GEMM or per workgroup)
   return t;
@@ -2028,7 +2034,7 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   hipStream_t s = (hipStream_t)stream;
   const int64_t R = g.R, H = C;
   const int64_t tiles = (R + 127) / 128;
-  const int s5 = tm_w5_splits(R), sz = tm_wz_splits(R);
+  const int s5 = tm_w5_splits(R, C), sz = tm_wz_splits(R);
   const TmPacked k = tm_packed(workspace, C);
   const TmWeights w{w_ap, w_ag, w_bp, w_bg, w_g, w_z};
   char* wp_ = (char*)workspace + tm_weights_bytes(C);
