@@ -38,7 +38,7 @@ constexpr int row_depth() { return KS <= 4 ? 4 : 3; }
 template <int KS, int MT>
 __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     const __bf16* __restrict__ x, int64_t ldx, const __bf16* __restrict__ w, int w_kc,
-    int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int R, int N, int64_t nblocks) {
+    int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int64_t R, int N, int64_t nblocks) {
   constexpr int K = 32 * KS;
   constexpr int CPR = K / 8;               // 16-byte chunks per x row
   constexpr int DEPTH = row_depth<KS>();
@@ -73,8 +73,9 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     }
   }
 
-  const i32x4 rs_x = buffer_rsrc(x);
-  const __amdgpu_buffer_rsrc_t rs_y = __builtin_amdgcn_make_buffer_rsrc(y, 0, 0x7FFFFFFF, 0x00020000);
+  // Buffer resources are based at each block's first row (64-bit address
+  // arithmetic on the scalar unit), so the 32-bit lane offsets stay small
+  // for any row count.
   const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
   const int64_t bbeg = blockIdx.x * per;
   const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
@@ -82,14 +83,14 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
   // r = ci / CPR, stored at slot (c + r) % CPR of its row.
   auto issue = [&](int64_t blk) {
     const int stage = (int)(blk % DEPTH);
+    const i32x4 rs_x = buffer_rsrc(x + (blk < bend ? blk : 0) * 32 * ldx);
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int ci = 256 * j + tid;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
-      const uint32_t m = (uint32_t)blk * 32 + r;
-      const bool ok = blk < bend && m < (uint32_t)R;
-      buf2lds16(rs_x, ok ? (uint32_t)(((int64_t)m * ldx + 8 * gc) * 2) : kBufOOB,
+      const bool ok = blk < bend && blk * 32 + r < R;
+      buf2lds16(rs_x, ok ? (uint32_t)((r * ldx + 8 * gc) * 2) : kBufOOB,
                 &Xs[stage][(256 * j + 64 * wv) * 8]);
     }
   };
@@ -138,16 +139,17 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
       constexpr int SIT = (32 * NMAX / 8 + 255) / 256;
       const int st = tid - 256, cpr = N / 8;
       const int nch = 32 * cpr;
+      const __amdgpu_buffer_rsrc_t rs_y =
+          __builtin_amdgcn_make_buffer_rsrc(y + blk * 32 * ldy, 0, 0x7FFFFFFF, 0x00020000);
       bf16x8 v[SIT];
       uint32_t off[SIT];
 #pragma unroll
       for (int i = 0; i < SIT; ++i) {
         const int q = st + 256 * i;
         const int row = q / cpr, k = q - row * cpr;
-        const uint32_t m = (uint32_t)blk * 32 + row;
-        const bool ok = q < nch && m < (uint32_t)R;
+        const bool ok = q < nch && blk * 32 + row < R;
         v[i] = *reinterpret_cast<const bf16x8*>(&Yb[(q < nch ? row * YP + 8 * k : 0)]);
-        off[i] = ok ? (uint32_t)(((int64_t)m * ldy + 8 * k) * 2) : kBufOOB;
+        off[i] = ok ? (uint32_t)((row * ldy + 8 * k) * 2) : kBufOOB;
       }
 #pragma unroll
       for (int i = 0; i < SIT; ++i)
@@ -160,22 +162,23 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
 }
 
 // Runs y = x W^T on the row kernel when the shape has an instance (K = 128,
-// N a multiple of 16 with N / 16 <= 8 MT, 16-byte aligned rows,
-// every byte offset below 2^31); returns false (nothing launched) otherwise.
+// N a multiple of 16 with N / 16 <= 8 MT, 16-byte aligned rows and
+// row pitches below 2^26 bytes); returns false (nothing launched) otherwise.
 bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_t ldw, __bf16* y,
                  int64_t ldy, int64_t R, int64_t N, int64_t K, hipStream_t stream, int* rc,
                  const char* fn) {
   if (R < 1 || N < 16 || N % 16 || N > 640 || ldx % 8 || ldy % 8 || ldx < K || ldy < N ||
       (uintptr_t)x % 16 || (uintptr_t)y % 16 || (w_kc && (ldw % 8 || (uintptr_t)w % 16)))
     return false;
-  if (R * ldx * 2 >= (int64_t)kBufOOB || R * ldy * 2 >= (int64_t)kBufOOB) return false;
+  // Lane offsets inside one 32-row block stay below 2^31 bytes.
+  if (32 * ldx * 2 >= (int64_t)kBufOOB || 32 * ldy * 2 >= (int64_t)kBufOOB) return false;
   const int tiles = (int)(N / 16);
   const int64_t nblocks = (R + 31) / 32;
   const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
 #define TPF_ROW_CASE(KS, MT)                                                                   \
   if (K == 32 * KS && tiles <= kRowNW * MT) {                                                  \
     hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT>), dim3(grid), dim3(64 * kRowNW), 0, stream,   \
-                       x, ldx, w, w_kc, ldw, y, ldy, (int)R, (int)N, nblocks);                 \
+                       x, ldx, w, w_kc, ldw, y, ldy, R, (int)N, nblocks);                      \
     *rc = check_launch(fn);                                                                    \
     return true;                                                                               \
   }

@@ -130,3 +130,33 @@ def test_row_gemm(gpu, case, w_kc):
     ref = x.double().cpu() @ w.double().cpu().t()
     assert max_rel(y.float().cpu().numpy(), ref.numpy()) <= 8e-3
     assert torch.equal(part.view(torch.int16), y[lo:hi].view(torch.int16)), "row chunk differs"
+
+
+@pytest.mark.gpu
+def test_row_gemm_output_beyond_2gib(gpu):
+    """An output larger than 2 GiB (buffer offsets are per 32-row block):
+    the last rows match a separate call on them bitwise and the FP32
+    product within the bf16 tolerance."""
+    from openfold3_triangle_kernel_amd import _native
+
+    R, N, K = 1_900_000, 576, 128
+    assert R * N * 2 > 2**31
+    g = torch.Generator(device=gpu).manual_seed(11)
+    x = torch.randn(R, K, device=gpu, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, device=gpu, generator=g).to(torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    print(f"row gemm R={R} N={N} K={K} (> 2 GiB output)", flush=True)
+
+    def run(xs):
+        y = torch.empty((xs.shape[0], N), device=gpu, dtype=torch.bfloat16)
+        _native.call("tpf_gemm_bf16", xs.data_ptr(), 1, K, 0, w.data_ptr(), 1, K, 0, y.data_ptr(), 0,
+                     N, 0, xs.shape[0], N, K, 1, 1.0, stream)
+        return y
+
+    y = run(x)
+    tail = run(x[R - 1000:].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(tail.view(torch.int16), y[R - 1000:].view(torch.int16))
+    ref = x[R - 1000:].float() @ w.float().t()
+    assert max_rel(y[R - 1000:].float().cpu().numpy(), ref.cpu().numpy()) <= 8e-3
+    del y
