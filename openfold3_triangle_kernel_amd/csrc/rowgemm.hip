@@ -168,7 +168,8 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
                  int64_t ldy, int64_t R, int64_t N, int64_t K, hipStream_t stream, int* rc,
                  const char* fn) {
   if (R < 1 || N < 16 || N % 16 || N > 640 || ldx % 8 || ldy % 8 || ldx < K || ldy < N ||
-      (uintptr_t)x % 16 || (uintptr_t)y % 16 || (w_kc && (ldw % 8 || (uintptr_t)w % 16)))
+      (uintptr_t)x % 16 || (uintptr_t)y % 16 || (w_kc && (ldw % 8 || (uintptr_t)w % 16)) ||
+      ldw < (w_kc ? K : N))
     return false;
   // Lane offsets inside one 32-row block stay below 2^31 bytes.
   if (32 * ldx * 2 >= (int64_t)kBufOOB || 32 * ldy * 2 >= (int64_t)kBufOOB) return false;
