@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (5). */
+/* ABI revision of this header (6). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -383,40 +383,57 @@ int tpf_layer_norm_backward_bf16(const void* dy, const void* x, int64_t B, int64
                                  const float* w, void* dx, float* dw, float* db, void* workspace,
                                  int64_t workspace_bytes, void* stream);
 
-/* Attention core of the triangle-attention module over pair rows.  proj
- * [B, N, N, pitch] bf16 holds, per pair row (i, j), the module's projections
- * q | k | v | gate (H*D columns each, head-major inside) | pair bias (H) |
- * pad (pitch a multiple of 8); plane i attends over j.  mask f32 [B, N, N]
- * additive.  flags: TPF_PAIR_BIAS_TRANSPOSED selects bias[h, q, k] =
- * proj[b, k, q, 4HD + h] instead of proj[b, q, k, 4HD + h];
- * TPF_PAIR_OG_TRANSPOSED stores og (forward) and reads d_og (backward) of
- * pair row (i, j) at row (j, i), so the ending node's module output leaves
- * its output projection in the caller's pair order.  Forward writes o
- * [B, N, N, H*D], lse [B, N, H, N] f32 and the gated og = o * sigmoid(gate).
- * Backward takes d_og and writes the whole projection gradient row into
- * dproj (same layout as proj, pad columns zeroed).  residual (nullable, bf16 like o):
- * when given, the forward writes o's shadow residual there and the backward
- * forms delta from o + residual, as the standalone shadow entry points do.
- * Replaces the module glue around the
- * kernel (openfold3/core/model/layers/triangular_attention.py:160-243 with
+/* Attention core of the triangle-attention module over pair rows (row
+ * (b, i, j) = pair (i, j); plane i attends over j).  q, k, v are head-major
+ * planes qkv [3][B][N][H][N][D] bf16 (q | k | v, as tpf_pair_projection_bf16
+ * writes them); rest [B*N*N][rest_pitch] bf16 holds per pair row the gate
+ * logits (H*D) | the pair bias (H) | pad; mask f32 [B, N, N] additive.
+ * flags: TPF_PAIR_BIAS_TRANSPOSED selects bias[h, q, k] = rest[b, k, q, HD + h]
+ * instead of rest[b, q, k, HD + h]; TPF_PAIR_OG_TRANSPOSED stores og
+ * (forward) and reads d_og (backward) of pair row (i, j) at row (j, i), so the
+ * ending node's module output leaves its output projection in the caller's
+ * pair order.  Forward writes o [B, N, N, H*D], lse [B, N, H, N] f32 and the
+ * gated og = o * sigmoid(gate).  Backward takes d_og and writes the whole
+ * projection gradient row into dproj [B*N*N][dproj_pitch] = q | k | v | gate
+ * | bias | pad (pad zeroed).  residual (nullable, bf16 like o): when given,
+ * the forward writes o's shadow residual there and the backward forms delta
+ * from o + residual, as the standalone shadow entry points do.  Replaces the
+ * module glue around the kernel
+ * (openfold3/core/model/layers/triangular_attention.py:160-243 with
  * openfold3/core/model/primitives/attention.py:640-692: q/k/v/gate/bias
  * projections split into views, gating, and the gradient concatenation). */
 enum {
-  TPF_PAIR_BIAS_TRANSPOSED = 1, /* pair bias read as bias[h, q, k] = proj[b, k, q, 4HD + h] */
+  TPF_PAIR_BIAS_TRANSPOSED = 1, /* pair bias read as bias[h, q, k] = rest[b, k, q, HD + h] */
   TPF_PAIR_OG_TRANSPOSED = 2    /* og / d_og rows in transposed pair order */
 };
 int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H);
-int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int flags, void* o, float* lse, void* og, void* residual,
-                               void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
-                               int64_t H, int64_t D, double scale, void* stream);
+int tpf_attn_pair_forward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                               const float* mask, int flags, void* o, float* lse, void* og,
+                               void* residual, void* workspace, int64_t workspace_bytes,
+                               int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                               void* stream);
 int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t D);
-int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
-                                int flags, const void* o, const float* lse,
+int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                                const float* mask, int flags, const void* o, const float* lse,
                                 const void* residual, const void* d_og, void* dproj,
-                                void* workspace,
-                                int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
-                                int64_t D, double scale, void* stream);
+                                int64_t dproj_pitch, void* workspace, int64_t workspace_bytes,
+                                int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                                void* stream);
+
+/* The projection of the triangle-attention module, x [B*N*N, C] times
+ * W_all^T (W_all [P, C] = W_q; W_k; W_v; W_gate; W_bias; 0), with its output
+ * split as the pair-row core reads it: columns q | k | v into head-major
+ * planes qkv [3][B][N][H][N][D], the remaining P - 3*H*D columns (gate | bias
+ * | pad) into rows rest [B*N*N][P - 3*H*D].  bf16 in and out, f32
+ * accumulation, on the weight-stationary row kernel; supported when C = 128,
+ * P is a multiple of 16 up to 640 with P - 3*H*D >= 8 a multiple of 8, N a
+ * multiple of 32 and D a multiple of 8 (tpf_pair_projection_supported).  No
+ * reference counterpart as one call: the module's linear projections
+ * (openfold3/core/model/layers/triangular_attention.py:160-243). */
+int tpf_pair_projection_supported(int64_t P, int64_t C, int64_t N, int64_t H, int64_t D);
+int tpf_pair_projection_bf16(const void* x, const void* w, int64_t B, int64_t N, int64_t C,
+                             int64_t P, int64_t H, int64_t D, void* qkv, void* rest,
+                             void* stream);
 
 #ifdef __cplusplus
 }

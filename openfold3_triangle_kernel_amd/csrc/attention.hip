@@ -34,11 +34,14 @@ namespace tpf {
 
 struct AttnGeom {
   int B, O, H, N, D;
-  int64_t s_row, s_head;   // Q/K/V/dQ/dK/dV element strides
-  int64_t s_plane;         // elements between (b, o) planes of Q/K/V/dQ/dK/dV
+  int64_t s_row, s_head;   // Q/K/V element strides
+  int64_t s_plane;         // elements between (b, o) planes of Q/K/V
+  int64_t o_row, o_head;   // dQ/dK/dV element strides (the Q/K/V ones unless the
+  int64_t o_plane;         //   pair-row core writes the gradients into its projection rows)
   int64_t bias_bstride;    // elements between bias batches (0 = broadcast)
   float scale;             // softmax scale (1/sqrt(D_true))
   int og_t;                // pair-row core: og rows in transposed pair order (O == N)
+  int64_t gate_pitch;      // pair-row core: row pitch of the gate rows [B*O*N][gate_pitch]
 };
 
 // Element strides of a pair bias bias[bb, h, q, k]: the standalone op's
@@ -460,8 +463,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
           if (gate) {
             // Output gate of the pair-row module: og = o * sigmoid(g), with g
             // in Q's storage order (the gate columns of the projection rows).
-            const bf16x4 g4 = ld4(gate + (int64_t)plane[p] * g.s_plane + (int64_t)h * g.s_head +
-                                  (int64_t)qi * g.s_row + d0);
+            const bf16x4 g4 = ld4(gate + ((int64_t)plane[p] * N + qi) * g.gate_pitch + h * D + d0);
             bf16x4 og4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) og4[i] = f2bf(bf2f(o4[i]) * sigmoidf(bf2f(g4[i])));
@@ -1191,7 +1193,7 @@ __global__ __launch_bounds__(256 * bwd_kh(DP), 1) void attn_bwd_kernel(
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int key = key_base + cb * 32 + kl;
-      const int64_t row = plane_off + (int64_t)key * g.s_row;
+      const int64_t row = (int64_t)plane * g.o_plane + (int64_t)h * g.o_head + (int64_t)key * g.o_row;
       uint32_t pk[4][2], pv[4][2];  // [j][pair] packed bf16
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -1263,7 +1265,7 @@ __device__ __forceinline__ void dq_fold_block(const __bf16* __restrict__ part,
   bf16x8 o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = f2bf(acc[e] * g.scale);
-  st8(dq + plane * g.s_plane + hh * g.s_head + (int64_t)qq * g.s_row + d0, o);
+  st8(dq + plane * g.o_plane + hh * g.o_head + (int64_t)qq * g.o_row + d0, o);
 }
 
 // Grid: x = 256-item chunk, y = plane * H + h (strided past the grid limit).
@@ -1414,10 +1416,10 @@ __device__ __forceinline__ float gate_sigmoid(float x) { return sigmoidf(x); }
 template <bool SHADOW>
 __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
     const __bf16* __restrict__ d_og, const __bf16* __restrict__ o,
-    const __bf16* __restrict__ res, const __bf16* __restrict__ gate, int64_t pitch,
+    const __bf16* __restrict__ res, const __bf16* __restrict__ gate, int64_t gpitch,
     __bf16* __restrict__ d_o,
-    float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t items, int per, FastDiv fN,
-    int H, int D, FastDiv fhc8, int og_t) {
+    float* __restrict__ delta, __bf16* __restrict__ dgate, int64_t dpitch, int64_t items, int per,
+    FastDiv fN, int H, int D, FastDiv fhc8, int og_t) {
   // items < 2^31 (checked on the host): 32-bit item index; element offsets
   // (8 per item) are formed in 64 bits.
   __shared__ float part[256];
@@ -1437,7 +1439,7 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
       dog = (((size_t)bb * fN.d + j) * fN.d + i) * (8 * (size_t)fhc8.d) + (size_t)c * 8;
     }
     const bf16x8 dv = ld8(d_og + dog), ov = ld8(o + (size_t)t * 8),
-                 gv = ld8(gate + (size_t)row * pitch + c * 8);
+                 gv = ld8(gate + (size_t)row * gpitch + c * 8);
     bf16x8 rv;
     if (SHADOW) rv = ld8(res + (size_t)t * 8);
     bf16x8 r_do, r_dg;
@@ -1452,7 +1454,7 @@ __global__ __launch_bounds__(256) void attn_gate_bwd_kernel(
       sdot = fmaf(bf2f(r_do[e]), SHADOW ? oo + bf2f(rv[e]) : oo, sdot);
     }
     st8(d_o + (size_t)t * 8, r_do);
-    st8(dgate + (size_t)row * pitch + c * 8, r_dg);
+    st8(dgate + (size_t)row * dpitch + c * 8, r_dg);
   }
   part[tid] = sdot;
   __syncthreads();
@@ -1564,8 +1566,12 @@ static int make_geom(AttnGeom* g, int64_t B, int64_t O, int64_t H, int64_t N, in
     return set_error(TPF_ERR_SHAPE, "%s: bias batch count %lld must be 1 or B=%lld", fn,
                      (long long)bias_batches, (long long)B);
   g->bias_bstride = (bias_batches == 1) ? 0 : H * N * N;
+  g->o_row = g->s_row;
+  g->o_head = g->s_head;
+  g->o_plane = g->s_plane;
   g->scale = (float)scale;
   g->og_t = 0;
+  g->gate_pitch = 0;
   return check_geom(*g, fn);
 }
 
@@ -2265,31 +2271,40 @@ int tpf_attn_dq_dbias_bf16(const void* q, const void* k, const void* v, const vo
 }
 
 // ---------------------------------------------------------------------------
-// Pair-row entry points: the attention core of the triangle-attention module
-// over one projection buffer proj [B, N, N, pitch] (row = pair (i, j)) whose
-// columns are q | k | v | gate (H*D each) | pair bias (H) | pad.
+// Pair-row entry points: the attention core of the triangle-attention module.
+// q, k, v come as head-major planes qkv[part][b][i][h][j][d] (written so by
+// the projection, tpf_pair_projection_bf16), the gate and the pair bias as
+// rows rest[b][i][j][rest_pitch] = gate (H*D) | bias (H) | pad, and the
+// gradients go to rows dproj[b][i][j][dproj_pitch] = q | k | v | gate | bias
+// | pad.  Row (b, i, j) is pair (i, j); plane i attends over j.
 // ---------------------------------------------------------------------------
 
-static int pair_geom(AttnGeom* g, BiasView* bv, int64_t pitch, int flags, int64_t B,
-                     int64_t N, int64_t H, int64_t D, double scale, const char* fn) {
+static int pair_geom(AttnGeom* g, BiasView* bv, int64_t rest_pitch, int64_t dproj_pitch,
+                     int flags, int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                     const char* fn) {
   if (flags & ~(TPF_PAIR_BIAS_TRANSPOSED | TPF_PAIR_OG_TRANSPOSED))
     return set_error(TPF_ERR_ARG, "%s: unknown flags 0x%x", fn, flags);
-  int rc = make_geom(g, B, N, H, N, D, 1, B, scale, fn);
+  int rc = make_geom(g, B, N, H, N, D, 0, B, scale, fn);  // head-major q / k / v
   if (rc) return rc;
   const int transpose_bias = (flags & TPF_PAIR_BIAS_TRANSPOSED) != 0;
   g->og_t = (flags & TPF_PAIR_OG_TRANSPOSED) != 0;
   const int64_t hc = H * D;
-  if (pitch < 4 * hc + H || pitch % 8 != 0)
-    return set_error(TPF_ERR_SHAPE, "%s: pitch %lld must be a multiple of 8 >= 4*H*D + H", fn,
-                     (long long)pitch);
+  if (rest_pitch < hc + H || rest_pitch % 8 != 0)
+    return set_error(TPF_ERR_SHAPE, "%s: rest pitch %lld must be a multiple of 8 >= H*D + H", fn,
+                     (long long)rest_pitch);
+  if (dproj_pitch && (dproj_pitch < 4 * hc + H || dproj_pitch % 8 != 0))
+    return set_error(TPF_ERR_SHAPE, "%s: dproj pitch %lld must be a multiple of 8 >= 4*H*D + H",
+                     fn, (long long)dproj_pitch);
   if (H > 16) return set_error(TPF_ERR_SHAPE, "%s: H=%lld exceeds 16", fn, (long long)H);
-  g->s_row = pitch;
-  g->s_head = D;
-  g->s_plane = N * pitch;
-  bv->s_bb = N * N * pitch;
+  // Gradients into the projection-gradient rows.
+  g->o_row = dproj_pitch;
+  g->o_head = D;
+  g->o_plane = N * dproj_pitch;
+  g->gate_pitch = rest_pitch;
+  bv->s_bb = N * N * rest_pitch;
   bv->s_h = 1;
-  bv->s_q = transpose_bias ? pitch : N * pitch;
-  bv->s_k = transpose_bias ? N * pitch : pitch;
+  bv->s_q = transpose_bias ? rest_pitch : N * rest_pitch;
+  bv->s_k = transpose_bias ? N * rest_pitch : rest_pitch;
   bv->H = (int)H;
   return TPF_OK;
 }
@@ -2298,29 +2313,31 @@ int64_t tpf_attn_pair_forward_workspace_bytes(int64_t B, int64_t N, int64_t H) {
   return B * H * N * N * 4;
 }
 
-int tpf_attn_pair_forward_bf16(const void* proj, int64_t pitch, const float* mask,
-                               int flags, void* o, float* lse, void* og, void* residual,
-                               void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
-                               int64_t H, int64_t D, double scale, void* stream) {
+int tpf_attn_pair_forward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                               const float* mask, int flags, void* o, float* lse, void* og,
+                               void* residual, void* workspace, int64_t workspace_bytes,
+                               int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                               void* stream) {
   const char* fn = "tpf_attn_pair_forward_bf16";
   AttnGeom g;
   BiasView bv;
-  int rc = pair_geom(&g, &bv, pitch, flags, B, N, H, D, scale, fn);
+  int rc = pair_geom(&g, &bv, rest_pitch, 0, flags, B, N, H, D, scale, fn);
   if (rc) return rc;
-  if (!proj || !mask || !o || !lse || !og || !workspace)
+  if (!qkv || !rest || !mask || !o || !lse || !og || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  if ((uintptr_t)proj % 16 || (uintptr_t)o % 16 || (uintptr_t)og % 16)
-    return set_error(TPF_ERR_ARG, "%s: proj, o and og must be 16-byte aligned", fn);
+  if (((uintptr_t)qkv | (uintptr_t)rest | (uintptr_t)o | (uintptr_t)og) % 16)
+    return set_error(TPF_ERR_ARG, "%s: qkv, rest, o and og must be 16-byte aligned", fn);
   if (workspace_bytes < tpf_attn_pair_forward_workspace_bytes(B, N, H))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
-  const int64_t hc = H * D;
-  const __bf16* p = (const __bf16*)proj;
+  const int64_t hc = H * D, part = B * N * H * N * D;
+  const __bf16* q = (const __bf16*)qkv;
+  const __bf16* r = (const __bf16*)rest;
   hipStream_t s = (hipStream_t)stream;
   if (residual && (uintptr_t)residual % 16)
     return set_error(TPF_ERR_ARG, "%s: residual must be 16-byte aligned", fn);
   // The forward's epilogue applies the output gate (og = o * sigmoid(g)).
-  return attn_forward_impl(g, p, p + hc, p + 2 * hc, mask, p + 4 * hc, bv, B, o, lse, residual,
-                           workspace, s, fn, p + 3 * hc, og);
+  return attn_forward_impl(g, q, q + part, q + 2 * part, mask, r + hc, bv, B, o, lse, residual,
+                           workspace, s, fn, r, og);
 }
 
 // Workspace: the attention backward's, then d_o [B, N, N, H*D] bf16 and
@@ -2330,28 +2347,30 @@ int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, 
          a256(B * N * H * N * 4);
 }
 
-int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* mask,
-                                int flags, const void* o, const float* lse,
+int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                                const float* mask, int flags, const void* o, const float* lse,
                                 const void* residual, const void* d_og, void* dproj,
-                                void* workspace,
-                                int64_t workspace_bytes, int64_t B, int64_t N, int64_t H,
-                                int64_t D, double scale, void* stream) {
+                                int64_t dproj_pitch, void* workspace, int64_t workspace_bytes,
+                                int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                                void* stream) {
   const char* fn = "tpf_attn_pair_backward_bf16";
   AttnGeom g;
   BiasView bv;
-  int rc = pair_geom(&g, &bv, pitch, flags, B, N, H, D, scale, fn);
+  if (dproj_pitch < 1) return set_error(TPF_ERR_SHAPE, "%s: dproj pitch must be positive", fn);
+  int rc = pair_geom(&g, &bv, rest_pitch, dproj_pitch, flags, B, N, H, D, scale, fn);
   if (rc) return rc;
-  if (!proj || !mask || !o || !lse || !d_og || !dproj || !workspace)
+  if (!qkv || !rest || !mask || !o || !lse || !d_og || !dproj || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  if (((uintptr_t)proj | (uintptr_t)o | (uintptr_t)d_og | (uintptr_t)dproj) % 16)
-    return set_error(TPF_ERR_ARG, "%s: proj, o, d_og and dproj must be 16-byte aligned", fn);
+  if (((uintptr_t)qkv | (uintptr_t)rest | (uintptr_t)o | (uintptr_t)d_og | (uintptr_t)dproj) % 16)
+    return set_error(TPF_ERR_ARG, "%s: qkv, rest, o, d_og and dproj must be 16-byte aligned", fn);
   if (workspace_bytes < tpf_attn_pair_backward_workspace_bytes(B, N, H, D))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
-  const int64_t hc = H * D;
+  const int64_t hc = H * D, part = B * N * H * N * D;
   const int64_t main_bytes = bwd_full_bytes(B, N, H, N, D);
   __bf16* d_o = (__bf16*)((char*)workspace + main_bytes);
   float* delta = (float*)((char*)workspace + main_bytes + a256(B * N * N * hc * 2));
-  const __bf16* p = (const __bf16*)proj;
+  const __bf16* q = (const __bf16*)qkv;
+  const __bf16* r = (const __bf16*)rest;
   __bf16* dp = (__bf16*)dproj;
   hipStream_t s = (hipStream_t)stream;
   const int64_t items = B * N * N * (hc / 8);
@@ -2362,19 +2381,19 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   const FastDiv fN = make_fastdiv((uint32_t)N), fhc8 = make_fastdiv((uint32_t)(hc / 8));
   if (residual)
     hipLaunchKernelGGL(attn_gate_bwd_kernel<true>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
-                       (const __bf16*)o, (const __bf16*)residual, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
+                       (const __bf16*)o, (const __bf16*)residual, r, rest_pitch, d_o, delta,
+                       dp + 3 * hc, dproj_pitch, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
   else
     hipLaunchKernelGGL(attn_gate_bwd_kernel<false>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
-                       (const __bf16*)o, (const __bf16*)nullptr, p + 3 * hc, pitch, d_o, delta,
-                       dp + 3 * hc, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
+                       (const __bf16*)o, (const __bf16*)nullptr, r, rest_pitch, d_o, delta,
+                       dp + 3 * hc, dproj_pitch, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
   if ((rc = check_launch(fn))) return rc;
   BwdParts pt;
   bwd_layout(B, N, H, N, D, B * N, (char*)workspace, &pt);
   const BwdPlan plan = bwd_plan(B, N, H, N, D, INT64_MAX);
-  if ((rc = attn_backward_prep_impl(g, lse, delta, p + 4 * hc, bv, B, pt, s, fn))) return rc;
-  if ((rc = attn_backward_slab_impl(g, p, p + hc, p + 2 * hc, d_o, mask, dp + hc, dp + 2 * hc, pt,
-                                    plan, bwd_slab(plan, B, N, 0), s, fn)))
+  if ((rc = attn_backward_prep_impl(g, lse, delta, r + hc, bv, B, pt, s, fn))) return rc;
+  if ((rc = attn_backward_slab_impl(g, q, q + part, q + 2 * part, d_o, mask, dp + hc, dp + 2 * hc,
+                                    pt, plan, bwd_slab(plan, B, N, 0), s, fn)))
     return rc;
   const int64_t nph = B * N * H;
   hipLaunchKernelGGL(attn_dq_reduce_kernel,
@@ -2384,7 +2403,7 @@ int tpf_attn_pair_backward_bf16(const void* proj, int64_t pitch, const float* ma
   const int64_t groups = plan.runs;
   const dim3 db_grid((unsigned)(B * N * N / 512));
   hipLaunchKernelGGL(attn_dbias_pair_kernel, db_grid, dim3(256), 0, s, pt.db, (int)B, (int)B,
-                     (int)groups, (int)H, (int)N, dp, pitch, 4 * hc,
+                     (int)groups, (int)H, (int)N, dp, dproj_pitch, 4 * hc,
                      (flags & TPF_PAIR_BIAS_TRANSPOSED) != 0);
   return check_launch(fn);
 }

@@ -35,10 +35,23 @@ constexpr int row_depth() { return KS <= 4 ? 4 : 3; }
 // (K = 576, the dx = dproj W_all product, measured slower here than on the
 // tile GEMM, 216 against 197 us at 589,824 rows, and is left to it.)
 
-template <int KS, int MT>
+// Split destination of the triangle-attention projection (SPLIT = true):
+// output columns [0, 3 H D) are q | k | v and go to head-major planes
+// qkv[part][b][i][h][j][d] (the layout the attention kernels stream as
+// contiguous 2 KB tiles), the rest (gate | bias | pad) to rows of pitch
+// ldy in y.  Row r = (b, i, j) of the pair grid; a 32-row block lies in one
+// (b, i) because the sequence length is a multiple of 32.
+struct RowSplit {
+  __bf16* qkv;
+  int64_t part_elems;  // B * N * H * N * D
+  int Nseq, H, D;
+};
+
+template <int KS, int MT, bool SPLIT>
 __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     const __bf16* __restrict__ x, int64_t ldx, const __bf16* __restrict__ w, int w_kc,
-    int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int64_t R, int N, int64_t nblocks) {
+    int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int64_t R, int N, int64_t nblocks,
+    RowSplit sp) {
   constexpr int K = 32 * KS;
   constexpr int CPR = K / 8;               // 16-byte chunks per x row
   constexpr int DEPTH = row_depth<KS>();
@@ -94,6 +107,39 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
                 &Xs[stage][(256 * j + 64 * wv) * 8]);
     }
   };
+  // Split destination: storing thread st's chunks i (q = st + 256 i of the
+  // block) are numbered so that consecutive lanes write consecutive
+  // addresses: first the q | k | v segments (part, head) of 32 rows x D (2 KB
+  // contiguous in a plane at D = 32), a row's chunks fastest; then the rest
+  // rows (contiguous: their pitch is the rest width).  The map is the same
+  // for every block (offsets relative to the block's plane and row bases),
+  // so it is formed once, off the block loop.
+  struct SplitChunk { int64_t off; int lds, row; bool rest; };
+  constexpr int SIT = (32 * NMAX / 8 + 255) / 256;
+  SplitChunk smap[SPLIT ? SIT : 1];
+  if constexpr (SPLIT) {
+    const int st = tid - 256, cpr = N / 8, nch = 32 * cpr;
+    const int hc = sp.H * sp.D, dch = sp.D / 8;
+    const int seg_ch = 32 * dch, nq = 3 * sp.H * seg_ch, rcpr = cpr - 3 * hc / 8;
+#pragma unroll
+    for (int i = 0; i < SIT; ++i) {
+      const int q = st + 256 * i;
+      SplitChunk m{0, -1, 0, false};
+      if (!loader && q < nch) {
+        if (q < nq) {
+          const int seg = q / seg_ch, in = q - seg * seg_ch;
+          const int part = seg / sp.H, h = seg - part * sp.H;
+          const int row = in / dch, dc = in - row * dch;
+          m = SplitChunk{part * sp.part_elems + ((int64_t)h * sp.Nseq + row) * sp.D + 8 * dc,
+                         row * YP + part * hc + h * sp.D + 8 * dc, row, false};
+        } else {
+          const int u = q - nq, row = u / rcpr, k = u - row * rcpr;
+          m = SplitChunk{row * ldy + 8 * k, row * YP + 3 * hc + 8 * k, row, true};
+        }
+      }
+      smap[i] = m;
+    }
+  }
   if (loader) {
 #pragma unroll
     for (int d = 0; d < DEPTH - 1; ++d) issue(bbeg + d);
@@ -139,21 +185,42 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
       constexpr int SIT = (32 * NMAX / 8 + 255) / 256;
       const int st = tid - 256, cpr = N / 8;
       const int nch = 32 * cpr;
-      const __amdgpu_buffer_rsrc_t rs_y =
-          __builtin_amdgcn_make_buffer_rsrc(y + blk * 32 * ldy, 0, 0x7FFFFFFF, 0x00020000);
-      bf16x8 v[SIT];
-      uint32_t off[SIT];
+      if constexpr (!SPLIT) {
+        const __amdgpu_buffer_rsrc_t rs_y =
+            __builtin_amdgcn_make_buffer_rsrc(y + blk * 32 * ldy, 0, 0x7FFFFFFF, 0x00020000);
+        bf16x8 v[SIT];
+        uint32_t off[SIT];
 #pragma unroll
-      for (int i = 0; i < SIT; ++i) {
-        const int q = st + 256 * i;
-        const int row = q / cpr, k = q - row * cpr;
-        const bool ok = q < nch && blk * 32 + row < R;
-        v[i] = *reinterpret_cast<const bf16x8*>(&Yb[(q < nch ? row * YP + 8 * k : 0)]);
-        off[i] = ok ? (uint32_t)((row * ldy + 8 * k) * 2) : kBufOOB;
+        for (int i = 0; i < SIT; ++i) {
+          const int q = st + 256 * i;
+          const int row = q / cpr, k = q - row * cpr;
+          const bool ok = q < nch && blk * 32 + row < R;
+          v[i] = *reinterpret_cast<const bf16x8*>(&Yb[(q < nch ? row * YP + 8 * k : 0)]);
+          off[i] = ok ? (uint32_t)((row * ldy + 8 * k) * 2) : kBufOOB;
+        }
+#pragma unroll
+        for (int i = 0; i < SIT; ++i)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rs_y, off[i], 0, 0);
+      } else {
+        // Block rows r0 .. r0 + 31 = (b, i, j0 .. j0 + 31).
+        const int64_t r0 = blk * 32;
+        const int64_t bi = r0 / sp.Nseq;               // b * N + i
+        const int j0 = (int)(r0 - bi * sp.Nseq);
+        // Per-thread chunk map (the same for every block): see split_map.
+        __bf16* const qbase = sp.qkv + (bi * sp.H * sp.Nseq + j0) * sp.D;
+        __bf16* const rbase = y + r0 * ldy;
+        bf16x8 v[SIT];
+        __bf16* dst[SIT];
+#pragma unroll
+        for (int i = 0; i < SIT; ++i) {
+          const bool ok = smap[i].lds >= 0 && r0 + smap[i].row < R;
+          v[i] = *reinterpret_cast<const bf16x8*>(&Yb[ok ? smap[i].lds : 0]);
+          dst[i] = ok ? (smap[i].rest ? rbase : qbase) + smap[i].off : nullptr;
+        }
+#pragma unroll
+        for (int i = 0; i < SIT; ++i)
+          if (dst[i]) st8(dst[i], v[i]);
       }
-#pragma unroll
-      for (int i = 0; i < SIT; ++i)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rs_y, off[i], 0, 0);
     }
   }
   // The ring loads issued past the last block still write LDS: let them land
@@ -178,8 +245,8 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
   const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
 #define TPF_ROW_CASE(KS, MT)                                                                   \
   if (K == 32 * KS && tiles <= kRowNW * MT) {                                                  \
-    hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT>), dim3(grid), dim3(64 * kRowNW), 0, stream,   \
-                       x, ldx, w, w_kc, ldw, y, ldy, R, (int)N, nblocks);                      \
+    hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT, false>), dim3(grid), dim3(64 * kRowNW), 0,   \
+                       stream, x, ldx, w, w_kc, ldw, y, ldy, R, (int)N, nblocks, RowSplit{});  \
     *rc = check_launch(fn);                                                                    \
     return true;                                                                               \
   }
@@ -190,3 +257,31 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
 }
 
 }  // namespace tpf
+
+using namespace tpf;
+
+extern "C" int tpf_pair_projection_supported(int64_t P, int64_t K, int64_t N, int64_t H,
+                                             int64_t D) {
+  return K == 128 && P % 16 == 0 && P <= 640 && N % 32 == 0 && D % 8 == 0 && H >= 1 &&
+         P >= 3 * H * D + 8 && (P - 3 * H * D) % 8 == 0;
+}
+
+extern "C" int tpf_pair_projection_bf16(const void* x, const void* w, int64_t B, int64_t N,
+                                        int64_t C, int64_t P, int64_t H, int64_t D, void* qkv,
+                                        void* rest, void* stream) {
+  const char* fn = "tpf_pair_projection_bf16";
+  if (!x || !w || !qkv || !rest) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (B < 1 || N < 1 || !tpf_pair_projection_supported(P, C, N, H, D))
+    return set_error(TPF_ERR_SHAPE, "%s: unsupported shape (C=%lld P=%lld N=%lld H=%lld D=%lld)",
+                     fn, (long long)C, (long long)P, (long long)N, (long long)H, (long long)D);
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)qkv | (uintptr_t)rest) % 16)
+    return set_error(TPF_ERR_ARG, "%s: pointers must be 16-byte aligned", fn);
+  const int64_t R = B * N * N, rest_pitch = P - 3 * H * D;
+  const int64_t nblocks = (R + 31) / 32;
+  const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
+  const RowSplit sp{(__bf16*)qkv, B * N * H * N * D, (int)N, (int)H, (int)D};
+  hipLaunchKernelGGL((rowgemm_ws_kernel<4, 5, true>), dim3(grid), dim3(64 * kRowNW), 0,
+                     (hipStream_t)stream, (const __bf16*)x, C, (const __bf16*)w, 1, C,
+                     (__bf16*)rest, rest_pitch, R, (int)P, nblocks, sp);
+  return check_launch(fn);
+}

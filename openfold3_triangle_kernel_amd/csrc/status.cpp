@@ -27,6 +27,6 @@ extern "C" {
 
 const char* tpf_last_error(void) { return tpf::error_buffer(); }
 
-int tpf_abi_version(void) { return 5; }
+int tpf_abi_version(void) { return 6; }
 
 }  // extern "C"

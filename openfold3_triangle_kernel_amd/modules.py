@@ -126,6 +126,27 @@ def _mm(a: torch.Tensor, b: torch.Tensor, b_kc: bool) -> torch.Tensor:
     return out
 
 
+def _pair_projection(x2: torch.Tensor, wa: torch.Tensor, B: int, N: int, H: int, D: int):
+    """x2 [R, C] @ wa^T split as the pair-row core reads it: q | k | v as
+    head-major planes [3, B, N, H, N, D] and gate | bias | pad as rows
+    [R, P - 3 H D], in one pass of the row GEMM (``tpf_pair_projection_bf16``)
+    where the shape has an instance, else through the tile GEMM and a copy."""
+    R, C = x2.shape
+    P, hc = wa.shape[0], H * D
+    dev = x2.device
+    qkv = torch.empty((3, B, N, H, N, D), device=dev, dtype=torch.bfloat16)
+    if _native.query("tpf_pair_projection_supported", P, C, N, H, D):
+        rest = torch.empty((R, P - 3 * hc), device=dev, dtype=torch.bfloat16)
+        x2 = x2.contiguous()
+        with _device_ctx(dev):
+            _native.call("tpf_pair_projection_bf16", x2.data_ptr(), wa.data_ptr(), B, N, C, P, H,
+                         D, qkv.data_ptr(), rest.data_ptr(), _native.stream_of(x2))
+        return qkv, rest
+    proj = _mm(x2, wa, True)
+    qkv.copy_(proj[:, :3 * hc].view(B, N, N, 3, H, D).permute(3, 0, 1, 4, 2, 5))
+    return qkv, proj[:, 3 * hc:].contiguous()
+
+
 def _pair_flags(transpose_bias: bool, og_t: bool) -> int:
     """Flags of the pair-row entry points (TPF_PAIR_BIAS_TRANSPOSED = 1,
     TPF_PAIR_OG_TRANSPOSED = 2)."""
@@ -136,9 +157,12 @@ class _PairAttentionCore(torch.autograd.Function):
     """Projection -> triangle attention -> gate -> output projection of the
     triangle-attention module over BF16 pair rows, with explicit buffers.
 
-    One GEMM forms proj [R, P] = x W_all^T (columns q | k | v | gate | bias |
-    pad); ``tpf_attn_pair_forward_bf16`` reads q / k / v and the pair bias
-    from it in place and writes o and og = o * sigmoid(gate); out = og W_o^T.
+    One GEMM forms x W_all^T (W_all rows q | k | v | gate | bias | pad) and
+    stores q, k, v as head-major planes qkv [3, B, N, H, N, D] (the layout the
+    attention kernels stream as contiguous tiles) and gate | bias | pad as
+    rows ``rest`` [R, P - 3 H D] (``_pair_projection``);
+    ``tpf_attn_pair_forward_bf16`` reads them in place and writes o and
+    og = o * sigmoid(gate); out = og W_o^T.
     The backward's ``tpf_attn_pair_backward_bf16`` writes every column of the
     projection gradient row (gate, q, k, v, bias, zeroed pad) into one
     buffer, so dx = dproj W_all and dW_all = dproj^T x are single GEMMs.
@@ -158,7 +182,7 @@ class _PairAttentionCore(torch.autograd.Function):
         x2 = x.reshape(R, C)
         wa = w_all.to(torch.bfloat16)
         wo = w_o.to(torch.bfloat16)
-        proj = _mm(x2, wa, True)
+        qkv, rest = _pair_projection(x2, wa, B, N, H, D)
         o = torch.empty((R, hc), device=dev, dtype=torch.bfloat16)
         og = torch.empty_like(o)
         lse = torch.empty((B, N, H, N), device=dev, dtype=torch.float32)
@@ -169,13 +193,12 @@ class _PairAttentionCore(torch.autograd.Function):
         # backward's delta then sees o's f32 value.
         res = torch.empty_like(o) if shadow_enabled() else None
         with _device_ctx(dev):
-            _native.call("tpf_attn_pair_forward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
-                         _pair_flags(transpose_bias, og_t), o.data_ptr(), lse.data_ptr(),
-                         og.data_ptr(),
-                         _native.ptr(res), ws.data_ptr(), ws_bytes, B, N, H, D, scale,
-                         _native.stream_of(proj))
+            _native.call("tpf_attn_pair_forward_bf16", qkv.data_ptr(), rest.data_ptr(),
+                         rest.shape[1], mask_add.data_ptr(), _pair_flags(transpose_bias, og_t),
+                         o.data_ptr(), lse.data_ptr(), og.data_ptr(), _native.ptr(res),
+                         ws.data_ptr(), ws_bytes, B, N, H, D, scale, _native.stream_of(o))
         out = _mm(og, wo, True)
-        ctx.save_for_backward(x2, wa, wo, proj, o, og, lse, mask_add, res)
+        ctx.save_for_backward(x2, wa, wo, qkv, rest, o, og, lse, mask_add, res)
         ctx.dims = (B, N, H, D, C, P, _pair_flags(transpose_bias, og_t), scale)
         ctx.w_dtypes = (w_all.dtype, w_o.dtype)
         ctx.set_materialize_grads(False)
@@ -185,7 +208,7 @@ class _PairAttentionCore(torch.autograd.Function):
     def backward(ctx, dout):
         if dout is None:
             return (None,) * 8
-        x2, wa, wo, proj, o, og, lse, mask_add, res = ctx.saved_tensors
+        x2, wa, wo, qkv, rest, o, og, lse, mask_add, res = ctx.saved_tensors
         B, N, H, D, C, P, flags, scale = ctx.dims
         R = B * N * N
         dev = x2.device
@@ -196,11 +219,10 @@ class _PairAttentionCore(torch.autograd.Function):
         ws_bytes = int(_native.query("tpf_attn_pair_backward_workspace_bytes", B, N, H, D))
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
         with _device_ctx(dev):
-            _native.call("tpf_attn_pair_backward_bf16", proj.data_ptr(), P, mask_add.data_ptr(),
-                         flags, o.data_ptr(), lse.data_ptr(), _native.ptr(res),
-                         d_og.data_ptr(), dproj.data_ptr(), ws.data_ptr(), ws_bytes, B, N, H, D,
-                         scale,
-                         _native.stream_of(dproj))
+            _native.call("tpf_attn_pair_backward_bf16", qkv.data_ptr(), rest.data_ptr(),
+                         rest.shape[1], mask_add.data_ptr(), flags, o.data_ptr(), lse.data_ptr(),
+                         _native.ptr(res), d_og.data_ptr(), dproj.data_ptr(), P, ws.data_ptr(),
+                         ws_bytes, B, N, H, D, scale, _native.stream_of(dproj))
         dx = _mm(dproj, wa, False).view(B, N, N, C) if ctx.needs_input_grad[0] else None
         dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None
         return dx, dw_all, dw_o, None, None, None, None, None

@@ -160,3 +160,35 @@ def test_row_gemm_output_beyond_2gib(gpu):
     ref = x[R - 1000:].float() @ w.float().t()
     assert max_rel(y[R - 1000:].float().cpu().numpy(), ref.cpu().numpy()) <= 8e-3
     del y
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,N,H,D", [(1, 64, 4, 32), (2, 96, 2, 16), (1, 128, 4, 24)])
+def test_pair_projection_split(gpu, B, N, H, D):
+    """tpf_pair_projection_bf16: x W^T with q | k | v written as head-major
+    planes [3, B, N(i), H, N(j), D] and the remaining columns as rows, bitwise
+    equal to the row GEMM's plain output rearranged."""
+    from openfold3_triangle_kernel_amd import _native
+
+    C, hc = 128, H * D
+    P = (4 * hc + H + 63) // 64 * 64
+    R = B * N * N
+    assert _native.query("tpf_pair_projection_supported", P, C, N, H, D)
+    g = torch.Generator(device="cpu").manual_seed(B + N + H + D)
+    x = torch.randn(R, C, generator=g).to(torch.bfloat16).to(gpu)
+    w = torch.randn(P, C, generator=g).to(torch.bfloat16).to(gpu)
+    qkv = torch.full((3, B, N, H, N, D), float("nan"), device=gpu, dtype=torch.bfloat16)
+    rest = torch.full((R, P - 3 * hc), float("nan"), device=gpu, dtype=torch.bfloat16)
+    y = torch.empty((R, P), device=gpu, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    print(f"pair projection B={B} N={N} H={H} D={D} P={P}", flush=True)
+    _native.call("tpf_pair_projection_bf16", x.data_ptr(), w.data_ptr(), B, N, C, P, H, D,
+                 qkv.data_ptr(), rest.data_ptr(), stream)
+    _native.call("tpf_gemm_bf16", x.data_ptr(), 1, C, 0, w.data_ptr(), 1, C, 0, y.data_ptr(), 0, P,
+                 0, R, P, C, 1, 1.0, stream)
+    torch.cuda.synchronize()
+    want_qkv = y[:, :3 * hc].reshape(B, N, N, 3, H, D).permute(3, 0, 1, 4, 2, 5)
+    assert torch.equal(qkv.view(torch.int16), want_qkv.contiguous().view(torch.int16))
+    assert torch.equal(rest.view(torch.int16), y[:, 3 * hc:].contiguous().view(torch.int16))
+    ref = x.double().cpu() @ w.double().cpu().t()
+    assert max_rel(y.float().cpu().numpy(), ref.numpy()) <= 8e-3
