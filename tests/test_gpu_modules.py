@@ -120,13 +120,16 @@ def _graph_has(t, name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("N,transpose_bias", [(96, False), (128, False), (128, True)])
+@pytest.mark.parametrize("N,transpose_bias,C", [(96, False, 128), (128, False, 128),
+                                                (128, True, 128), (128, False, 64)])
 @pytest.mark.parametrize("starting", [True, False])
-def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
+def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias, C):
     """BF16 module forward + every parameter / input gradient vs the FP32
     stock math on the same (bf16-representable) weights.  N = 96 takes the
     per-projection route; N = 128 (a multiple of 64) the pair-row core
-    (tpf_attn_pair_*), with the pair bias plain or transposed.
+    (tpf_attn_pair_*), with the pair bias plain or transposed; C = 128 forms
+    the split projection on the row GEMM, C = 64 through the tile GEMM and a
+    copy (``_pair_projection``'s other branch).
 
     The reference's module check (scripts/benchmarks/
     turbopairformer_module_wiring_smoke.py:90-130) gates the output and the
@@ -138,16 +141,16 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
     from openfold3_triangle_kernel_amd import TriangleAttention
 
     torch.manual_seed(7)
-    m = TriangleAttention(128, 32, 4, starting=starting)
+    m = TriangleAttention(C, 32, 4, starting=starting)
     for p in m.parameters():
         p.data = p.data.normal_(std=0.1 if p.dim() == 2 else 1.0).bfloat16().float()
     m = m.to(gpu)
-    x = torch.randn(1, N, N, 128, device=gpu).bfloat16().float()
+    x = torch.randn(1, N, N, C, device=gpu).bfloat16().float()
     mask = (torch.rand(1, N, N, device=gpu) > 0.1).float()
-    dout = torch.randn(1, N, N, 128, device=gpu).bfloat16().float()
+    dout = torch.randn(1, N, N, C, device=gpu).bfloat16().float()
     ref_params = {n: p.detach().clone().requires_grad_(True) for n, p in m.named_parameters()}
     xr = x.clone().requires_grad_(True)
-    ref_m = TriangleAttention(128, 32, 4, starting=starting).to(gpu)
+    ref_m = TriangleAttention(C, 32, 4, starting=starting).to(gpu)
     ref_m.load_state_dict({n: p for n, p in ref_params.items()})
     for n, p in ref_m.named_parameters():
         p.requires_grad_(True)
@@ -168,7 +171,7 @@ def test_triangle_attention_module_backward(gpu, starting, N, transpose_bias):
     names = ["out", "x"] + [n for n, _ in mb.named_parameters()]
     for name, a, b in zip(names, [out] + list(grads), [ref] + list(ref_grads)):
         err = max_rel(a.detach().float().cpu().numpy(), b.detach().float().cpu().numpy())
-        print(f"module starting={starting} N={N} tb={transpose_bias} {name} max-rel {err:.3e}",
+        print(f"module starting={starting} N={N} tb={transpose_bias} C={C} {name} max-rel {err:.3e}",
               flush=True)
         assert err <= 2e-2, f"{name}: {err:.3e}"
 
