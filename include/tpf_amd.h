@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (6). */
+/* ABI revision of this header (7). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -419,6 +419,25 @@ int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_
                                 int64_t dproj_pitch, void* workspace, int64_t workspace_bytes,
                                 int64_t B, int64_t N, int64_t H, int64_t D, double scale,
                                 void* stream);
+/* tpf_attn_pair_backward_bf16 from the module's upstream gradient instead of
+ * d_og: dout [B*N*N, C] bf16 (rows in the caller's pair order, transposed
+ * with TPF_PAIR_OG_TRANSPOSED) and the output projection weight w_o [C, H*D]
+ * bf16 (out = og w_o^T).  The product d_og = dout w_o runs on the
+ * weight-stationary row kernel with the gate backward (d_o, the gate
+ * gradient, delta) in its epilogue, so d_og never reaches memory; results
+ * are bitwise those of tpf_gemm_bf16 (dout, w_o) followed by
+ * tpf_attn_pair_backward_bf16.  Same workspace.  Supported when C = 128, D in
+ * {8, 16, 32, 64} and H*D a multiple of 16 up to 128
+ * (tpf_attn_pair_backward_dout_supported).  Replaces the same module glue
+ * (openfold3/core/model/primitives/attention.py:640-692: linear_o's input
+ * gradient and the gating backward). */
+int tpf_attn_pair_backward_dout_supported(int64_t C, int64_t H, int64_t D);
+int tpf_attn_pair_backward_dout_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                                     const float* mask, int flags, const void* o,
+                                     const float* lse, const void* residual, const void* dout,
+                                     const void* w_o, int64_t C, void* dproj, int64_t dproj_pitch,
+                                     void* workspace, int64_t workspace_bytes, int64_t B,
+                                     int64_t N, int64_t H, int64_t D, double scale, void* stream);
 
 /* The projection of the triangle-attention module, x [B*N*N, C] times
  * W_all^T (W_all [P, C] = W_q; W_k; W_v; W_gate; W_bias; 0), with its output

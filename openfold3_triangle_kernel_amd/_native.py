@@ -87,6 +87,10 @@ SIGNATURES: dict[str, tuple] = {
     "tpf_attn_pair_backward_bf16": (
         _I32, [_P, _P, _I64, _P, _I32, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64,
                _I64, _F64, _P]),
+    "tpf_attn_pair_backward_dout_supported": (_I32, [_I64] * 3),
+    "tpf_attn_pair_backward_dout_bf16": (
+        _I32, [_P, _P, _I64, _P, _I32, _P, _P, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64,
+               _I64, _I64, _F64, _P]),
     "tpf_pair_projection_supported": (_I32, [_I64] * 5),
     "tpf_pair_projection_bf16": (_I32, [_P, _P] + [_I64] * 6 + [_P, _P, _P]),
     "tpf_layer_norm_forward_bf16": (_I32, [_P] + [_I64] * 7 + [_P, _P, _F64, _P, _P, _P, _P]),

@@ -28,6 +28,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "tpf_gemm.hpp"
 #include "tpf_status.hpp"
 
 namespace tpf {
@@ -2347,22 +2348,30 @@ int64_t tpf_attn_pair_backward_workspace_bytes(int64_t B, int64_t N, int64_t H, 
          a256(B * N * H * N * 4);
 }
 
-int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
-                                const float* mask, int flags, const void* o, const float* lse,
-                                const void* residual, const void* d_og, void* dproj,
-                                int64_t dproj_pitch, void* workspace, int64_t workspace_bytes,
-                                int64_t B, int64_t N, int64_t H, int64_t D, double scale,
-                                void* stream) {
-  const char* fn = "tpf_attn_pair_backward_bf16";
+}  // extern "C"
+
+namespace tpf {
+// The pair-row backward from d_og (d_og set) or, fused, from the module's
+// upstream gradient dout [R, C] and W_o [C, H*D] (d_og null): the d_og
+// product then runs with the gate backward in its epilogue
+// (rowgemm_gate_bwd) and d_og never reaches memory.
+static int pair_backward_impl(const void* qkv, const void* rest, int64_t rest_pitch,
+                              const float* mask, int flags, const void* o, const float* lse,
+                              const void* residual, const void* d_og, const void* dout,
+                              const void* w_o, int64_t C, void* dproj, int64_t dproj_pitch,
+                              void* workspace, int64_t workspace_bytes, int64_t B, int64_t N,
+                              int64_t H, int64_t D, double scale, void* stream, const char* fn) {
   AttnGeom g;
   BiasView bv;
   if (dproj_pitch < 1) return set_error(TPF_ERR_SHAPE, "%s: dproj pitch must be positive", fn);
   int rc = pair_geom(&g, &bv, rest_pitch, dproj_pitch, flags, B, N, H, D, scale, fn);
   if (rc) return rc;
-  if (!qkv || !rest || !mask || !o || !lse || !d_og || !dproj || !workspace)
+  if (!qkv || !rest || !mask || !o || !lse || !(d_og || (dout && w_o)) || !dproj || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
-  if (((uintptr_t)qkv | (uintptr_t)rest | (uintptr_t)o | (uintptr_t)d_og | (uintptr_t)dproj) % 16)
-    return set_error(TPF_ERR_ARG, "%s: qkv, rest, o, d_og and dproj must be 16-byte aligned", fn);
+  if (((uintptr_t)qkv | (uintptr_t)rest | (uintptr_t)o | (uintptr_t)d_og | (uintptr_t)dout |
+       (uintptr_t)w_o | (uintptr_t)dproj) % 16)
+    return set_error(TPF_ERR_ARG, "%s: qkv, rest, o, the gradients and dproj must be 16-byte "
+                     "aligned", fn);
   if (workspace_bytes < tpf_attn_pair_backward_workspace_bytes(B, N, H, D))
     return set_error(TPF_ERR_ARG, "%s: workspace too small", fn);
   const int64_t hc = H * D, part = B * N * H * N * D;
@@ -2379,7 +2388,12 @@ int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_
   const int per = 256 - 256 % (int)(D / 8);
   const dim3 ggrid((unsigned)((items + per - 1) / per));
   const FastDiv fN = make_fastdiv((uint32_t)N), fhc8 = make_fastdiv((uint32_t)(hc / 8));
-  if (residual)
+  if (!d_og) {
+    if ((rc = rowgemm_gate_bwd((const __bf16*)dout, (const __bf16*)w_o, C, (const __bf16*)o,
+                               (const __bf16*)residual, r, rest_pitch, d_o, delta, dp + 3 * hc,
+                               dproj_pitch, B, N, H, D, g.og_t, s, fn)))
+      return rc;
+  } else if (residual)
     hipLaunchKernelGGL(attn_gate_bwd_kernel<true>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)residual, r, rest_pitch, d_o, delta,
                        dp + 3 * hc, dproj_pitch, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
@@ -2387,7 +2401,7 @@ int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_
     hipLaunchKernelGGL(attn_gate_bwd_kernel<false>, ggrid, dim3(256), 0, s, (const __bf16*)d_og,
                        (const __bf16*)o, (const __bf16*)nullptr, r, rest_pitch, d_o, delta,
                        dp + 3 * hc, dproj_pitch, items, per, fN, (int)H, (int)D, fhc8, g.og_t);
-  if ((rc = check_launch(fn))) return rc;
+  if (d_og && (rc = check_launch(fn))) return rc;
   BwdParts pt;
   bwd_layout(B, N, H, N, D, B * N, (char*)workspace, &pt);
   const BwdPlan plan = bwd_plan(B, N, H, N, D, INT64_MAX);
@@ -2406,6 +2420,42 @@ int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_
                      (int)groups, (int)H, (int)N, dp, dproj_pitch, 4 * hc,
                      (flags & TPF_PAIR_BIAS_TRANSPOSED) != 0);
   return check_launch(fn);
+}
+}  // namespace tpf
+
+extern "C" {
+
+int tpf_attn_pair_backward_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                                const float* mask, int flags, const void* o, const float* lse,
+                                const void* residual, const void* d_og, void* dproj,
+                                int64_t dproj_pitch, void* workspace, int64_t workspace_bytes,
+                                int64_t B, int64_t N, int64_t H, int64_t D, double scale,
+                                void* stream) {
+  const char* fn = "tpf_attn_pair_backward_bf16";
+  if (!d_og) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  return pair_backward_impl(qkv, rest, rest_pitch, mask, flags, o, lse, residual, d_og, nullptr,
+                            nullptr, 0, dproj, dproj_pitch, workspace, workspace_bytes, B, N, H,
+                            D, scale, stream, fn);
+}
+
+int tpf_attn_pair_backward_dout_supported(int64_t C, int64_t H, int64_t D) {
+  return rowgemm_gate_supported(C, H, D) ? 1 : 0;
+}
+
+int tpf_attn_pair_backward_dout_bf16(const void* qkv, const void* rest, int64_t rest_pitch,
+                                     const float* mask, int flags, const void* o,
+                                     const float* lse, const void* residual, const void* dout,
+                                     const void* w_o, int64_t C, void* dproj, int64_t dproj_pitch,
+                                     void* workspace, int64_t workspace_bytes, int64_t B,
+                                     int64_t N, int64_t H, int64_t D, double scale, void* stream) {
+  const char* fn = "tpf_attn_pair_backward_dout_bf16";
+  if (!dout || !w_o) return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
+  if (!rowgemm_gate_supported(C, H, D))
+    return set_error(TPF_ERR_SHAPE, "%s: no fused instance for C=%lld H=%lld D=%lld", fn,
+                     (long long)C, (long long)H, (long long)D);
+  return pair_backward_impl(qkv, rest, rest_pitch, mask, flags, o, lse, residual, nullptr, dout,
+                            w_o, C, dproj, dproj_pitch, workspace, workspace_bytes, B, N, H, D,
+                            scale, stream, fn);
 }
 
 }  // extern "C"

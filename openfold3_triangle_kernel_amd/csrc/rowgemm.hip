@@ -47,20 +47,53 @@ struct RowSplit {
   int Nseq, H, D;
 };
 
-template <int KS, int MT, bool SPLIT>
+// Gate-backward epilogue of the triangle-attention module (MODE = kRowGate /
+// kRowGateShadow): the product is d_og = dout W_o (hc = H D columns) of the
+// pair rows r = (b, i, j), and instead of storing it the kernel applies the
+// backward of og = o * sigmoid(g):
+//   d_o   = d_og * s                      (bf16, rows [R, hc])
+//   dgate = d_og * o * s * (1 - s)        (bf16, columns [0, hc) of rows of
+//                                          pitch dpitch)
+//   delta[b, i, h, j] = sum_d d_o * o~    (f32; o~ = o, or o + its rounding
+//                                          residual res with the shadow)
+// with s = sigmoid(gate).  o, res and the gate rows (pitch gpitch) stream
+// through the LDS ring beside x.  og_t: dout holds pair row (b, i, j) at row
+// (b, j, i) (the ending node's caller order), gathered by the loader.
+struct RowGate {
+  const __bf16* o;
+  const __bf16* res;
+  const __bf16* gate;
+  int64_t gpitch;
+  __bf16* d_o;
+  float* delta;
+  __bf16* dgate;
+  int64_t dpitch;
+  int Nseq, H, D, og_t;
+};
+
+constexpr int kRowPlain = 0, kRowSplit = 1, kRowGate = 2, kRowGateShadow = 3;
+
+template <int KS, int MT, int MODE>
 __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     const __bf16* __restrict__ x, int64_t ldx, const __bf16* __restrict__ w, int w_kc,
     int64_t ldw, __bf16* __restrict__ y, int64_t ldy, int64_t R, int N, int64_t nblocks,
-    RowSplit sp) {
+    RowSplit sp, RowGate gt) {
+  constexpr bool SPLIT = MODE == kRowSplit;
+  constexpr bool GATE = MODE >= kRowGate;
   constexpr int K = 32 * KS;
   constexpr int CPR = K / 8;               // 16-byte chunks per x row
   constexpr int DEPTH = row_depth<KS>();
   constexpr int XCH = 32 * CPR;            // chunks of one x block
-  constexpr int LPT = XCH / 256;           // loads per loading thread per block
   static_assert(XCH % 256 == 0, "x block splits evenly over the loading waves");
   constexpr int NMAX = 16 * kRowNW * MT;  // widest output the instance serves
+  // Gate mode: side arrays o, gate (and res) of a block, N / 8 chunks per row.
+  constexpr int NSIDE = MODE == kRowGateShadow ? 3 : 2;
+  constexpr int LPS = GATE ? 32 * NMAX / 8 / 256 : 0;  // side loads per array and thread
+  static_assert(!GATE || MT == 1, "the gate epilogue serves N <= 128");
+  constexpr int LPT = XCH / 256 + (GATE ? NSIDE * LPS : 0);  // loads per loading thread per block
   __shared__ __attribute__((aligned(1024))) __bf16 Xs[DEPTH][32 * K];
   __shared__ __attribute__((aligned(16))) __bf16 Ys[2 * 32 * (NMAX + 8)];  // [2][32][N + 8]
+  __shared__ __attribute__((aligned(16))) __bf16 Ss[GATE ? DEPTH * NSIDE : 1][GATE ? 32 * NMAX : 8];
   const int YP = N + 8;
 
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -94,17 +127,57 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
   const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
   // Loading thread i of 256 takes chunks ci = 256 j + i of the block: row
   // r = ci / CPR, stored at slot (c + r) % CPR of its row.
+  // Gate mode: a loading thread's side chunks ci = 256 j + tid are (row
+  // ci / (N / 8), chunk ci % (N / 8)) of the block, stored unrotated at
+  // element 8 ci of the stage; their byte offsets are the same every block.
+  uint32_t side_o[GATE ? LPS : 1], side_g[GATE ? LPS : 1];
+  if constexpr (GATE) {
+    const int cpr = N / 8;
+#pragma unroll
+    for (int j = 0; j < LPS; ++j) {
+      const int ci = 256 * j + tid, r = ci / cpr, c = ci - r * cpr;
+      const bool ok = loader && ci < 32 * cpr;
+      side_o[j] = ok ? (uint32_t)((r * N + 8 * c) * 2) : kBufOOB;
+      side_g[j] = ok ? (uint32_t)((r * gt.gpitch + 8 * c) * 2) : kBufOOB;
+    }
+  }
   auto issue = [&](int64_t blk) {
     const int stage = (int)(blk % DEPTH);
-    const i32x4 rs_x = buffer_rsrc(x + (blk < bend ? blk : 0) * 32 * ldx);
+    const int64_t bb = blk < bend ? blk : 0;
+    // x rows of the block: consecutive, or (og_t) the pair rows
+    // (b, i, j0 + r) at dout rows (b, j0 + r, i), N rows apart.
+    int64_t xrow0 = bb * 32, xstride = ldx;
+    if constexpr (GATE) {
+      if (gt.og_t) {
+        const int64_t bi = xrow0 / gt.Nseq, j0 = xrow0 - bi * gt.Nseq;
+        const int64_t b = bi / gt.Nseq, i = bi - b * gt.Nseq;
+        xrow0 = (b * gt.Nseq + j0) * gt.Nseq + i;
+        xstride = gt.Nseq * ldx;
+      }
+    }
+    const i32x4 rs_x = buffer_rsrc(x + xrow0 * ldx);
 #pragma unroll
-    for (int j = 0; j < LPT; ++j) {
+    for (int j = 0; j < XCH / 256; ++j) {
       const int ci = 256 * j + tid;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
       const bool ok = blk < bend && blk * 32 + r < R;
-      buf2lds16(rs_x, ok ? (uint32_t)((r * ldx + 8 * gc) * 2) : kBufOOB,
+      buf2lds16(rs_x, ok ? (uint32_t)((r * xstride + 8 * gc) * 2) : kBufOOB,
                 &Xs[stage][(256 * j + 64 * wv) * 8]);
+    }
+    if constexpr (GATE) {
+      const bool ok = blk < bend;
+      const i32x4 rs_o = buffer_rsrc(gt.o + bb * 32 * N);
+      const i32x4 rs_g = buffer_rsrc(gt.gate + bb * 32 * gt.gpitch);
+#pragma unroll
+      for (int j = 0; j < LPS; ++j) {
+        const int dst = (256 * j + 64 * wv) * 8;
+        buf2lds16(rs_o, ok ? side_o[j] : kBufOOB, &Ss[stage * NSIDE][dst]);
+        buf2lds16(rs_g, ok ? side_g[j] : kBufOOB, &Ss[stage * NSIDE + 1][dst]);
+        if constexpr (NSIDE == 3)
+          buf2lds16(buffer_rsrc(gt.res + bb * 32 * N), ok ? side_o[j] : kBufOOB,
+                    &Ss[stage * NSIDE + 2][dst]);
+      }
     }
   };
   // Split destination: storing thread st's chunks i (q = st + 256 i of the
@@ -177,9 +250,62 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
         *reinterpret_cast<bf16x4*>(&Yb[(16 * rt + l16) * YP + 16 * t + 4 * lg]) = o;
       }
     }
+    // Gate mode: the storing waves take block blk's side chunks out of the
+    // ring now, before the barrier after which the loaders refill the stage.
+    constexpr int GIT = GATE ? 32 * NMAX / 8 / 256 : 1;
+    bf16x8 so[GIT], sg[GIT], sr[GIT];
+    if constexpr (GATE) {
+      if (!loader) {
+#pragma unroll
+        for (int i = 0; i < GIT; ++i) {
+          const int e = 8 * (tid - 256 + 256 * i);
+          so[i] = *reinterpret_cast<const bf16x8*>(&Ss[stage * NSIDE][e]);
+          sg[i] = *reinterpret_cast<const bf16x8*>(&Ss[stage * NSIDE + 1][e]);
+          if constexpr (NSIDE == 3) sr[i] = *reinterpret_cast<const bf16x8*>(&Ss[stage * NSIDE + 2][e]);
+        }
+      }
+    }
     if (loader) wait_vmcnt<LPT * (DEPTH - 2)>();  // block blk + 1 landed
     __syncthreads();
-    if (!loader) {
+    if constexpr (GATE) {
+      if (!loader) {
+        // Block rows r0 .. r0 + 31 = (b, i, j0 .. j0 + 31); chunk q = st +
+        // 256 i is (row q / (N / 8), chunk c = q % (N / 8)); the D / 8
+        // chunks of head h = c / (D / 8) are consecutive lanes of one wave
+        // (D / 8 divides 64), so the head's sum gathers them by lane.
+        const int st = tid - 256, cpr = N / 8, d8 = gt.D / 8;
+        const int64_t r0 = blk * 32;
+        const int64_t bi = r0 / gt.Nseq;
+        const int j0 = (int)(r0 - bi * gt.Nseq);
+#pragma unroll
+        for (int i = 0; i < GIT; ++i) {
+          const int q = st + 256 * i, row = q / cpr, c = q - row * cpr;
+          const bool act = q < 32 * cpr;
+          float sdot = 0.f;
+          if (act) {
+            const bf16x8 dv = *reinterpret_cast<const bf16x8*>(&Yb[row * YP + 8 * c]);
+            bf16x8 r_do, r_dg;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float sgm = sigmoidf(bf2f(sg[i][e]));
+              const float dd = bf2f(dv[e]), oo = bf2f(so[i][e]);
+              r_do[e] = f2bf(dd * sgm);
+              r_dg[e] = f2bf(dd * oo * sgm * (1.f - sgm));
+              // delta pairs the bf16 d_o the attention backward reads with
+              // o (with the shadow, o + its residual, summed in f32).
+              sdot = fmaf(bf2f(r_do[e]), NSIDE == 3 ? oo + bf2f(sr[i][e]) : oo, sdot);
+            }
+            st8(gt.d_o + (r0 + row) * N + 8 * c, r_do);
+            st8(gt.dgate + (r0 + row) * gt.dpitch + 8 * c, r_dg);
+          }
+          const int lane_q = lane;
+          float hs = 0.f;
+          for (int u = 0; u < d8; ++u) hs += __shfl(sdot, lane_q + u);
+          if (act && c % d8 == 0)
+            gt.delta[(bi * gt.H + c / d8) * gt.Nseq + j0 + row] = hs;
+        }
+      }
+    } else if (!loader) {
       // 32 rows x N / 8 chunks over the 256 storing threads: every LDS read
       // first, then the stores back to back.
       constexpr int SIT = (32 * NMAX / 8 + 255) / 256;
@@ -245,8 +371,9 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
   const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
 #define TPF_ROW_CASE(KS, MT)                                                                   \
   if (K == 32 * KS && tiles <= kRowNW * MT) {                                                  \
-    hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT, false>), dim3(grid), dim3(64 * kRowNW), 0,   \
-                       stream, x, ldx, w, w_kc, ldw, y, ldy, R, (int)N, nblocks, RowSplit{});  \
+    hipLaunchKernelGGL((rowgemm_ws_kernel<KS, MT, kRowPlain>), dim3(grid), dim3(64 * kRowNW),  \
+                       0, stream, x, ldx, w, w_kc, ldw, y, ldy, R, (int)N, nblocks, RowSplit{}, \
+                       RowGate{});                                                             \
     *rc = check_launch(fn);                                                                    \
     return true;                                                                               \
   }
@@ -254,6 +381,40 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
   TPF_ROW_CASE(4, 5)   // K = 128, N <= 640: the q | k | v | gate | bias projection
 #undef TPF_ROW_CASE
   return false;
+}
+
+bool rowgemm_gate_supported(int64_t C, int64_t H, int64_t D) {
+  const int64_t hc = H * D;
+  return C == 128 && (D == 8 || D == 16 || D == 32 || D == 64) && hc % 16 == 0 && hc <= 128;
+}
+
+int rowgemm_gate_bwd(const __bf16* dout, const __bf16* w_o, int64_t C, const __bf16* o,
+                     const __bf16* res, const __bf16* gate, int64_t gpitch, __bf16* d_o,
+                     float* delta, __bf16* dgate, int64_t dpitch, int64_t B, int64_t N, int64_t H,
+                     int64_t D, int og_t, hipStream_t stream, const char* fn) {
+  const int64_t hc = H * D, R = B * N * N;
+  if (!rowgemm_gate_supported(C, H, D) || N % 32 || gpitch % 8 || dpitch % 8)
+    return set_error(TPF_ERR_SHAPE, "%s: no fused gate-backward instance for C=%lld H=%lld D=%lld",
+                     fn, (long long)C, (long long)H, (long long)D);
+  if (((uintptr_t)dout | (uintptr_t)w_o | (uintptr_t)o | (uintptr_t)res | (uintptr_t)gate |
+       (uintptr_t)d_o | (uintptr_t)dgate) % 16)
+    return set_error(TPF_ERR_ARG, "%s: operands must be 16-byte aligned", fn);
+  // Lane offsets within one 32-row block (dout rows N apart with og_t).
+  if (32 * (og_t ? N : 1) * C * 2 >= (int64_t)kBufOOB || 32 * gpitch * 2 >= (int64_t)kBufOOB)
+    return set_error(TPF_ERR_SHAPE, "%s: N=%lld too large for 32-bit block offsets", fn,
+                     (long long)N);
+  const int64_t nblocks = R / 32;
+  const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
+  const RowGate gt{o, res, gate, gpitch, d_o, delta, dgate, dpitch, (int)N, (int)H, (int)D, og_t};
+  if (res)
+    hipLaunchKernelGGL((rowgemm_ws_kernel<4, 1, kRowGateShadow>), dim3(grid), dim3(64 * kRowNW),
+                       0, stream, dout, C, w_o, 0, hc, (__bf16*)nullptr, hc, R, (int)hc, nblocks,
+                       RowSplit{}, gt);
+  else
+    hipLaunchKernelGGL((rowgemm_ws_kernel<4, 1, kRowGate>), dim3(grid), dim3(64 * kRowNW), 0,
+                       stream, dout, C, w_o, 0, hc, (__bf16*)nullptr, hc, R, (int)hc, nblocks,
+                       RowSplit{}, gt);
+  return check_launch(fn);
 }
 
 }  // namespace tpf
@@ -280,8 +441,8 @@ extern "C" int tpf_pair_projection_bf16(const void* x, const void* w, int64_t B,
   const int64_t nblocks = (R + 31) / 32;
   const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
   const RowSplit sp{(__bf16*)qkv, B * N * H * N * D, (int)N, (int)H, (int)D};
-  hipLaunchKernelGGL((rowgemm_ws_kernel<4, 5, true>), dim3(grid), dim3(64 * kRowNW), 0,
+  hipLaunchKernelGGL((rowgemm_ws_kernel<4, 5, kRowSplit>), dim3(grid), dim3(64 * kRowNW), 0,
                      (hipStream_t)stream, (const __bf16*)x, C, (const __bf16*)w, 1, C,
-                     (__bf16*)rest, rest_pitch, R, (int)P, nblocks, sp);
+                     (__bf16*)rest, rest_pitch, R, (int)P, nblocks, sp, RowGate{});
   return check_launch(fn);
 }

@@ -72,4 +72,12 @@ bool rowgemm_try(const __bf16* x, int64_t ldx, const __bf16* w, int w_kc, int64_
                  int64_t ldy, int64_t R, int64_t N, int64_t K, hipStream_t stream, int* rc,
                  const char* fn);
 
+// Fused d_og = dout W_o with the backward of the module's output gate
+// (rowgemm.hip): writes d_o, the gate gradient and delta of the pair rows.
+bool rowgemm_gate_supported(int64_t C, int64_t H, int64_t D);
+int rowgemm_gate_bwd(const __bf16* dout, const __bf16* w_o, int64_t C, const __bf16* o,
+                     const __bf16* res, const __bf16* gate, int64_t gpitch, __bf16* d_o,
+                     float* delta, __bf16* dgate, int64_t dpitch, int64_t B, int64_t N, int64_t H,
+                     int64_t D, int og_t, hipStream_t stream, const char* fn);
+
 }  // namespace tpf

@@ -181,7 +181,7 @@ class _PairAttentionCore(torch.autograd.Function):
         dev = x.device
         x2 = x.reshape(R, C)
         wa = w_all.to(torch.bfloat16)
-        wo = w_o.to(torch.bfloat16)
+        wo = w_o.to(torch.bfloat16).contiguous()
         qkv, rest = _pair_projection(x2, wa, B, N, H, D)
         o = torch.empty((R, hc), device=dev, dtype=torch.bfloat16)
         og = torch.empty_like(o)
@@ -213,16 +213,22 @@ class _PairAttentionCore(torch.autograd.Function):
         R = B * N * N
         dev = x2.device
         dout2 = dout.reshape(R, C).to(torch.bfloat16).contiguous()
-        d_og = _mm(dout2, wo, False)
         dw_o = _wgrad(dout2, og, ctx.w_dtypes[1]) if ctx.needs_input_grad[2] else None
         dproj = torch.empty((R, P), device=dev, dtype=torch.bfloat16)
         ws_bytes = int(_native.query("tpf_attn_pair_backward_workspace_bytes", B, N, H, D))
         ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        common = (qkv.data_ptr(), rest.data_ptr(), rest.shape[1], mask_add.data_ptr(), flags,
+                  o.data_ptr(), lse.data_ptr(), _native.ptr(res))
+        tail = (dproj.data_ptr(), P, ws.data_ptr(), ws_bytes, B, N, H, D, scale,
+                _native.stream_of(dproj))
         with _device_ctx(dev):
-            _native.call("tpf_attn_pair_backward_bf16", qkv.data_ptr(), rest.data_ptr(),
-                         rest.shape[1], mask_add.data_ptr(), flags, o.data_ptr(), lse.data_ptr(),
-                         _native.ptr(res), d_og.data_ptr(), dproj.data_ptr(), P, ws.data_ptr(),
-                         ws_bytes, B, N, H, D, scale, _native.stream_of(dproj))
+            if _native.query("tpf_attn_pair_backward_dout_supported", C, H, D):
+                # d_og = dout W_o with the gate backward in its epilogue.
+                _native.call("tpf_attn_pair_backward_dout_bf16", *common, dout2.data_ptr(),
+                             wo.data_ptr(), C, *tail)
+            else:
+                d_og = _mm(dout2, wo, False)
+                _native.call("tpf_attn_pair_backward_bf16", *common, d_og.data_ptr(), *tail)
         dx = _mm(dproj, wa, False).view(B, N, N, C) if ctx.needs_input_grad[0] else None
         dw_all = _wgrad(dproj, x2, ctx.w_dtypes[0]) if ctx.needs_input_grad[1] else None
         return dx, dw_all, dw_o, None, None, None, None, None

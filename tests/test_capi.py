@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), f"{name} not exported"
         assert name in _native.SIGNATURES, f"{name} missing from the ctypes binding"
         assert len(_native.SIGNATURES[name][1]) == nargs, f"{name}: arg count mismatch"
-    assert lib.tpf_abi_version() == 6
+    assert lib.tpf_abi_version() == 7
 
 
 def test_shape_errors_are_reported_without_launch(lib):
@@ -120,3 +120,14 @@ def test_backward_workspace_budget_plan(lib):
     ws = _native.query("tpf_attn_backward_workspace_bytes_budget", 1, 768, 8, 768, 64, 4 << 30)
     assert ws <= 4 << 30
     assert _native.query("tpf_attn_backward_slab_count", 1, 768, 8, 768, 64, ws) == 2
+
+
+def test_pair_backward_dout_instances(lib):
+    """Head shapes the fused d_og + gate-backward row kernel serves (C = 128,
+    D in {8, 16, 32, 64}, H*D a multiple of 16 up to 128); others take the
+    two-step route."""
+    from openfold3_triangle_kernel_amd import _native
+
+    q = lambda C, H, D: _native.query("tpf_attn_pair_backward_dout_supported", C, H, D)
+    assert q(128, 4, 32) and q(128, 2, 64) and q(128, 16, 8) and q(128, 1, 16)
+    assert not q(64, 4, 32) and not q(128, 4, 24) and not q(128, 8, 32) and not q(128, 1, 8)
