@@ -69,6 +69,7 @@ struct RowGate {
   __bf16* dgate;
   int64_t dpitch;
   int Nseq, H, D, og_t;
+  FastDiv fbp, fN;  // 32-row blocks per (b, i) plane (N / 32), and N
 };
 
 constexpr int kRowPlain = 0, kRowSplit = 1, kRowGate = 2, kRowGateShadow = 3;
@@ -149,9 +150,9 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     int64_t xrow0 = bb * 32, xstride = ldx;
     if constexpr (GATE) {
       if (gt.og_t) {
-        const int64_t bi = xrow0 / gt.Nseq, j0 = xrow0 - bi * gt.Nseq;
-        const int64_t b = bi / gt.Nseq, i = bi - b * gt.Nseq;
-        xrow0 = (b * gt.Nseq + j0) * gt.Nseq + i;
+        const uint32_t bi = fdiv((uint32_t)bb, gt.fbp), j0 = ((uint32_t)bb - bi * gt.fbp.d) * 32;
+        const uint32_t b = fdiv(bi, gt.fN), i = bi - b * gt.fN.d;
+        xrow0 = ((int64_t)b * gt.Nseq + j0) * gt.Nseq + i;
         xstride = gt.Nseq * ldx;
       }
     }
@@ -275,8 +276,8 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
         // (D / 8 divides 64), so the head's sum gathers them by lane.
         const int st = tid - 256, cpr = N / 8, d8 = gt.D / 8;
         const int64_t r0 = blk * 32;
-        const int64_t bi = r0 / gt.Nseq;
-        const int j0 = (int)(r0 - bi * gt.Nseq);
+        const uint32_t bi = fdiv((uint32_t)blk, gt.fbp);
+        const int j0 = (int)((uint32_t)blk - bi * gt.fbp.d) * 32;
 #pragma unroll
         for (int i = 0; i < GIT; ++i) {
           const int q = st + 256 * i, row = q / cpr, c = q - row * cpr;
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
           float hs = 0.f;
           for (int u = 0; u < d8; ++u) hs += __shfl(sdot, lane_q + u);
           if (act && c % d8 == 0)
-            gt.delta[(bi * gt.H + c / d8) * gt.Nseq + j0 + row] = hs;
+            gt.delta[((int64_t)bi * gt.H + c / d8) * gt.Nseq + j0 + row] = hs;
         }
       }
     } else if (!loader) {
@@ -404,8 +405,11 @@ int rowgemm_gate_bwd(const __bf16* dout, const __bf16* w_o, int64_t C, const __b
     return set_error(TPF_ERR_SHAPE, "%s: N=%lld too large for 32-bit block offsets", fn,
                      (long long)N);
   const int64_t nblocks = R / 32;
+  if (nblocks >= (int64_t)1 << 31)
+    return set_error(TPF_ERR_SHAPE, "%s: %lld row blocks exceed 2^31", fn, (long long)nblocks);
   const unsigned grid = (unsigned)(nblocks < device_cus() ? nblocks : device_cus());
-  const RowGate gt{o, res, gate, gpitch, d_o, delta, dgate, dpitch, (int)N, (int)H, (int)D, og_t};
+  const RowGate gt{o, res, gate, gpitch, d_o, delta, dgate, dpitch, (int)N, (int)H, (int)D, og_t,
+                   make_fastdiv((uint32_t)(N / 32)), make_fastdiv((uint32_t)N)};
   if (res)
     hipLaunchKernelGGL((rowgemm_ws_kernel<4, 1, kRowGateShadow>), dim3(grid), dim3(64 * kRowNW),
                        0, stream, dout, C, w_o, 0, hc, (__bf16*)nullptr, hc, R, (int)hc, nblocks,
