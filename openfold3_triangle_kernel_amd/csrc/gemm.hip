@@ -107,10 +107,20 @@ int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
 }
 
 int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
-                hipStream_t stream, const char* fn) {
+                hipStream_t stream, const char* fn, int tm) {
   GemmArgs g = g0;
   int rc = gemm_prepare(g, a_kc, b_kc, out_f32, batch, fn);
   if (rc) return rc;
+  if (tm == 192) {
+    if (a_kc != 1 || b_kc != 1 || out_f32)
+      return set_error(TPF_ERR_ARG, "%s: 192 tiles not instantiated for this layout", fn);
+    const int64_t blocks = (gemm_tiles(g, 192) + 7) / 8 * 8;
+    if (blocks > INT32_MAX) return set_error(TPF_ERR_SHAPE, "%s: GEMM grid too large", fn);
+    hipLaunchKernelGGL((gemm_bf16_kernel<true, true, false, 192>), dim3((unsigned)blocks),
+                       dim3(256), 0, stream, g);
+    return check_launch(fn);
+  }
+  if (tm != 128) return set_error(TPF_ERR_ARG, "%s: tile size %d", fn, tm);
   dim3 grid((unsigned)((gemm_tiles(g) + 7) / 8 * 8));
 #define TPF_GEMM_CASE(AK, BK, OF)                                                            \
   if (a_kc == AK && b_kc == BK && out_f32 == OF) {                                            \
@@ -130,21 +140,23 @@ int gemm_launch(const GemmArgs& g0, int a_kc, int b_kc, int out_f32, int batch,
 }
 
 int gemm_launch_pair(const GemmArgs& p0, int a_kc0, int b_kc0, const GemmArgs& p1, int a_kc1,
-                     int b_kc1, int out_f32, hipStream_t stream, const char* fn) {
+                     int b_kc1, int out_f32, hipStream_t stream, const char* fn, int tm) {
   GemmArgs g0 = p0, g1 = p1;
   int rc = gemm_prepare(g0, a_kc0, b_kc0, out_f32, p0.batch > 0 ? p0.batch : 1, fn);
   if (rc) return rc;
   if ((rc = gemm_prepare(g1, a_kc1, b_kc1, out_f32, p1.batch > 0 ? p1.batch : 1, fn))) return rc;
-  const int64_t blocks = (gemm_tiles(g0) + 7) / 8 * 8 + (gemm_tiles(g1) + 7) / 8 * 8;
+  if (tm != 128 && tm != 192) return set_error(TPF_ERR_ARG, "%s: tile size %d", fn, tm);
+  const int64_t blocks = (gemm_tiles(g0, tm) + 7) / 8 * 8 + (gemm_tiles(g1, tm) + 7) / 8 * 8;
   if (blocks > INT32_MAX) return set_error(TPF_ERR_SHAPE, "%s: GEMM grid too large", fn);
   dim3 grid((unsigned)blocks);
-#define TPF_GEMM_PAIR_CASE(A0, B0, A1, B1, OF)                                                \
-  if (a_kc0 == A0 && b_kc0 == B0 && a_kc1 == A1 && b_kc1 == B1 && out_f32 == OF) {             \
-    hipLaunchKernelGGL((gemm_bf16_pair_kernel<A0, B0, A1, B1, OF>), grid, dim3(256), 0, stream,  \
-                       g0, g1);                                                               \
+#define TPF_GEMM_PAIR_CASE(A0, B0, A1, B1, OF, TM)                                            \
+  if (a_kc0 == A0 && b_kc0 == B0 && a_kc1 == A1 && b_kc1 == B1 && out_f32 == OF && tm == TM) { \
+    hipLaunchKernelGGL((gemm_bf16_pair_kernel<A0, B0, A1, B1, OF, TM>), grid, dim3(256), 0,     \
+                       stream, g0, g1);                                                       \
     return check_launch(fn);                                                                  \
   }
-  TPF_GEMM_PAIR_CASE(1, 0, 0, 0, 0)  // TriMul contraction backward (dA, dB)
+  TPF_GEMM_PAIR_CASE(1, 0, 0, 0, 0, 128)  // TriMul contraction backward (dA, dB)
+  TPF_GEMM_PAIR_CASE(1, 0, 0, 0, 0, 192)
 #undef TPF_GEMM_PAIR_CASE
   return set_error(TPF_ERR_ARG, "%s: GEMM pair layout not instantiated", fn);
 }

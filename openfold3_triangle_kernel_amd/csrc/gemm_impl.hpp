@@ -18,16 +18,27 @@ namespace TPF_GEMM_IMPL {
 
 // Tile T of problem g (T < tiles of g, in (n-tile, m-tile, split, batch)
 // order) into C.
-template <bool A_KC, bool B_KC, bool OUT_F32>
+// TM: the square tile size (128, or 192 for the TriMul contractions whose
+// sizes are multiples of 192).
+template <int TM>
+constexpr int gemm_smem_bytes() {
+  // The ring, and the bf16 epilogue's staging of four TM/2 x TM/2 sub-tiles.
+  return gemm_ring_bytes(kGNS, TM) > 4 * (TM / 2) * (TM / 2 + 8) * 2
+             ? gemm_ring_bytes(kGNS, TM)
+             : 4 * (TM / 2) * (TM / 2 + 8) * 2;
+}
+
+template <bool A_KC, bool B_KC, bool OUT_F32, int TM = kGM>
 __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, char* smem) {
-  const int tm = (g.M + kGM - 1) / kGM, tn = (g.N + kGN - 1) / kGN;
+  constexpr int NB = TM / 64, HT = TM / 2;
+  const int tm = (g.M + TM - 1) / TM, tn = (g.N + TM - 1) / TM;
   const int nt = (int)(T % tn);
   int64_t r = T / tn;
   const int mt = (int)(r % tm);
   r /= tm;
   const int split = (int)(r % g.ksplit);
   const int z = (int)(r / g.ksplit);
-  const int m0 = mt * kGM, n0 = nt * kGN;
+  const int m0 = mt * TM, n0 = nt * TM;
   const int kbeg = split * g.k_chunk;
   const int kend = min(g.K, kbeg + g.k_chunk);
   GemmOperand A{g.A + (int64_t)z * g.a_bs, g.a_ld, g.M, g.a_gather_n, g.a_div_n, g.a_div_nn};
@@ -35,18 +46,18 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int rl = lane & 31, hl = lane >> 5, wm = w >> 1, wn = w & 1;
   char* Cb = (char*)g.C + ((int64_t)z * g.c_bs + (int64_t)split * g.c_split) * (OUT_F32 ? 4 : 2);
-  f32x16 acc[2][2];
+  f32x16 acc[NB][NB];
   if constexpr (OUT_F32) {
-    gemm_tile<A_KC, B_KC>(A, B, m0, n0, kbeg, kend, smem, acc);
+    gemm_tile<A_KC, B_KC, kGNS, TM>(A, B, m0, n0, kbeg, kend, smem, acc);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + wn * 64 + j * 32 + rl;
+      for (int j = 0; j < NB; ++j) {
+        const int col = n0 + wn * HT + j * 32 + rl;
         if (col >= g.N) continue;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) {
-          const int row = m0 + wm * 64 + i * 32 + 8 * (rr >> 2) + 4 * hl + (rr & 3);
+          const int row = m0 + wm * HT + i * 32 + 8 * (rr >> 2) + 4 * hl + (rr & 3);
           if (row < g.M)
             reinterpret_cast<float*>(Cb)[(int64_t)row * g.c_ld + col] = acc[i][j][rr] * g.alpha;
         }
@@ -54,17 +65,17 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
   } else {
     // bf16 output: the tile is formed transposed (C^T = B A^T), so each lane's
     // four consecutive accumulator registers are four consecutive columns of
-    // C; wave w stages its 64 x 64 sub-tile (rows 64 (w & 1), columns
-    // 64 (w >> 1)) in LDS as bf16 rows and writes it back with 16-byte stores,
-    // eight full 128-byte row segments per store instruction.
-    gemm_tile<B_KC, A_KC>(B, A, n0, m0, kbeg, kend, smem, acc);
-    constexpr int EP = 72;  // staged row pitch (bf16)
-    static_assert(4 * 64 * EP * 2 <= gemm_ring_bytes(kGNS), "epilogue staging fits the ring");
-    __bf16* Ls = reinterpret_cast<__bf16*>(smem) + w * 64 * EP;
+    // C; wave w stages its TM/2 x TM/2 sub-tile (rows TM/2 (w & 1), columns
+    // TM/2 (w >> 1)) in LDS as bf16 rows and writes it back with 16-byte
+    // stores, whole row segments of TM bytes per group of TM / 16 lanes.
+    gemm_tile<B_KC, A_KC, kGNS, TM>(B, A, n0, m0, kbeg, kend, smem, acc);
+    constexpr int EP = HT + 8;  // staged row pitch (bf16)
+    static_assert(4 * HT * EP * 2 <= gemm_smem_bytes<TM>(), "epilogue staging fits");
+    __bf16* Ls = reinterpret_cast<__bf16*>(smem) + w * HT * EP;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
           bf16x4 v;
@@ -75,10 +86,12 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
     __syncthreads();
     const bool vec = ((g.c_ld | g.c_bs) % 8 == 0) && ((uintptr_t)g.C % 16 == 0);
     __bf16* Cw = reinterpret_cast<__bf16*>(Cb);
+    constexpr int CPR = HT / 8;  // 16-byte chunks per staged row
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int rr = 8 * it + (lane >> 3), ch = lane & 7;
-      const int row = m0 + 64 * wn + rr, col = n0 + 64 * wm + 8 * ch;
+    for (int it = 0; it < HT * CPR / 64; ++it) {
+      const int q = 64 * it + lane;
+      const int rr = q / CPR, ch = q % CPR;
+      const int row = m0 + HT * wn + rr, col = n0 + HT * wm + 8 * ch;
       if (row >= g.M || col >= g.N) continue;
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(&Ls[rr * EP + 8 * ch]);
       __bf16* dst = Cw + (int64_t)row * g.c_ld + col;
@@ -93,33 +106,33 @@ __device__ __forceinline__ void gemm_bf16_tile(const GemmArgs& g, int64_t T, cha
   }
 }
 
-__host__ __device__ inline int64_t gemm_tiles(const GemmArgs& g) {
-  return (int64_t)((g.M + kGM - 1) / kGM) * ((g.N + kGN - 1) / kGN) * g.batch * g.ksplit;
+__host__ __device__ inline int64_t gemm_tiles(const GemmArgs& g, int tm = kGM) {
+  return (int64_t)((g.M + tm - 1) / tm) * ((g.N + tm - 1) / tm) * g.batch * g.ksplit;
 }
 
-template <bool A_KC, bool B_KC, bool OUT_F32>
+template <bool A_KC, bool B_KC, bool OUT_F32, int TM = kGM>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[gemm_ring_bytes(kGNS)];
-  const int64_t T = xcd_order(gemm_tiles(g));
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_smem_bytes<TM>()];
+  const int64_t T = xcd_order(gemm_tiles(g, TM));
   if (T < 0) return;
-  gemm_bf16_tile<A_KC, B_KC, OUT_F32>(g, T, smem);
+  gemm_bf16_tile<A_KC, B_KC, OUT_F32, TM>(g, T, smem);
 }
 
 // Two problems of one layout in one grid: workgroups [0, p0) take the
 // tiles of g0 and the rest those of g1 (p0 = g0's tiles rounded up to 8),
 // each in its own XCD-aware order, so both problems spread over all XCDs
 // and independent small GEMMs stay in flight together.
-template <bool AK0, bool BK0, bool AK1, bool BK1, bool OUT_F32>
+template <bool AK0, bool BK0, bool AK1, bool BK1, bool OUT_F32, int TM = kGM>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_pair_kernel(GemmArgs g0, GemmArgs g1) {
-  __shared__ __attribute__((aligned(1024))) char smem[gemm_ring_bytes(kGNS)];
-  const int64_t t0 = gemm_tiles(g0), p0 = (t0 + 7) / 8 * 8;
+  __shared__ __attribute__((aligned(1024))) char smem[gemm_smem_bytes<TM>()];
+  const int64_t t0 = gemm_tiles(g0, TM), p0 = (t0 + 7) / 8 * 8;
   const int64_t L = blockIdx.x;
   if (L < p0) {
     const int64_t T = xcd_order_of(L, t0);
-    if (T >= 0) gemm_bf16_tile<AK0, BK0, OUT_F32>(g0, T, smem);
+    if (T >= 0) gemm_bf16_tile<AK0, BK0, OUT_F32, TM>(g0, T, smem);
   } else {
-    const int64_t T = xcd_order_of(L - p0, gemm_tiles(g1));
-    if (T >= 0) gemm_bf16_tile<AK1, BK1, OUT_F32>(g1, T, smem);
+    const int64_t T = xcd_order_of(L - p0, gemm_tiles(g1, TM));
+    if (T >= 0) gemm_bf16_tile<AK1, BK1, OUT_F32, TM>(g1, T, smem);
   }
 }
 

@@ -34,13 +34,15 @@ struct GemmArgsF32 {
   int batch;
 };
 
-// a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).
+// a_kc / b_kc: operand is K-contiguous (1) or MN-contiguous (0).  tm: square
+// tile size, 128 or 192 (192 instantiated for the TriMul contraction layouts:
+// bf16 out, (1, 1) alone and the (1, 0) + (0, 0) pair).
 int gemm_launch(const GemmArgs& g, int a_kc, int b_kc, int out_f32, int batch,
-                hipStream_t stream, const char* fn);
+                hipStream_t stream, const char* fn, int tm = 128);
 // Two GEMMs in one launch (g.batch of each, 0 meaning 1), each with its own
 // operand layout; instantiated for the layout pairs TriMul uses.
 int gemm_launch_pair(const GemmArgs& g0, int a_kc0, int b_kc0, const GemmArgs& g1, int a_kc1,
-                     int b_kc1, int out_f32, hipStream_t stream, const char* fn);
+                     int b_kc1, int out_f32, hipStream_t stream, const char* fn, int tm = 128);
 // Split-K weight-gradient products (both operands MN-contiguous, f32 output):
 // one problem, or two in one launch (gemm_wgrad.hip).
 int gemm_launch_wgrad(const GemmArgs& g, hipStream_t stream, const char* fn);

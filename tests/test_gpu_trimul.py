@@ -55,9 +55,10 @@ def run_turbo(z, mask, w, dout, outgoing, dev):
 
 # N % 8 == 0 runs the persistent weight-stationary kernels (B = 2 crosses a
 # batch item inside the walk; N = 200 gives workgroups several 32-row blocks
-# and an uneven last share), other N the tile kernels.
+# and an uneven last share), other N the tile kernels.  N % 192 == 0 runs
+# the channel contractions on 192 x 192 tiles (128 x 128 otherwise).
 CASES = [(1, 64, 128), (1, 128, 128), (2, 33, 64), (1, 101, 32), (1, 113, 96), (1, 17, 128),
-         (2, 48, 64), (1, 72, 96), (1, 40, 32), (1, 200, 128)]
+         (2, 48, 64), (1, 72, 96), (1, 40, 32), (1, 200, 128), (1, 192, 64), (2, 192, 32)]
 
 
 @pytest.mark.gpu
