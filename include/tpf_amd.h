@@ -29,7 +29,7 @@ enum {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tpf_last_error(void);
-/* ABI revision of this header (7). */
+/* ABI revision of this header (8). */
 int tpf_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -286,6 +286,21 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
                              float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
                              float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
                              void* stream);
+/* tpf_trimul_backward_bf16 with the W5 gradient delivered as the gradients
+ * of turbo_trimul's named weights (README.md:137-143, `p_in_weight`,
+ * `g_in_weight`, `g_out_weight`): d_p_in [2H, C] = [d w_ap; d w_bp], d_g_in
+ * [2H, C] = [d w_ag; d w_bg], d_w_g [C, C].  The fold writes each row block
+ * straight to its place (same values, bit for bit, as the d_w5 rows), so
+ * the caller needs no row gather. */
+int tpf_trimul_backward_named_bf16(
+    const void* grad_out, const void* z, const float* mask, const float* w_ap, const float* w_ag,
+    const float* w_bp, const float* w_bg, const float* w_g, const float* w_z,
+    const float* ln_in_w, const float* ln_out_w, const void* zln, const void* gate, const void* a,
+    const void* b, const void* x, const void* xln, const float* mean_in, const float* rstd_in,
+    const float* mean_out, const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
+    void* dz, float* d_p_in, float* d_g_in, float* d_w_g, float* d_w_z, float* d_ln_in_w,
+    float* d_ln_in_b, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
+    int64_t workspace_bytes, void* stream);
 
 /* Weight gradient of a linear layer over R rows, dW[m][n] = sum_r dy[r][m] x[r][n]
  * (dy [R, M], x [R, N] row-major bf16 with leading dimensions ld_dy, ld_x;

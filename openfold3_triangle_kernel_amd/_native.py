@@ -130,6 +130,10 @@ SIGNATURES: dict[str, tuple] = {
         _I32,
         [_P] * 21 + [_I32, _I64, _I64, _I64] + [_P] * 8 + [_I64, _P],
     ),
+    "tpf_trimul_backward_named_bf16": (
+        _I32,
+        [_P] * 21 + [_I32, _I64, _I64, _I64] + [_P] * 10 + [_I64, _P],
+    ),
 }
 
 _LOCK = threading.Lock()

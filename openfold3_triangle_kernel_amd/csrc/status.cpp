@@ -27,6 +27,6 @@ extern "C" {
 
 const char* tpf_last_error(void) { return tpf::error_buffer(); }
 
-int tpf_abi_version(void) { return 7; }
+int tpf_abi_version(void) { return 8; }
 
 }  // extern "C"

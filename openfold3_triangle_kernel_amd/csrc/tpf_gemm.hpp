@@ -57,7 +57,7 @@ int fold_launch(const float* part, float* out, int64_t n, int64_t stride, int sp
 // is the one-segment case).  Segment sg folds `splits` partial vectors of n
 // floats spaced `stride` apart into dst[sg][i / piece][i % piece]; the
 // partials are left unchanged.
-constexpr int kFoldMaxSegs = 4;
+constexpr int kFoldMaxSegs = 5;
 struct FoldSegs {
   const float* part[kFoldMaxSegs];
   float* dst[kFoldMaxSegs][4];

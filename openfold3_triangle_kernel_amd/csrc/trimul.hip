@@ -2018,25 +2018,27 @@ int64_t tpf_trimul_backward_workspace_bytes(int64_t B, int64_t N, int64_t C) {
   return t;
 }
 
-int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
-                             const float* w_ap, const float* w_ag, const float* w_bp,
-                             const float* w_bg, const float* w_g, const float* w_z,
-                             const float* ln_in_w, const float* ln_out_w, const void* zln,
-                             const void* gate, const void* a, const void* b, const void* x,
-                             const void* xln, const float* mean_in, const float* rstd_in,
-                             const float* mean_out, const float* rstd_out, int outgoing, int64_t B,
-                             int64_t N, int64_t C, void* dz, float* d_w5, float* d_w_z,
-                             float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
-                             float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
-  const char* fn = "tpf_trimul_backward_bf16";
+}  // extern "C"
+
+// The TriMul backward; the five H x C row blocks of the W5 gradient
+// (ap, ag, bp, bg, g) land at w5dst[0..4].
+static int trimul_backward_impl(
+    const void* grad_out, const void* z, const float* mask, const float* w_ap,
+    const float* w_ag, const float* w_bp, const float* w_bg, const float* w_g, const float* w_z,
+    const float* ln_in_w, const float* ln_out_w, const void* zln, const void* gate, const void* a,
+    const void* b, const void* x, const void* xln, const float* mean_in, const float* rstd_in,
+    const float* mean_out, const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
+    void* dz, float* const w5dst[5], float* d_w_z, float* d_ln_in_w, float* d_ln_in_b,
+    float* d_ln_out_w, float* d_ln_out_b, void* workspace, int64_t workspace_bytes, void* stream,
+    const char* fn) {
+  float* const d_w5 = w5dst[0];
   TmGeom g;
   int rc = tm_geom(&g, B, N, C, outgoing, fn);
   if (rc) return rc;
   if (!grad_out || !z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !ln_in_w ||
       !ln_out_w || !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in || !mean_out ||
-      !rstd_out || !dz || !d_w5 || !d_w_z || !d_ln_in_w || !d_ln_in_b || !d_ln_out_w ||
-      !d_ln_out_b || !workspace)
+      !rstd_out || !dz || !d_w5 || !w5dst[1] || !w5dst[2] || !w5dst[3] || !w5dst[4] || !d_w_z ||
+      !d_ln_in_w || !d_ln_in_b || !d_ln_out_w || !d_ln_out_b || !workspace)
     return set_error(TPF_ERR_ARG, "%s: null pointer", fn);
   const int64_t need = tpf_trimul_backward_workspace_bytes(B, N, C);
   if (workspace_bytes < need)
@@ -2171,10 +2173,15 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   // The four weight-gradient folds in one launch per pass; the LayerNorm
   // partials ([tiles][ln_out_w | ln_out_b] and [workgroups][ln_in_w |
   // ln_in_b]) land directly in the four parameter gradients.
+  // The W5 partials fold as two segments: rows ap | ag | bp | bg (four
+  // H x C pieces) and g; each element's fold is the same either way.
   FoldSegs f{};
-  f.nseg = 4;
-  f.part[0] = w5p; f.n[0] = 5 * C * C; f.stride[0] = 5 * C * C; f.splits[0] = s5;
-  f.piece[0] = 5 * C * C; f.dst[0][0] = d_w5;
+  f.nseg = 5;
+  f.part[0] = w5p; f.n[0] = 4 * H * C; f.stride[0] = 5 * C * C; f.splits[0] = s5;
+  f.piece[0] = H * C;
+  for (int j = 0; j < 4; ++j) f.dst[0][j] = w5dst[j];
+  f.part[4] = w5p + 4 * H * C; f.n[4] = C * C; f.stride[4] = 5 * C * C; f.splits[4] = s5;
+  f.piece[4] = C * C; f.dst[4][0] = w5dst[4];
   f.part[1] = wzp; f.n[1] = C * H; f.stride[1] = C * H; f.splits[1] = wz_fused ? lnp_splits : sz;
   f.piece[1] = C * H; f.dst[1][0] = d_w_z;
   f.part[2] = lnp; f.n[2] = 2 * C; f.stride[2] = 2 * C; f.splits[2] = lnp_splits;
@@ -2184,6 +2191,48 @@ int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* m
   f.piece[3] = C;
   f.dst[3][0] = d_ln_in_w; f.dst[3][1] = d_ln_in_b;
   return fold_multi(f, s, fn);
+}
+
+extern "C" {
+
+int tpf_trimul_backward_bf16(const void* grad_out, const void* z, const float* mask,
+                             const float* w_ap, const float* w_ag, const float* w_bp,
+                             const float* w_bg, const float* w_g, const float* w_z,
+                             const float* ln_in_w, const float* ln_out_w, const void* zln,
+                             const void* gate, const void* a, const void* b, const void* x,
+                             const void* xln, const float* mean_in, const float* rstd_in,
+                             const float* mean_out, const float* rstd_out, int outgoing, int64_t B,
+                             int64_t N, int64_t C, void* dz, float* d_w5, float* d_w_z,
+                             float* d_ln_in_w, float* d_ln_in_b, float* d_ln_out_w,
+                             float* d_ln_out_b, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  const int64_t hc = C * C;  // H = C
+  float* const w5dst[5] = {d_w5, d_w5 ? d_w5 + hc : nullptr, d_w5 ? d_w5 + 2 * hc : nullptr,
+                           d_w5 ? d_w5 + 3 * hc : nullptr, d_w5 ? d_w5 + 4 * hc : nullptr};
+  return trimul_backward_impl(grad_out, z, mask, w_ap, w_ag, w_bp, w_bg, w_g, w_z, ln_in_w,
+                              ln_out_w, zln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
+                              rstd_out, outgoing, B, N, C, dz, w5dst, d_w_z, d_ln_in_w, d_ln_in_b,
+                              d_ln_out_w, d_ln_out_b, workspace, workspace_bytes, stream,
+                              "tpf_trimul_backward_bf16");
+}
+
+int tpf_trimul_backward_named_bf16(
+    const void* grad_out, const void* z, const float* mask, const float* w_ap, const float* w_ag,
+    const float* w_bp, const float* w_bg, const float* w_g, const float* w_z,
+    const float* ln_in_w, const float* ln_out_w, const void* zln, const void* gate, const void* a,
+    const void* b, const void* x, const void* xln, const float* mean_in, const float* rstd_in,
+    const float* mean_out, const float* rstd_out, int outgoing, int64_t B, int64_t N, int64_t C,
+    void* dz, float* d_p_in, float* d_g_in, float* d_w_g, float* d_w_z, float* d_ln_in_w,
+    float* d_ln_in_b, float* d_ln_out_w, float* d_ln_out_b, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  const int64_t hc = C * C;  // H = C
+  float* const w5dst[5] = {d_p_in, d_g_in, d_p_in ? d_p_in + hc : nullptr,
+                           d_g_in ? d_g_in + hc : nullptr, d_w_g};
+  return trimul_backward_impl(grad_out, z, mask, w_ap, w_ag, w_bp, w_bg, w_g, w_z, ln_in_w,
+                              ln_out_w, zln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
+                              rstd_out, outgoing, B, N, C, dz, w5dst, d_w_z, d_ln_in_w, d_ln_in_b,
+                              d_ln_out_w, d_ln_out_b, workspace, workspace_bytes, stream,
+                              "tpf_trimul_backward_named_bf16");
 }
 
 }  // extern "C"

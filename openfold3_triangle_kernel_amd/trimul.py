@@ -196,6 +196,19 @@ def _trimul_bwd_v1(
 ]:
     """Backward: (d_z, d_w5 [ap;ag;bp;bg;g], d_wz, d_gin, d_bin, d_gout, d_bout), all but
     d_z in f32.  ``xlnT`` carries the row-major ``xln`` saved by the forward op."""
+    d_z, (d_w5,), rest = _trimul_bwd_native(
+        grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in, mean_out, rstd_out,
+        w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, outgoing, named=False)
+    return (d_z, d_w5, *rest)
+
+
+def _trimul_bwd_native(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in,
+                       mean_out, rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out,
+                       outgoing, named):
+    """The native backward.  The W5 gradient comes as ``(d_w5,)`` [5H, C] in the
+    reference's [ap; ag; bp; bg; g] order, or (``named``) as the gradients of
+    the named weights ``(d_p_in [ap; bp], d_g_in [ag; bg], d_w_g)``, written
+    in place by the native fold (``tpf_trimul_backward_named_bf16``)."""
     B, N, _, C = (int(s) for s in z_bf.shape)
     H = C
     dev = z_bf.device
@@ -204,7 +217,11 @@ def _trimul_bwd_v1(
     *wts, gin, gout = _f32_all((w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out))
     f32 = dict(device=dev, dtype=torch.float32)
     d_z = torch.empty((B, N, N, C), device=dev, dtype=torch.bfloat16)
-    d_w5 = torch.empty((5 * H, C), **f32)  # [ap; ag; bp; bg; g]
+    if named:
+        w5 = (torch.empty((2 * H, C), **f32), torch.empty((2 * H, C), **f32),
+              torch.empty((C, C), **f32))
+    else:
+        w5 = (torch.empty((5 * H, C), **f32),)  # [ap; ag; bp; bg; g]
     d_wz = torch.empty((C, H), **f32)
     d_gin, d_bin = torch.empty(C, **f32), torch.empty(C, **f32)
     d_gout, d_bout = torch.empty(H, **f32), torch.empty(H, **f32)
@@ -212,16 +229,49 @@ def _trimul_bwd_v1(
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     with _device_ctx(dev):
         _native.call(
-            "tpf_trimul_backward_bf16",
+            "tpf_trimul_backward_named_bf16" if named else "tpf_trimul_backward_bf16",
             grad.data_ptr(), z_bf.data_ptr(), mask_f.data_ptr(), *[t.data_ptr() for t in wts],
             gin.data_ptr(), gout.data_ptr(), z_ln.data_ptr(), gate.data_ptr(), a.data_ptr(),
             b.data_ptr(), x.data_ptr(), xlnT.data_ptr(), mean_in.data_ptr(), rstd_in.data_ptr(),
             mean_out.data_ptr(), rstd_out.data_ptr(), int(bool(outgoing)), B, N, C,
-            d_z.data_ptr(), d_w5.data_ptr(), d_wz.data_ptr(), d_gin.data_ptr(),
+            d_z.data_ptr(), *[t.data_ptr() for t in w5], d_wz.data_ptr(), d_gin.data_ptr(),
             d_bin.data_ptr(), d_gout.data_ptr(), d_bout.data_ptr(), ws.data_ptr(), ws_bytes,
             _native.stream_of(z_bf),
         )
-    return d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout
+    return d_z, w5, (d_wz, d_gin, d_bin, d_gout, d_bout)
+
+
+@torch.library.custom_op(
+    "openfold3_turbopairformer_amd::trimul_bwd_named", mutates_args=(), device_types="cuda"
+)
+def _trimul_bwd_named(
+    grad_out: torch.Tensor, z_bf: torch.Tensor, mask_f: torch.Tensor, z_ln: torch.Tensor,
+    gate: torch.Tensor, a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, xlnT: torch.Tensor,
+    mean_in: torch.Tensor, rstd_in: torch.Tensor, mean_out: torch.Tensor, rstd_out: torch.Tensor,
+    w_ap: torch.Tensor, w_ag: torch.Tensor, w_bp: torch.Tensor, w_bg: torch.Tensor,
+    w_g: torch.Tensor, w_z: torch.Tensor, g_in: torch.Tensor, g_out: torch.Tensor,
+    outgoing: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+           torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``_trimul_bwd_v1`` for ``turbo_trimul``'s named weights: (d_z, d_p_in,
+    d_g_in, d_w_g, d_wz, d_gin, d_bin, d_gout, d_bout)."""
+    d_z, w5, rest = _trimul_bwd_native(
+        grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in, mean_out, rstd_out,
+        w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, outgoing, named=True)
+    return (d_z, *w5, *rest)
+
+
+@torch.library.register_fake("openfold3_turbopairformer_amd::trimul_bwd_named")
+def _trimul_bwd_named_fake(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in,
+                           mean_out, rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out,
+                           outgoing):
+    C = z_bf.shape[-1]
+    H = w_ap.shape[0]
+    f = dict(dtype=torch.float32)
+    return (z_bf.new_empty(z_bf.shape), z_bf.new_empty((2 * H, C), **f),
+            z_bf.new_empty((2 * H, C), **f), z_bf.new_empty((C, C), **f),
+            z_bf.new_empty((C, H), **f), z_bf.new_empty((C,), **f), z_bf.new_empty((C,), **f),
+            z_bf.new_empty((H,), **f), z_bf.new_empty((H,), **f))
 
 
 @torch.library.register_fake("openfold3_turbopairformer::_trimul_bwd_v1")
@@ -434,7 +484,8 @@ class _TurboTrimulFn(torch.autograd.Function):
     ``p_in`` / ``g_in`` into them under autograd would make every slice's
     backward zero-fill and copy a full-size gradient and then sum the
     pieces.  This node owns the concatenated weights instead and returns
-    their gradients as two row gathers of ``d_w5``.
+    their gradients directly (the native fold writes the p_in / g_in row
+    blocks in place).
     """
 
     @staticmethod
@@ -457,15 +508,13 @@ class _TurboTrimulFn(torch.autograd.Function):
         (z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out, p_in, g_in,
          g_out_w, p_out_w, n_in_w, n_out_w, out) = ctx.saved_tensors
         H = int(p_in.shape[0]) // 2
-        d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout = _trimul_bwd_v1(
+        # The native fold writes d(p_in) = [d a_p; d b_p] and d(g_in) =
+        # [d a_g; d b_g] in place: no row gather of a [5H, C] d_w5.
+        grads = _trimul_bwd_named(
             grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
             rstd_out, p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w, n_in_w, n_out_w,
-            out, ctx.outgoing)
-        # d_w5 rows: [a_p | a_g | b_p | b_g | g]; p_in = [a_p; b_p], g_in = [a_g; b_g]:
-        # one transposing copy to [p | g][branch], both gradients views of it.
-        pg = d_w5[:4 * H].view(2, 2, H, -1).transpose(0, 1).contiguous()
-        grads = (pg[0].view(2 * H, -1), pg[1].view(2 * H, -1), d_w5[4 * H:], d_wz,
-                 d_gin, d_bin, d_gout, d_bout)
+            ctx.outgoing)
+        d_z, grads = grads[0], grads[1:]
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
         return (d_z, None, *grads, None)
 

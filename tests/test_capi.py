@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), f"{name} not exported"
         assert name in _native.SIGNATURES, f"{name} missing from the ctypes binding"
         assert len(_native.SIGNATURES[name][1]) == nargs, f"{name}: arg count mismatch"
-    assert lib.tpf_abi_version() == 7
+    assert lib.tpf_abi_version() == 8
 
 
 def test_shape_errors_are_reported_without_launch(lib):

@@ -88,6 +88,30 @@ def test_trimul_bitwise_replay(gpu):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
+def test_named_weight_gradients_equal_d_w5_rows(gpu, outgoing):
+    """turbo_trimul's gradients of p_in / g_in / g_out (written in place by
+    tpf_trimul_backward_named_bf16's fold) are bitwise the matching row
+    blocks of the op route's d_w5 [ap; ag; bp; bg; g]."""
+    from openfold3_triangle_kernel_amd import trimul as tm
+
+    z, mask, w, dout = trimul_case(1, 64, 64, seed=4)
+    got = run_turbo(z, mask, w, dout, outgoing, gpu)
+    zb = z.to(gpu, torch.bfloat16)
+    names = ("w_ap", "w_ag", "w_bp", "w_bg", "w_g", "w_z")
+    res = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(
+        zb, mask.to(gpu), *[w[k].to(gpu) for k in names], w["g_in"].to(gpu),
+        w["b_in"].to(gpu), w["g_out"].to(gpu), w["b_out"].to(gpu), outgoing, True)
+    out, z_ln, gate, a, b, x, xln, mi, ri, mo, ro = res
+    d_w5 = tm._trimul_bwd_v1(dout.to(gpu, torch.bfloat16), zb, mask.to(gpu), z_ln, gate, a, b, x,
+                             xln, mi, ri, mo, ro, *[w[k].to(gpu) for k in names],
+                             w["g_in"].to(gpu), w["g_out"].to(gpu), out, outgoing)[1]
+    rows = d_w5.view(5, 64, 64).cpu().numpy()
+    for i, k in enumerate(("w_ap", "w_ag", "w_bp", "w_bg", "w_g")):
+        assert np.array_equal(got[k], rows[i]), k
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("outgoing", [1, 0], ids=["outgoing", "incoming"])
 def test_trimul_backward_ignores_memory_past_the_planes(gpu, outgoing):
     """N % 8 != 0: the dA contraction runs K over the plane pitch Np (dX's zero
