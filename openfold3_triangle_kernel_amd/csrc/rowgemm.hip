@@ -7,8 +7,8 @@
 // each x tile once per output tile column, while here every workgroup keeps
 // its slice of W in registers for the whole launch and streams x once.
 //
-// Launch: one persistent workgroup of 8 waves per CU walks contiguous
-// 32-row blocks.  Wave w owns the output tiles t = w, w + 8, ... (16
+// Launch: one persistent workgroup of 8 waves per CU walks 32-row blocks
+// strided by the grid size.  Wave w owns the output tiles t = w, w + 8, ... (16
 // channels each, t < N / 16) and holds their weight rows as the A operands
 // of v_mfma_f32_16x16x32_bf16 (MT x KS registers of 8 bf16, K = 32 KS).
 // Waves 0-3 stream x blocks into a DEPTH-deep LDS ring with direct
@@ -120,12 +120,16 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
     }
   }
 
-  // Buffer resources are based at each block's first row (64-bit address
-  // arithmetic on the scalar unit), so the 32-bit lane offsets stay small
-  // for any row count.
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  // Workgroup g takes blocks g, g + G, g + 2 G, ... (G = grid size), so at
+  // any time the grid works on a compact window of consecutive blocks (DRAM
+  // pages shared across workgroups): measured 56 -> 51 us on the plain
+  // product and 219 -> 207 us on the gate epilogue at 589,824 rows, against
+  // one contiguous range per workgroup.  Buffer resources are based at each
+  // block's first row (64-bit address arithmetic on the scalar unit), so the
+  // 32-bit lane offsets stay small for any row count.
+  const int64_t nit =
+      blockIdx.x < nblocks ? (nblocks - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  auto gb = [&](int64_t it) { return (int64_t)blockIdx.x + it * gridDim.x; };
   // Loading thread i of 256 takes chunks ci = 256 j + i of the block: row
   // r = ci / CPR, stored at slot (c + r) % CPR of its row.
   // Gate mode: a loading thread's side chunks ci = 256 j + tid are (row
@@ -142,9 +146,10 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
       side_g[j] = ok ? (uint32_t)((r * gt.gpitch + 8 * c) * 2) : kBufOOB;
     }
   }
-  auto issue = [&](int64_t blk) {
-    const int stage = (int)(blk % DEPTH);
-    const int64_t bb = blk < bend ? blk : 0;
+  auto issue = [&](int64_t it) {
+    const int stage = (int)(it % DEPTH);
+    const bool vb = it < nit;
+    const int64_t bb = vb ? gb(it) : 0;
     // x rows of the block: consecutive, or (og_t) the pair rows
     // (b, i, j0 + r) at dout rows (b, j0 + r, i), N rows apart.
     int64_t xrow0 = bb * 32, xstride = ldx;
@@ -162,12 +167,12 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
       const int ci = 256 * j + tid;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
-      const bool ok = blk < bend && blk * 32 + r < R;
+      const bool ok = vb && bb * 32 + r < R;
       buf2lds16(rs_x, ok ? (uint32_t)((r * xstride + 8 * gc) * 2) : kBufOOB,
                 &Xs[stage][(256 * j + 64 * wv) * 8]);
     }
     if constexpr (GATE) {
-      const bool ok = blk < bend;
+      const bool ok = vb;
       const i32x4 rs_o = buffer_rsrc(gt.o + bb * 32 * N);
       const i32x4 rs_g = buffer_rsrc(gt.gate + bb * 32 * gt.gpitch);
 #pragma unroll
@@ -216,15 +221,16 @@ __global__ __launch_bounds__(64 * kRowNW) void rowgemm_ws_kernel(
   }
   if (loader) {
 #pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d) issue(bbeg + d);
-    wait_vmcnt<LPT * (DEPTH - 2)>();  // block bbeg landed
+    for (int d = 0; d < DEPTH - 1; ++d) issue(d);
+    wait_vmcnt<LPT * (DEPTH - 2)>();  // the first block landed
   }
   __syncthreads();
 #pragma unroll 1
-  for (int64_t blk = bbeg; blk < bend; ++blk) {
-    const int stage = (int)(blk % DEPTH);
-    __bf16* Yb = Ys + (int)(blk & 1) * 32 * YP;
-    if (loader) issue(blk + DEPTH - 1);
+  for (int64_t it = 0; it < nit; ++it) {
+    const int64_t blk = gb(it);
+    const int stage = (int)(it % DEPTH);
+    __bf16* Yb = Ys + (int)(it & 1) * 32 * YP;
+    if (loader) issue(it + DEPTH - 1);
     const __bf16* Xb = Xs[stage];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {

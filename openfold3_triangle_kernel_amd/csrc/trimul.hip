@@ -53,6 +53,26 @@ struct TmGeom {
 constexpr int kSP = 136;  // bf16 pitch of 128-wide LDS staging tiles
 // LDS of a kernel = max(main loop ring, epilogue staging).
 // LDS of a kernel whose epilogue staging reuses its NS-stage GEMM ring.
+// Block walk of the persistent row kernels: a workgroup runs the virtual
+// blocks [bbeg, bend) and pb(blk) is the 32-row block a virtual block reads:
+// one contiguous range per workgroup, or (strided) blocks g, g + G, ... for
+// workgroup g of G, which keeps the grid on a compact window of rows.  Each
+// kernel takes the walk measured faster for it at N = 384 (strided: LN_in
+// backward 59.2 -> 55.8 us, output projection 23.8 -> 21.4 us; contiguous:
+// the projection backward, whose 64-byte plane stores of consecutive blocks
+// merge, 71.6 against 79.7 us, the projection forward and the output
+// backward).  Either walk depends on the shape and grid only.
+#define TM_BLOCKS_CONTIGUOUS(nblocks)                                            \
+  const int64_t per = ((nblocks) + gridDim.x - 1) / gridDim.x;                   \
+  const int64_t bbeg = blockIdx.x * per;                                         \
+  const int64_t bend = bbeg + per < (nblocks) ? bbeg + per : (nblocks);          \
+  auto pb = [&](int64_t v) { return v; }
+#define TM_BLOCKS_STRIDED(nblocks)                                               \
+  const int64_t bbeg = 0;                                                        \
+  const int64_t bend =                                                           \
+      blockIdx.x < (nblocks) ? ((nblocks) - blockIdx.x + gridDim.x - 1) / gridDim.x : 0; \
+  auto pb = [&](int64_t v) { return v * (int64_t)gridDim.x + blockIdx.x; }
+
 // Tile size of the channel contractions (forward x = A B^T, backward dA and
 // dB): 192 x 192 when N is a multiple of 192 (N = 384: 4 tiles per channel
 // instead of 9, one round of 512 workgroups on 256 CUs instead of 2.25, and
@@ -535,9 +555,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
   const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(b_pl, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_g = __builtin_amdgcn_make_buffer_rsrc(gl, 0, 0x7FFFFFFF, 0x00020000);
   // Workgroup c takes the contiguous blocks [c per, (c + 1) per).
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  TM_BLOCKS_CONTIGUOUS(nblocks);
   // Loader: instruction j of wave w fills LDS chunks (2 w + j) * 64 + lane
   // (row ci / CPR, slot ci % CPR) with global chunk (slot - row) mod CPR.
   auto issue = [&](int64_t blk) {
@@ -547,13 +565,13 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
       const int ci = (2 * w + j) * 64 + lane;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
-      const int64_t m = blk * 32 + r;
+      const int64_t m = pb(blk) * 32 + r;
       const bool ok = blk < bend && m < g.R;
       const uint32_t off = ok ? (uint32_t)((tm_phys_row(g, m) * C + 8 * gc) * 2) : kBufOOB;
       buf2lds16(rs_z, off, &As[stage][(2 * w + j) * 512]);
     }
     if (w == 0) {
-      const int64_t m = blk * 32 + lane;
+      const int64_t m = pb(blk) * 32 + lane;
       const bool ok = lane < 32 && blk < bend && m < g.R;
       buf2lds4(rs_m, ok ? (uint32_t)(tm_phys_row(g, m) * 4) : kBufOOB, &Ms[stage][0]);
     }
@@ -603,7 +621,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_fwd_kernel(
     const int sb = (int)(blk & 1);
     const __bf16* G = Sg[sb];
     const int st = tid - 2 * C;
-    const int64_t mb0 = blk * 32;
+    const int64_t mb0 = pb(blk) * 32;
     bf16x8 v[6];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -752,9 +770,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
   const i32x4 rs_da = buffer_rsrc(da);
   const i32x4 rs_db = buffer_rsrc(db);
   const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(dproj5, 0, 0x7FFFFFFF, 0x00020000);
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  TM_BLOCKS_CONTIGUOUS(nblocks);
   // Loads of a block per loading wave: 2 zln, 4 plane-segment, (wave 0) 1 mask.
   auto issue = [&](int64_t blk) {
     const int stage = (int)(blk % kInBwdDepth);
@@ -763,7 +779,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
       const int ci = (2 * w + j) * 64 + lane;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
-      const uint32_t m = (uint32_t)blk * 32 + r;
+      const uint32_t m = (uint32_t)pb(blk) * 32 + r;
       const bool ok = blk < bend && m < (uint32_t)g.R;
       const uint32_t off = ok ? (tm_phys_row32(g, m) * C + 8 * gc) * 2 : kBufOOB;
       buf2lds16(rs_z, off, &As[stage][(2 * w + j) * 512]);
@@ -774,7 +790,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
       const int gi = (4 * w + j) * 64 + lane;
       const int t = (4 * w + j) * 64 / (4 * C), rem = gi - t * 4 * C;  // t wave-uniform
       const int c = rem >> 2, part = rem & 3;
-      const uint32_t mb = (uint32_t)blk * 32 + 8 * part;
+      const uint32_t mb = (uint32_t)pb(blk) * 32 + 8 * part;
       const bool ok = blk < bend && mb < (uint32_t)g.R;
       const uint32_t off = ok ? tm_plane_elem32(g, mb, c) * 2 : kBufOOB;
       // The first 4C chunks are da, the rest db (each wave's 4 instructions
@@ -782,7 +798,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
       buf2lds16(t ? rs_db : rs_da, off, &Ds[stage][(4 * w + j) * 512]);
     }
     if (w == 0) {
-      const uint32_t m = (uint32_t)blk * 32 + lane;
+      const uint32_t m = (uint32_t)pb(blk) * 32 + lane;
       const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
       buf2lds4(rs_m, ok ? tm_phys_row32(g, m) * 4 : kBufOOB, &Ms[stage][0]);
     }
@@ -835,7 +851,7 @@ __global__ __launch_bounds__(4 * C) void tm_in_proj_bwd_ws_kernel(
     // 16 C chunks (32 rows x C / 2) over the 2 C storing threads, four LDS
     // reads ahead of their stores.
     const int st = tid - 2 * C;
-    const int64_t mb0 = blk * 32;
+    const int64_t mb0 = pb(blk) * 32;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       bf16x8 v[4];
@@ -1248,9 +1264,7 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
   const i32x4 rs_mu = buffer_rsrc(mean);
   const i32x4 rs_rs = buffer_rsrc(rstd);
   const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(dz, 0, 0x7FFFFFFF, 0x00020000);
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  TM_BLOCKS_STRIDED(nblocks);
   // Loads per block and loading wave: 2 z instructions and, by wave 0, the
   // two statistics rows (load j < 2, block blk, into the 2-deep ring), then PI
   // dproj5 instructions (load j >= 2, into the 3-deep ring).
@@ -1260,11 +1274,11 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
       const int ci = (2 * w + j) * 64 + lane;
       const int r = ci / CPR, slot = ci % CPR;
       const int gc = (slot - r % CPR + CPR) % CPR;
-      const uint32_t m = (uint32_t)blk * 32 + r;
+      const uint32_t m = (uint32_t)pb(blk) * 32 + r;
       const bool ok = blk < bend && m < (uint32_t)g.R;
       buf2lds16(rs_z, ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Zs[stage][(2 * w + j) * 512]);
       if (j == 1 && w == 0) {
-        const uint32_t mr = (uint32_t)blk * 32 + lane;
+        const uint32_t mr = (uint32_t)pb(blk) * 32 + lane;
         const bool okr = lane < 32 && blk < bend && mr < (uint32_t)g.R;
         buf2lds4(rs_mu, okr ? mr * 4 : kBufOOB, &Ss[stage][0][0]);
         buf2lds4(rs_rs, okr ? mr * 4 : kBufOOB, &Ss[stage][1][0]);
@@ -1274,7 +1288,7 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
       const int ci = (PI * w + j - 2) * 64 + lane;
       const int r = ci / KC, slot = ci % KC;
       const int gc = (slot - r % KC + KC) % KC;
-      const uint32_t m = (uint32_t)blk * 32 + r;
+      const uint32_t m = (uint32_t)pb(blk) * 32 + r;
       const bool ok = blk < bend && m < (uint32_t)g.R;
       buf2lds16(rs_p, ok ? (m * K + 8 * gc) * 2 : kBufOOB, &Ps[stage][(PI * w + j - 2) * 512]);
     }
@@ -1400,7 +1414,7 @@ __global__ __launch_bounds__(4 * C) void tm_ln_in_bwd_ws_kernel(
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         const int qq = st + 2 * C * it, row = qq / CPR, k = qq % CPR;
-        const uint32_t m = (uint32_t)blk * 32 + row;
+        const uint32_t m = (uint32_t)pb(blk) * 32 + row;
         const uint32_t off = m < (uint32_t)g.R ? (m * C + 8 * k) * 2 : kBufOOB;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o, off, 0, 0);
       }
@@ -1487,9 +1501,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
   const i32x4 rs_rs = buffer_rsrc(rstd);
   const __amdgpu_buffer_rsrc_t rs_dp = __builtin_amdgcn_make_buffer_rsrc(dproj5, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_dx = __builtin_amdgcn_make_buffer_rsrc(dx, 0, 0x7FFFFFFF, 0x00020000);
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  TM_BLOCKS_CONTIGUOUS(nblocks);
   // Loads per block and loading wave: 2 instructions for each of xln, gl,
   // dout (rows, chunk-rotated) and x (plane segments); wave 0 also loads the
   // two statistics rows.
@@ -1502,7 +1514,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
         const int ci = (2 * w + j) * 64 + lane;
         const int r = ci / CPR, slot = ci % CPR;
         const int gc = (slot - r % CPR + CPR) % CPR;
-        const uint32_t m = (uint32_t)blk * 32 + r;
+        const uint32_t m = (uint32_t)pb(blk) * 32 + r;
         const bool ok = blk < bend && m < (uint32_t)g.R;
         buf2lds16(rs_in[t], ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Rg[stage][t][(2 * w + j) * 512]);
       }
@@ -1510,12 +1522,12 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
     for (int j = 0; j < 2; ++j) {
       const int ci = (2 * w + j) * 64 + lane;  // (channel ci / 4, 8-position part ci % 4)
       const int c = ci >> 2, part = ci & 3;
-      const uint32_t mb = (uint32_t)blk * 32 + 8 * part;
+      const uint32_t mb = (uint32_t)pb(blk) * 32 + 8 * part;
       const bool ok = blk < bend && mb < (uint32_t)g.R;
       buf2lds16(rs_x, ok ? tm_plane_elem32(g, mb, c) * 2 : kBufOOB, &Rg[stage][3][(2 * w + j) * 512]);
     }
     if (w == 0) {
-      const uint32_t m = (uint32_t)blk * 32 + lane;
+      const uint32_t m = (uint32_t)pb(blk) * 32 + lane;
       const bool ok = lane < 32 && blk < bend && m < (uint32_t)g.R;
       buf2lds4(rs_mu, ok ? m * 4 : kBufOOB, &Ss[stage][0][0]);
       buf2lds4(rs_rs, ok ? m * 4 : kBufOOB, &Ss[stage][1][0]);
@@ -1659,11 +1671,11 @@ __global__ __launch_bounds__(4 * C) void tm_out_bwd_ws_kernel(
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
-        const uint32_t m = (uint32_t)blk * 32 + row;
+        const uint32_t m = (uint32_t)pb(blk) * 32 + row;
         const bool ok = m < (uint32_t)g.R;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[2 + it]), rs_dp,
                                                ok ? (m * 5 * C + 4 * C + 8 * k) * 2 : kBufOOB, 0, 0);
-        const uint32_t mb = (uint32_t)blk * 32 + 8 * (q & 3);
+        const uint32_t mb = (uint32_t)pb(blk) * 32 + 8 * (q & 3);
         __builtin_amdgcn_raw_buffer_store_b128(
             __builtin_bit_cast(u32x4, v[4 + it]), rs_dx,
             mb < (uint32_t)g.R ? tm_plane_elem32(g, mb, q >> 2) * 2 : kBufOOB, 0, 0);
@@ -1717,9 +1729,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_proj_fwd_ws_kernel(
   for (int ks = 0; ks < KS; ++ks) wf[ks] = ld8(wz + (int64_t)ch * C + 8 * (4 * ks + lg));
   const i32x4 rs_in[2] = {buffer_rsrc(xln), buffer_rsrc(gl)};
   const __amdgpu_buffer_rsrc_t rs_o = __builtin_amdgcn_make_buffer_rsrc(out, 0, 0x7FFFFFFF, 0x00020000);
-  const int64_t per = (nblocks + gridDim.x - 1) / gridDim.x;
-  const int64_t bbeg = blockIdx.x * per;
-  const int64_t bend = bbeg + per < nblocks ? bbeg + per : nblocks;
+  TM_BLOCKS_STRIDED(nblocks);
   // Loads per block and loading wave: 2 instructions each for xln and gl.
   auto issue = [&](int64_t blk) {
     const int stage = (int)(blk % kOutFwdDepth);
@@ -1730,7 +1740,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_proj_fwd_ws_kernel(
         const int ci = (2 * w + j) * 64 + lane;
         const int r = ci / CPR, slot = ci % CPR;
         const int gc = (slot - r % CPR + CPR) % CPR;
-        const uint32_t m = (uint32_t)blk * 32 + r;
+        const uint32_t m = (uint32_t)pb(blk) * 32 + r;
         const bool ok = blk < bend && m < (uint32_t)g.R;
         buf2lds16(rs_in[t], ok ? (m * C + 8 * gc) * 2 : kBufOOB, &Rg[stage][t][(2 * w + j) * 512]);
       }
@@ -1783,7 +1793,7 @@ __global__ __launch_bounds__(4 * C) void tm_out_proj_fwd_ws_kernel(
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         const int q = st + 2 * C * it, row = q / CPR, k = q % CPR;
-        const uint32_t m = (uint32_t)blk * 32 + row;
+        const uint32_t m = (uint32_t)pb(blk) * 32 + row;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[it]), rs_o,
                                                m < (uint32_t)g.R ? (m * C + 8 * k) * 2 : kBufOOB, 0, 0);
       }
