@@ -208,7 +208,22 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
 // LN_in over rows of z (16 lanes per row, 8 channels per lane).  A thread
 // handles kLnRowsRPT rows 16 apart, their loads issued together.
 // ---------------------------------------------------------------------------
-constexpr int kLnRowsRPT = 2;
+#ifndef TPF_LNR_RPT
+#define TPF_LNR_RPT 2
+#endif
+#ifndef TPF_LNR_WAVES_PER_CU
+#define TPF_LNR_WAVES_PER_CU 0
+#endif
+constexpr int kLnRowsRPT = TPF_LNR_RPT;
+// Workgroups of the LN_in launch: one per 16 * kLnRowsRPT rows, or (when a
+// per-CU count is set) a grid-stride walk in which each workgroup loads its
+// next rows while it normalises the current ones.
+static inline int64_t tm_ln_rows_grid(int64_t R) {
+  const int64_t nb = (R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT);
+  if (TPF_LNR_WAVES_PER_CU == 0) return nb;
+  const int64_t cap = (int64_t)device_cus() * TPF_LNR_WAVES_PER_CU / 4;
+  return nb < cap ? nb : cap;
+}
 template <int C>
 __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restrict__ z,
                                                          const float* __restrict__ w,
@@ -217,44 +232,67 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
                                                          float* __restrict__ mean_out,
                                                          float* __restrict__ rstd_out, int64_t R) {
   const int l16 = threadIdx.x & 15;
-  const int64_t row0 = (int64_t)blockIdx.x * 16 * kLnRowsRPT + (threadIdx.x >> 4);
-  float x[kLnRowsRPT][8];
+  const bool chan = l16 < C / 8;
+  const int64_t nb = (R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT);
+  // The lane's 8 LayerNorm weights and biases.
+  f32x4 wv[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}}, bv[2] = {wv[0], wv[1]};
+  if (chan) {
 #pragma unroll
-  for (int k = 0; k < kLnRowsRPT; ++k) {
-    const int64_t row = row0 + 16 * k;
-    bf16x8 v = zero8();
-    if (row < R && l16 < C / 8) v = ld8(z + row * C + l16 * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[k][e] = bf2f(v[e]);
-  }
-#pragma unroll
-  for (int k = 0; k < kLnRowsRPT; ++k) {
-    const int64_t row = row0 + 16 * k;
-    const bool act = (row < R) && (l16 < C / 8);
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += x[k][e];
-    s = row16_sum(s);
-    const float mean = s * (1.f / C);
-    float v2 = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float d = act ? x[k][e] - mean : 0.f;
-      v2 = fmaf(d, d, v2);
+    for (int h = 0; h < 2; ++h) {
+      wv[h] = *reinterpret_cast<const f32x4*>(w + l16 * 8 + 4 * h);
+      bv[h] = *reinterpret_cast<const f32x4*>(bias + l16 * 8 + 4 * h);
     }
-    v2 = row16_sum(v2);
-    const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
-    if (act) {
-      bf16x8 o;
+  }
+  // Rows of block blk: row0 + 16 k.  Loads are unconditional (rows past R
+  // re-read row R - 1, lanes past C read channel 0) so the loads of the next
+  // block stay in flight while the current one is normalised.
+  auto load = [&](int64_t blk, bf16x8 (&v)[kLnRowsRPT]) {
+    const int64_t row0 = blk * 16 * kLnRowsRPT + (threadIdx.x >> 4);
+#pragma unroll
+    for (int k = 0; k < kLnRowsRPT; ++k) {
+      const int64_t row = min(row0 + 16 * k, R - 1);
+      v[k] = ld8(z + row * C + (chan ? l16 * 8 : 0));
+    }
+  };
+  bf16x8 nxt[kLnRowsRPT];
+  int64_t blk = blockIdx.x;
+  load(blk, nxt);
+#pragma unroll 1
+  for (; blk < nb; blk += gridDim.x) {
+    float x[kLnRowsRPT][8];
+#pragma unroll
+    for (int k = 0; k < kLnRowsRPT; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] = chan ? bf2f(nxt[k][e]) : 0.f;
+    if (blk + gridDim.x < nb) load(blk + gridDim.x, nxt);
+    const int64_t row0 = blk * 16 * kLnRowsRPT + (threadIdx.x >> 4);
+#pragma unroll
+    for (int k = 0; k < kLnRowsRPT; ++k) {
+      const int64_t row = row0 + 16 * k;
+      const bool act = (row < R) && chan;
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += x[k][e];
+      s = row16_sum(s);
+      const float mean = s * (1.f / C);
+      float v2 = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int c = l16 * 8 + e;
-        o[e] = f2bf((x[k][e] - mean) * rstd * w[c] + bias[c]);
+        const float d = act ? x[k][e] - mean : 0.f;
+        v2 = fmaf(d, d, v2);
       }
-      st8(out + row * C + l16 * 8, o);
-      if (l16 == 0) {
-        mean_out[row] = mean;
-        rstd_out[row] = rstd;
+      v2 = row16_sum(v2);
+      const float rstd = rsqrtf(v2 * (1.f / C) + 1e-5f);
+      if (act) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          o[e] = f2bf((x[k][e] - mean) * rstd * wv[e >> 2][e & 3] + bv[e >> 2][e & 3]);
+        st8(out + row * C + l16 * 8, o);
+        if (l16 == 0) {
+          mean_out[row] = mean;
+          rstd_out[row] = rstd;
+        }
       }
     }
   }
@@ -271,6 +309,18 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
 // sum of squares (two passes, as before).  Each thread then writes its 8
 // channels of its 8 rows as 16-byte stores.
 // ---------------------------------------------------------------------------
+#ifndef TPF_LNP_WGS_PER_CU
+#define TPF_LNP_WGS_PER_CU 2
+#endif
+// Workgroups of the LN_out launch per batch: one per 128-position tile, or
+// (when a per-CU count is set) a grid-stride walk over the tiles in which
+// each workgroup loads its next tile while it normalises the current one.
+static inline int64_t tm_ln_planes_grid(int64_t NN, int64_t B) {
+  const int64_t nt = (NN + 127) / 128;
+  if (TPF_LNP_WGS_PER_CU == 0) return nt;
+  const int64_t cap = ((int64_t)device_cus() * TPF_LNP_WGS_PER_CU + B - 1) / B;
+  return nt < cap ? nt : cap;
+}
 template <int H>
 __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restrict__ x,
                                                            const float* __restrict__ w,
@@ -279,94 +329,113 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
                                                            float* __restrict__ mean_out,
                                                            float* __restrict__ rstd_out,
                                                            TmGeom g) {
-  constexpr int T = 128;  // positions per workgroup
-  __shared__ float red[4][16][8];
+  constexpr int T = 128;  // positions per tile
+  __shared__ float red[2][4][16][8];
   const int tid = threadIdx.x, wv = tid >> 6, b = blockIdx.y;
   const int pg = tid & 15, cg = tid >> 4;
   const bool chan = cg * 8 < H;
-  const int64_t pb = (int64_t)blockIdx.x * T + pg * 8;  // first position of this thread
-  bf16x8 v[8];  // v[c][e]: channel cg*8 + c, position pb + e
-  if (chan) {
-    const bool vec = (g.Np == g.N) && (pb + 8 <= g.NN);
+  const int64_t nt = (g.NN + T - 1) / T;
+  const bool vec = g.Np == g.N;
+  const int cgl = chan ? cg : 0;
+  float wc[8], bc[8];
+  {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + cgl * 8);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + cgl * 8 + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + cgl * 8);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + cgl * 8 + 4);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const __bf16* plane = x + ((int64_t)b * H + cg * 8 + c) * g.PS;
-      if (vec) {
-        v[c] = ld8(plane + pb);
-      } else {
+    for (int i = 0; i < 4; ++i) {
+      wc[i] = w0[i]; wc[4 + i] = w1[i];
+      bc[i] = b0[i]; bc[4 + i] = b1[i];
+    }
+  }
+  // v[c][e]: channel cg*8 + c, position pb + e of tile t.  Full tiles of
+  // unpadded planes load unconditionally, 16 bytes per channel.
+  auto load = [&](int64_t t, bf16x8 (&v)[8]) {
+    const int64_t pb = t * T + pg * 8;
+    if (vec && pb + 8 <= g.NN) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v[c] = ld8(x + ((int64_t)b * H + cgl * 8 + c) * g.PS + pb);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const __bf16* plane = x + ((int64_t)b * H + cgl * 8 + c) * g.PS;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           v[c][e] = pb + e < g.NN ? plane[tm_plane_off(g, pb + e)] : static_cast<__bf16>(0.f);
       }
     }
-  } else {
+  };
+  // Sum over all channels of q[e] (this thread's 8 channels already summed);
+  // the two sums of a tile use the two halves of `red`, so one barrier each.
+  auto channel_sum = [&](float (&q)[8], int half) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = zero8();
-  }
-  // Sum over all channels of q[e] (this thread's 8 channels already summed).
-  auto channel_sum = [&](float (&q)[8]) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      q[e] = xor32_sum(xor16_sum(q[e]));
-    }
+    for (int e = 0; e < 8; ++e) q[e] = xor32_sum(xor16_sum(q[e]));
     if ((tid & 48) == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wv][pg][e] = q[e];
+      for (int e = 0; e < 8; ++e) red[half][wv][pg][e] = q[e];
     }
     __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = ((red[0][pg][e] + red[1][pg][e]) + red[2][pg][e]) + red[3][pg][e];
-    __syncthreads();
-  };
-  float mean[8], rstd[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) s += bf2f(v[c][e]);
-    mean[e] = s;
-  }
-  channel_sum(mean);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) mean[e] *= 1.f / H;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float s = 0.f;
-    if (chan) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float d = bf2f(v[c][e]) - mean[e];
-        s = fmaf(d, d, s);
-      }
-    }
-    rstd[e] = s;
-  }
-  channel_sum(rstd);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) rstd[e] = rsqrtf(rstd[e] * (1.f / H) + 1e-5f);
-  if (chan) {
-    const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + cg * 8);
-    const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + cg * 8 + 4);
-    const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + cg * 8);
-    const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + cg * 8 + 4);
-    const float wc[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-    const float bc[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (pb + e >= g.NN) continue;
-      bf16x8 o;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = f2bf((bf2f(v[c][e]) - mean[e]) * rstd[e] * wc[c] + bc[c]);
-      st8(xln + ((int64_t)b * g.NN + pb + e) * H + cg * 8, o);
-    }
-  }
-  if (cg == 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (pb + e < g.NN) {
-        mean_out[(int64_t)b * g.NN + pb + e] = mean[e];
-        rstd_out[(int64_t)b * g.NN + pb + e] = rstd[e];
+      q[e] = ((red[half][0][pg][e] + red[half][1][pg][e]) + red[half][2][pg][e]) + red[half][3][pg][e];
+  };
+  bf16x8 nxt[8];
+  int64_t t = blockIdx.x;
+  if (t < nt) load(t, nxt);
+#pragma unroll 1
+  for (; t < nt; t += gridDim.x) {
+    bf16x8 v[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = chan ? nxt[c] : zero8();
+    if (t + gridDim.x < nt) load(t + gridDim.x, nxt);
+    const int64_t pb = t * T + pg * 8;  // first position of this thread
+    float mean[8], rstd[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) s += bf2f(v[c][e]);
+      mean[e] = s;
+    }
+    // red[0] was last read before the previous tile's second barrier, red[1]
+    // before this tile's first: no barrier is needed between tiles.
+    channel_sum(mean, 0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mean[e] *= 1.f / H;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float s = 0.f;
+      if (chan) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float d = bf2f(v[c][e]) - mean[e];
+          s = fmaf(d, d, s);
+        }
       }
+      rstd[e] = s;
+    }
+    channel_sum(rstd, 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rstd[e] = rsqrtf(rstd[e] * (1.f / H) + 1e-5f);
+    if (chan) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (pb + e >= g.NN) continue;
+        bf16x8 o;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[c] = f2bf((bf2f(v[c][e]) - mean[e]) * rstd[e] * wc[c] + bc[c]);
+        st8(xln + ((int64_t)b * g.NN + pb + e) * H + cg * 8, o);
+      }
+    }
+    if (cg == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (pb + e < g.NN) {
+          mean_out[(int64_t)b * g.NN + pb + e] = mean[e];
+          rstd_out[(int64_t)b * g.NN + pb + e] = rstd[e];
+        }
+    }
   }
 }
 
@@ -1929,7 +1998,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
     if ((rc = zero_fill(b, B * C * g.PS * 2, s, fn))) return rc;
     if ((rc = zero_fill(x, B * C * g.PS * 2, s, fn))) return rc;
   }
-  TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)((g.R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT))), (const __bf16*)z, ln_in_w,
+  TM_DISPATCH_C(C, tm_ln_rows_kernel, dim3((unsigned)tm_ln_rows_grid(g.R)), (const __bf16*)z, ln_in_w,
                 ln_in_b, (__bf16*)zln, mean_in, rstd_in, g.R);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_in)"))) return rc;
   const int64_t tiles = (g.R + 127) / 128;
@@ -1963,7 +2032,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
   if ((rc = gemm_launch(ga, 1, 1, 0, (int)(B * C), s, "tpf_trimul_forward_bf16(contract)",
                         tm_contract_tile(N))))
     return rc;
-  TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)((g.NN + 127) / 128), (unsigned)B),
+  TM_DISPATCH_C(C, tm_ln_planes_kernel, dim3((unsigned)tm_ln_planes_grid(g.NN, B), (unsigned)B),
                 (const __bf16*)x, ln_out_w, ln_out_b, (__bf16*)xln, mean_out, rstd_out, g);
   if ((rc = check_launch("tpf_trimul_forward_bf16(ln_out)"))) return rc;
   {
