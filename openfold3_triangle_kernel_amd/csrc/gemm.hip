@@ -23,35 +23,38 @@ using namespace gk32;
 
 // Several fixed-order folds in one launch.  Segment sg owns workgroups
 // [gbase[sg], gbase[sg + 1]); a workgroup covers 256 / RC consecutive
-// elements x RC ranges of splits (RC = ranges[sg], a power of two chosen so
-// that a range holds at most 16 splits): thread (range r, element i)
+// element groups x RC ranges of splits (RC = ranges[sg], a power of two
+// chosen so that a range holds at most 16 splits); an element group is 4
+// consecutive elements read as one 16-byte load when the segment's sizes and
+// pointers allow it (vec[sg]), else one element.  Thread (range r, group i)
 // sums splits [r * per, min((r + 1) * per, splits)) in ascending order with
 // all of its loads in flight, and the ranges meet in LDS in the fixed order
 // ((r0 + r1) + r2) + ...; element i of the segment lands in
-// dst[i / piece][i % piece].  The order depends only on the shapes.
-__global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
-  __shared__ float red[256];
-  int sg = 0;
-  while (sg + 1 < f.nseg && (int)blockIdx.x >= f.gbase[sg + 1]) ++sg;
+// dst[i / piece][i % piece].  Every element's order depends only on the
+// shapes (the grouping changes no sum).
+template <int EPT>
+__device__ __forceinline__ void fold_multi_body(const FoldSegs& f, int sg) {
+  typedef float VT __attribute__((ext_vector_type(EPT)));
+  __shared__ VT red[256];
   const int rc = f.ranges[sg], epw = 256 / rc;
   const int r = threadIdx.x / epw, el = threadIdx.x - r * epw;
-  const int64_t i = (int64_t)((int)blockIdx.x - f.gbase[sg]) * epw + el;
+  const int64_t i = ((int64_t)((int)blockIdx.x - f.gbase[sg]) * epw + el) * EPT;
   const bool act = i < f.n[sg];
   const int splits = f.splits[sg];
   const int per = (splits + rc - 1) / rc;
   const int s0 = r * per, s1 = min(splits, s0 + per);
   const float* part = f.part[sg];
   const int64_t stride = f.stride[sg];
-  float acc = 0.f;
+  VT acc = (VT)0.f;
   if (act && s0 < s1) {
     // Up to 16 loads go out together (a range holds at most 16 splits
     // unless the range count is capped), then they are added in ascending
     // order.
     for (int s = s0; s < s1; s += 16) {
-      float v[16];
+      VT v[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        if (s + e < s1) v[e] = part[(int64_t)(s + e) * stride + i];
+        if (s + e < s1) v[e] = *reinterpret_cast<const VT*>(part + (int64_t)(s + e) * stride + i);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         if (s + e < s1) acc = (s + e == s0) ? v[e] : acc + v[e];
@@ -63,7 +66,16 @@ __global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
   for (int q = 1; q < rc; ++q)
     if (q * per < splits) acc += red[q * epw + el];
   const int64_t pc = i / f.piece[sg];
-  f.dst[sg][pc][i - pc * f.piece[sg]] = acc;
+  *reinterpret_cast<VT*>(f.dst[sg][pc] + (i - pc * f.piece[sg])) = acc;
+}
+
+__global__ __launch_bounds__(256) void fold_multi_kernel(FoldSegs f) {
+  int sg = 0;
+  while (sg + 1 < f.nseg && (int)blockIdx.x >= f.gbase[sg + 1]) ++sg;
+  if (f.vec[sg])
+    fold_multi_body<4>(f, sg);
+  else
+    fold_multi_body<1>(f, sg);
 }
 
 // The weight-gradient fold contract of the reference
@@ -98,8 +110,14 @@ int fold_multi(FoldSegs f, hipStream_t stream, const char* fn) {
     int rc = 1;
     while (rc < 64 && (f.splits[sg] + rc - 1) / rc > 16) rc *= 2;
     f.ranges[sg] = rc;
+    bool vec = f.n[sg] % 4 == 0 && f.stride[sg] % 4 == 0 && f.piece[sg] % 4 == 0 &&
+               (uintptr_t)f.part[sg] % 16 == 0;
+    for (int pc = 0; pc < 4 && vec; ++pc)
+      if ((int64_t)pc * f.piece[sg] < f.n[sg] && (uintptr_t)f.dst[sg][pc] % 16 != 0) vec = false;
+    f.vec[sg] = vec ? 1 : 0;
     f.gbase[sg] = (int)blocks;
-    blocks += (f.n[sg] + 256 / rc - 1) / (256 / rc);
+    const int64_t per_wg = (int64_t)(256 / rc) * (vec ? 4 : 1);
+    blocks += (f.n[sg] + per_wg - 1) / per_wg;
   }
   if (blocks > 0x7fffffff) return set_error(TPF_ERR_ARG, "%s: fold grid too large", fn);
   hipLaunchKernelGGL(fold_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, f);

@@ -64,6 +64,7 @@ struct FoldSegs {
   int64_t n[kFoldMaxSegs], stride[kFoldMaxSegs], piece[kFoldMaxSegs];
   int splits[kFoldMaxSegs], gbase[kFoldMaxSegs];
   int ranges[kFoldMaxSegs];  // set by fold_multi
+  int vec[kFoldMaxSegs];     // set by fold_multi: 4 elements per thread
   int nseg;
 };
 int fold_multi(FoldSegs f, hipStream_t stream, const char* fn);
