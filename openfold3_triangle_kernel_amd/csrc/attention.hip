@@ -143,13 +143,13 @@ constexpr int kFwdMaskLdsMaxN = 8192;
 //
 // Memory pipeline.  K and V tiles are staged row-major in LDS (16-byte
 // chunks XOR-swizzled per row) and double-buffered; each wave fetches its
-// share of tile t+2 into registers during tile t (buffer loads, two
-// register sets) and writes tile t+1 to LDS at the end of tile t, so a
-// tile's loads have a full tile of compute to arrive.  V^T operands come
+// share of tile t+1 into registers (buffer loads) between the two 32-key
+// blocks of tile t and writes it to the other LDS buffer at the end of tile
+// t, so the loads have one block of compute to arrive.  V^T operands come
 // from the row-major V tile through transposing LDS reads.  The prescaled
-// bias of a 32-key block (fragment-major, one 4 KiB read per wave) is loaded
-// two blocks ahead into two register sets (even / odd blocks) and seeds the
-// S^T accumulator.  Every load is issued unconditionally (past the last
+// bias of a 32-key block (fragment-major, one 4 KiB read per wave) seeds
+// the S^T accumulator; the next block's bias is loaded into the same
+// registers as soon as the current block's S MFMAs have consumed them.  Every load is issued unconditionally (past the last
 // tile or block it reloads the last one, whose copy is never consumed; lane
 // chunks past D read zeros through the buffer range check) and is visible
 // to the compiler's wait counting, and loads are issued in the
