@@ -208,21 +208,13 @@ __global__ __launch_bounds__(256) void tm_pack_weights_kernel(TmWeights w, __bf1
 // LN_in over rows of z (16 lanes per row, 8 channels per lane).  A thread
 // handles kLnRowsRPT rows 16 apart, their loads issued together.
 // ---------------------------------------------------------------------------
-#ifndef TPF_LNR_RPT
-#define TPF_LNR_RPT 2
-#endif
-#ifndef TPF_LNR_WAVES_PER_CU
-#define TPF_LNR_WAVES_PER_CU 0
-#endif
-constexpr int kLnRowsRPT = TPF_LNR_RPT;
-// Workgroups of the LN_in launch: one per 16 * kLnRowsRPT rows, or (when a
-// per-CU count is set) a grid-stride walk in which each workgroup loads its
-// next rows while it normalises the current ones.
+constexpr int kLnRowsRPT = 2;
+// Workgroups of the LN_in launch: one per 16 * kLnRowsRPT rows (the kernel
+// also walks grid-stride, loading its next rows while it normalises the
+// current ones, when launched with fewer; 8 or 16 workgroups per CU measured
+// no faster at N = 384).
 static inline int64_t tm_ln_rows_grid(int64_t R) {
-  const int64_t nb = (R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT);
-  if (TPF_LNR_WAVES_PER_CU == 0) return nb;
-  const int64_t cap = (int64_t)device_cus() * TPF_LNR_WAVES_PER_CU / 4;
-  return nb < cap ? nb : cap;
+  return (R + 16 * kLnRowsRPT - 1) / (16 * kLnRowsRPT);
 }
 template <int C>
 __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restrict__ z,
@@ -309,16 +301,14 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
 // sum of squares (two passes, as before).  Each thread then writes its 8
 // channels of its 8 rows as 16-byte stores.
 // ---------------------------------------------------------------------------
-#ifndef TPF_LNP_WGS_PER_CU
-#define TPF_LNP_WGS_PER_CU 2
-#endif
-// Workgroups of the LN_out launch per batch: one per 128-position tile, or
-// (when a per-CU count is set) a grid-stride walk over the tiles in which
-// each workgroup loads its next tile while it normalises the current one.
+// Workgroups of the LN_out launch per batch: a grid-stride walk over the
+// 128-position tiles at 2 workgroups per CU (over all batches), each loading
+// its next tile while it normalises the current one.  Tiles are independent,
+// so the results do not depend on the grid.
+constexpr int kLnPlanesWgsPerCu = 2;
 static inline int64_t tm_ln_planes_grid(int64_t NN, int64_t B) {
   const int64_t nt = (NN + 127) / 128;
-  if (TPF_LNP_WGS_PER_CU == 0) return nt;
-  const int64_t cap = ((int64_t)device_cus() * TPF_LNP_WGS_PER_CU + B - 1) / B;
+  const int64_t cap = ((int64_t)device_cus() * kLnPlanesWgsPerCu + B - 1) / B;
   return nt < cap ? nt : cap;
 }
 template <int H>
