@@ -247,6 +247,16 @@ int tpf_attn_forward_f32(const float* q, const float* k, const float* v, const f
 /* Row pitch Np (N rounded up to 8) of the channel-major a / b / x buffers. */
 int64_t tpf_trimul_plane_pitch(int64_t N);
 
+/* 1 when the bf16 TriMul kernels take a [B, N, N, C] pair (C in {32, 64, 96,
+ * 128}): every [B*N*N, C] row tensor and [B*C, N, Np] plane tensor below
+ * 2 GiB (the kernels' 32-bit buffer offsets), and, for the backward
+ * (backward != 0), the [B*N*N, 5C] dproj5 scratch too (at C = 128: N <= 2896
+ * forward, N <= 1295 backward, B = 1); else 0.  Host-only, no launch.  The
+ * reference's kernels index in 64 bits (check_pair_extent,
+ * turbopairformer_trimul_cuda.cu:147-166); larger pairs take the stock path
+ * through check_stable_trimul_support. */
+int tpf_trimul_shape_supported(int64_t B, int64_t N, int64_t C, int backward);
+
 /* Bytes of device workspace tpf_trimul_forward_bf16 needs (packed bf16 weights). */
 int64_t tpf_trimul_forward_workspace_bytes(int64_t C);
 

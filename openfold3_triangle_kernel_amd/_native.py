@@ -120,6 +120,7 @@ SIGNATURES: dict[str, tuple] = {
     "tpf_wgrad_bf16": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "tpf_trimul_wgrad_fixed_fold": (_I32, [_P, _I64, _I64, _P, _I32, _P]),
     "tpf_trimul_plane_pitch": (_I64, [_I64]),
+    "tpf_trimul_shape_supported": (_I32, [_I64, _I64, _I64, _I32]),
     "tpf_trimul_forward_workspace_bytes": (_I64, [_I64]),
     "tpf_trimul_forward_bf16": (
         _I32,

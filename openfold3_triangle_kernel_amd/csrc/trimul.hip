@@ -1885,16 +1885,32 @@ static int zero_fill(void* p, int64_t bytes, hipStream_t s, const char* fn) {
 // ---------------------------------------------------------------------------
 using namespace tpf;
 
-static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, const char* fn) {
+// Whether the kernels' 32-bit buffer offsets cover a B x N x N x C pair:
+// every row tensor of C channels and every channel-major plane tensor within
+// a 2 GiB window, and row indices within int32 / 2; the backward also holds
+// dproj5, rows of 5 C channels.
+static bool tm_extent_ok(int64_t B, int64_t N, int64_t C, bool backward) {
+  if (B < 1 || N < 1 || B > INT32_MAX || N > INT32_MAX / 8) return false;
+  const int64_t Np = (N + 7) / 8 * 8;
+  const double R = (double)B * (double)N * (double)N;
+  if (R > (double)(INT32_MAX / 2)) return false;
+  const double lim = (double)kBufOOB;
+  const int64_t pitch = backward ? 5 * C : C;
+  return R * (double)pitch * 2 < lim && (double)B * C * N * Np * 2 < lim;
+}
+
+static int tm_geom(TmGeom* g, int64_t B, int64_t N, int64_t C, int outgoing, const char* fn,
+                   bool backward) {
   if (B < 1 || N < 1) return set_error(TPF_ERR_SHAPE, "%s: B and N must be positive", fn);
   if (C != 32 && C != 64 && C != 96 && C != 128)
     return set_error(TPF_ERR_SHAPE, "%s: C=%lld must be one of 32, 64, 96, 128", fn, (long long)C);
   const int64_t Np = (N + 7) / 8 * 8;
   const int64_t R = B * N * N;
-  // 32-bit row indices in the GEMM and 2 GiB buffer windows per operand.
-  if (R * 5 * C * 2 >= (int64_t)kBufOOB || B * C * N * Np * 2 >= (int64_t)kBufOOB ||
-      R > INT32_MAX / 2)
-    return set_error(TPF_ERR_SHAPE, "%s: B=%lld N=%lld too large", fn, (long long)B, (long long)N);
+  if (!tm_extent_ok(B, N, C, backward))
+    return set_error(TPF_ERR_SHAPE,
+                     "%s: B=%lld N=%lld C=%lld too large (a %s tensor would exceed 2 GiB)", fn,
+                     (long long)B, (long long)N, (long long)C,
+                     backward ? "pair, plane or dproj5" : "pair or plane");
   g->B = (int)B; g->N = (int)N; g->Np = (int)Np; g->H = (int)C;
   g->NN = N * N; g->PS = N * Np; g->R = R; g->outgoing = outgoing ? 1 : 0;
   g->ntg = (int)((C + 63) / 64);
@@ -1955,6 +1971,11 @@ extern "C" {
 
 int64_t tpf_trimul_plane_pitch(int64_t N) { return (N + 7) / 8 * 8; }
 
+int tpf_trimul_shape_supported(int64_t B, int64_t N, int64_t C, int backward) {
+  if (C != 32 && C != 64 && C != 96 && C != 128) return 0;
+  return tm_extent_ok(B, N, C, backward != 0) ? 1 : 0;
+}
+
 int64_t tpf_trimul_forward_workspace_bytes(int64_t C) { return tm_weights_bytes(C); }
 
 int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap, const float* w_ag,
@@ -1967,7 +1988,7 @@ int tpf_trimul_forward_bf16(const void* z, const float* mask, const float* w_ap,
                             int64_t workspace_bytes, void* stream) {
   const char* fn = "tpf_trimul_forward_bf16";
   TmGeom g;
-  int rc = tm_geom(&g, B, N, C, outgoing, fn);
+  int rc = tm_geom(&g, B, N, C, outgoing, fn, false);
   if (rc) return rc;
   if (!z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !ln_in_w || !ln_in_b ||
       !ln_out_w || !ln_out_b || !out || !zln || !gate || !a || !b || !x || !xln || !mean_in ||
@@ -2102,7 +2123,7 @@ static int trimul_backward_impl(
     const char* fn) {
   float* const d_w5 = w5dst[0];
   TmGeom g;
-  int rc = tm_geom(&g, B, N, C, outgoing, fn);
+  int rc = tm_geom(&g, B, N, C, outgoing, fn, true);
   if (rc) return rc;
   if (!grad_out || !z || !mask || !w_ap || !w_ag || !w_bp || !w_bg || !w_g || !w_z || !ln_in_w ||
       !ln_out_w || !zln || !gate || !a || !b || !x || !xln || !mean_in || !rstd_in || !mean_out ||

@@ -52,7 +52,20 @@ def _f32_all(ts) -> list:
     return [p.view(t.shape) for p, t in zip(parts, ts)]
 
 
-def _check_op_inputs(z_bf, w_ap):
+def _extent_reason(B: int, N: int, C: int, backward: bool) -> str | None:
+    """Why the bf16 kernels cannot take a [B, N, N, C] pair, or None.
+
+    Their buffer offsets are 32-bit: every pair-row and channel-plane tensor
+    stays below 2 GiB, and the backward's [B*N*N, 5C] dproj5 scratch too
+    (``tpf_trimul_shape_supported``; at C = 128, B = 1: N <= 2896 forward,
+    N <= 1295 backward)."""
+    if _native.query("tpf_trimul_shape_supported", B, N, C, 1 if backward else 0):
+        return None
+    part = "backward" if backward else "forward"
+    return f"pair extent B={B} N={N} C={C} exceeds the 2 GiB buffer windows of the {part} kernels"
+
+
+def _check_op_inputs(z_bf, w_ap, backward=False):
     if z_bf.dim() != 4 or z_bf.shape[1] != z_bf.shape[2]:
         raise ValueError(f"expected square pair input [B,N,N,C], got {tuple(z_bf.shape)}")
     if z_bf.dtype != torch.bfloat16:
@@ -62,6 +75,10 @@ def _check_op_inputs(z_bf, w_ap):
         raise ValueError("TurboPairFormer TriMul requires c_hidden == c_z")
     if channels not in _SUPPORTED_CHANNELS:
         raise ValueError(f"channels must be one of {_SUPPORTED_CHANNELS}, got {channels}")
+    B, N = int(z_bf.shape[0]), int(z_bf.shape[1])
+    reason = _extent_reason(B, N, channels, backward)
+    if reason is not None:
+        raise ValueError(reason)
 
 
 @torch.library.custom_op(
@@ -209,6 +226,7 @@ def _trimul_bwd_native(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_i
     reference's [ap; ag; bp; bg; g] order, or (``named``) as the gradients of
     the named weights ``(d_p_in [ap; bp], d_g_in [ag; bg], d_w_g)``, written
     in place by the native fold (``tpf_trimul_backward_named_bf16``)."""
+    _check_op_inputs(z_bf, w_ap, backward=True)
     B, N, _, C = (int(s) for s in z_bf.shape)
     H = C
     dev = z_bf.device
@@ -387,6 +405,13 @@ def check_stable_trimul_support(module, z, mask) -> tuple[bool, str]:
             torch.broadcast_shapes(tuple(mask.shape), tuple(z.shape[:-1]))
         except RuntimeError:
             return False, "mask must broadcast to z[..., 0]"
+    # The bf16 kernels' extent (FP32 z is cast to bf16 on this path).
+    B = math.prod(int(d) for d in z.shape[:-3])
+    backward = torch.is_grad_enabled() and (
+        z.requires_grad or any(p.requires_grad for p in module.parameters()))
+    reason = _extent_reason(B, int(z.shape[-2]), C, backward)
+    if reason is not None:
+        return False, reason
     return True, "supported"
 
 

@@ -78,6 +78,32 @@ def test_shape_errors_are_reported_without_launch(lib):
                      16, None, 16, 16, 16, 16, 8, None)
 
 
+def test_trimul_shape_supported_boundaries(lib):
+    """The bf16 TriMul extent: a tensor fits the kernels' 32-bit buffer
+    windows when its bytes stay below 2^31.  Forward: [B*N*N, C] rows and
+    [B*C, N, Np] planes; backward also [B*N*N, 5C] rows.  The boundaries
+    below follow from that closed form, e.g. at C = 128, B = 1 the largest
+    forward N has N^2 * 128 * 2 < 2^31 (2896^2 * 256 = 2,147,024,896)."""
+    from openfold3_triangle_kernel_amd import _native
+
+    def ok(B, N, C, bwd):
+        return _native.query("tpf_trimul_shape_supported", B, N, C, bwd)
+
+    def fits(B, N, C, bwd):
+        Np = (N + 7) // 8 * 8
+        rows = B * N * N * (5 * C if bwd else C) * 2
+        planes = B * C * N * Np * 2
+        return int(rows < 2**31 and planes < 2**31 and B * N * N <= (2**31 - 1) // 2)
+
+    assert ok(1, 2896, 128, 0) == 1 and ok(1, 2897, 128, 0) == 0
+    assert ok(1, 1295, 128, 1) == 1 and ok(1, 1296, 128, 1) == 0
+    assert ok(1, 768, 128, 1) == 1 and ok(2, 2048, 128, 0) == 0
+    assert ok(1, 64, 48, 0) == 0 and ok(0, 64, 128, 0) == 0
+    for B, N, C in ((1, 1831, 64), (1, 1832, 64), (3, 1672, 32), (1, 4095, 32), (2, 1025, 96)):
+        for bwd in (0, 1):
+            assert ok(B, N, C, bwd) == fits(B, N, C, bwd), (B, N, C, bwd)
+
+
 def test_workspace_sizes(lib):
     from openfold3_triangle_kernel_amd import _native
 

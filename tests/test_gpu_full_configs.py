@@ -145,3 +145,39 @@ def test_trimul_full(gpu, N, outgoing):
         err = ((a.float() - b).abs().max() / b.abs().max()).item()
         print(f"trimul N{N} {'out' if outgoing else 'in'} {name} max-rel {err:.3e}", flush=True)
         assert err <= TOL, f"{name}: {err:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
+def test_trimul_forward_past_backward_extent(gpu, outgoing):
+    """N = 1320 at C = 128: past the backward's 2 GiB dproj5 window (N <= 1295)
+    but inside the forward's (N <= 2896).  Inference runs the bf16 kernels
+    (max-rel <= 2e-2 against the FP32 restatement); with gradients the support
+    verdict declines with a reason and the direct backward raises before any
+    launch."""
+    from openfold3_triangle_kernel_amd import TriangleMultiplicationOutgoing, turbo_trimul
+    from openfold3_triangle_kernel_amd.trimul import check_stable_trimul_support
+
+    N, C = 1320, 128
+    z, w, mask, _ = _trimul_case(N, C, gpu, seed=11)
+    args = (mask, w["g_in"], w["b_in"], torch.cat([w["w_ap"], w["w_bp"]]),
+            torch.cat([w["w_ag"], w["w_bg"]]), w["g_out"], w["b_out"], w["w_z"], w["w_g"])
+    direction = "outgoing" if outgoing else "incoming"
+    with torch.no_grad():
+        out = turbo_trimul(z, direction, *args)
+        ref = _trimul_ref(z.float(), mask, w, outgoing)
+        err = ((out.float() - ref).abs().max() / ref.abs().max()).item()
+    del ref
+    print(f"trimul N{N} {direction} forward max-rel {err:.3e}", flush=True)
+    assert err <= TOL, f"out: {err:.3e}"
+
+    m = TriangleMultiplicationOutgoing(C, C).to(gpu)
+    ok, reason = check_stable_trimul_support(m, z, mask)
+    assert not ok and "backward" in reason
+    with torch.no_grad():
+        assert check_stable_trimul_support(m, z, mask) == (True, "supported")
+
+    zt = z.detach().requires_grad_(True)
+    out = turbo_trimul(zt, direction, *args)
+    with pytest.raises(ValueError, match="2 GiB"):
+        torch.autograd.grad(out, zt, torch.ones_like(out))
