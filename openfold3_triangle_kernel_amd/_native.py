@@ -12,6 +12,7 @@ without its manifest/hash attestation (the library is built in-tree).
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from pathlib import Path
@@ -181,8 +182,25 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """The current HIP stream of the tensor's device (0 = null stream off-GPU)."""
-    if t.device.type != "cuda":
+    dev = t.device
+    if dev.type != "cuda":
         return 0
-    return torch.cuda.current_stream(t.device).cuda_stream
+    if _RAW_STREAM is not None and dev.index is not None:
+        return _RAW_STREAM(dev.index)  # no Stream object per call
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def device_ctx(device: torch.device):
+    """Make ``device`` current for a native call; no switch (and no guard
+    object) when it already is, which is the common case."""
+    if device.type != "cuda" or device.index is None or device.index == torch.cuda.current_device():
+        return _NO_SWITCH
+    return torch.cuda.device(device)

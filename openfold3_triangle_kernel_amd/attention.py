@@ -20,7 +20,6 @@ without a copy, and their gradients come back in the same storage order.
 
 from __future__ import annotations
 
-import contextlib
 import math
 import os
 
@@ -102,7 +101,7 @@ def _device_supported(t: torch.Tensor) -> tuple[bool, str]:
 
 
 def _device_ctx(device: torch.device):
-    return torch.cuda.device(device) if device.type == "cuda" else contextlib.nullcontext()
+    return _native.device_ctx(device)
 
 
 def is_turbopairformer_supported(q, k, v, res_mask, pair_bias) -> tuple[bool, str]:

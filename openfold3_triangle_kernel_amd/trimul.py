@@ -22,7 +22,7 @@ in this implementation's layouts (``xln`` row-major); the schema is unchanged.
 
 from __future__ import annotations
 
-import contextlib
+import functools
 import math
 
 import torch
@@ -33,7 +33,7 @@ _SUPPORTED_CHANNELS = (32, 64, 96, 128)
 
 
 def _device_ctx(device: torch.device):
-    return torch.cuda.device(device) if device.type == "cuda" else contextlib.nullcontext()
+    return _native.device_ctx(device)
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
@@ -52,17 +52,53 @@ def _f32_all(ts) -> list:
     return [p.view(t.shape) for p, t in zip(parts, ts)]
 
 
-def _extent_reason(B: int, N: int, C: int, backward: bool) -> str | None:
-    """Why the bf16 kernels cannot take a [B, N, N, C] pair, or None.
+_BUF_WINDOW = 1 << 31  # the kernels' 32-bit buffer offsets (bytes)
 
-    Their buffer offsets are 32-bit: every pair-row and channel-plane tensor
-    stays below 2 GiB, and the backward's [B*N*N, 5C] dproj5 scratch too
-    (``tpf_trimul_shape_supported``; at C = 128, B = 1: N <= 2896 forward,
-    N <= 1295 backward)."""
-    if _native.query("tpf_trimul_shape_supported", B, N, C, 1 if backward else 0):
+
+def _extent_fits(B, N, C, backward) -> bool:
+    """Closed form of ``tpf_trimul_shape_supported`` in plain arithmetic, so
+    the support verdict stays traceable under ``torch.compile``: every pair-row
+    tensor [B*N*N, C] and channel plane [B*C, N, Np] below 2 GiB, rows within
+    int32 / 2, and for the backward the [B*N*N, 5C] dproj5 scratch too (at
+    C = 128, B = 1: N <= 2896 forward, N <= 1295 backward)."""
+    rows = B * N * N
+    Np = (N + 7) // 8 * 8
+    pitch = 5 * C if backward else C
+    return (B >= 1 and N >= 1 and rows <= (2**31 - 1) // 2 and rows * pitch * 2 < _BUF_WINDOW
+            and B * C * N * Np * 2 < _BUF_WINDOW)
+
+
+def _extent_reason(B, N, C, backward) -> str | None:
+    """Why the bf16 kernels cannot take a [B, N, N, C] pair, or None."""
+    if _extent_fits(B, N, C, backward):
         return None
     part = "backward" if backward else "forward"
     return f"pair extent B={B} N={N} C={C} exceeds the 2 GiB buffer windows of the {part} kernels"
+
+
+@functools.lru_cache(maxsize=256)
+def _native_extent_ok(B: int, N: int, C: int, backward: bool) -> bool:
+    """``tpf_trimul_shape_supported``, asked once per shape (no host call per op)."""
+    return bool(_native.query("tpf_trimul_shape_supported", B, N, C, 1 if backward else 0))
+
+
+def _eager(t: torch.Tensor) -> bool:
+    """Plain tensors outside torch.compile call the ops' implementations
+    directly: the custom-op dispatch adds host time to every call, and the
+    TriMul step launches few, short kernels (the host would otherwise set its
+    pace).  Under torch.compile, and for fake or functional tensors of any
+    other tracing, the registered ops keep the graph opaque."""
+    return type(t) is torch.Tensor and not torch.compiler.is_compiling()
+
+
+def _check_devices(dev: torch.device, tensors) -> None:
+    """Every operand on the pair's GPU (the registered ops dispatch on CUDA
+    only; the direct calls check it here, before any pointer reaches a kernel)."""
+    if dev.type != "cuda":
+        raise RuntimeError("TurboPairFormer TriMul runs on GPU tensors only")
+    for t in tensors:
+        if t.device != dev:
+            raise RuntimeError(f"TurboPairFormer TriMul operands must share {dev}, got {t.device}")
 
 
 def _check_op_inputs(z_bf, w_ap, backward=False):
@@ -76,15 +112,11 @@ def _check_op_inputs(z_bf, w_ap, backward=False):
     if channels not in _SUPPORTED_CHANNELS:
         raise ValueError(f"channels must be one of {_SUPPORTED_CHANNELS}, got {channels}")
     B, N = int(z_bf.shape[0]), int(z_bf.shape[1])
-    reason = _extent_reason(B, N, channels, backward)
-    if reason is not None:
-        raise ValueError(reason)
+    if not _native_extent_ok(B, N, channels, bool(backward)):
+        raise ValueError(_extent_reason(B, N, channels, backward) or "pair extent unsupported")
 
 
-@torch.library.custom_op(
-    "openfold3_turbopairformer::_trimul_fwd_v1", mutates_args=(), device_types="cuda"
-)
-def _trimul_fwd_v1(
+def _trimul_fwd_impl(
     z_bf: torch.Tensor,
     mask_f: torch.Tensor,
     w_ap: torch.Tensor,
@@ -117,6 +149,7 @@ def _trimul_fwd_v1(
     B, N, _, C = (int(s) for s in z_bf.shape)
     H = C
     dev = z_bf.device
+    _check_devices(dev, (mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_out))
     z_bf = z_bf.contiguous()
     mask_f = mask_f.to(torch.float32).contiguous()
     Np = int(_native.query("tpf_trimul_plane_pitch", N))
@@ -157,6 +190,11 @@ def _trimul_fwd_v1(
     return (out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out)
 
 
+_trimul_fwd_v1 = torch.library.custom_op(
+    "openfold3_turbopairformer::_trimul_fwd_v1", mutates_args=(), device_types="cuda"
+)(_trimul_fwd_impl)
+
+
 @torch.library.register_fake("openfold3_turbopairformer::_trimul_fwd_v1")
 def _trimul_fwd_v1_fake(z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out,
                         b_out, outgoing, save_state):
@@ -180,10 +218,7 @@ def _trimul_fwd_v1_fake(z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_
     )
 
 
-@torch.library.custom_op(
-    "openfold3_turbopairformer::_trimul_bwd_v1", mutates_args=(), device_types="cuda"
-)
-def _trimul_bwd_v1(
+def _trimul_bwd_v1_impl(
     grad_out: torch.Tensor,
     z_bf: torch.Tensor,
     mask_f: torch.Tensor,
@@ -219,6 +254,11 @@ def _trimul_bwd_v1(
     return (d_z, d_w5, *rest)
 
 
+_trimul_bwd_v1 = torch.library.custom_op(
+    "openfold3_turbopairformer::_trimul_bwd_v1", mutates_args=(), device_types="cuda"
+)(_trimul_bwd_v1_impl)
+
+
 def _trimul_bwd_native(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in,
                        mean_out, rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out,
                        outgoing, named):
@@ -230,6 +270,8 @@ def _trimul_bwd_native(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_i
     B, N, _, C = (int(s) for s in z_bf.shape)
     H = C
     dev = z_bf.device
+    _check_devices(dev, (grad_out, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in, mean_out,
+                         rstd_out, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out))
     grad = grad_out.to(torch.bfloat16).contiguous()
     mask_f = mask_f.to(torch.float32).contiguous()
     *wts, gin, gout = _f32_all((w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out))
@@ -259,10 +301,7 @@ def _trimul_bwd_native(grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_i
     return d_z, w5, (d_wz, d_gin, d_bin, d_gout, d_bout)
 
 
-@torch.library.custom_op(
-    "openfold3_turbopairformer_amd::trimul_bwd_named", mutates_args=(), device_types="cuda"
-)
-def _trimul_bwd_named(
+def _trimul_bwd_named_impl(
     grad_out: torch.Tensor, z_bf: torch.Tensor, mask_f: torch.Tensor, z_ln: torch.Tensor,
     gate: torch.Tensor, a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, xlnT: torch.Tensor,
     mean_in: torch.Tensor, rstd_in: torch.Tensor, mean_out: torch.Tensor, rstd_out: torch.Tensor,
@@ -277,6 +316,11 @@ def _trimul_bwd_named(
         grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xlnT, mean_in, rstd_in, mean_out, rstd_out,
         w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, outgoing, named=True)
     return (d_z, *w5, *rest)
+
+
+_trimul_bwd_named = torch.library.custom_op(
+    "openfold3_turbopairformer_amd::trimul_bwd_named", mutates_args=(), device_types="cuda"
+)(_trimul_bwd_named_impl)
 
 
 @torch.library.register_fake("openfold3_turbopairformer_amd::trimul_bwd_named")
@@ -332,7 +376,8 @@ def _fwd_backward(ctx, grad_out, *unused_grads):
         return (None,) * 14
     (z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out, w_ap, w_ag,
      w_bp, w_bg, w_g, w_z, g_in, g_out, out) = ctx.saved_tensors
-    d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout = _trimul_bwd_v1(
+    bwd = _trimul_bwd_v1_impl if _eager(grad_out) else _trimul_bwd_v1
+    d_z, d_w5, d_wz, d_gin, d_bin, d_gout, d_bout = bwd(
         grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out,
         w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, g_out, out, ctx.outgoing,
     )
@@ -362,6 +407,22 @@ torch.library.register_autograd(
 )
 
 
+class _TrimulOpFn(torch.autograd.Function):
+    """``_trimul_fwd_v1`` with its registered autograd, for eager calls: the
+    same implementation, context and backward as the op, without the custom-op
+    dispatch (``_eager``)."""
+
+    @staticmethod
+    def forward(ctx, *inputs):
+        output = _trimul_fwd_impl(*inputs)
+        _fwd_setup_context(ctx, inputs, output)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_out, *unused_grads):
+        return _fwd_backward(ctx, grad_out, *unused_grads)
+
+
 def _run_trimul(z, mask, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_out, outgoing):
     """Flatten the batch prefix, run the custom op, restore shape and dtype."""
     if mask is None:
@@ -376,7 +437,11 @@ def _run_trimul(z, mask, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_
     mask_f = mask.expand(*orig_shape[:-1]).reshape(batch, N, N).to(torch.float32).contiguous()
     inputs = (z_bf, mask_f, w_ap, w_ag, w_bp, w_bg, w_g, w_z, g_in, b_in, g_out, b_out)
     save_state = any(t.requires_grad for t in inputs)
-    out = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(*inputs, bool(outgoing), save_state)[0]
+    if _eager(z_bf):
+        out = _TrimulOpFn.apply(*inputs, bool(outgoing), save_state)[0]
+    else:
+        out = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(*inputs, bool(outgoing),
+                                                                 save_state)[0]
     return out.view(orig_shape).to(z.dtype)
 
 
@@ -406,7 +471,9 @@ def check_stable_trimul_support(module, z, mask) -> tuple[bool, str]:
         except RuntimeError:
             return False, "mask must broadcast to z[..., 0]"
     # The bf16 kernels' extent (FP32 z is cast to bf16 on this path).
-    B = math.prod(int(d) for d in z.shape[:-3])
+    B = 1
+    for d in z.shape[:-3]:
+        B = B * d
     backward = torch.is_grad_enabled() and (
         z.requires_grad or any(p.requires_grad for p in module.parameters()))
     reason = _extent_reason(B, int(z.shape[-2]), C, backward)
@@ -518,8 +585,8 @@ class _TurboTrimulFn(torch.autograd.Function):
                 n_out_b, outgoing):
         H = int(p_in.shape[0]) // 2
         ws = (p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w)
-        res = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(
-            z_bf, mask_f, *ws, n_in_w, n_in_b, n_out_w, n_out_b, bool(outgoing), True)
+        fwd = _trimul_fwd_impl if _eager(z_bf) else torch.ops.openfold3_turbopairformer._trimul_fwd_v1
+        res = fwd(z_bf, mask_f, *ws, n_in_w, n_in_b, n_out_w, n_out_b, bool(outgoing), True)
         out, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out, rstd_out = res
         ctx.save_for_backward(z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
                               rstd_out, p_in, g_in, g_out_w, p_out_w, n_in_w, n_out_w, out)
@@ -535,7 +602,8 @@ class _TurboTrimulFn(torch.autograd.Function):
         H = int(p_in.shape[0]) // 2
         # The native fold writes d(p_in) = [d a_p; d b_p] and d(g_in) =
         # [d a_g; d b_g] in place: no row gather of a [5H, C] d_w5.
-        grads = _trimul_bwd_named(
+        bwd = _trimul_bwd_named_impl if _eager(grad_out) else _trimul_bwd_named
+        grads = bwd(
             grad_out, z_bf, mask_f, z_ln, gate, a, b, x, xln, mean_in, rstd_in, mean_out,
             rstd_out, p_in[:H], g_in[:H], p_in[H:], g_in[H:], g_out_w, p_out_w, n_in_w, n_out_w,
             ctx.outgoing)

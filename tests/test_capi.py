@@ -103,6 +103,15 @@ def test_trimul_shape_supported_boundaries(lib):
         for bwd in (0, 1):
             assert ok(B, N, C, bwd) == fits(B, N, C, bwd), (B, N, C, bwd)
 
+    # The host layer's traceable restatement agrees with the library.
+    from openfold3_triangle_kernel_amd.trimul import _extent_fits
+
+    for B in (1, 2, 3):
+        for N in (1, 64, 1295, 1296, 1831, 1832, 2048, 2896, 2897, 4095, 4096):
+            for C in (32, 64, 96, 128):
+                for bwd in (0, 1):
+                    assert int(_extent_fits(B, N, C, bool(bwd))) == ok(B, N, C, bwd), (B, N, C, bwd)
+
 
 def test_workspace_sizes(lib):
     from openfold3_triangle_kernel_amd import _native
