@@ -563,9 +563,9 @@ def turbo_trimul(
     if torch.is_grad_enabled() and any(t.requires_grad for t in (z_bf,) + params):
         out = _TurboTrimulFn.apply(z_bf, mask_f, *params, direction == "outgoing")
     else:  # no autograd: no saved state (the op's save_state rule)
-        out = torch.ops.openfold3_turbopairformer._trimul_fwd_v1(
-            z_bf, mask_f, p_in_weight[:H], g_in_weight[:H], p_in_weight[H:], g_in_weight[H:],
-            g_out_weight, p_out_weight, *params[4:], direction == "outgoing", False)[0]
+        fwd = _trimul_fwd_impl if _eager(z_bf) else torch.ops.openfold3_turbopairformer._trimul_fwd_v1
+        out = fwd(z_bf, mask_f, p_in_weight[:H], g_in_weight[:H], p_in_weight[H:], g_in_weight[H:],
+                  g_out_weight, p_out_weight, *params[4:], direction == "outgoing", False)[0]
     return out.view(orig_shape).to(z.dtype)
 
 

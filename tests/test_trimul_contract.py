@@ -101,3 +101,20 @@ def test_turbo_trimul_rejects_bad_direction_and_shapes():
         turbo_trimul(z, direction="sideways")
     with pytest.raises(ValueError, match="p_in_weight"):
         turbo_trimul(z, p_in_weight=torch.zeros(32, 32))
+
+
+def test_eager_trimul_rejects_host_tensors_before_any_launch(monkeypatch):
+    """Eager calls run the op implementations directly (not through the CUDA-only
+    custom-op dispatch): host tensors must be refused before a pointer reaches
+    the library.  The native entry points are replaced by a tripwire."""
+    from openfold3_triangle_kernel_amd import _native, turbo_trimul
+
+    def tripwire(*args, **kwargs):
+        raise AssertionError("a native entry point was called with host tensors")
+
+    monkeypatch.setattr(_native, "call", tripwire)
+    z = torch.zeros(1, 8, 8, 32, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        turbo_trimul(z)
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        turbo_trimul(z.requires_grad_(True))
