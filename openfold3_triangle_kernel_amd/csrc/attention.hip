@@ -303,17 +303,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 
   // Tiles whose 64 mask entries are all zero in every plane skip the mask
   // add (uniform flags); computed up front so no wait on the mask sits
-  // inside the pipelined loop.
-  uint64_t mbits = ~0ull;
-  if (ntiles <= 64) mbits = 0ull;
+  // inside the pipelined loop.  Each wave ballots the 64-key tiles it
+  // stages (its 64 lanes take one tile per pass; N % 64 == 0), so the flags
+  // cost no round trips to memory beyond the staging loads (one ballot
+  // load per tile and plane measured 3 us slower at N = 384); the waves'
+  // words meet after the first barrier of the tile loop.
+  __shared__ uint64_t Mw[NW];
+  uint64_t wbits = 0ull;
 #pragma unroll
   for (int p = 0; p < PL; ++p) {
     const float* mrow = mask + (int64_t)plane[p] * N;
-    for (int i = tid; i < N; i += 64 * NW) Ms[p * N + i] = mrow[i] * inv_scale;
-    if (ntiles <= 64)
-      for (int t = 0; t < ntiles; ++t)
-        if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
+    for (int i = tid; i < N; i += 64 * NW) {
+      const float mv = mrow[i];
+      Ms[p * N + i] = mv * inv_scale;
+      if (__any(mv != 0.f)) wbits |= 1ull << ((i >> 6) & 63);
+    }
   }
+  if (lane == 0) Mw[w] = ntiles <= 64 ? wbits : ~0ull;
+  uint64_t mbits = ~0ull;
+  bool mbits_ready = false;
 
   // Pipeline fill: K / V of tile 0 (to LDS), bias of block 0.
   bf16x8 kvr[CPT];
@@ -429,6 +437,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
 #pragma unroll 1
   for (int t = 0; t < ntiles; ++t) {
     __syncthreads();
+    if (!mbits_ready) {  // after the loop's first barrier: every wave's word is in
+      mbits = 0ull;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) mbits |= Mw[ww];
+      mbits_ready = true;
+    }
     const bool masked = (mbits >> (t & 63)) & 1ull;
     block(t & 1, 0, 2 * t, masked, t * 64);
     load_kv(t + 1, kvr);

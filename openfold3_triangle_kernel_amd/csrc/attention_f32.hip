@@ -133,9 +133,16 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(
   const int ntiles = N / 64;
   uint64_t mbits = ~0ull;
   if (ntiles <= 64) {
+    // Four tiles' mask loads in flight per ballot round.
     mbits = 0ull;
-    for (int t = 0; t < ntiles; ++t)
-      if (__any(mrow[t * 64 + lane] != 0.f)) mbits |= 1ull << t;
+    for (int t = 0; t < ntiles; t += 4) {
+      float mv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mv[u] = t + u < ntiles ? mrow[(t + u) * 64 + lane] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (__any(mv[u] != 0.f)) mbits |= 1ull << (t + u);
+    }
   }
   auto load_bias = [&](int blk) {
     f32x16 r;
