@@ -301,6 +301,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
     return r;
   };
 
+  // Pipeline fill issued first: K / V of tile 0 and the bias of block 0 are
+  // in flight while the mask rows are staged (−0.7 us at N = 384).
+  bf16x8 kvr[CPT];
+  load_kv(0, kvr);
+  f32x16 bset = load_bias(0);
   // Tiles whose 64 mask entries are all zero in every plane skip the mask
   // add (uniform flags); computed up front so no wait on the mask sits
   // inside the pipelined loop.  Each wave ballots the 64-key tiles it
@@ -323,10 +328,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3, 8)))
   uint64_t mbits = ~0ull;
   bool mbits_ready = false;
 
-  // Pipeline fill: K / V of tile 0 (to LDS), bias of block 0.
-  bf16x8 kvr[CPT];
-  load_kv(0, kvr);
-  f32x16 bset = load_bias(0);
   store_kv(0, kvr);
 
   f32x16 acc[PL][DP / 32];
