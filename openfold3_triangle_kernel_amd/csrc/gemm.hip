@@ -33,8 +33,8 @@ using namespace gk32;
 // dst[i / piece][i % piece].  Every element's order depends only on the
 // shapes (the grouping changes no sum).
 // Splits per range: 32 (two batches of 16 loads per thread) measured
-// 13.8 -> 12.2 us against 16 on the TriMul weight-gradient fold at N=384
-// (8 and 4: 18.3 and 26.8 us; 64: 13.9 us).
+// 13.8 -> 12.2 us against 16 on the TriMul weight-gradient fold at N=768
+// (8 and 4: 18.3 and 26.8 us; 64: 13.9 us), 14.4 -> 12.8 us at N=384.
 constexpr int kFoldRangeSplits = 32;
 
 template <int EPT>

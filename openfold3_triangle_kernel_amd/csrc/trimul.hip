@@ -292,14 +292,17 @@ __global__ __launch_bounds__(256) void tm_ln_rows_kernel(const __bf16* __restric
 
 // ---------------------------------------------------------------------------
 // LN_out over the channels of the channel-major product x, written as
-// row-major xln.  Workgroup = 128 positions (natural order) x all channels;
-// thread = (8-position group pg = tid % 16, 8-channel group cg = tid / 16):
-// it reads its 8 channels' 16-byte position runs (coalesced along pg) and
-// keeps the 8 x 8 block in registers, so no LDS transpose is needed.  Per-
-// position sums over channels: the 4 channel groups of a wave by shuffles,
-// the 4 waves through LDS in fixed order; mean first, then the centred
-// sum of squares (two passes, as before).  Each thread then writes its 8
-// channels of its 8 rows as 16-byte stores.
+// row-major xln.  Workgroup = 128 positions (natural order) x up to 128
+// channels; wave = (64-position half wv / 2) x (64-channel half wv % 2);
+// lane = (8-position group pg = lane % 8, 8-channel group lane / 8): it
+// reads its 8 channels' 16-byte position runs (128-byte runs per plane
+// along pg) and keeps the 8 x 8 block in registers, so no LDS transpose is
+// needed.  Per-position sums over channels: the 8 channel groups of a wave
+// by lane exchanges, the two channel halves through LDS; mean first, then
+// the centred sum of squares.  Each thread then writes its 8 channels of
+// its 8 rows as 16-byte stores, so a store instruction covers 8 rows x 128
+// contiguous bytes (16 rows x 64 bytes with 16 position groups per wave:
+// 17.3 -> 16.4 us at N=384, C=128).
 // ---------------------------------------------------------------------------
 // Workgroups of the LN_out launch per batch: a grid-stride walk over the
 // 128-position tiles at 2 workgroups per CU (over all batches), each loading
@@ -320,9 +323,10 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
                                                            float* __restrict__ rstd_out,
                                                            TmGeom g) {
   constexpr int T = 128;  // positions per tile
-  __shared__ float red[2][4][16][8];
-  const int tid = threadIdx.x, wv = tid >> 6, b = blockIdx.y;
-  const int pg = tid & 15, cg = tid >> 4;
+  __shared__ float red[2][4][8][8];
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, b = blockIdx.y;
+  const int pg = lane & 7, cg = (lane >> 3) + 8 * (wv & 1);
+  const int p0 = 64 * (wv >> 1) + pg * 8;  // first position in the tile
   const bool chan = cg * 8 < H;
   const int64_t nt = (g.NN + T - 1) / T;
   const bool vec = g.Np == g.N;
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
   // v[c][e]: channel cg*8 + c, position pb + e of tile t.  Full tiles of
   // unpadded planes load unconditionally, 16 bytes per channel.
   auto load = [&](int64_t t, bf16x8 (&v)[8]) {
-    const int64_t pb = t * T + pg * 8;
+    const int64_t pb = t * T + p0;
     if (vec && pb + 8 <= g.NN) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) v[c] = ld8(x + ((int64_t)b * H + cgl * 8 + c) * g.PS + pb);
@@ -360,15 +364,15 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
   // the two sums of a tile use the two halves of `red`, so one barrier each.
   auto channel_sum = [&](float (&q)[8], int half) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = xor32_sum(xor16_sum(q[e]));
-    if ((tid & 48) == 0) {
+    for (int e = 0; e < 8; ++e) q[e] = xor32_sum(xor16_sum(q[e] + dpp_f<kDppXor8>(q[e])));
+    if ((lane & 56) == 0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) red[half][wv][pg][e] = q[e];
     }
     __syncthreads();
+    const int w0 = wv & 2;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      q[e] = ((red[half][0][pg][e] + red[half][1][pg][e]) + red[half][2][pg][e]) + red[half][3][pg][e];
+    for (int e = 0; e < 8; ++e) q[e] = red[half][w0][pg][e] + red[half][w0 + 1][pg][e];
   };
   bf16x8 nxt[8];
   int64_t t = blockIdx.x;
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(256) void tm_ln_planes_kernel(const __bf16* __restr
 #pragma unroll
     for (int c = 0; c < 8; ++c) v[c] = chan ? nxt[c] : zero8();
     if (t + gridDim.x < nt) load(t + gridDim.x, nxt);
-    const int64_t pb = t * T + pg * 8;  // first position of this thread
+    const int64_t pb = t * T + p0;  // first position of this thread
     float mean[8], rstd[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
